@@ -1,0 +1,230 @@
+/*
+ * intent_amd.h — C ABI of the MI355X (gfx950) quantized-contraction library.
+ *
+ * One flat C entry per kernel family. Every view is passed as a device pointer
+ * plus int64 extents and an int64 leading (row) stride in ELEMENTS; the inner
+ * axis must be unit-stride. This is the slot model the reference host uses for
+ * natively compiled entries (python/intent/runtime/native.py:14-120: pointer,
+ * extent and stride slots per view, one C symbol per entry), with three
+ * additions:
+ *   - a `stream` argument (a hipStream_t passed as void*): launches are
+ *     asynchronous on that stream, as GPU artifact calls run on the provider's
+ *     current stream (python/intent/runtime/artifact.py:149-162);
+ *   - an int status return (INTENT_OK or a negative INTENT_ERR_* code) instead
+ *     of void (python/intent/runtime/mojo/program.py:255);
+ *   - intent_amd_last_error(), a thread-local message for the last failure.
+ *
+ * The library never allocates user-visible memory: outputs and workspaces
+ * belong to the caller. No entry synchronises the stream.
+ *
+ * Quantized formats (row-major, K contiguous):
+ *   W4 asymmetric group quant: packed uint8 [N, K/2]; byte j of row n holds
+ *       k = 2j in its low nibble and k = 2j+1 in its high nibble; scales f16
+ *       [N, K/group]; zeros uint8 [N, K/group] (values 0..15);
+ *       w[n,k] = (q[n,k] - zero[n,k/g]) * scale[n,k/g].
+ *   W8 per-channel symmetric: int8 [N, K]; scales f16 [N]; w = q * scale[n].
+ *   W8A8: int8 activations [M, K] with f32 per-token scales [M]; int8 weights
+ *       [N, K] with f32 per-channel scales [N].
+ */
+#ifndef INTENT_AMD_H
+#define INTENT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define INTENT_AMD_ABI_VERSION 1
+
+#define INTENT_OK 0
+#define INTENT_ERR_INVALID_ARGUMENT (-1) /* bad extent, stride, null pointer */
+#define INTENT_ERR_ALIGNMENT (-2)        /* pointer/stride not 16-byte aligned */
+#define INTENT_ERR_UNSUPPORTED (-3)      /* shape outside what the kernels cover */
+#define INTENT_ERR_LAUNCH (-4)           /* HIP launch or device query failed */
+#define INTENT_ERR_WORKSPACE (-5)        /* workspace too small */
+
+/* Library facts. */
+int intent_amd_abi_version(void);
+const char* intent_amd_last_error(void);
+/* Writes the gcnArchName of `device` into buf; returns INTENT_OK or an error. */
+int intent_amd_device_arch(int device, char* buf, int64_t buf_len);
+
+/*
+ * W8A16: y[m,n] = f16( scale[n] * sum_k f32(x[m,k]) * f32(w[n,k]) ), fp32
+ * accumulation.
+ * Replaces: weight-only int8 contraction written as I.cast(W_i8, f16) ->
+ * I.matmul(acc_dtype=f32) -> scale (doc/dsl/core.en.md:246,
+ * lib/Conversion/KIRToCPU/Contractions.cpp:12-41).
+ * x f16 [M,K] (stride x_ld); w int8 [N,K] (w_ld); scales f16 [N]; y f16 [M,N].
+ * Requires K % 64 == 0.
+ */
+int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld,
+                        const int8_t* w, int64_t N, int64_t w_ld,
+                        const void* scales,
+                        void* y, int64_t y_ld, void* stream);
+
+/*
+ * W4A16 asymmetric group-dequant contraction:
+ * y[m,n] = f16( sum_k f32(x[m,k]) * (q[n,k] - z[n,k/g]) * s[n,k/g] ).
+ * Replaces weight_only_int4_matmul (examples/kernels/contraction/
+ * weight_only_int4.py:18-51; CPU oracle experiments/cpu/baselines/pytorch/
+ * cpu_runtime.py:97-102) for the asymmetric uint4, [N, K/2]-packed format.
+ * Requires K % 128 == 0 and group % 32 == 0, K % group == 0.
+ * `intent_w4a16_matmul` picks the decode GEMV kernel for M <= 16 and the
+ * MFMA tile kernel otherwise; the _gemv / _gemm entries force one kernel.
+ */
+int intent_w4a16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld,
+                        const uint8_t* packed, int64_t N, int64_t packed_ld,
+                        const void* scales, const uint8_t* zeros, int64_t qparam_ld,
+                        int64_t group_size,
+                        void* y, int64_t y_ld, void* stream);
+int intent_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t x_ld,
+                      const uint8_t* packed, int64_t N, int64_t packed_ld,
+                      const void* scales, const uint8_t* zeros, int64_t qparam_ld,
+                      int64_t group_size,
+                      void* y, int64_t y_ld, void* stream);
+int intent_w4a16_gemm(const void* x, int64_t M, int64_t K, int64_t x_ld,
+                      const uint8_t* packed, int64_t N, int64_t packed_ld,
+                      const void* scales, const uint8_t* zeros, int64_t qparam_ld,
+                      int64_t group_size,
+                      void* y, int64_t y_ld, void* stream);
+
+/*
+ * W8A8: out[m,n] = bf16( f32(acc[m,n]) * a_scale[m] * w_scale[n] ), with
+ * acc[m,n] = sum_k i32(a[m,k]) * i32(w[n,k]) computed exactly in int32
+ * (modulo 2^32). The two multiplies are evaluated left to right in fp32 and
+ * rounded to bf16 to nearest-even.
+ * Replaces the integer contraction branch (lib/Conversion/KIRToCPU/
+ * Contractions.cpp:30-35,79-80) plus per-token/per-channel scale epilogue
+ * (examples/kernels/contraction/gemm.py:83-106 pattern).
+ * Requires K % 64 == 0.
+ */
+int intent_w8a8_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                     const float* a_scales,
+                     const int8_t* w, int64_t N, int64_t w_ld,
+                     const float* w_scales,
+                     void* out, int64_t out_ld, void* stream);
+
+/*
+ * int8 x int8 -> int32 contraction with optional int32 bias (nullable):
+ * c[m,n] = sum_k i32(a[m,k]) * i32(w[n,k]) + bias[n], modulo 2^32.
+ * Replaces gemm_i8 (examples/kernels/contraction/gemm.py:29-39), with the
+ * weight given K-contiguous as [N, K]. Requires K % 64 == 0.
+ */
+int intent_i8_gemm_i32(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                       const int8_t* w, int64_t N, int64_t w_ld,
+                       const int32_t* bias,
+                       int32_t* c, int64_t c_ld, void* stream);
+
+/*
+ * MoE router: per token, top_k experts by logit (ties -> lower expert index)
+ * and their softmax probabilities (fp32, over all E experts; renormalised
+ * over the selected top_k when `renormalize` != 0).
+ * No reference counterpart exists (the reference takes topk_ids as an input,
+ * experiments/_common/support.py:113-130); this is the producer of that input.
+ * logits f32 [T,E]; topk_ids i32 [T,top_k]; topk_weights f32 [T,top_k].
+ * Requires 1 <= top_k <= min(E, 8), E <= 256.
+ */
+int intent_moe_route(const float* logits, int64_t T, int64_t E, int64_t top_k,
+                     int renormalize, int32_t* topk_ids, float* topk_weights,
+                     void* stream);
+
+/*
+ * MoE alignment: expert histogram, block-padded exclusive prefix, STABLE
+ * scatter of route ids (route = token*top_k + choice) into expert segments,
+ * and the expert id of every block.
+ * Replaces moe_count_routes / moe_prefix_routes / moe_scatter_routes /
+ * moe_mark_expert_blocks (examples/kernels/routing/moe_align.py:14-86) as
+ * composed by MoEAlignment (examples/programs/composition.py:134-174), with
+ * the deterministic order of moe_align_block_size
+ * (experiments/cpu/baselines/pytorch/cpu_runtime.py:1081-1098).
+ *   sorted_route_ids i32 [capacity], capacity >= R + E*(block_size-1),
+ *     R = T*top_k; unused slots hold the sentinel R;
+ *   expert_blocks i32 [num_blocks], num_blocks >= ceil(capacity/block_size);
+ *     blocks past the padded total hold -1;
+ *   expert_offsets i32 [E+1]; total_padded i32 [1].
+ * Route ids whose expert is outside [0,E) are dropped.
+ * Requires E <= 512.
+ */
+int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_k, int64_t E,
+                     int64_t block_size,
+                     int32_t* sorted_route_ids, int64_t capacity,
+                     int32_t* expert_blocks, int64_t num_blocks,
+                     int32_t* expert_offsets, int32_t* total_padded, void* stream);
+
+/*
+ * Grouped W4 gate/up projection with SiLU gating over the aligned routes:
+ * for every padded row p with route r = sorted_route_ids[p] < R, token
+ * t = r / top_k and expert e = expert_blocks[p / block_size]:
+ *   g[f] = sum_h x[t,h] * Wgu[e][f, h],  u[f] = sum_h x[t,h] * Wgu[e][F+f, h]
+ *   act[p,f] = f16( silu(g) * u ),  silu(g) = g / (1 + exp(-g))  (fp32)
+ * Rows with r == R are written as zeros.
+ * Wgu: packed [E][2F, H/2], scales f16 / zeros u8 [E][2F, H/g].
+ * act f16 [num_blocks*block_size, F].
+ * Replaces the first contraction + activation of moe_expert_ffn
+ * (examples/kernels/ragged/moe.py:28-45) for SiLU-gated W4 experts.
+ * Requires block_size == 128, H % 128 == 0, F % 64 == 0.
+ */
+int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_t x_ld,
+                          const int32_t* sorted_route_ids, const int32_t* expert_blocks,
+                          int64_t num_blocks, int64_t block_size, int64_t top_k,
+                          const uint8_t* w_packed, const void* w_scales,
+                          const uint8_t* w_zeros, int64_t E, int64_t F, int64_t group_size,
+                          void* act, int64_t act_ld, void* stream);
+
+/*
+ * Grouped W4 down projection: for every padded row p with route r < R,
+ *   out[r, d] = sum_f f32(act[p,f]) * Wd[e][d, f]   (fp32 result)
+ * Wd: packed [E][H, F/2], scales/zeros [E][H, F/g]; out f32 [R, H].
+ * Replaces the second contraction of moe_expert_ffn
+ * (examples/kernels/ragged/moe.py:46-53).
+ * Requires block_size == 128, F % 128 == 0.
+ */
+int intent_moe_down_w4(const void* act, int64_t act_ld,
+                       const int32_t* sorted_route_ids, const int32_t* expert_blocks,
+                       int64_t num_blocks, int64_t block_size, int64_t R,
+                       const uint8_t* w_packed, const void* w_scales,
+                       const uint8_t* w_zeros, int64_t E, int64_t H, int64_t F,
+                       int64_t group_size,
+                       float* out, int64_t out_ld, void* stream);
+
+/*
+ * Weighted combine: y[t,:] += w[t,0]*out[t*k+0,:]; y[t,:] += w[t,1]*out[...]
+ * ... slot by slot in order (each step one fp32 multiply then one fp32 add).
+ * Replaces the scatter_reduce(add) of moe_expert_ffn
+ * (examples/kernels/ragged/moe.py:48-53), in a fixed order.
+ * y f32 [T,H] is read and written.
+ */
+int intent_moe_combine(const float* route_out, int64_t out_ld,
+                       const float* topk_weights, int64_t T, int64_t top_k,
+                       float* y, int64_t H, int64_t y_ld, void* stream);
+
+/*
+ * Whole quantized MoE expert FFN from router logits: route -> align ->
+ * gate/up(SiLU) -> down -> combine into y (f32 [T,H], accumulated).
+ * Replaces moe_expert_ffn (examples/kernels/ragged/moe.py:12-53) together
+ * with its host alignment (examples/programs/composition.py:134-174).
+ * `workspace` must hold intent_moe_workspace_size(...) bytes (16-byte aligned).
+ * block_size is 128. If topk_ids_out / topk_weights_out are non-null the
+ * routing results are also copied there ([T,top_k] each).
+ */
+size_t intent_moe_workspace_size(int64_t T, int64_t top_k, int64_t E, int64_t H,
+                                 int64_t F, int64_t block_size);
+int intent_moe_expert_ffn_w4(const float* router_logits, const void* x, int64_t T,
+                             int64_t H, int64_t E, int64_t top_k, int renormalize,
+                             const uint8_t* wgu_packed, const void* wgu_scales,
+                             const uint8_t* wgu_zeros,
+                             const uint8_t* wd_packed, const void* wd_scales,
+                             const uint8_t* wd_zeros,
+                             int64_t F, int64_t group_size,
+                             float* y, void* workspace, size_t workspace_bytes,
+                             int32_t* topk_ids_out, float* topk_weights_out,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INTENT_AMD_H */

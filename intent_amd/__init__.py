@@ -1,0 +1,48 @@
+"""intent_amd — MI355X-native (gfx950) quantized-contraction hot path of IntentDSL.
+
+Operator surface (same names and behaviour as the reference's
+``intent.compile`` / ``CompiledArtifact``):
+
+    import intent_amd as intent
+    art = intent.compile(intent.weight_only_int4_asym_matmul, target=intent.MI355XTarget())
+    y = art.run(x, packed, scales, zeros)          # allocates the Out buffer
+    art(x, packed, scales, zeros, y)               # explicit outputs
+    op = art.as_torch_op("mylib::w4a16")           # torch custom op
+
+Every definition is backed by hand-written HIP kernels in
+``intent_amd/_lib/libintent_amd.so`` (C ABI: ``include/intent_amd.h``).
+"""
+from .artifact import CompiledArtifact
+from .compiler import CompileOptions, MI355XTarget, compile
+from .definitions import (
+    ALL_DEFINITIONS,
+    KernelDefinition,
+    gemm_i8_nt,
+    moe_align_block_size,
+    moe_combine,
+    moe_down_w4,
+    moe_expert_ffn_w4,
+    moe_gate_up_w4,
+    moe_route_topk,
+    w8a8_scaled_matmul,
+    weight_only_int4_asym_matmul,
+    weight_only_int8_matmul,
+)
+from .errors import CompilationStageError, LanguageUseError, NativeLibraryError
+from .interface import DType, PublicInterface, ScalarParameter, ViewKind, ViewParameter
+
+
+def kernel(function=None):
+    """The reference's ``@intent.kernel`` compiles arbitrary DSL functions; this
+    build only ships the fixed quantized-contraction definitions."""
+    raise NotImplementedError("intent_amd compiles only its fixed quantized-contraction definitions "
+                              f"({', '.join(d.name for d in ALL_DEFINITIONS)})")
+
+
+__all__ = [
+    "ALL_DEFINITIONS", "CompilationStageError", "CompileOptions", "CompiledArtifact", "DType", "KernelDefinition",
+    "LanguageUseError", "MI355XTarget", "NativeLibraryError", "PublicInterface", "ScalarParameter", "ViewKind",
+    "ViewParameter", "compile", "gemm_i8_nt", "kernel", "moe_align_block_size", "moe_combine", "moe_down_w4",
+    "moe_expert_ffn_w4", "moe_gate_up_w4", "moe_route_topk", "w8a8_scaled_matmul", "weight_only_int4_asym_matmul",
+    "weight_only_int8_matmul",
+]

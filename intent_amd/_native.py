@@ -1,0 +1,92 @@
+"""ctypes binding of ``libintent_amd.so`` (the C ABI in ``include/intent_amd.h``).
+
+The reference binds natively compiled entries the same way: ``ctypes.CDLL``
+plus one flat C symbol per entry with pointer / int64 extent slots
+(python/intent/runtime/native_artifact.py:194-262, runtime/native.py:14-120).
+There is no fallback: if the library is missing every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+from .errors import INTENT_OK, NativeLibraryError, status_error
+
+PACKAGE = Path(__file__).resolve().parent
+LIBRARY_PATH = PACKAGE / "_lib" / "libintent_amd.so"
+ABI_VERSION = 1
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+INT = ctypes.c_int
+SIZE = ctypes.c_size_t
+
+# Entry -> (argtypes, restype). Mirrors include/intent_amd.h.
+SIGNATURES: dict[str, tuple[list, object]] = {
+    "intent_amd_abi_version": ([], INT),
+    "intent_amd_last_error": ([], ctypes.c_char_p),
+    "intent_amd_device_arch": ([INT, ctypes.c_char_p, I64], INT),
+    "intent_w8a16_matmul": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P], INT),
+    "intent_w4a16_matmul": ([P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, I64, P], INT),
+    "intent_w4a16_gemv": ([P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, I64, P], INT),
+    "intent_w4a16_gemm": ([P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, I64, P], INT),
+    "intent_w8a8_gemm": ([P, I64, I64, I64, P, P, I64, I64, P, P, I64, P], INT),
+    "intent_i8_gemm_i32": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P], INT),
+    "intent_moe_route": ([P, I64, I64, I64, INT, P, P, P], INT),
+    "intent_moe_align": ([P, I64, I64, I64, I64, P, I64, P, I64, P, P, P], INT),
+    "intent_moe_gate_up_w4": ([P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, P], INT),
+    "intent_moe_down_w4": ([P, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, I64, P, I64, P], INT),
+    "intent_moe_combine": ([P, I64, P, I64, I64, P, I64, I64, P], INT),
+    "intent_moe_workspace_size": ([I64, I64, I64, I64, I64, I64], SIZE),
+    "intent_moe_expert_ffn_w4": ([P, P, I64, I64, I64, I64, INT, P, P, P, P, P, P, I64, I64, P, P, SIZE, P, P, P],
+                                 INT),
+}
+
+_lock = threading.Lock()
+_library: ctypes.CDLL | None = None
+
+
+def library() -> ctypes.CDLL:
+    """Load (once) and return the gfx950 library; raises if it is not built."""
+    global _library
+    if _library is not None:
+        return _library
+    with _lock:
+        if _library is not None:
+            return _library
+        if not LIBRARY_PATH.exists():
+            raise NativeLibraryError(
+                f"{LIBRARY_PATH} is not built; run `python -m intent_amd.build` (hipcc, gfx950). "
+                "There is no CPU fallback for the quantized-contraction kernels.")
+        lib = ctypes.CDLL(str(LIBRARY_PATH))
+        for name, (argtypes, restype) in SIGNATURES.items():
+            try:
+                fn = getattr(lib, name)
+            except AttributeError as error:
+                raise NativeLibraryError(f"{LIBRARY_PATH} does not export {name}") from error
+            fn.argtypes = argtypes
+            fn.restype = restype
+        version = lib.intent_amd_abi_version()
+        if version != ABI_VERSION:
+            raise NativeLibraryError(f"ABI version {version} != expected {ABI_VERSION}")
+        _library = lib
+        return lib
+
+
+def last_error() -> str:
+    raw = library().intent_amd_last_error()
+    return raw.decode("utf-8", "replace") if raw else ""
+
+
+def call(entry: str, *arguments) -> None:
+    """Invoke an int-status entry and raise the mapped exception on failure."""
+    status = getattr(library(), entry)(*arguments)
+    if status != INTENT_OK:
+        raise status_error(status, entry, last_error())
+
+
+def device_arch(device: int) -> str:
+    buf = ctypes.create_string_buffer(128)
+    call("intent_amd_device_arch", device, buf, len(buf))
+    return buf.value.decode()

@@ -1,0 +1,27 @@
+// Host-side helpers shared by the entry points (error state, checks).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/intent_amd.h"
+
+namespace intent {
+
+// Records a formatted message for intent_amd_last_error() and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Clears the thread's error message.
+void clear_error();
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks hipGetLastError() after a launch.
+int launch_status(const char* kernel);
+
+}  // namespace intent
+
+#define INTENT_REQUIRE(cond, code, ...)            \
+  do {                                             \
+    if (!(cond)) return ::intent::fail(code, __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,437 @@
+// Quantized MoE on gfx950: router top-k, deterministic alignment, grouped W4
+// gate/up (+SiLU) and down projections, fixed-order weighted combine.
+#include <math.h>
+
+#include "common.h"
+#include "gemm_f16.h"
+#include "internal.h"
+
+namespace {
+
+using namespace gemm;
+
+constexpr int kMaxTopK = 8;
+constexpr int kMaxRouteExperts = 256;
+constexpr int kAlignThreads = 1024;
+constexpr int kAlignWaves = kAlignThreads / 64;
+constexpr int kMaxAlignExperts = 512;
+
+// ---- router ---------------------------------------------------------------
+// One thread per token. Selection compares raw logits (softmax is monotonic),
+// strictly greater wins, so ties keep the lower expert index.
+__global__ void moe_route_kernel(const float* __restrict__ logits, int T, int E, int top_k, int renorm,
+                                 int32_t* __restrict__ ids, float* __restrict__ weights) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  const float* l = logits + (int64_t)t * E;
+  float mx = l[0];
+  for (int e = 1; e < E; ++e) mx = l[e] > mx ? l[e] : mx;
+  float sum = 0.f;
+  for (int e = 0; e < E; ++e) sum += expf(l[e] - mx);
+  uint32_t taken[kMaxRouteExperts / 32];
+  for (int i = 0; i < kMaxRouteExperts / 32; ++i) taken[i] = 0;
+  float p[kMaxTopK];
+  float psum = 0.f;
+  for (int j = 0; j < top_k; ++j) {
+    int best = -1;
+    float bv = 0.f;
+    for (int e = 0; e < E; ++e) {
+      if (taken[e >> 5] & (1u << (e & 31))) continue;
+      if (best < 0 || l[e] > bv) {
+        best = e;
+        bv = l[e];
+      }
+    }
+    taken[best >> 5] |= 1u << (best & 31);
+    ids[(int64_t)t * top_k + j] = best;
+    p[j] = expf(bv - mx) / sum;
+    psum += p[j];
+  }
+  for (int j = 0; j < top_k; ++j) weights[(int64_t)t * top_k + j] = renorm ? p[j] / psum : p[j];
+}
+
+// ---- alignment --------------------------------------------------------------
+// One workgroup. Counts use LDS atomics (order-free). The scatter is stable:
+// routes are processed in chunks of 1024 in route order; inside a wave the rank
+// of a route among same-expert lanes comes from ballots, across waves from a
+// prefix over per-wave counts, across chunks from a running base per expert.
+// The result equals a stable argsort of the expert ids.
+__global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t* __restrict__ ids, int R, int E, int B,
+                                                                  int32_t* __restrict__ sorted, int capacity,
+                                                                  int32_t* __restrict__ blocks, int nblocks,
+                                                                  int32_t* __restrict__ offsets,
+                                                                  int32_t* __restrict__ total) {
+  __shared__ int cnt[kMaxAlignExperts];
+  __shared__ int off[kMaxAlignExperts + 1];
+  __shared__ int base[kMaxAlignExperts];
+  __shared__ int wcnt[kAlignWaves][kMaxAlignExperts];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  for (int e = tid; e < E; e += kAlignThreads) {
+    cnt[e] = 0;
+    base[e] = 0;
+  }
+  __syncthreads();
+  for (int r = tid; r < R; r += kAlignThreads) {
+    const int e = ids[r];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int acc = 0;
+    off[0] = 0;
+    for (int e = 0; e < E; ++e) {
+      acc += (cnt[e] + B - 1) / B * B;
+      off[e + 1] = acc;
+    }
+    total[0] = acc;
+  }
+  __syncthreads();
+  for (int e = tid; e <= E; e += kAlignThreads) offsets[e] = off[e];
+  for (int i = tid; i < capacity; i += kAlignThreads) sorted[i] = R;
+  for (int b = tid; b < nblocks; b += kAlignThreads) {
+    const int pos = b * B;
+    int owner = -1;
+    if (pos < off[E]) {
+      int lo = 0, hi = E;  // largest e with off[e] <= pos
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (off[mid] <= pos) lo = mid; else hi = mid;
+      }
+      owner = lo;
+    }
+    blocks[b] = owner;
+  }
+  __syncthreads();  // sentinel fill is complete before any scatter store
+
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int c = 0; c < R; c += kAlignThreads) {
+    for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wcnt[i / E][i % E] = 0;
+    const int r = c + tid;
+    int e = r < R ? ids[r] : -1;
+    const bool valid = e >= 0 && e < E;
+    if (!valid) e = -1;
+    __syncthreads();
+    int rank = 0;
+    uint64_t remaining = __ballot(valid);
+    while (remaining) {
+      const int leader = __ffsll((unsigned long long)remaining) - 1;
+      const int le = __shfl(e, leader);
+      const uint64_t same = __ballot(e == le) & remaining;
+      if (e == le) rank = __popcll(same & lt_mask);
+      if (lane == leader) wcnt[wave][le] = __popcll(same);
+      remaining &= ~same;
+    }
+    __syncthreads();
+    for (int x = tid; x < E; x += kAlignThreads) {
+      int run = base[x];
+      for (int w = 0; w < kAlignWaves; ++w) {
+        const int n = wcnt[w][x];
+        wcnt[w][x] = run;
+        run += n;
+      }
+      base[x] = run;
+    }
+    __syncthreads();
+    if (valid) sorted[off[e] + wcnt[wave][e] + rank] = r;
+    __syncthreads();
+  }
+}
+
+// ---- grouped projections ------------------------------------------------------
+
+// B-tile row c of a gate/up tile: waves wn = c/64 own output columns
+// f0 + wn*32 + c%32; their first 32-wide MFMA tile reads the gate row, the
+// second the up row of the same f, so each lane holds gate and up of one
+// output element.
+struct GateUpRowMap {
+  int f0;
+  int F;
+  INTENT_DEVICE int operator()(int c) const {
+    const int f = f0 + (c >> 6) * 32 + (c & 31);
+    return ((c >> 5) & 1) ? F + f : f;
+  }
+};
+
+struct ClampRows {
+  int n0;
+  int N;
+  INTENT_DEVICE int operator()(int c) const {
+    const int n = n0 + c;
+    return n < N ? n : N - 1;
+  }
+};
+
+__global__ __launch_bounds__(NTHREADS) void moe_gate_up_kernel(const f16* __restrict__ x, int64_t ldx, int H,
+                                                               const int32_t* __restrict__ sorted,
+                                                               const int32_t* __restrict__ blocks, int mblocks, int R,
+                                                               int top_k, const uint8_t* __restrict__ wq,
+                                                               const f16* __restrict__ ws,
+                                                               const uint8_t* __restrict__ wz, int F, int gs,
+                                                               f16* __restrict__ act, int64_t ld_act) {
+  __shared__ SharedTile tile;
+  const int mb = blockIdx.x % mblocks;
+  const int f0 = (blockIdx.x / mblocks) * 64;
+  const int e = blocks[mb];
+  if (e < 0) return;
+  const int64_t ldq = H / 2;
+  const int64_t ldp = H / gs;
+  W4Source w{wq + (int64_t)e * 2 * F * ldq, ldq, ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs};
+  const int m0 = mb * BM;
+  f32x16 acc[2][2];
+  mainloop(GatherRows{x, ldx, sorted, R, top_k}, m0, w, GateUpRowMap{f0, F}, H, tile, acc);
+  const int lane = threadIdx.x & 63;
+  const int wn = threadIdx.x >> 7;
+  const int f = f0 + wn * 32 + (lane & 31);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int p = m0 + acc_row(i, v);
+      const int r = sorted[p];
+      f16 out = (f16)0.f;
+      if (r >= 0 && r < R) {
+        const float g = acc[i][0][v];
+        const float u = acc[i][1][v];
+        const float silu = g / (1.0f + expf(-g));
+        out = (f16)(silu * u);
+      }
+      act[(int64_t)p * ld_act + f] = out;
+    }
+}
+
+__global__ __launch_bounds__(NTHREADS) void moe_down_kernel(const f16* __restrict__ act, int64_t ld_act,
+                                                            const int32_t* __restrict__ sorted,
+                                                            const int32_t* __restrict__ blocks, int mblocks, int R,
+                                                            const uint8_t* __restrict__ wq, const f16* __restrict__ ws,
+                                                            const uint8_t* __restrict__ wz, int H, int F, int gs,
+                                                            float* __restrict__ out, int64_t ldo) {
+  __shared__ SharedTile tile;
+  const int mb = blockIdx.x % mblocks;
+  const int n0 = (blockIdx.x / mblocks) * BN;
+  const int e = blocks[mb];
+  if (e < 0) return;
+  const int64_t ldq = F / 2;
+  const int64_t ldp = F / gs;
+  W4Source w{wq + (int64_t)e * H * ldq, ldq, ws + (int64_t)e * H * ldp, wz + (int64_t)e * H * ldp, ldp, gs};
+  const int m0 = mb * BM;
+  f32x16 acc[2][2];
+  mainloop(PaddedRows{act, ld_act}, m0, w, ClampRows{n0, H}, F, tile, acc);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + acc_col(j);
+    if (col >= H) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = sorted[m0 + acc_row(i, v)];
+        if (r >= 0 && r < R) out[(int64_t)r * ldo + col] = acc[i][j][v];
+      }
+  }
+}
+
+// y[t, d] += w[t, s] * out[t*k + s, d], slot by slot (mul then add, no fma).
+__global__ void moe_combine_kernel(const float* __restrict__ route_out, int64_t ldo,
+                                   const float* __restrict__ weights, int T, int top_k, float* __restrict__ y, int H,
+                                   int64_t ldy) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)T * H;
+  if (i >= total) return;
+  const int t = (int)(i / H);
+  const int d = (int)(i % H);
+  float acc = y[(int64_t)t * ldy + d];
+  for (int s = 0; s < top_k; ++s) {
+    const float prod = __fmul_rn(weights[(int64_t)t * top_k + s], route_out[((int64_t)t * top_k + s) * ldo + d]);
+    acc = __fadd_rn(acc, prod);
+  }
+  y[(int64_t)t * ldy + d] = acc;
+}
+
+int64_t align_capacity(int64_t R, int64_t E, int64_t B) { return R + E * (B - 1); }
+
+}  // namespace
+
+extern "C" int intent_moe_route(const float* logits, int64_t T, int64_t E, int64_t top_k, int renormalize,
+                                int32_t* topk_ids, float* topk_weights, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(T >= 0 && T <= INT32_MAX, INTENT_ERR_INVALID_ARGUMENT, "bad token count %lld", (long long)T);
+  INTENT_REQUIRE(E >= 1 && E <= kMaxRouteExperts, INTENT_ERR_UNSUPPORTED, "experts must be in [1, %d], got %lld",
+                 kMaxRouteExperts, (long long)E);
+  INTENT_REQUIRE(top_k >= 1 && top_k <= E && top_k <= kMaxTopK, INTENT_ERR_UNSUPPORTED,
+                 "top_k must be in [1, min(E, %d)], got %lld", kMaxTopK, (long long)top_k);
+  if (T == 0) return INTENT_OK;
+  INTENT_REQUIRE(logits && topk_ids && topk_weights, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  const int threads = 256;
+  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + threads - 1) / threads)), dim3(threads), 0,
+                     (hipStream_t)stream, logits, (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights);
+  return intent::launch_status("moe_route");
+}
+
+extern "C" int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_k, int64_t E, int64_t block_size,
+                                int32_t* sorted_route_ids, int64_t capacity, int32_t* expert_blocks,
+                                int64_t num_blocks, int32_t* expert_offsets, int32_t* total_padded, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(T >= 0 && top_k >= 1 && T * top_k <= (1ll << 30), INTENT_ERR_INVALID_ARGUMENT,
+                 "bad route count (T=%lld top_k=%lld)", (long long)T, (long long)top_k);
+  INTENT_REQUIRE(E >= 1 && E <= kMaxAlignExperts, INTENT_ERR_UNSUPPORTED, "experts must be in [1, %d], got %lld",
+                 kMaxAlignExperts, (long long)E);
+  INTENT_REQUIRE(block_size >= 1 && block_size <= (1 << 16), INTENT_ERR_INVALID_ARGUMENT, "bad block size %lld",
+                 (long long)block_size);
+  const int64_t R = T * top_k;
+  const int64_t need = align_capacity(R, E, block_size);
+  INTENT_REQUIRE(capacity >= need, INTENT_ERR_INVALID_ARGUMENT, "sorted_route_ids needs %lld entries, got %lld",
+                 (long long)need, (long long)capacity);
+  INTENT_REQUIRE(num_blocks >= (capacity + block_size - 1) / block_size, INTENT_ERR_INVALID_ARGUMENT,
+                 "expert_blocks needs %lld entries, got %lld", (long long)((capacity + block_size - 1) / block_size),
+                 (long long)num_blocks);
+  INTENT_REQUIRE(capacity <= INT32_MAX && num_blocks <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "capacity exceeds int32");
+  INTENT_REQUIRE(sorted_route_ids && expert_blocks && expert_offsets && total_padded && (R == 0 || topk_ids),
+                 INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, (hipStream_t)stream, topk_ids, (int)R, (int)E,
+                     (int)block_size, sorted_route_ids, (int)capacity, expert_blocks, (int)num_blocks,
+                     expert_offsets, total_padded);
+  return intent::launch_status("moe_align");
+}
+
+extern "C" int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_t x_ld,
+                                     const int32_t* sorted_route_ids, const int32_t* expert_blocks, int64_t num_blocks,
+                                     int64_t block_size, int64_t top_k, const uint8_t* w_packed, const void* w_scales,
+                                     const uint8_t* w_zeros, int64_t E, int64_t F, int64_t group_size, void* act,
+                                     int64_t act_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(block_size == BM, INTENT_ERR_UNSUPPORTED, "block_size must be %d, got %lld", BM,
+                 (long long)block_size);
+  INTENT_REQUIRE(H > 0 && H % 128 == 0 && H <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "H must be a positive multiple of 128");
+  INTENT_REQUIRE(F > 0 && F % 64 == 0 && F <= INT32_MAX / 2, INTENT_ERR_UNSUPPORTED, "F must be a positive multiple of 64");
+  INTENT_REQUIRE(group_size > 0 && group_size % 32 == 0 && H % group_size == 0, INTENT_ERR_UNSUPPORTED,
+                 "group_size must be a multiple of 32 dividing H");
+  INTENT_REQUIRE(T >= 0 && top_k >= 1 && E >= 1 && num_blocks >= 0, INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  if (num_blocks == 0 || T == 0) return INTENT_OK;
+  INTENT_REQUIRE(x && sorted_route_ids && expert_blocks && w_packed && w_scales && w_zeros && act,
+                 INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(x_ld >= H && act_ld >= F, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(x) && x_ld % 8 == 0 && intent::aligned16(w_packed), INTENT_ERR_ALIGNMENT,
+                 "x and weights must be 16-byte aligned");
+  const int64_t grid = num_blocks * (F / 64);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+  hipLaunchKernelGGL(moe_gate_up_kernel, dim3((unsigned)grid), dim3(NTHREADS), 0, (hipStream_t)stream, (const f16*)x,
+                     x_ld, (int)H, sorted_route_ids, expert_blocks, (int)num_blocks, (int)(T * top_k), (int)top_k,
+                     w_packed, (const f16*)w_scales, w_zeros, (int)F, (int)group_size, (f16*)act, act_ld);
+  return intent::launch_status("moe_gate_up_w4");
+}
+
+extern "C" int intent_moe_down_w4(const void* act, int64_t act_ld, const int32_t* sorted_route_ids,
+                                  const int32_t* expert_blocks, int64_t num_blocks, int64_t block_size, int64_t R,
+                                  const uint8_t* w_packed, const void* w_scales, const uint8_t* w_zeros, int64_t E,
+                                  int64_t H, int64_t F, int64_t group_size, float* out, int64_t out_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(block_size == BM, INTENT_ERR_UNSUPPORTED, "block_size must be %d, got %lld", BM,
+                 (long long)block_size);
+  INTENT_REQUIRE(F > 0 && F % 128 == 0 && F <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "F must be a positive multiple of 128");
+  INTENT_REQUIRE(H > 0 && H <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "bad H");
+  INTENT_REQUIRE(group_size > 0 && group_size % 32 == 0 && F % group_size == 0, INTENT_ERR_UNSUPPORTED,
+                 "group_size must be a multiple of 32 dividing F");
+  INTENT_REQUIRE(R >= 0 && E >= 1 && num_blocks >= 0, INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  if (num_blocks == 0 || R == 0) return INTENT_OK;
+  INTENT_REQUIRE(act && sorted_route_ids && expert_blocks && w_packed && w_scales && w_zeros && out,
+                 INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(act_ld >= F && out_ld >= H, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(act) && act_ld % 8 == 0 && intent::aligned16(w_packed), INTENT_ERR_ALIGNMENT,
+                 "activations and weights must be 16-byte aligned");
+  const int64_t grid = num_blocks * ((H + BN - 1) / BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+  hipLaunchKernelGGL(moe_down_kernel, dim3((unsigned)grid), dim3(NTHREADS), 0, (hipStream_t)stream, (const f16*)act,
+                     act_ld, sorted_route_ids, expert_blocks, (int)num_blocks, (int)R, w_packed, (const f16*)w_scales,
+                     w_zeros, (int)H, (int)F, (int)group_size, out, out_ld);
+  return intent::launch_status("moe_down_w4");
+}
+
+extern "C" int intent_moe_combine(const float* route_out, int64_t out_ld, const float* topk_weights, int64_t T,
+                                  int64_t top_k, float* y, int64_t H, int64_t y_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(T >= 0 && H >= 0 && top_k >= 1 && T * H < (1ll << 40), INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  if (T == 0 || H == 0) return INTENT_OK;
+  INTENT_REQUIRE(route_out && topk_weights && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(out_ld >= H && y_ld >= H, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  const int threads = 256;
+  const int64_t blocks = (T * H + threads - 1) / threads;
+  INTENT_REQUIRE(blocks < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, route_out,
+                     out_ld, topk_weights, (int)T, (int)top_k, y, (int)H, y_ld);
+  return intent::launch_status("moe_combine");
+}
+
+namespace {
+
+struct MoEWorkspace {
+  size_t ids, weights, sorted, blocks, offsets, total, act, out, bytes;
+  int64_t capacity, nblocks;
+};
+
+size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+MoEWorkspace moe_layout(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t F, int64_t B) {
+  MoEWorkspace w{};
+  const int64_t R = T * top_k;
+  w.capacity = align_capacity(R, E, B);
+  w.nblocks = (w.capacity + B - 1) / B;
+  size_t o = 0;
+  w.ids = o;     o = round256(o + sizeof(int32_t) * R);
+  w.weights = o; o = round256(o + sizeof(float) * R);
+  w.sorted = o;  o = round256(o + sizeof(int32_t) * w.capacity);
+  w.blocks = o;  o = round256(o + sizeof(int32_t) * w.nblocks);
+  w.offsets = o; o = round256(o + sizeof(int32_t) * (E + 1));
+  w.total = o;   o = round256(o + sizeof(int32_t));
+  w.act = o;     o = round256(o + sizeof(uint16_t) * (size_t)(w.nblocks * B) * F);
+  w.out = o;     o = round256(o + sizeof(float) * (size_t)R * H);
+  w.bytes = o;
+  return w;
+}
+
+}  // namespace
+
+extern "C" size_t intent_moe_workspace_size(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t F,
+                                            int64_t block_size) {
+  if (T < 0 || top_k < 1 || E < 1 || H < 0 || F < 0 || block_size < 1) return 0;
+  return moe_layout(T, top_k, E, H, F, block_size).bytes;
+}
+
+extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* x, int64_t T, int64_t H, int64_t E,
+                                        int64_t top_k, int renormalize, const uint8_t* wgu_packed,
+                                        const void* wgu_scales, const uint8_t* wgu_zeros, const uint8_t* wd_packed,
+                                        const void* wd_scales, const uint8_t* wd_zeros, int64_t F,
+                                        int64_t group_size, float* y, void* workspace, size_t workspace_bytes,
+                                        int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
+  intent::clear_error();
+  const int64_t B = BM;
+  INTENT_REQUIRE(T >= 0 && top_k >= 1 && E >= 1 && H > 0 && F > 0, INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  if (T == 0) return INTENT_OK;
+  const MoEWorkspace L = moe_layout(T, top_k, E, H, F, B);
+  INTENT_REQUIRE(workspace && workspace_bytes >= L.bytes, INTENT_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
+                 L.bytes, workspace_bytes);
+  INTENT_REQUIRE(intent::aligned16(workspace), INTENT_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+  INTENT_REQUIRE(y, INTENT_ERR_INVALID_ARGUMENT, "null output");
+  char* ws = (char*)workspace;
+  int32_t* ids = topk_ids_out ? topk_ids_out : (int32_t*)(ws + L.ids);
+  float* wts = topk_weights_out ? topk_weights_out : (float*)(ws + L.weights);
+  int32_t* sorted = (int32_t*)(ws + L.sorted);
+  int32_t* blocks = (int32_t*)(ws + L.blocks);
+  int32_t* offsets = (int32_t*)(ws + L.offsets);
+  int32_t* total = (int32_t*)(ws + L.total);
+  void* act = ws + L.act;
+  float* out = (float*)(ws + L.out);
+  int st = intent_moe_route(router_logits, T, E, top_k, renormalize, ids, wts, stream);
+  if (st != INTENT_OK) return st;
+  st = intent_moe_align(ids, T, top_k, E, B, sorted, L.capacity, blocks, L.nblocks, offsets, total, stream);
+  if (st != INTENT_OK) return st;
+  st = intent_moe_gate_up_w4(x, T, H, H, sorted, blocks, L.nblocks, B, top_k, wgu_packed, wgu_scales, wgu_zeros, E, F,
+                             group_size, act, F, stream);
+  if (st != INTENT_OK) return st;
+  st = intent_moe_down_w4(act, F, sorted, blocks, L.nblocks, B, T * top_k, wd_packed, wd_scales, wd_zeros, E, H, F,
+                          group_size, out, H, stream);
+  if (st != INTENT_OK) return st;
+  return intent_moe_combine(out, H, wts, T, top_k, y, H, H, stream);
+}

@@ -1,0 +1,417 @@
+"""Fixed kernel definitions of the quantized-contraction hot path.
+
+Each definition plays the role of an ``@intent.kernel`` function of the
+reference (python/intent/api/definitions.py:76): an author-ordered parameter
+list with In / Out / InOut views over symbolic extents. Instead of being
+lowered by a compiler, each one is bound to a hand-written gfx950 entry of
+``libintent_amd.so``. Reference kernels each definition replaces are cited on
+the definition.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Callable
+
+from . import _native
+from .errors import LanguageUseError
+from .interface import PublicInterface, ScalarParameter, ViewKind, ViewParameter, dtype
+
+IN, OUT, INOUT = ViewKind.IN, ViewKind.OUT, ViewKind.INOUT
+
+Dim = Any  # str symbol | int | Callable[[dict], int]
+
+
+@dataclass(frozen=True)
+class Param:
+    name: str
+    dtype: str
+    dims: tuple
+    access: ViewKind = IN
+    leading_stride: bool = False  # 2-D views may carry a leading stride; others must be contiguous
+
+
+@dataclass(frozen=True)
+class Scalar:
+    name: str
+    dtype: str
+
+
+@dataclass
+class KernelDefinition:
+    name: str
+    params: tuple
+    launch: Callable[..., str]
+    constexprs: dict = field(default_factory=dict)
+    check: Callable[[dict], None] | None = None
+    workspace: Callable[[dict], int] | None = None
+    reference: str = ""
+    doc: str = ""
+
+    @property
+    def __name__(self) -> str:  # the reference uses definition.__name__ as the entry name
+        return self.name
+
+    def __call__(self, *args, **kwargs):
+        raise LanguageUseError(f"kernel {self.name} must be compiled before runtime invocation")
+
+    def __repr__(self) -> str:
+        return f"<intent_amd kernel {self.name}>"
+
+    def resolve_constexprs(self, overrides: dict | None) -> dict:
+        values = dict(self.constexprs)
+        for key, value in (overrides or {}).items():
+            if key not in values:
+                raise ValueError(f"{self.name} has no constexpr {key!r}; known: {sorted(values)}")
+            values[key] = value
+        missing = [k for k, v in values.items() if v is None]
+        if missing:
+            raise ValueError(f"{self.name} requires constexprs {missing}")
+        return values
+
+    def interface(self) -> PublicInterface:
+        identities: dict[str, int] = {}
+        parameters = []
+        for position, p in enumerate(self.params):
+            if isinstance(p, Scalar):
+                parameters.append(ScalarParameter(position, p.name, dtype(p.dtype)))
+                continue
+            shape, dims = [], []
+            for d in p.dims:
+                if isinstance(d, int):
+                    shape.append(d)
+                    dims.append(0)
+                elif isinstance(d, str):
+                    shape.append(-1)
+                    dims.append(identities.setdefault(d, len(identities) + 1))
+                else:
+                    shape.append(-1)
+                    dims.append(0)
+            rank = len(p.dims)
+            strides = tuple([None] * (rank - 1) + [1]) if p.leading_stride else tuple(
+                None if i < rank - 1 else 1 for i in range(rank))
+            parameters.append(ViewParameter(position, p.name, dtype(p.dtype), tuple(shape), tuple(dims), strides,
+                                            p.access))
+        return PublicInterface(tuple(parameters))
+
+
+def _ptr(t) -> int:
+    return t.data_ptr()
+
+
+def _ld(t) -> int:
+    return t.stride(0) if t.dim() >= 2 else t.shape[0]
+
+
+# ---- W4A16 ------------------------------------------------------------------------
+
+def _w4_check(env: dict) -> None:
+    if env["P"] * 2 != env["K"]:
+        raise ValueError(f"packed_weight.shape[1] ({env['P']}) must be K/2 ({env['K']}/2)")
+    if env["G"] <= 0 or env["K"] % env["G"]:
+        raise ValueError(f"K ({env['K']}) must be a multiple of the number of groups ({env['G']})")
+    env["GROUP"] = env["K"] // env["G"]
+    if env["KERNEL"] not in ("auto", "gemv", "gemm"):
+        raise ValueError("KERNEL must be 'auto', 'gemv' or 'gemm'")
+
+
+def _w4_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    x, q, s, z, y = v["activation"], v["packed_weight"], v["scales"], v["zeros"], v["output"]
+    if s.stride(0) != z.stride(0):
+        raise ValueError("scales and zeros must share a row stride")
+    kernel = env["KERNEL"]
+    if kernel == "auto":
+        kernel = "gemv" if env["M"] <= 16 else "gemm"
+    entry = {"gemv": "intent_w4a16_gemv", "gemm": "intent_w4a16_gemm"}[kernel]
+    _native.call(entry, _ptr(x), env["M"], env["K"], _ld(x), _ptr(q), env["N"], _ld(q), _ptr(s), _ptr(z),
+                 s.stride(0), env["GROUP"], _ptr(y), _ld(y), stream)
+    return entry
+
+
+weight_only_int4_asym_matmul = KernelDefinition(
+    name="weight_only_int4_asym_matmul",
+    params=(
+        Param("activation", "f16", ("M", "K"), leading_stride=True),
+        Param("packed_weight", "u8", ("N", "P"), leading_stride=True),
+        Param("scales", "f16", ("N", "G"), leading_stride=True),
+        Param("zeros", "u8", ("N", "G"), leading_stride=True),
+        Param("output", "f16", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_w4_launch,
+    constexprs={"KERNEL": "auto"},
+    check=_w4_check,
+    reference="examples/kernels/contraction/weight_only_int4.py:18-51",
+    doc="y = f16(x @ ((q - z) * s).T), asymmetric uint4 group quant, packed [N, K/2]",
+)
+
+
+# ---- W8A16 ------------------------------------------------------------------------
+
+def _w8a16_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    x, w, s, y = v["activation"], v["weight"], v["scales"], v["output"]
+    _native.call("intent_w8a16_matmul", _ptr(x), env["M"], env["K"], _ld(x), _ptr(w), env["N"], _ld(w), _ptr(s),
+                 _ptr(y), _ld(y), stream)
+    return "intent_w8a16_matmul"
+
+
+weight_only_int8_matmul = KernelDefinition(
+    name="weight_only_int8_matmul",
+    params=(
+        Param("activation", "f16", ("M", "K"), leading_stride=True),
+        Param("weight", "i8", ("N", "K"), leading_stride=True),
+        Param("scales", "f16", ("N",)),
+        Param("output", "f16", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_w8a16_launch,
+    reference="doc/dsl/core.en.md:246 (I.cast(W_i8, f16) -> I.matmul(acc f32) -> scale)",
+    doc="y = f16(scale[n] * (x @ w.T)), per-channel int8 weights",
+)
+
+
+# ---- W8A8 -------------------------------------------------------------------------
+
+def _w8a8_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    a, sa, w, sw, out = v["activation"], v["activation_scales"], v["weight"], v["weight_scales"], v["output"]
+    _native.call("intent_w8a8_gemm", _ptr(a), env["M"], env["K"], _ld(a), _ptr(sa), _ptr(w), env["N"], _ld(w),
+                 _ptr(sw), _ptr(out), _ld(out), stream)
+    return "intent_w8a8_gemm"
+
+
+w8a8_scaled_matmul = KernelDefinition(
+    name="w8a8_scaled_matmul",
+    params=(
+        Param("activation", "i8", ("M", "K"), leading_stride=True),
+        Param("activation_scales", "f32", ("M",)),
+        Param("weight", "i8", ("N", "K"), leading_stride=True),
+        Param("weight_scales", "f32", ("N",)),
+        Param("output", "bf16", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_w8a8_launch,
+    reference="lib/Conversion/KIRToCPU/Contractions.cpp:30-35 + examples/kernels/contraction/gemm.py:83-106",
+    doc="out = bf16(f32(int32 acc) * sa[m] * sw[n])",
+)
+
+
+def _gemm_i8_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    a, b, bias, c = v["a"], v["b"], v["bias"], v["c"]
+    _native.call("intent_i8_gemm_i32", _ptr(a), env["M"], env["K"], _ld(a), _ptr(b), env["N"], _ld(b), _ptr(bias),
+                 _ptr(c), _ld(c), stream)
+    return "intent_i8_gemm_i32"
+
+
+gemm_i8_nt = KernelDefinition(
+    name="gemm_i8_nt",
+    params=(
+        Param("a", "i8", ("M", "K"), leading_stride=True),
+        Param("b", "i8", ("N", "K"), leading_stride=True),
+        Param("bias", "i32", ("N",)),
+        Param("c", "i32", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_gemm_i8_launch,
+    reference="examples/kernels/contraction/gemm.py:29-39 (gemm_i8, weight given as [N, K])",
+    doc="c = a @ b.T + bias in int32 (modulo 2^32)",
+)
+
+
+# ---- MoE --------------------------------------------------------------------------
+
+def _route_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    _native.call("intent_moe_route", _ptr(v["logits"]), env["T"], env["E"], env["TOP_K"], int(bool(env["RENORMALIZE"])),
+                 _ptr(v["topk_ids"]), _ptr(v["topk_weights"]), stream)
+    return "intent_moe_route"
+
+
+moe_route_topk = KernelDefinition(
+    name="moe_route_topk",
+    params=(
+        Param("logits", "f32", ("T", "E")),
+        Param("topk_ids", "i32", ("T", lambda env: env["TOP_K"]), OUT),
+        Param("topk_weights", "f32", ("T", lambda env: env["TOP_K"]), OUT),
+    ),
+    launch=_route_launch,
+    constexprs={"TOP_K": 2, "RENORMALIZE": True},
+    reference="experiments/_common/support.py:113-130 (the producer of topk_ids)",
+    doc="top-k experts by logit (ties -> lower index) and their softmax weights",
+)
+
+
+def align_sizes(routes: int, experts: int, block: int) -> tuple[int, int]:
+    capacity = routes + experts * (block - 1)
+    return capacity, (capacity + block - 1) // block
+
+
+def _align_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    cap, nb = align_sizes(env["T"] * env["K"], env["EXPERTS"], env["BLOCK_SIZE"])
+    _native.call("intent_moe_align", _ptr(v["topk_ids"]), env["T"], env["K"], env["EXPERTS"], env["BLOCK_SIZE"],
+                 _ptr(v["sorted_route_ids"]), cap, _ptr(v["expert_blocks"]), nb, _ptr(v["expert_offsets"]),
+                 _ptr(v["total_padded"]), stream)
+    return "intent_moe_align"
+
+
+moe_align_block_size = KernelDefinition(
+    name="moe_align_block_size",
+    params=(
+        Param("topk_ids", "i32", ("T", "K")),
+        Param("sorted_route_ids", "i32",
+              (lambda env: align_sizes(env["T"] * env["K"], env["EXPERTS"], env["BLOCK_SIZE"])[0],), OUT),
+        Param("expert_blocks", "i32",
+              (lambda env: align_sizes(env["T"] * env["K"], env["EXPERTS"], env["BLOCK_SIZE"])[1],), OUT),
+        Param("expert_offsets", "i32", (lambda env: env["EXPERTS"] + 1,), OUT),
+        Param("total_padded", "i32", (1,), OUT),
+    ),
+    launch=_align_launch,
+    constexprs={"EXPERTS": None, "BLOCK_SIZE": 128},
+    reference="examples/kernels/routing/moe_align.py:14-86 + examples/programs/composition.py:134-174",
+    doc="count / block-padded prefix / stable scatter / block->expert map",
+)
+
+
+def _ffn_check(env: dict) -> None:
+    H, F2 = env["H"], env["F2"]
+    if env["HP"] * 2 != H:
+        raise ValueError("w_gate_up.shape[2] must be H/2")
+    if F2 % 2:
+        raise ValueError("w_gate_up.shape[1] must be 2*F")
+    F = F2 // 2
+    env["F"] = F
+    if env["FP"] * 2 != F:
+        raise ValueError("w_down.shape[2] must be F/2")
+    if H % env["G1"] or F % env["G2"] or H // env["G1"] != F // env["G2"]:
+        raise ValueError("gate/up and down weights must share one group size")
+    env["GROUP"] = H // env["G1"]
+    if env["TOP_K"] > env["E"]:
+        raise ValueError("TOP_K exceeds the number of experts")
+
+
+def _ffn_workspace(env: dict) -> int:
+    lib = _native.library()
+    return int(lib.intent_moe_workspace_size(env["T"], env["TOP_K"], env["E"], env["H"], env["F"], 128))
+
+
+def _ffn_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    _native.call("intent_moe_expert_ffn_w4", _ptr(v["router_logits"]), _ptr(v["x"]), env["T"], env["H"], env["E"],
+                 env["TOP_K"], int(bool(env["RENORMALIZE"])), _ptr(v["w_gate_up"]), _ptr(v["gate_up_scales"]),
+                 _ptr(v["gate_up_zeros"]), _ptr(v["w_down"]), _ptr(v["down_scales"]), _ptr(v["down_zeros"]),
+                 env["F"], env["GROUP"], _ptr(v["y"]), workspace.data_ptr(), workspace.numel(), None, None, stream)
+    return "intent_moe_expert_ffn_w4"
+
+
+moe_expert_ffn_w4 = KernelDefinition(
+    name="moe_expert_ffn_w4",
+    params=(
+        Param("router_logits", "f32", ("T", "E")),
+        Param("x", "f16", ("T", "H")),
+        Param("w_gate_up", "u8", ("E", "F2", "HP")),
+        Param("gate_up_scales", "f16", ("E", "F2", "G1")),
+        Param("gate_up_zeros", "u8", ("E", "F2", "G1")),
+        Param("w_down", "u8", ("E", "H", "FP")),
+        Param("down_scales", "f16", ("E", "H", "G2")),
+        Param("down_zeros", "u8", ("E", "H", "G2")),
+        Param("y", "f32", ("T", "H"), INOUT),
+    ),
+    launch=_ffn_launch,
+    constexprs={"TOP_K": 2, "RENORMALIZE": True},
+    check=_ffn_check,
+    workspace=_ffn_workspace,
+    reference="examples/kernels/ragged/moe.py:12-53 (+ routing/moe_align.py, programs/composition.py:134-174)",
+    doc="y += sum_slots w * (silu(x Wg) * (x Wu)) Wd over the top-k experts, W4 experts",
+)
+
+
+def _gate_up_check(env: dict) -> None:
+    if env["HP"] * 2 != env["H"] or env["F2"] % 2 or env["H"] % env["G1"]:
+        raise ValueError("inconsistent gate/up weight shapes")
+    env["F"] = env["F2"] // 2
+    env["GROUP"] = env["H"] // env["G1"]
+
+
+def _gate_up_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    x, act = v["x"], v["act"]
+    _native.call("intent_moe_gate_up_w4", _ptr(x), env["T"], env["H"], _ld(x), _ptr(v["sorted_route_ids"]),
+                 _ptr(v["expert_blocks"]), env["NB"], env["BLOCK_SIZE"], env["TOP_K"], _ptr(v["w_gate_up"]),
+                 _ptr(v["gate_up_scales"]), _ptr(v["gate_up_zeros"]), env["E"], env["F"], env["GROUP"], _ptr(act),
+                 _ld(act), stream)
+    return "intent_moe_gate_up_w4"
+
+
+moe_gate_up_w4 = KernelDefinition(
+    name="moe_gate_up_w4",
+    params=(
+        Param("x", "f16", ("T", "H"), leading_stride=True),
+        Param("sorted_route_ids", "i32", ("CAP",)),
+        Param("expert_blocks", "i32", ("NB",)),
+        Param("w_gate_up", "u8", ("E", "F2", "HP")),
+        Param("gate_up_scales", "f16", ("E", "F2", "G1")),
+        Param("gate_up_zeros", "u8", ("E", "F2", "G1")),
+        Param("act", "f16", (lambda env: env["NB"] * env["BLOCK_SIZE"], lambda env: env["F"]), OUT),
+    ),
+    launch=_gate_up_launch,
+    constexprs={"TOP_K": 2, "BLOCK_SIZE": 128},
+    check=_gate_up_check,
+    reference="examples/kernels/ragged/moe.py:28-45",
+    doc="act[p] = f16(silu(x[t] Wg[e]) * (x[t] Wu[e])) over aligned padded rows",
+)
+
+
+def _down_check(env: dict) -> None:
+    if env["FP"] * 2 != env["F"] or env["F"] % env["G2"]:
+        raise ValueError("inconsistent down weight shapes")
+    env["GROUP"] = env["F"] // env["G2"]
+
+
+def _down_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    act, out = v["act"], v["route_out"]
+    _native.call("intent_moe_down_w4", _ptr(act), _ld(act), _ptr(v["sorted_route_ids"]), _ptr(v["expert_blocks"]),
+                 env["NB"], env["BLOCK_SIZE"], env["ROUTES"], _ptr(v["w_down"]), _ptr(v["down_scales"]),
+                 _ptr(v["down_zeros"]), env["E"], env["H"], env["F"], env["GROUP"], _ptr(out), _ld(out), stream)
+    return "intent_moe_down_w4"
+
+
+moe_down_w4 = KernelDefinition(
+    name="moe_down_w4",
+    params=(
+        Param("act", "f16", ("PR", "F"), leading_stride=True),
+        Param("sorted_route_ids", "i32", ("CAP",)),
+        Param("expert_blocks", "i32", ("NB",)),
+        Param("w_down", "u8", ("E", "H", "FP")),
+        Param("down_scales", "f16", ("E", "H", "G2")),
+        Param("down_zeros", "u8", ("E", "H", "G2")),
+        Param("route_out", "f32", (lambda env: env["ROUTES"], "H"), OUT, leading_stride=True),
+    ),
+    launch=_down_launch,
+    constexprs={"ROUTES": None, "BLOCK_SIZE": 128},
+    check=_down_check,
+    reference="examples/kernels/ragged/moe.py:46-53",
+    doc="route_out[r] = act[p] Wd[e] (fp32) for every aligned row p holding route r",
+)
+
+
+def _combine_check(env: dict) -> None:
+    if env["R"] != env["T"] * env["K"]:
+        raise ValueError("route_out rows must equal T * top_k")
+
+
+def _combine_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    ro, y = v["route_out"], v["y"]
+    _native.call("intent_moe_combine", _ptr(ro), _ld(ro), _ptr(v["topk_weights"]), env["T"], env["K"], _ptr(y),
+                 env["H"], _ld(y), stream)
+    return "intent_moe_combine"
+
+
+moe_combine = KernelDefinition(
+    name="moe_combine",
+    params=(
+        Param("route_out", "f32", ("R", "H"), leading_stride=True),
+        Param("topk_weights", "f32", ("T", "K")),
+        Param("y", "f32", ("T", "H"), INOUT, leading_stride=True),
+    ),
+    launch=_combine_launch,
+    check=_combine_check,
+    reference="examples/kernels/ragged/moe.py:48-53 (scatter_reduce add, fixed slot order)",
+    doc="y[t] += w[t,0] * route_out[t*k] + ... slot by slot",
+)
+
+
+ALL_DEFINITIONS = (
+    weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
+    moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
+)

@@ -1,0 +1,274 @@
+"""CPU oracle for the quantized-contraction hot path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker (never as the thing
+measured or shipped). The product path in ``intent_amd`` never touches it.
+
+Two layers:
+  * ``liboracle.so`` (``oracle.c``): the plain-C restatement of the reference's
+    CPU numerics, one function per hot-path function (each cites the reference
+    file:line it follows). Built by ``oracle/Makefile``.
+  * numpy restatements in this module, written independently of the C file,
+    used to pin the C oracle (tests compare the two and compare both with
+    float64 / int64 brute force, closed forms and known answers).
+
+Parity status of every function is pinned by tests in ``tests/test_oracle.py``:
+  w8a16, w4a16, i8_gemm_i32, w8a8, moe_route, moe_align, moe_ffn_w4 and the
+  f16/bf16 conversions all have independent checks (numpy float64 / int64
+  brute force, known-answer vectors, invariants, and the committed fixtures in
+  ``tests/golden/``). No function is "parity unpinned".
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBRARY = HERE / "liboracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile oracle.c with the committed Makefile."""
+    proc = subprocess.run(["make", "-s", "-C", str(HERE)], capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{proc.stdout}\n{proc.stderr}")
+    return LIBRARY
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIBRARY.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIBRARY))
+        i64, ci = ctypes.c_int64, ctypes.c_int
+        p = ctypes.c_void_p
+        _lib.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        _lib.orc_f16_to_f32.restype = ctypes.c_float
+        _lib.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        _lib.orc_f32_to_f16.restype = ctypes.c_uint16
+        _lib.orc_f32_to_bf16.argtypes = [ctypes.c_float]
+        _lib.orc_f32_to_bf16.restype = ctypes.c_uint16
+        _lib.orc_w8a16.argtypes = [p, i64, i64, p, i64, p, p, ci]
+        _lib.orc_w4a16.argtypes = [p, i64, i64, p, i64, p, p, i64, p, ci]
+        _lib.orc_i8_gemm_i32.argtypes = [p, i64, i64, p, i64, p, p, ci]
+        _lib.orc_w8a8.argtypes = [p, i64, i64, p, p, i64, p, p, ci]
+        _lib.orc_moe_route.argtypes = [p, i64, i64, i64, ci, p, p]
+        _lib.orc_moe_align.argtypes = [p, i64, i64, i64, i64, p, i64, p, i64, p, p]
+        _lib.orc_moe_ffn_w4.argtypes = [p, i64, i64, p, p, i64, i64, p, p, p, p, p, p, i64, i64, p, ci]
+        for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
+                     "orc_moe_ffn_w4"):
+            getattr(_lib, name).restype = None
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle inputs must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+# ---- C oracle wrappers --------------------------------------------------------
+
+def w8a16(x, w, scales, threads: int = 1) -> np.ndarray:
+    x, w, s = _c(x, np.float16), _c(w, np.int8), _c(scales, np.float16)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), np.float16)
+    lib().orc_w8a16(_ptr(x), M, K, _ptr(w), N, _ptr(s), _ptr(y), threads)
+    return y
+
+
+def w4a16(x, packed, scales, zeros, threads: int = 1) -> np.ndarray:
+    x, q = _c(x, np.float16), _c(packed, np.uint8)
+    s, z = _c(scales, np.float16), _c(zeros, np.uint8)
+    M, K = x.shape
+    N = q.shape[0]
+    gs = K // s.shape[1]
+    y = np.empty((M, N), np.float16)
+    lib().orc_w4a16(_ptr(x), M, K, _ptr(q), N, _ptr(s), _ptr(z), gs, _ptr(y), threads)
+    return y
+
+
+def i8_gemm_i32(a, w, bias=None, threads: int = 1) -> np.ndarray:
+    a, w = _c(a, np.int8), _c(w, np.int8)
+    M, K = a.shape
+    N = w.shape[0]
+    c = np.empty((M, N), np.int32)
+    b = None if bias is None else _c(bias, np.int32)
+    lib().orc_i8_gemm_i32(_ptr(a), M, K, _ptr(w), N, None if b is None else _ptr(b), _ptr(c), threads)
+    return c
+
+
+def w8a8(a, sa, w, sw, threads: int = 1) -> np.ndarray:
+    """Returns the bf16 bit patterns (uint16) of the W8A8 output."""
+    a, w = _c(a, np.int8), _c(w, np.int8)
+    sa, sw = _c(sa, np.float32), _c(sw, np.float32)
+    M, K = a.shape
+    N = w.shape[0]
+    out = np.empty((M, N), np.uint16)
+    lib().orc_w8a8(_ptr(a), M, K, _ptr(sa), _ptr(w), N, _ptr(sw), _ptr(out), threads)
+    return out
+
+
+def moe_route(logits, top_k: int, renormalize: bool = True):
+    lg = _c(logits, np.float32)
+    T, E = lg.shape
+    ids = np.empty((T, top_k), np.int32)
+    wts = np.empty((T, top_k), np.float32)
+    lib().orc_moe_route(_ptr(lg), T, E, top_k, int(renormalize), _ptr(ids), _ptr(wts))
+    return ids, wts
+
+
+def align_sizes(routes: int, experts: int, block: int) -> tuple[int, int]:
+    capacity = routes + experts * (block - 1)
+    return capacity, (capacity + block - 1) // block
+
+
+def moe_align(ids, experts: int, block: int):
+    ids = _c(ids, np.int32)
+    T, k = ids.shape
+    cap, nb = align_sizes(T * k, experts, block)
+    sorted_ids = np.empty(cap, np.int32)
+    blocks = np.empty(nb, np.int32)
+    offsets = np.empty(experts + 1, np.int32)
+    total = np.empty(1, np.int32)
+    lib().orc_moe_align(_ptr(ids), T, k, experts, block, _ptr(sorted_ids), cap, _ptr(blocks), nb, _ptr(offsets),
+                        _ptr(total))
+    return sorted_ids, blocks, offsets, total
+
+
+def moe_ffn_w4(x, ids, weights, wgu, sgu, zgu, wd, sd, zd, y=None, threads: int = 1) -> np.ndarray:
+    """y (f32 [T,H]) accumulated in place; a zero y is created when None."""
+    x = _c(x, np.float16)
+    ids, weights = _c(ids, np.int32), _c(weights, np.float32)
+    wgu, sgu, zgu = _c(wgu, np.uint8), _c(sgu, np.float16), _c(zgu, np.uint8)
+    wd, sd, zd = _c(wd, np.uint8), _c(sd, np.float16), _c(zd, np.uint8)
+    T, H = x.shape
+    top_k = ids.shape[1]
+    E, F2, _ = wgu.shape
+    F = F2 // 2
+    gs = H // sgu.shape[2]
+    assert F // sd.shape[2] == gs, "gate/up and down must share the group size"
+    y = np.zeros((T, H), np.float32) if y is None else y
+    assert y.dtype == np.float32 and y.flags["C_CONTIGUOUS"]
+    lib().orc_moe_ffn_w4(_ptr(x), T, H, _ptr(ids), _ptr(weights), top_k, E, _ptr(wgu), _ptr(sgu), _ptr(zgu),
+                         _ptr(wd), _ptr(sd), _ptr(zd), F, gs, _ptr(y), threads)
+    return y
+
+
+# ---- independent numpy restatements (used to pin the C oracle) ------------------
+
+def unpack_nibbles(packed: np.ndarray) -> np.ndarray:
+    """[N, K/2] uint8 -> [N, K] uint8; even k = low nibble."""
+    packed = np.asarray(packed, np.uint8)
+    out = np.empty((packed.shape[0], packed.shape[1] * 2), np.uint8)
+    out[:, 0::2] = packed & 15
+    out[:, 1::2] = packed >> 4
+    return out
+
+
+def dequant_w4_f64(packed, scales, zeros) -> np.ndarray:
+    q = unpack_nibbles(packed).astype(np.float64)
+    gs = q.shape[1] // scales.shape[1]
+    z = np.repeat(np.asarray(zeros, np.float64), gs, axis=1)
+    s = np.repeat(np.asarray(scales, np.float16).astype(np.float64), gs, axis=1)
+    return (q - z) * s
+
+
+def w4a16_f64(x, packed, scales, zeros) -> np.ndarray:
+    """float64 brute force (no rounding until the caller's comparison)."""
+    return np.asarray(x, np.float16).astype(np.float64) @ dequant_w4_f64(packed, scales, zeros).T
+
+
+def w8a16_f64(x, w, scales) -> np.ndarray:
+    acc = np.asarray(x, np.float16).astype(np.float64) @ np.asarray(w, np.int8).astype(np.float64).T
+    return acc * np.asarray(scales, np.float16).astype(np.float64)[None, :]
+
+
+def i8_gemm_i64(a, w, bias=None) -> np.ndarray:
+    acc = np.asarray(a, np.int64) @ np.asarray(w, np.int64).T
+    if bias is not None:
+        acc = acc + np.asarray(bias, np.int64)[None, :]
+    return acc
+
+
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(f: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 in numpy (independent of oracle.c)."""
+    u = np.asarray(f, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def w8a8_numpy(a, sa, w, sw) -> np.ndarray:
+    acc = i8_gemm_i64(a, w).astype(np.int32)  # exact: |acc| < 2^31 for these ranges
+    f = acc.astype(np.float32) * np.asarray(sa, np.float32)[:, None]
+    f = f * np.asarray(sw, np.float32)[None, :]
+    return f32_to_bf16_bits(f)
+
+
+def moe_route_numpy(logits, top_k: int, renormalize: bool = True):
+    lg = np.asarray(logits, np.float64)
+    order = np.argsort(-lg, axis=1, kind="stable")[:, :top_k]  # ties: lower index first
+    p = np.exp(lg - lg.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    w = np.take_along_axis(p, order, axis=1)
+    if renormalize:
+        w = w / w.sum(axis=1, keepdims=True)
+    return order.astype(np.int32), w
+
+
+def moe_align_numpy(ids, experts: int, block: int):
+    """Direct restatement of moe_align_block_size (cpu_runtime.py:1081-1098)."""
+    flat = np.asarray(ids, np.int64).reshape(-1)
+    R = flat.size
+    valid = (flat >= 0) & (flat < experts)
+    counts = np.bincount(flat[valid], minlength=experts)
+    padded = (counts + block - 1) // block * block
+    offsets = np.concatenate(([0], np.cumsum(padded))).astype(np.int32)
+    routes = np.argsort(np.where(valid, flat, experts), kind="stable")
+    cap, nb = align_sizes(R, experts, block)
+    sorted_ids = np.full(cap, R, np.int32)
+    blocks = np.full(nb, -1, np.int32)
+    src = 0
+    for e in range(experts):
+        b, c = int(offsets[e]), int(counts[e])
+        sorted_ids[b:b + c] = routes[src:src + c]
+        blocks[b // block:int(offsets[e + 1]) // block] = e
+        src += c
+    return sorted_ids, blocks, offsets, np.array([offsets[-1]], np.int32)
+
+
+def moe_ffn_f64(x, ids, weights, wgu, sgu, zgu, wd, sd, zd) -> np.ndarray:
+    """float64 brute force of the SiLU-gated W4 expert FFN (hidden kept in f64)."""
+    x = np.asarray(x, np.float16).astype(np.float64)
+    T, H = x.shape
+    top_k = ids.shape[1]
+    F = wgu.shape[1] // 2
+    y = np.zeros((T, H), np.float64)
+    for e in range(wgu.shape[0]):
+        toks, slots = np.nonzero(ids == e)
+        if toks.size == 0:
+            continue
+        gu = dequant_w4_f64(wgu[e], sgu[e], zgu[e])
+        dn = dequant_w4_f64(wd[e], sd[e], zd[e])
+        h = x[toks] @ gu.T
+        g, u = h[:, :F], h[:, F:]
+        a = g / (1.0 + np.exp(-g)) * u
+        o = a @ dn.T
+        np.add.at(y, toks, np.asarray(weights, np.float64)[toks, slots][:, None] * o)
+    return y

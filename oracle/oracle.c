@@ -1,0 +1,313 @@
+/*
+ * CPU oracle for the quantized-contraction hot path — TEST INFRASTRUCTURE ONLY.
+ *
+ * This file restates, in plain C, the numerics of the reference's CPU path for
+ * each function of the hot path. It is the checker: only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it, and
+ * never as the thing measured or shipped.
+ *
+ * Numerics follow the reference's CPU contraction semantics:
+ *   - float contraction: acc = fma(f32(a), f32(b), acc), zero-initialised,
+ *     sequential in k (lib/Conversion/KIRToCPU/Contractions.cpp:12-41,53-112);
+ *   - integer contraction: i8 x i8 sign-extended, int32 accumulate modulo 2^32
+ *     (Contractions.cpp:30-35,79-83; doc/dsl/types-numerics-and-effects.en.md:40);
+ *   - casts to f16/bf16 round to nearest even
+ *     (doc/dsl/types-numerics-and-effects.en.md:80).
+ * Build with -ffp-contract=off so that only the explicit fmaf() fuses.
+ * OpenMP splits whole output elements across threads; every element is
+ * computed by one thread in a fixed order, so results do not depend on the
+ * thread count.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oracle.h"
+
+/* ---- scalar conversions --------------------------------------------------- */
+
+float orc_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t mant = h & 0x3ffu;
+  uint32_t bits;
+  if (exp == 0) {
+    if (mant == 0) {
+      bits = sign;
+    } else { /* subnormal: normalise */
+      int e = -1;
+      do {
+        mant <<= 1;
+        ++e;
+      } while ((mant & 0x400u) == 0);
+      mant &= 0x3ffu;
+      bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (mant << 13);
+    }
+  } else if (exp == 0x1f) {
+    bits = sign | 0x7f800000u | (mant << 13);
+  } else {
+    bits = sign | ((exp + 127 - 15) << 23) | (mant << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t absx = x & 0x7fffffffu;
+  if (absx > 0x7f800000u) return sign | 0x7e00u; /* NaN */
+  if (absx >= 0x47800000u) return sign | 0x7c00u; /* >= 65536 (and inf) */
+  const int e = (int)(absx >> 23) - 127 + 15;
+  const uint32_t mant = absx & 0x7fffffu;
+  if (e >= 1) {
+    uint32_t h = ((uint32_t)e << 10) | (mant >> 13);
+    const uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h; /* carry may reach inf: correct */
+    return sign | (uint16_t)h;
+  }
+  /* f16 subnormal or zero: value / 2^-24 rounded to nearest even */
+  const int shift = 14 - e;
+  if (shift > 24) return sign;
+  const uint32_t m = mant | 0x800000u;
+  uint32_t h = m >> shift;
+  const uint32_t rem = m & ((1u << shift) - 1u);
+  const uint32_t half = 1u << (shift - 1);
+  if (rem > half || (rem == half && (h & 1u))) ++h;
+  return sign | (uint16_t)h;
+}
+
+uint16_t orc_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+/* ---- W8A16 ------------------------------------------------------------------
+ * y[m,n] = f16( f32(s[n]) * sum_k fma(f32(x[m,k]), f32(w[n,k])) ).
+ * Weight-only int8 written as I.cast(W, f16) -> I.matmul(acc f32) -> scale
+ * (doc/dsl/core.en.md:246); the int8 -> f32 decode is exact.
+ */
+void orc_w8a16(const uint16_t* x, int64_t M, int64_t K, const int8_t* w, int64_t N, const uint16_t* s, uint16_t* y,
+               int threads) {
+  int64_t i;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (i = 0; i < M * N; ++i) {
+    const int64_t m = i / N, n = i % N;
+    float acc = 0.f;
+    for (int64_t k = 0; k < K; ++k) acc = fmaf(orc_f16_to_f32(x[m * K + k]), (float)w[n * K + k], acc);
+    y[m * N + n] = orc_f32_to_f16(acc * orc_f16_to_f32(s[n]));
+  }
+}
+
+/* ---- W4A16 asymmetric group dequant ---------------------------------------------
+ * deq[n,k] = f32(q[n,k] - z[n,k/g]) * f32(s[n,k/g]) (dequantization in f32, as
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:97-102 does for the signed
+ * variant of examples/kernels/contraction/weight_only_int4.py:18-51);
+ * q from packed[n, k/2]: low nibble for even k, high nibble for odd k
+ * (weight_only_int4.py:66-70 packing; doc/dsl/quantized-operations.en.md:17).
+ * y[m,n] = f16( sum_k fma(f32(x[m,k]), deq[n,k]) ).
+ */
+void orc_w4a16(const uint16_t* x, int64_t M, int64_t K, const uint8_t* packed, int64_t N, const uint16_t* scales,
+               const uint8_t* zeros, int64_t gs, uint16_t* y, int threads) {
+  const int64_t G = K / gs;
+  int64_t i;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (i = 0; i < M * N; ++i) {
+    const int64_t m = i / N, n = i % N;
+    float acc = 0.f;
+    for (int64_t k = 0; k < K; ++k) {
+      const uint8_t byte = packed[n * (K / 2) + k / 2];
+      const int q = (k & 1) ? (byte >> 4) : (byte & 15);
+      const int64_t g = k / gs;
+      const float deq = (float)(q - (int)zeros[n * G + g]) * orc_f16_to_f32(scales[n * G + g]);
+      acc = fmaf(orc_f16_to_f32(x[m * K + k]), deq, acc);
+    }
+    y[m * N + n] = orc_f32_to_f16(acc);
+  }
+}
+
+/* ---- int8 contractions ------------------------------------------------------------
+ * acc[m,n] = sum_k i32(a[m,k]) * i32(w[n,k]) modulo 2^32 (gemm_i8,
+ * examples/kernels/contraction/gemm.py:29-39, weight K-contiguous [N,K]).
+ */
+static int32_t i8_dot(const int8_t* a, const int8_t* w, int64_t K) {
+  uint32_t acc = 0;
+  for (int64_t k = 0; k < K; ++k) acc += (uint32_t)((int32_t)a[k] * (int32_t)w[k]);
+  return (int32_t)acc;
+}
+
+void orc_i8_gemm_i32(const int8_t* a, int64_t M, int64_t K, const int8_t* w, int64_t N, const int32_t* bias,
+                     int32_t* c, int threads) {
+  int64_t i;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (i = 0; i < M * N; ++i) {
+    const int64_t m = i / N, n = i % N;
+    uint32_t v = (uint32_t)i8_dot(a + m * K, w + n * K, K);
+    if (bias) v += (uint32_t)bias[n];
+    c[m * N + n] = (int32_t)v;
+  }
+}
+
+/* out[m,n] = bf16( (f32(acc) * sa[m]) * sw[n] ), two fp32 multiplies left to
+ * right, then round to nearest even. */
+void orc_w8a8(const int8_t* a, int64_t M, int64_t K, const float* sa, const int8_t* w, int64_t N, const float* sw,
+              uint16_t* out, int threads) {
+  int64_t i;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (i = 0; i < M * N; ++i) {
+    const int64_t m = i / N, n = i % N;
+    float f = (float)i8_dot(a + m * K, w + n * K, K);
+    f = f * sa[m];
+    f = f * sw[n];
+    out[m * N + n] = orc_f32_to_bf16(f);
+  }
+}
+
+/* ---- MoE router ---------------------------------------------------------------------
+ * Top-k by raw logit (softmax is monotonic); a later expert replaces the best
+ * only if strictly greater, so ties keep the lower index (argmax convention,
+ * doc/dsl/types-numerics-and-effects.en.md:129). Probabilities:
+ * p_e = expf(l_e - max) / sum_e' expf(l_e' - max), sums sequential in e;
+ * renormalised as p_j / sum_{selected} p when renorm != 0.
+ */
+void orc_moe_route(const float* logits, int64_t T, int64_t E, int64_t top_k, int renorm, int32_t* ids,
+                   float* weights) {
+  for (int64_t t = 0; t < T; ++t) {
+    const float* l = logits + t * E;
+    float mx = l[0];
+    for (int64_t e = 1; e < E; ++e) mx = l[e] > mx ? l[e] : mx;
+    float sum = 0.f;
+    for (int64_t e = 0; e < E; ++e) sum += expf(l[e] - mx);
+    unsigned char taken[1024];
+    memset(taken, 0, sizeof(taken));
+    float p[64];
+    float psum = 0.f;
+    for (int64_t j = 0; j < top_k; ++j) {
+      int64_t best = -1;
+      float bv = 0.f;
+      for (int64_t e = 0; e < E; ++e) {
+        if (taken[e]) continue;
+        if (best < 0 || l[e] > bv) {
+          best = e;
+          bv = l[e];
+        }
+      }
+      taken[best] = 1;
+      ids[t * top_k + j] = (int32_t)best;
+      p[j] = expf(bv - mx) / sum;
+      psum += p[j];
+    }
+    for (int64_t j = 0; j < top_k; ++j) weights[t * top_k + j] = renorm ? p[j] / psum : p[j];
+  }
+}
+
+/* ---- MoE alignment ---------------------------------------------------------------------
+ * moe_align_block_size (experiments/cpu/baselines/pytorch/cpu_runtime.py:
+ * 1081-1098): histogram, block-padded cumulative offsets, route ids in stable
+ * order (the order of a stable argsort of the expert ids) inside each expert
+ * segment, sentinel R = T*top_k in unused slots, expert id per block
+ * (-1 past the padded total). Ids outside [0,E) are dropped.
+ */
+void orc_moe_align(const int32_t* ids, int64_t T, int64_t top_k, int64_t E, int64_t B, int32_t* sorted,
+                   int64_t capacity, int32_t* blocks, int64_t nblocks, int32_t* offsets, int32_t* total) {
+  const int64_t R = T * top_k;
+  int64_t* counts = (int64_t*)calloc((size_t)E, sizeof(int64_t));
+  int64_t* cursor = (int64_t*)calloc((size_t)E, sizeof(int64_t));
+  for (int64_t r = 0; r < R; ++r)
+    if (ids[r] >= 0 && ids[r] < E) counts[ids[r]]++;
+  offsets[0] = 0;
+  for (int64_t e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + (int32_t)((counts[e] + B - 1) / B * B);
+  total[0] = offsets[E];
+  for (int64_t i = 0; i < capacity; ++i) sorted[i] = (int32_t)R;
+  for (int64_t r = 0; r < R; ++r) {
+    const int32_t e = ids[r];
+    if (e < 0 || e >= E) continue;
+    sorted[offsets[e] + cursor[e]++] = (int32_t)r;
+  }
+  for (int64_t b = 0; b < nblocks; ++b) blocks[b] = -1;
+  for (int64_t e = 0; e < E; ++e)
+    for (int64_t b = offsets[e] / B; b < offsets[e + 1] / B; ++b) blocks[b] = (int32_t)e;
+  free(counts);
+  free(cursor);
+}
+
+/* ---- MoE expert FFN (W4, SiLU-gated) -------------------------------------------------------
+ * For route r = t*top_k + j with expert e = ids[r] (moe_expert_ffn,
+ * examples/kernels/ragged/moe.py:12-53, with a SiLU-gated first layer):
+ *   g[f] = sum_h fma(x[t,h], deq(Wgu[e])[f,h]);  u[f] = same with row F+f
+ *   a[f] = f16( (g / (1 + expf(-g))) * u )       (hidden cast to f16, moe.py:43)
+ *   o[d] = sum_f fma(f32(a[f]), deq(Wd[e])[d,f])
+ * and y[t,:] (f32, accumulated) gets y = y + w[r]*o slot by slot in order.
+ */
+static float w4_deq(const uint8_t* packed, const uint16_t* scales, const uint8_t* zeros, int64_t Kdim, int64_t gs,
+                    int64_t row, int64_t k) {
+  const uint8_t byte = packed[row * (Kdim / 2) + k / 2];
+  const int q = (k & 1) ? (byte >> 4) : (byte & 15);
+  const int64_t G = Kdim / gs;
+  return (float)(q - (int)zeros[row * G + k / gs]) * orc_f16_to_f32(scales[row * G + k / gs]);
+}
+
+void orc_moe_ffn_w4(const uint16_t* x, int64_t T, int64_t H, const int32_t* ids, const float* weights, int64_t top_k,
+                    int64_t E, const uint8_t* wgu, const uint16_t* sgu, const uint8_t* zgu, const uint8_t* wd,
+                    const uint16_t* sd, const uint8_t* zd, int64_t F, int64_t gs, float* y, int threads) {
+  const int64_t R = T * top_k;
+  float* out = (float*)malloc(sizeof(float) * (size_t)(R * H));
+  uint16_t* act = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)(R * F));
+  const int64_t gu_rows = 2 * F;
+  int64_t i;
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (i = 0; i < R * F; ++i) {
+    const int64_t r = i / F, f = i % F;
+    const int64_t t = r / top_k;
+    const int32_t e = ids[r];
+    if (e < 0 || e >= E) {
+      act[i] = 0;
+      continue;
+    }
+    const uint8_t* q = wgu + (int64_t)e * gu_rows * (H / 2);
+    const uint16_t* s = sgu + (int64_t)e * gu_rows * (H / gs);
+    const uint8_t* z = zgu + (int64_t)e * gu_rows * (H / gs);
+    float g = 0.f, u = 0.f;
+    for (int64_t h = 0; h < H; ++h) {
+      const float xv = orc_f16_to_f32(x[t * H + h]);
+      g = fmaf(xv, w4_deq(q, s, z, H, gs, f, h), g);
+      u = fmaf(xv, w4_deq(q, s, z, H, gs, F + f, h), u);
+    }
+    const float silu = g / (1.0f + expf(-g));
+    act[i] = orc_f32_to_f16(silu * u);
+  }
+#pragma omp parallel for num_threads(threads) schedule(static)
+  for (i = 0; i < R * H; ++i) {
+    const int64_t r = i / H, d = i % H;
+    const int32_t e = ids[r];
+    if (e < 0 || e >= E) {
+      out[i] = 0.f;
+      continue;
+    }
+    const uint8_t* q = wd + (int64_t)e * H * (F / 2);
+    const uint16_t* s = sd + (int64_t)e * H * (F / gs);
+    const uint8_t* z = zd + (int64_t)e * H * (F / gs);
+    float acc = 0.f;
+    for (int64_t f = 0; f < F; ++f) acc = fmaf(orc_f16_to_f32(act[r * F + f]), w4_deq(q, s, z, F, gs, d, f), acc);
+    out[i] = acc;
+  }
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t d = 0; d < H; ++d) {
+      float acc = y[t * H + d];
+      for (int64_t j = 0; j < top_k; ++j) {
+        const int64_t r = t * top_k + j;
+        if (ids[r] < 0 || ids[r] >= E) continue;
+        const float prod = weights[r] * out[r * H + d];
+        acc = acc + prod;
+      }
+      y[t * H + d] = acc;
+    }
+  free(out);
+  free(act);
+}

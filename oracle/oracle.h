@@ -1,0 +1,29 @@
+/* CPU oracle of the quantized-contraction hot path — test infrastructure only.
+ * f16 / bf16 values are passed as their uint16 bit patterns. `threads` is the
+ * OpenMP thread count (results do not depend on it). */
+#ifndef INTENT_ORACLE_H
+#define INTENT_ORACLE_H
+
+#include <stdint.h>
+
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+uint16_t orc_f32_to_bf16(float f);
+
+void orc_w8a16(const uint16_t* x, int64_t M, int64_t K, const int8_t* w, int64_t N, const uint16_t* s, uint16_t* y,
+               int threads);
+void orc_w4a16(const uint16_t* x, int64_t M, int64_t K, const uint8_t* packed, int64_t N, const uint16_t* scales,
+               const uint8_t* zeros, int64_t gs, uint16_t* y, int threads);
+void orc_i8_gemm_i32(const int8_t* a, int64_t M, int64_t K, const int8_t* w, int64_t N, const int32_t* bias,
+                     int32_t* c, int threads);
+void orc_w8a8(const int8_t* a, int64_t M, int64_t K, const float* sa, const int8_t* w, int64_t N, const float* sw,
+              uint16_t* out, int threads);
+void orc_moe_route(const float* logits, int64_t T, int64_t E, int64_t top_k, int renorm, int32_t* ids,
+                   float* weights);
+void orc_moe_align(const int32_t* ids, int64_t T, int64_t top_k, int64_t E, int64_t B, int32_t* sorted,
+                   int64_t capacity, int32_t* blocks, int64_t nblocks, int32_t* offsets, int32_t* total);
+void orc_moe_ffn_w4(const uint16_t* x, int64_t T, int64_t H, const int32_t* ids, const float* weights, int64_t top_k,
+                    int64_t E, const uint8_t* wgu, const uint16_t* sgu, const uint8_t* zgu, const uint8_t* wd,
+                    const uint16_t* sd, const uint8_t* zd, int64_t F, int64_t gs, float* y, int threads);
+
+#endif
