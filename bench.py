@@ -1,0 +1,252 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-contraction hot path (one JSON line).
+
+Headline: W4A16 decode GEMV, M=1, K=N=4096, asymmetric
+uint4 g=128 -> ``value`` in GB/s of algorithmic HBM bytes per second.
+The ``extra`` object carries the other configurations (decode M=16, prefill
+M=2048 TFLOP/s, W8A8, quantized MoE, W8A16), each measured the same way.
+
+A step is one pass of the hot path over one batch already resident in HBM.
+Steps are captured into a HIP graph and replayed; HIP events on the launch
+stream bracket the replay, so the per-step time is the average kernel
+duration plus inter-kernel gaps. Inputs rotate over enough copies to exceed
+the 256 MB Infinity Cache, so decode weights stream from HBM, not MALL.
+``cpu_baseline`` times the C oracle (a port of the reference's CPU numerics)
+on this host's cores over a bounded sample of the headline workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "W4A16 GEMM TFLOP/s & HBM GB/s (% of MI355X peak), decode M=1 + prefill M=2048"
+HBM_PEAK_GBS = 8000.0
+F16_PEAK_TFLOPS = 2516.6  # dense MFMA, no sparsity
+I8_PEAK_TOPS = 5033.2
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", choices=["decode", "all"], default="all",
+                    help="'decode' times only the headline workload")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+def graph_time(launches, steps: int, warmup: int) -> float:
+    """Average ms per step of `launches[i % len](...)` replayed from a HIP graph."""
+    import torch
+
+    for i in range(warmup):
+        launches[i % len(launches)]()
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            launches[i % len(launches)]()
+    graph.replay()  # warm replay
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def copies_for(bytes_per_set: int, minimum: int = 1) -> int:
+    return max(minimum, int(np.ceil(1.25 * MALL_BYTES / max(bytes_per_set, 1))) + 1)
+
+
+def bench_w4a16(M: int, K: int, N: int, steps: int, warmup: int, kernel: str = "auto") -> dict:
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    d = inputs.to_device(inputs.config1_w4a16_decode(0, M=M, K=K, N=N))
+    work = inputs.w4a16_work(M, K, N)
+    art = intent.compile(intent.weight_only_int4_asym_matmul, target=intent.MI355XTarget(0),
+                         constexprs={"KERNEL": kernel})
+    n = copies_for(work.bytes)
+    sets = [(d["x"].clone(), d["packed"].clone(), d["scales"].clone(), d["zeros"].clone()) for _ in range(n)]
+    calls = [art.prepare(*s) for s in sets]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    entry = art.observation.entry
+    del calls, sets
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "entry": entry, "copies": n}
+
+
+def bench_w8a16(steps: int, warmup: int) -> dict:
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    d = inputs.to_device(inputs.config0_w8a16(0))
+    work = inputs.w8a16_work(16, 1024, 1024)
+    art = intent.compile(intent.weight_only_int8_matmul, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes)
+    calls = [art.prepare(d["x"].clone(), d["w"].clone(), d["scales"].clone()) for _ in range(n)]
+    return {"ms": graph_time([c.launch for c in calls], steps, warmup), "work": work, "copies": n}
+
+
+def bench_w8a8(steps: int, warmup: int) -> dict:
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    d = inputs.to_device(inputs.config3_w8a8(0))
+    work = inputs.w8a8_work(4096, 8192, 8192)
+    art = intent.compile(intent.w8a8_scaled_matmul, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes, minimum=2)
+    sets = [tuple(d[k].clone() for k in ("a", "a_scales", "w", "w_scales")) for _ in range(n)]
+    calls = [art.prepare(*s) for s in sets]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls, sets
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
+def bench_moe(steps: int, warmup: int) -> dict:
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    h = inputs.config4_moe(0)
+    d = inputs.to_device(h)
+    T, H = h["x"].shape
+    E, F2, _ = h["wgu"].shape
+    work = inputs.moe_work(T, H, E, 2, F2 // 2)
+    art = intent.compile(intent.moe_expert_ffn_w4, target=intent.MI355XTarget(0), constexprs={"TOP_K": 2})
+    y = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    call = art.prepare(d["logits"], d["x"], d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"], y)
+    ms = graph_time([call.launch], steps, warmup)
+    return {"ms": ms, "work": work, "copies": 1}
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """C oracle (plain-C port of the reference CPU numerics) on the headline workload."""
+    import oracle
+    from intent_amd import inputs
+
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    d = inputs.config1_w4a16_decode(0, M=1)
+    work = inputs.w4a16_work(1, 4096, 4096)
+    oracle.w4a16(d["x"], d["packed"], d["scales"], d["zeros"], cores)  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.w4a16(d["x"], d["packed"], d["scales"], d["zeros"], cores)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= budget_s:
+            break
+    gbs = work.bytes * reps / elapsed / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{reps} full W4A16 M=1 K=N=4096 g128 GEMVs ({elapsed:.1f} s), oracle/oracle.c with OpenMP",
+            "ms_per_step": round(elapsed / reps * 1e3, 3)}
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is described in DESIGN.md, not launched)"}))
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device visible"}))
+        return 1
+    from intent_amd import _native
+
+    arch = _native.device_arch(0)
+    log(f"[bench] device 0: {arch}; decode M=1 steps={args.steps} warmup={args.warmup}")
+    dec = bench_w4a16(1, 4096, 4096, args.steps, args.warmup)
+    ms = dec["ms"]
+    gbs = dec["work"].bytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: seeded numpy draws of BASELINE configs (weights copied to exceed MALL)",
+        "config": {"workload": "w4a16 decode GEMV M=1 K=4096 N=4096 g128 asymmetric uint4 (BASELINE configs[1])",
+                   "kernel": dec["entry"], "weight_copies": dec["copies"], "arch": arch},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": dec["work"].bytes, "kernel": "w4a16_gemv_kernel"},
+    }
+    extra = {}
+    if args.only == "all":
+        steps = max(10, min(args.steps, 50))
+        warm = max(2, min(args.warmup, 5))
+        log("[bench] decode M=16")
+        r = bench_w4a16(16, 4096, 4096, args.steps, args.warmup)
+        extra["w4a16_decode_m16"] = _hbm_entry(r)
+        log("[bench] prefill M=2048 N=11008")
+        r = bench_w4a16(2048, 4096, 11008, steps, warm)
+        extra["w4a16_prefill_m2048"] = _flop_entry(r, F16_PEAK_TFLOPS, "TFLOP/s")
+        log("[bench] w8a8 M=4096 K=N=8192")
+        r = bench_w8a8(steps, warm)
+        extra["w8a8_m4096"] = _flop_entry(r, I8_PEAK_TOPS, "TOP/s")
+        log("[bench] moe T=512 E8 top2")
+        r = bench_moe(max(5, steps // 5), warm)
+        e = _flop_entry(r, F16_PEAK_TFLOPS, "TFLOP/s")
+        e["GB/s"] = round(r["work"].bytes / (r["ms"] * 1e-3) / 1e9, 2)
+        e["hbm_frac"] = round(e["GB/s"] / HBM_PEAK_GBS, 4)
+        extra["moe_w4_t512"] = e
+        log("[bench] w8a16 M=16")
+        r = bench_w8a16(args.steps, args.warmup)
+        extra["w8a16_m16"] = _hbm_entry(r)
+    line["extra"] = extra
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _hbm_entry(r: dict) -> dict:
+    gbs = r["work"].bytes / (r["ms"] * 1e-3) / 1e9
+    return {"workload": r["work"].name, "ms": round(r["ms"], 6), "GB/s": round(gbs, 2),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "TFLOP/s": round(r["work"].flops / (r["ms"] * 1e-3) / 1e12, 3)}
+
+
+def _flop_entry(r: dict, peak: float, unit: str) -> dict:
+    tf = r["work"].flops / (r["ms"] * 1e-3) / 1e12
+    return {"workload": r["work"].name, "ms": round(r["ms"], 6), unit: round(tf, 2), "peak": peak,
+            "frac": round(tf / peak, 4), "GB/s": round(r["work"].bytes / (r["ms"] * 1e-3) / 1e9, 2)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())
