@@ -79,7 +79,7 @@ def copies_for(bytes_per_set: int, minimum: int = 1) -> int:
     return max(minimum, int(np.ceil(1.25 * MALL_BYTES / max(bytes_per_set, 1))) + 1)
 
 
-def bench_w4a16(M: int, K: int, N: int, steps: int, warmup: int, kernel: str = "auto") -> dict:
+def bench_w4a16(M: int, K: int, N: int, steps: int, warmup: int, kernel: str = "auto", copies: int | None = None) -> dict:
     import torch
 
     import intent_amd as intent
@@ -89,7 +89,7 @@ def bench_w4a16(M: int, K: int, N: int, steps: int, warmup: int, kernel: str = "
     work = inputs.w4a16_work(M, K, N)
     art = intent.compile(intent.weight_only_int4_asym_matmul, target=intent.MI355XTarget(0),
                          constexprs={"KERNEL": kernel})
-    n = copies_for(work.bytes)
+    n = copies if copies is not None else copies_for(work.bytes)
     sets = [(d["x"].clone(), d["packed"].clone(), d["scales"].clone(), d["zeros"].clone()) for _ in range(n)]
     calls = [art.prepare(*s) for s in sets]
     ms = graph_time([c.launch for c in calls], steps, warmup)

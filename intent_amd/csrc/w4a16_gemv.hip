@@ -53,29 +53,39 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
   int s = wave;
   u32x4 wv[NT];
   u32x4 xv[4];
+  f16 sv[NT];
+  uint8_t zv[NT];
   if (s < nsteps) {
+    const int g = (s * 128 + quad * 32) / gs;
 #pragma unroll
-    for (int j = 0; j < NT; ++j) wv[j] = load16(wrow[j] + (int64_t)s * 64);
+    for (int j = 0; j < NT; ++j) {
+      wv[j] = load16(wrow[j] + (int64_t)s * 64);
+      sv[j] = srow[j][g];
+      zv[j] = zrow[j][g];
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) xv[t] = mvalid ? load16(xrow + (int64_t)s * 128 + t * 8) : u32x4{0, 0, 0, 0};
   }
   while (s < nsteps) {
-    const int g = (s * 128 + quad * 32) / gs;
     f16x2 zoff[NT], scale[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      zoff[j] = splat2((f16)(float)(1024 + zrow[j][g]));
-      scale[j] = splat2(srow[j][g]);
-    }
     u32x4 wc[NT], xc[4];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) wc[j] = wv[j];
+    for (int j = 0; j < NT; ++j) {
+      zoff[j] = splat2((f16)(float)(1024 + zv[j]));
+      scale[j] = splat2(sv[j]);
+      wc[j] = wv[j];
+    }
 #pragma unroll
     for (int t = 0; t < 4; ++t) xc[t] = xv[t];
     const int sn = s + KW;
-    if (sn < nsteps) {  // prefetch the next step before the math of this one
+    if (sn < nsteps) {  // prefetch the next step (weights, scales, zeros) before the math of this one
+      const int gn = (sn * 128 + quad * 32) / gs;
 #pragma unroll
-      for (int j = 0; j < NT; ++j) wv[j] = load16(wrow[j] + (int64_t)sn * 64);
+      for (int j = 0; j < NT; ++j) {
+        wv[j] = load16(wrow[j] + (int64_t)sn * 64);
+        sv[j] = srow[j][gn];
+        zv[j] = zrow[j][gn];
+      }
 #pragma unroll
       for (int t = 0; t < 4; ++t) xv[t] = mvalid ? load16(xrow + (int64_t)sn * 128 + t * 8) : u32x4{0, 0, 0, 0};
     }
@@ -106,6 +116,202 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
     const int n = n_base + j * 16 + nc;
     if (m < M && n < N) y[(int64_t)m * ldy + n] = (f16)sum;
   }
+}
+
+
+// ---- M <= 4: K-resident dot-product GEMV --------------------------------------
+//
+// A lane owns CH fixed 32-element K chunks (chunk c = lane + 64*i: bytes
+// [16c, 16c+16) of every weight row, so a wave reads 1 KB contiguous per row
+// and load). Its activations for those chunks are loaded once and kept in
+// registers, pre-paired to match the nibble decode below; each wave then
+// streams RW weight rows, issuing every load of the kernel up front.
+//
+// Decode without per-element dequantization: for a weight dword d (8 nibbles,
+// byte b = k 2b low / 2b+1 high), 0x64006400 | (d & 0x000F000F) is the f16
+// pair (1024+q0, 1024+q4) and 0x64006400 | (d & 0x00F000F0) is
+// (1024+16*q1, 1024+16*q5); the same on d >> 8 gives (q2, q6) and (q3, q7).
+// v_dot2_f32_f16 multiplies each pair with the matching activation pair
+// (products are exact in fp32), into acc1 (x1 pairs) and acc16 (x16 pairs).
+// Per chunk (one quant group): sum_k x_k (q_k - z) =
+//   acc1 + acc16/16 - (1024*xs1 + 64*xs16) - z*(xs1 + xs16),
+// where xs1 / xs16 are the activation sums over the x1 / x16 positions; the
+// result is scaled by s once per chunk. Lane partials are reduced across the
+// wave with cross-lane shuffles in a fixed order.
+template <int M, int CH, int RW>
+__global__ __launch_bounds__(256) void w4a16_gemv_dot_kernel(const f16* __restrict__ x, int64_t ldx, int K,
+                                                             const uint8_t* __restrict__ wq, int64_t ldw,
+                                                             const f16* __restrict__ sc,
+                                                             const uint8_t* __restrict__ zp, int64_t ldq, int gs,
+                                                             f16* __restrict__ y, int64_t ldy, int N) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * RW;
+  if (row0 >= N) return;  // wave-uniform
+  const int nchunks = K >> 5;
+
+  // Every load is unconditional (chunks past K are clamped to a valid address
+  // and zeroed later through their scale) and raw values are converted only
+  // where they are consumed, so all loads of the wave are in flight together.
+  int cc[CH];
+  bool cvalid[CH];
+  int grp[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = lane + 64 * i;
+    cvalid[i] = c < nchunks;
+    cc[i] = cvalid[i] ? c : nchunks - 1;
+    grp[i] = (cc[i] << 5) / gs;
+  }
+  u32x4 wv[RW][CH];
+  f16 sraw[RW][CH];
+  uint8_t zraw[RW][CH];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = row0 + r < N ? row0 + r : N - 1;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) wv[r][i] = load16(wq + (int64_t)n * ldw + (int64_t)cc[i] * 16);
+  }
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = row0 + r < N ? row0 + r : N - 1;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      sraw[r][i] = sc[(int64_t)n * ldq + grp[i]];
+      zraw[r][i] = zp[(int64_t)n * ldq + grp[i]];
+    }
+  }
+  u32x4 xraw[M][CH][4];
+#pragma unroll
+  for (int m = 0; m < M; ++m)
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xraw[m][i][j] = load16(x + (int64_t)m * ldx + (int64_t)cc[i] * 32 + j * 8);
+
+  // Activation pairs: for weight dword j of chunk i, a1 = (x0,x4), b1 = (x2,x6)
+  // meet the x1 nibble pairs, a16 = (x1,x5), b16 = (x3,x7) the x16 pairs.
+  f16x2 xa1[M][CH][4], xb1[M][CH][4], xa16[M][CH][4], xb16[M][CH][4];
+  float c0[M][CH], c1[M][CH];
+#pragma unroll
+  for (int m = 0; m < M; ++m) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      float s1 = 0.f, s16 = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4 v = xraw[m][i][j];
+        const uint32_t a1 = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+        const uint32_t a16 = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+        const uint32_t b1 = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+        const uint32_t b16 = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+        xa1[m][i][j] = bit_cast<f16x2>(a1);
+        xa16[m][i][j] = bit_cast<f16x2>(a16);
+        xb1[m][i][j] = bit_cast<f16x2>(b1);
+        xb16[m][i][j] = bit_cast<f16x2>(b16);
+        s1 += (float)xa1[m][i][j][0] + (float)xa1[m][i][j][1] + (float)xb1[m][i][j][0] + (float)xb1[m][i][j][1];
+        s16 += (float)xa16[m][i][j][0] + (float)xa16[m][i][j][1] + (float)xb16[m][i][j][0] +
+               (float)xb16[m][i][j][1];
+      }
+      c0[m][i] = 1024.f * s1 + 64.f * s16;
+      c1[m][i] = s1 + s16;
+    }
+  }
+
+  float part[M][RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) part[m][r] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      float acc1[M], acc16[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc1[m] = acc16[m] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t d = wv[r][i][j];
+        const uint32_t d8 = d >> 8;
+        const f16x2 lo = bit_cast<f16x2>((d & 0x000F000Fu) | 0x64006400u);
+        const f16x2 hi = bit_cast<f16x2>((d & 0x00F000F0u) | 0x64006400u);
+        const f16x2 lo8 = bit_cast<f16x2>((d8 & 0x000F000Fu) | 0x64006400u);
+        const f16x2 hi8 = bit_cast<f16x2>((d8 & 0x00F000F0u) | 0x64006400u);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          acc1[m] = __builtin_amdgcn_fdot2(lo, xa1[m][i][j], acc1[m], false);
+          acc1[m] = __builtin_amdgcn_fdot2(lo8, xb1[m][i][j], acc1[m], false);
+          acc16[m] = __builtin_amdgcn_fdot2(hi, xa16[m][i][j], acc16[m], false);
+          acc16[m] = __builtin_amdgcn_fdot2(hi8, xb16[m][i][j], acc16[m], false);
+        }
+      }
+      const float sv = (float)sraw[r][i] * (cvalid[i] ? 1.f : 0.f);
+      const float zv = (float)zraw[r][i];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const float t = (acc1[m] + acc16[m] * 0.0625f) - (c0[m][i] + zv * c1[m][i]);
+        part[m][r] = __builtin_fmaf(sv, t, part[m][r]);
+      }
+    }
+  }
+
+  // Butterfly reduction over the 64 lanes; every lane ends with the total.
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int r = 0; r < RW; ++r) part[m][r] += __shfl_xor(part[m][r], off);
+  }
+  if (lane < M * RW) {
+    const int m = lane / RW;
+    const int r = lane % RW;
+    float v = 0.f;
+#pragma unroll
+    for (int mm = 0; mm < M; ++mm)
+#pragma unroll
+      for (int rr = 0; rr < RW; ++rr)
+        if (mm == m && rr == r) v = part[mm][rr];
+    if (row0 + r < N) y[(int64_t)m * ldy + row0 + r] = (f16)v;
+  }
+}
+
+template <int M, int CH>
+void launch_dot(const f16* x, int64_t ldx, int K, const uint8_t* wq, int64_t ldw, const f16* sc, const uint8_t* zp,
+                int64_t ldq, int gs, f16* y, int64_t ldy, int N, hipStream_t st) {
+  constexpr int RW = CH >= 8 ? 1 : 8 / CH;
+  const int waves = (N + RW - 1) / RW;
+  const int blocks = (waves + 3) / 4;
+  hipLaunchKernelGGL((w4a16_gemv_dot_kernel<M, CH, RW>), dim3(blocks), dim3(256), 0, st, x, ldx, K, wq, ldw, sc, zp,
+                     ldq, gs, y, ldy, N);
+}
+
+// Picks the chunk count CH (K <= 2048*CH) for the dot kernel; returns false if
+// M*CH exceeds the register budget.
+template <int M>
+bool dispatch_dot(const f16* x, int64_t ldx, int K, const uint8_t* wq, int64_t ldw, const f16* sc, const uint8_t* zp,
+                  int64_t ldq, int gs, f16* y, int64_t ldy, int N, hipStream_t st) {
+  const int ch = (K + 2047) / 2048;
+  if (ch <= 1) {
+    launch_dot<M, 1>(x, ldx, K, wq, ldw, sc, zp, ldq, gs, y, ldy, N, st);
+    return true;
+  }
+  if (ch <= 2) {
+    launch_dot<M, 2>(x, ldx, K, wq, ldw, sc, zp, ldq, gs, y, ldy, N, st);
+    return true;
+  }
+  if constexpr (M <= 2) {
+    if (ch <= 4) {
+      launch_dot<M, 4>(x, ldx, K, wq, ldw, sc, zp, ldq, gs, y, ldy, N, st);
+      return true;
+    }
+  }
+  if constexpr (M == 1) {
+    if (ch <= 8) {
+      launch_dot<M, 8>(x, ldx, K, wq, ldw, sc, zp, ldq, gs, y, ldy, N, st);
+      return true;
+    }
+  }
+  return false;
 }
 
 template <int NT, int KW>
@@ -149,6 +355,15 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
   const f16* xx = (const f16*)x;
   const f16* ss = (const f16*)scales;
   f16* yy = (f16*)y;
+  bool done = false;
+  switch (M) {
+    case 1: done = dispatch_dot<1>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
+    case 2: done = dispatch_dot<2>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
+    case 3: done = dispatch_dot<3>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
+    case 4: done = dispatch_dot<4>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
+    default: break;
+  }
+  if (done) return launch_status("w4a16_gemv_dot");
   const int steps = (int)(K / 128);
   if (steps >= 16)
     launch_gemv<1, 16>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
