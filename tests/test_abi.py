@@ -1,0 +1,106 @@
+"""The C ABI: every symbol declared in include/intent_amd.h is exported, and the
+argument checks that run before any HIP call return the documented status codes.
+CPU only: no call here reaches a kernel launch."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from intent_amd import _native
+from intent_amd import errors
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "intent_amd.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(intent_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_expected_entries():
+    names = declared_symbols()
+    assert len(names) >= 16
+    assert set(names) == set(_native.SIGNATURES), "ctypes signature table and header disagree"
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.library()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.intent_amd_abi_version() == _native.ABI_VERSION
+
+
+def status(entry, *args):
+    return getattr(_native.library(), entry)(*args)
+
+
+P = ctypes.c_void_p
+FAKE = 0x1000  # a 16-byte aligned non-null address; never dereferenced by the checks
+
+
+def test_w4a16_argument_checks():
+    # K not a multiple of 128
+    assert status("intent_w4a16_matmul", FAKE, 1, 100, 100, FAKE, 8, 50, FAKE, FAKE, 4, 32, FAKE, 8, None) == \
+        errors.INTENT_ERR_UNSUPPORTED
+    assert "multiple of 128" in _native.last_error()
+    # group not a multiple of 32
+    assert status("intent_w4a16_gemv", FAKE, 1, 256, 256, FAKE, 8, 128, FAKE, FAKE, 16, 16, FAKE, 8, None) == \
+        errors.INTENT_ERR_UNSUPPORTED
+    # null pointer
+    assert status("intent_w4a16_gemm", None, 4, 256, 256, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT
+    # misaligned activation
+    assert status("intent_w4a16_gemm", FAKE + 2, 4, 256, 256, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None) == \
+        errors.INTENT_ERR_ALIGNMENT
+    # row stride smaller than the row
+    assert status("intent_w4a16_gemm", FAKE, 4, 256, 128, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT
+    # GEMV covers M <= 16 only
+    assert status("intent_w4a16_gemv", FAKE, 17, 256, 256, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None) == \
+        errors.INTENT_ERR_UNSUPPORTED
+    # empty problems are a no-op success
+    assert status("intent_w4a16_matmul", FAKE, 0, 256, 256, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None) == 0
+
+
+def test_int8_and_w8a16_checks():
+    assert status("intent_w8a8_gemm", FAKE, 4, 100, 100, FAKE, FAKE, 4, 100, FAKE, FAKE, 4, None) == \
+        errors.INTENT_ERR_UNSUPPORTED
+    assert status("intent_w8a8_gemm", FAKE, 4, 128, 128, None, FAKE, 4, 128, FAKE, FAKE, 4, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT
+    assert status("intent_i8_gemm_i32", FAKE, 4, 128, 136, FAKE, 4, 128, None, FAKE, 4, None) == \
+        errors.INTENT_ERR_ALIGNMENT
+    assert status("intent_w8a16_matmul", FAKE, 4, 96, 96, FAKE, 4, 96, FAKE, FAKE, 4, None) == \
+        errors.INTENT_ERR_UNSUPPORTED
+    assert status("intent_i8_gemm_i32", FAKE, 0, 128, 128, FAKE, 4, 128, None, FAKE, 4, None) == 0
+
+
+def test_moe_checks():
+    assert status("intent_moe_route", FAKE, 8, 8, 9, 1, FAKE, FAKE, None) == errors.INTENT_ERR_UNSUPPORTED
+    assert status("intent_moe_route", FAKE, 8, 300, 2, 1, FAKE, FAKE, None) == errors.INTENT_ERR_UNSUPPORTED
+    assert status("intent_moe_route", FAKE, 0, 8, 2, 1, FAKE, FAKE, None) == 0
+    # capacity below R + E*(B-1)
+    assert status("intent_moe_align", FAKE, 16, 2, 4, 128, FAKE, 100, FAKE, 10, FAKE, FAKE, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT
+    assert "needs" in _native.last_error()
+    assert status("intent_moe_align", FAKE, 16, 2, 1000, 128, FAKE, 10 ** 6, FAKE, 10 ** 4, FAKE, FAKE, None) == \
+        errors.INTENT_ERR_UNSUPPORTED
+    assert status("intent_moe_gate_up_w4", FAKE, 4, 256, 256, FAKE, FAKE, 2, 64, 2, FAKE, FAKE, FAKE, 2, 128, 128,
+                  FAKE, 128, None) == errors.INTENT_ERR_UNSUPPORTED  # block size 64
+    assert status("intent_moe_down_w4", FAKE, 96, FAKE, FAKE, 2, 128, 8, FAKE, FAKE, FAKE, 2, 256, 96, 32,
+                  FAKE, 256, None) == errors.INTENT_ERR_UNSUPPORTED  # F % 128
+    need = _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 128)
+    assert need >= 16 * 128 * 14336 * 2 + 1024 * 4096 * 4  # padded activations + route outputs
+    assert status("intent_moe_expert_ffn_w4", FAKE, FAKE, 512, 4096, 8, 2, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                  14336, 128, FAKE, FAKE, need - 1, None, None, None) == errors.INTENT_ERR_WORKSPACE
+    assert _native.library().intent_moe_workspace_size(-1, 2, 8, 64, 64, 128) == 0
+
+
+def test_status_mapping():
+    assert isinstance(errors.status_error(-1, "e", "m"), ValueError)
+    assert isinstance(errors.status_error(-2, "e", "m"), ValueError)
+    assert isinstance(errors.status_error(-3, "e", "m"), NotImplementedError)
+    assert isinstance(errors.status_error(-4, "e", "m"), RuntimeError)
+    assert isinstance(errors.status_error(-5, "e", "m"), ValueError)
+    with pytest.raises(NotImplementedError, match="multiple of 128"):
+        _native.call("intent_w4a16_matmul", FAKE, 1, 100, 100, FAKE, 8, 50, FAKE, FAKE, 4, 32, FAKE, 8, None)

@@ -1,0 +1,256 @@
+"""Pins the C oracle (oracle/oracle.c) with checks a plausible mistake would fail.
+
+Each function is checked against (a) the committed golden fixtures, (b) an
+independent numpy float64 / int64 restatement, and (c) closed forms and
+known answers (all-equal nibbles and zeros give 0, one-hot activations pick a
+single dequantized column, nibble order, integer wraparound, tie-breaking,
+stable scatter order). CPU only.
+"""
+from itertools import permutations
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from intent_amd import inputs
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def f16_close(y, y64):
+    err = np.abs(np.asarray(y, np.float64) - y64)
+    bound = 2.0 ** -11 * np.abs(y64) + 1e-5 * rms(y64) + 2.0 ** -25
+    assert np.all(err <= bound), f"max excess {np.max(err - bound)}"
+
+
+# ---- scalar conversions ----------------------------------------------------------
+
+def test_f16_to_f32_all_patterns():
+    lib = oracle.lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([lib.orc_f16_to_f32(int(b)) for b in bits], np.float32)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+
+
+def test_f32_to_f16_round_to_nearest_even():
+    lib = oracle.lib()
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 20000),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 65536.0, 1e9, -1e9, np.inf, -np.inf,
+                  2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -14, 2.0 ** -14 - 2.0 ** -25,
+                  1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11], np.float32),
+        # exact halfway points between adjacent f16 values
+        ((np.arange(-300, 300, dtype=np.float32) + 0.5) * 2.0 ** -10 + 1.0).astype(np.float32),
+    ])
+    want = vals.astype(np.float16).view(np.uint16)
+    got = np.array([lib.orc_f32_to_f16(float(v)) for v in vals], np.uint16)
+    assert np.array_equal(got, want)
+    assert lib.orc_f32_to_f16(float("nan")) & 0x7C00 == 0x7C00
+
+
+def test_f32_to_bf16_matches_torch():
+    lib = oracle.lib()
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([rng.standard_normal(5000).astype(np.float32) * 1e3,
+                           np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 3.3895314e38, np.inf, -0.0], np.float32)])
+    want = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = np.array([lib.orc_f32_to_bf16(float(v)) for v in vals], np.uint16)
+    assert np.array_equal(got, want)
+    assert np.array_equal(oracle.f32_to_bf16_bits(vals), want)
+
+
+# ---- W4A16 ------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["w4a16_m3_k256_n40_g128", "w4a16_m17_k512_n24_g64"])
+def test_w4a16_golden(name):
+    g = np.load(GOLDEN / f"{name}.npz")
+    y = oracle.w4a16(g["x"], g["packed"], g["scales"], g["zeros"], threads=2)
+    assert np.array_equal(y.view(np.uint16), g["y"].view(np.uint16))
+    f16_close(y, g["y_f64"])
+
+
+@pytest.mark.parametrize("M,K,N,group", [(1, 4096, 64, 128), (4, 384, 16, 32), (2, 1024, 8, 256)])
+def test_w4a16_vs_float64(M, K, N, group):
+    d = inputs.config1_w4a16_decode(3, M=M, K=K, N=N, group=group)
+    y = oracle.w4a16(d["x"], d["packed"], d["scales"], d["zeros"])
+    f16_close(y, oracle.w4a16_f64(d["x"], d["packed"], d["scales"], d["zeros"]))
+
+
+def test_w4a16_known_answers():
+    K, N = 256, 4
+    rng = np.random.default_rng(2)
+    nib = rng.integers(0, 16, (N, K), dtype=np.uint8)
+    zeros = rng.integers(0, 16, (N, 2), dtype=np.uint8)
+    scales = np.full((N, 2), 0.5, np.float16)
+    # q == z everywhere -> exactly zero whatever x is
+    q_eq = np.repeat(zeros, 128, axis=1)
+    x = inputs.normal_f16(rng, (3, K))
+    y = oracle.w4a16(x, inputs.pack_nibbles(q_eq), scales, zeros)
+    assert np.all(y == 0)
+    # one-hot activation picks (q[n,k] - z[n,g]) * s[n,g] exactly; covers nibble order (even k low)
+    for k in (0, 1, 2, 127, 128, 129, 255):
+        xo = np.zeros((1, K), np.float16)
+        xo[0, k] = 1
+        y = oracle.w4a16(xo, inputs.pack_nibbles(nib), scales, zeros)
+        want = (nib[:, k].astype(np.float32) - zeros[:, k // 128]) * 0.5
+        assert np.array_equal(y[0].astype(np.float32), want), k
+    # packed byte 0x21 holds k=0 -> 1 and k=1 -> 2
+    packed = np.zeros((1, K // 2), np.uint8)
+    packed[0, 0] = 0x21
+    xo = np.zeros((1, K), np.float16)
+    xo[0, 1] = 1
+    y = oracle.w4a16(xo, packed, np.ones((1, 2), np.float16), np.zeros((1, 2), np.uint8))
+    assert y[0, 0] == 2
+
+
+# ---- W8A16 ------------------------------------------------------------------------
+
+def test_w8a16_golden_and_f64():
+    g = np.load(GOLDEN / "w8a16_m5_k192_n33.npz")
+    y = oracle.w8a16(g["x"], g["w"], g["scales"])
+    assert np.array_equal(y.view(np.uint16), g["y"].view(np.uint16))
+    d = inputs.config0_w8a16(4, M=3, K=1024, N=16)
+    f16_close(oracle.w8a16(d["x"], d["w"], d["scales"]), oracle.w8a16_f64(d["x"], d["w"], d["scales"]))
+    # one-hot: y[n] = w[n,k] * s[n]
+    xo = np.zeros((1, 1024), np.float16)
+    xo[0, 7] = 1
+    y = oracle.w8a16(xo, d["w"], d["scales"])
+    want = (d["w"][:, 7].astype(np.float32) * d["scales"].astype(np.float32)).astype(np.float16)
+    assert np.array_equal(y[0], want)
+
+
+# ---- int8 -------------------------------------------------------------------------
+
+def test_i8_golden_and_exact():
+    g = np.load(GOLDEN / "w8a8_m9_k256_n20.npz")
+    assert np.array_equal(oracle.i8_gemm_i32(g["a"], g["w"], g["bias"]), g["acc_i32"])
+    assert np.array_equal(oracle.w8a8(g["a"], g["a_scales"], g["w"], g["w_scales"]), g["out_bf16_bits"])
+    rng = np.random.default_rng(5)
+    a = rng.integers(-128, 128, (7, 320), dtype=np.int8)
+    w = rng.integers(-128, 128, (11, 320), dtype=np.int8)
+    assert np.array_equal(oracle.i8_gemm_i32(a, w).astype(np.int64), oracle.i8_gemm_i64(a, w))
+
+
+def test_i8_wraps_modulo_2_32():
+    K = 140000  # 127*127*K exceeds 2^31
+    a = np.full((1, K), 127, np.int8)
+    w = np.full((1, K), 127, np.int8)
+    exact = 127 * 127 * K
+    wrapped = (exact + 2 ** 31) % 2 ** 32 - 2 ** 31
+    assert oracle.i8_gemm_i32(a, w)[0, 0] == wrapped
+    assert oracle.i8_gemm_i32(-a, w)[0, 0] == (-exact + 2 ** 31) % 2 ** 32 - 2 ** 31
+
+
+def test_w8a8_epilogue_order_matches_torch():
+    d = inputs.config3_w8a8(6, M=16, K=512, N=24)
+    acc = torch.from_numpy(oracle.i8_gemm_i64(d["a"], d["w"]).astype(np.float32))
+    f = acc * torch.from_numpy(d["a_scales"])[:, None]
+    f = f * torch.from_numpy(d["w_scales"])[None, :]
+    want = f.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.w8a8(d["a"], d["a_scales"], d["w"], d["w_scales"]), want)
+    assert np.array_equal(oracle.w8a8_numpy(d["a"], d["a_scales"], d["w"], d["w_scales"]), want)
+
+
+# ---- MoE routing ------------------------------------------------------------------
+
+def test_route_vs_numpy_and_ties():
+    rng = np.random.default_rng(7)
+    logits = rng.standard_normal((300, 8), dtype=np.float32)
+    logits[::3, 5] = logits[::3, 2]  # ties -> lower index first
+    logits[::7] = 0.5  # all-equal rows -> experts 0, 1
+    for k, renorm in ((2, True), (3, False), (1, True)):
+        ids, w = oracle.moe_route(logits, k, renorm)
+        nid, nw = oracle.moe_route_numpy(logits, k, renorm)
+        assert np.array_equal(ids, nid)
+        np.testing.assert_allclose(w, nw, rtol=1e-5)
+    ids, w = oracle.moe_route(logits[::7], 2, True)
+    assert np.all(ids == [0, 1]) and np.allclose(w, 0.5)
+
+
+def test_route_brute_force_orderings():
+    base = np.array([0.1, 0.7, -0.4, 1.3], np.float32)
+    for perm in permutations(range(4)):
+        lg = base[list(perm)][None, :]
+        ids, w = oracle.moe_route(lg, 2, True)
+        order = sorted(range(4), key=lambda e: -lg[0, e])
+        assert list(ids[0]) == order[:2]
+        p = np.exp(lg[0] - lg[0].max())
+        assert abs(w[0, 0] - p[order[0]] / (p[order[0]] + p[order[1]])) < 1e-6
+
+
+# ---- MoE alignment ----------------------------------------------------------------
+
+@pytest.mark.parametrize("T,k,E,B", [(24, 2, 4, 16), (4096, 2, 64, 128), (333, 3, 7, 32), (1, 1, 1, 128)])
+def test_align_vs_numpy_and_invariants(T, k, E, B):
+    rng = np.random.default_rng(T + E)
+    ids = rng.integers(0, E, (T, k), dtype=np.int32)
+    if T > 4:
+        ids[0, 0], ids[2, 0] = -1, E  # dropped
+    got = oracle.moe_align(ids, E, B)
+    for g, r in zip(got, oracle.moe_align_numpy(ids, E, B)):
+        assert np.array_equal(g, r)
+    sorted_ids, blocks, offsets, total = got
+    R = T * k
+    flat = ids.reshape(-1)
+    valid = np.nonzero((flat >= 0) & (flat < E))[0]
+    assert sorted(sorted_ids[sorted_ids < R].tolist()) == valid.tolist()  # each valid route exactly once
+    assert np.all(offsets % B == 0) and total[0] == offsets[-1]
+    for e in range(E):
+        seg = sorted_ids[offsets[e]:offsets[e + 1]]
+        live = seg[seg < R]
+        assert np.all(flat[live] == e) and np.all(np.diff(live) > 0)  # stable order
+        assert np.all(seg[len(live):] == R)  # padding after the routes
+        assert np.all(blocks[offsets[e] // B:offsets[e + 1] // B] == e)
+    assert np.all(blocks[total[0] // B:] == -1)
+
+
+def test_align_reference_case_canonical():
+    """The reference's moe_alignment case: ids = arange(T*k) % E (routing.py:46-115)."""
+    T, k, E, B = 4096, 2, 64, 128
+    ids = (np.arange(T * k) % E).astype(np.int32).reshape(T, k)
+    sorted_ids, blocks, offsets, total = oracle.moe_align(ids, E, B)
+    assert total[0] == E * B and np.array_equal(blocks[:E], np.arange(E))
+    for e in range(E):
+        assert np.array_equal(sorted_ids[e * B:(e + 1) * B], np.arange(e, T * k, E))
+
+
+def test_align_golden():
+    g = np.load(GOLDEN / "moe_t24_h128_e4_f128.npz")
+    got = oracle.moe_align(g["topk_ids"], 4, 16)
+    for a, name in zip(got, ("sorted_ids_b16", "blocks_b16", "offsets_b16", "total_b16")):
+        assert np.array_equal(a, g[name])
+
+
+# ---- MoE expert FFN ---------------------------------------------------------------
+
+def test_moe_ffn_golden_and_f64():
+    g = np.load(GOLDEN / "moe_t24_h128_e4_f128.npz")
+    ids, w = oracle.moe_route(g["logits"], 2, True)
+    assert np.array_equal(ids, g["topk_ids"])
+    y = oracle.moe_ffn_w4(g["x"], ids, w, g["wgu"], g["sgu"], g["zgu"], g["wd"], g["sd"], g["zd"], threads=2)
+    assert np.array_equal(y, g["y"])
+    assert np.max(np.abs(y - g["y_f64"])) <= 1e-2 * rms(g["y_f64"])
+
+
+def test_moe_ffn_accumulates_in_slot_order():
+    m = inputs.config4_moe(8, T=4, H=128, E=3, top_k=2, F=128)
+    ids, w = oracle.moe_route(m["logits"], 2, True)
+    zero = oracle.moe_ffn_w4(m["x"], ids, w, m["wgu"], m["sgu"], m["zgu"], m["wd"], m["sd"], m["zd"])
+    y0 = np.full((4, 128), 3.0, np.float32)
+    acc = oracle.moe_ffn_w4(m["x"], ids, w, m["wgu"], m["sgu"], m["zgu"], m["wd"], m["sd"], m["zd"], y=y0.copy())
+    np.testing.assert_allclose(acc - 3.0, zero, atol=1e-5)
+    # a single expert with weight 1 equals the dense SiLU-gated FFN brute force
+    ids1 = np.zeros((4, 1), np.int32)
+    w1 = np.ones((4, 1), np.float32)
+    y = oracle.moe_ffn_w4(m["x"], ids1, w1, m["wgu"], m["sgu"], m["zgu"], m["wd"], m["sd"], m["zd"])
+    y64 = oracle.moe_ffn_f64(m["x"], ids1, w1, m["wgu"], m["sgu"], m["zgu"], m["wd"], m["sd"], m["zd"])
+    assert np.max(np.abs(y - y64)) <= 1e-2 * rms(y64)
