@@ -256,3 +256,45 @@ def test_torch_op_roundtrip(gpu):
     assert cop(ro, w, y1) is None
     comb.run(ro, w, y2)
     assert torch.equal(y1, y2)
+
+
+# ---- committed golden fixtures ----------------------------------------------------
+
+from pathlib import Path  # noqa: E402
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+@pytest.mark.parametrize("name", ["w4a16_m3_k256_n40_g128", "w4a16_m17_k512_n24_g64"])
+@pytest.mark.parametrize("kernel", ["gemv", "gemm", "auto"])
+def test_golden_w4a16(gpu, name, kernel):
+    g = np.load(GOLDEN / f"{name}.npz")
+    if kernel == "gemv" and g["x"].shape[0] > 16:
+        pytest.skip("GEMV covers M <= 16")
+    y = art(intent.weight_only_int4_asym_matmul, KERNEL=kernel).run(dev(g["x"]), dev(g["packed"]), dev(g["scales"]),
+                                                                     dev(g["zeros"]))
+    assert_close_rms(host(y), g["y_f64"], what=name)
+
+
+def test_golden_w8a16_w8a8(gpu):
+    g = np.load(GOLDEN / "w8a16_m5_k192_n33.npz")
+    y = art(intent.weight_only_int8_matmul).run(dev(g["x"]), dev(g["w"]), dev(g["scales"]))
+    assert_close_rms(host(y), g["y_f64"], what="w8a16 golden")
+    g = np.load(GOLDEN / "w8a8_m9_k256_n20.npz")
+    out = art(intent.w8a8_scaled_matmul).run(dev(g["a"]), dev(g["a_scales"]), dev(g["w"]), dev(g["w_scales"]))
+    assert np.array_equal(host(out.view(torch.int16)).view(np.uint16), g["out_bf16_bits"])
+    acc = art(intent.gemm_i8_nt).run(dev(g["a"]), dev(g["w"]), dev(g["bias"]))
+    assert np.array_equal(host(acc), g["acc_i32"])
+
+
+def test_golden_moe(gpu):
+    g = np.load(GOLDEN / "moe_t24_h128_e4_f128.npz")
+    ids, wts = art(intent.moe_route_topk, TOP_K=2).run(dev(g["logits"]))
+    assert np.array_equal(host(ids), g["topk_ids"])
+    outs = art(intent.moe_align_block_size, EXPERTS=4, BLOCK_SIZE=16).run(ids)
+    for got, name in zip(outs, ("sorted_ids_b16", "blocks_b16", "offsets_b16", "total_b16")):
+        assert np.array_equal(host(got), g[name]), name
+    y = torch.zeros(24, 128, dtype=torch.float32, device="cuda")
+    art(intent.moe_expert_ffn_w4, TOP_K=2)(dev(g["logits"]), dev(g["x"]), dev(g["wgu"]), dev(g["sgu"]),
+                                           dev(g["zgu"]), dev(g["wd"]), dev(g["sd"]), dev(g["zd"]), y)
+    assert_close_rms(host(y), g["y_f64"], what="moe golden")
