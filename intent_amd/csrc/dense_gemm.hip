@@ -68,6 +68,9 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
                       int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld, int64_t gs,
                       void* y, int64_t y_ld, void* stream);
 
+int w8a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const int8_t* w, int64_t N, int64_t w_ld,
+                      const void* scales, void* y, int64_t y_ld, void* stream);
+
 int w4a16_gemm_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t N,
                       int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld, int64_t gs,
                       void* y, int64_t y_ld, void* stream) {
@@ -123,6 +126,7 @@ extern "C" int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t 
   INTENT_REQUIRE(x_ld >= K && w_ld >= K && y_ld >= N, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
   INTENT_REQUIRE(intent::aligned16(x) && intent::aligned16(w) && x_ld % 8 == 0 && w_ld % 16 == 0, INTENT_ERR_ALIGNMENT,
                  "x and w must be 16-byte aligned with 16-byte row strides");
+  if (M <= 16) return intent::w8a16_gemv_launch(x, M, K, x_ld, w, N, w_ld, scales, y, y_ld, stream);
   W8Source ws{w, w_ld};
   return launch_dense<W8Source, true>((const f16*)x, x_ld, (int)M, (int)N, (int)K, ws, (f16*)y, y_ld,
                                       (const f16*)scales, (hipStream_t)stream, "w8a16_matmul");

@@ -43,8 +43,8 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
     srow[j] = sc + (int64_t)n * ldq;
     zrow[j] = zp + (int64_t)n * ldq;
   }
-  const bool mvalid = r < M;
-  const f16* xrow = x + (int64_t)(mvalid ? r : 0) * ldx + quad * 32;
+  // Rows m >= M read row M-1 (unpredicated loads); their outputs are dropped.
+  const f16* xrow = x + (int64_t)(r < M ? r : M - 1) * ldx + quad * 32;
 
   f32x4 acc[NT];
 #pragma unroll
@@ -64,7 +64,7 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
       zv[j] = zrow[j][g];
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) xv[t] = mvalid ? load16(xrow + (int64_t)s * 128 + t * 8) : u32x4{0, 0, 0, 0};
+    for (int t = 0; t < 4; ++t) xv[t] = load16(xrow + (int64_t)s * 128 + t * 8);
   }
   while (s < nsteps) {
     f16x2 zoff[NT], scale[NT];
@@ -87,7 +87,7 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
         zv[j] = zrow[j][gn];
       }
 #pragma unroll
-      for (int t = 0; t < 4; ++t) xv[t] = mvalid ? load16(xrow + (int64_t)sn * 128 + t * 8) : u32x4{0, 0, 0, 0};
+      for (int t = 0; t < 4; ++t) xv[t] = load16(xrow + (int64_t)sn * 128 + t * 8);
     }
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
@@ -314,6 +314,51 @@ bool dispatch_dot(const f16* x, int64_t ldx, int K, const uint8_t* wq, int64_t l
   return false;
 }
 
+
+// ---- W8A16 GEMV (M <= 16) ----------------------------------------------------
+// Same split as the W4 MFMA GEMV: a workgroup owns 16 weight rows, its KW
+// waves take 64-wide K steps in turn. Lane (r = lane%16, quad = lane/16) loads
+// 16 int8 weights of row n0+r (k = step*64 + quad*16 ..) and the matching 16
+// activations of row r; two v_mfma_f32_16x16x32_f16 cover the step. The int8 ->
+// f16 conversion is exact; the channel scale multiplies the fp32 sum once.
+template <int KW>
+__global__ __launch_bounds__(64 * KW) void w8a16_gemv_kernel(const f16* __restrict__ x, int64_t ldx, int M, int K,
+                                                             const int8_t* __restrict__ w, int64_t ldw,
+                                                             const f16* __restrict__ sc, f16* __restrict__ y,
+                                                             int64_t ldy, int N) {
+  __shared__ f32x4 red[KW][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;
+  const int quad = lane >> 4;
+  const int n_base = blockIdx.x * 16;
+  const int n = n_base + r < N ? n_base + r : N - 1;
+  const int8_t* wrow = w + (int64_t)n * ldw + quad * 16;
+  const f16* xrow = x + (int64_t)(r < M ? r : M - 1) * ldx + quad * 16;
+  const int nsteps = K >> 6;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int s = wave; s < nsteps; s += KW) {
+    const u32x4 wv = load16(wrow + (int64_t)s * 64);
+    const u32x4 x0 = load16(xrow + (int64_t)s * 64);
+    const u32x4 x1 = load16(xrow + (int64_t)s * 64 + 8);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(bit_cast<f16x8>(x0), int8x8_to_f16(wv[0], wv[1]), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(bit_cast<f16x8>(x1), int8x8_to_f16(wv[2], wv[3]), acc, 0, 0, 0);
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  // 16x16 MFMA result layout: lane l holds column l%16, rows (l/16)*4 + i.
+  for (int o = threadIdx.x; o < 256; o += 64 * KW) {
+    const int m = o >> 4;
+    const int nc = o & 15;
+    const int src = (m >> 2) * 16 + nc;
+    float sum = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < KW; ++ww) sum += red[ww][src][m & 3];
+    const int nn = n_base + nc;
+    if (m < M && nn < N) y[(int64_t)m * ldy + nn] = (f16)(sum * (float)sc[nn]);
+  }
+}
+
 template <int NT, int KW>
 void launch_gemv(const f16* x, int64_t ldx, int M, int K, const uint8_t* wq, int64_t ldw, const f16* sc,
                  const uint8_t* zp, int64_t ldq, int gs, f16* y, int64_t ldy, int N, hipStream_t st) {
@@ -359,8 +404,6 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
   switch (M) {
     case 1: done = dispatch_dot<1>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
     case 2: done = dispatch_dot<2>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
-    case 3: done = dispatch_dot<3>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
-    case 4: done = dispatch_dot<4>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
     default: break;
   }
   if (done) return launch_status("w4a16_gemv_dot");
@@ -372,6 +415,23 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
   else
     launch_gemv<1, 4>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
   return launch_status("w4a16_gemv");
+}
+
+int w8a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const int8_t* w, int64_t N, int64_t w_ld,
+                      const void* scales, void* y, int64_t y_ld, void* stream) {
+  const int steps = (int)(K / 64);
+  const unsigned tiles = (unsigned)((N + 15) / 16);
+  hipStream_t st = (hipStream_t)stream;
+  if (steps >= 16)
+    hipLaunchKernelGGL(w8a16_gemv_kernel<16>, dim3(tiles), dim3(1024), 0, st, (const f16*)x, x_ld, (int)M, (int)K, w,
+                       w_ld, (const f16*)scales, (f16*)y, y_ld, (int)N);
+  else if (steps >= 4)
+    hipLaunchKernelGGL(w8a16_gemv_kernel<4>, dim3(tiles), dim3(256), 0, st, (const f16*)x, x_ld, (int)M, (int)K, w,
+                       w_ld, (const f16*)scales, (f16*)y, y_ld, (int)N);
+  else
+    hipLaunchKernelGGL(w8a16_gemv_kernel<1>, dim3(tiles), dim3(64), 0, st, (const f16*)x, x_ld, (int)M, (int)K, w,
+                       w_ld, (const f16*)scales, (f16*)y, y_ld, (int)N);
+  return launch_status("w8a16_gemv");
 }
 
 }  // namespace intent
