@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
 }
 
 
-// ---- M <= 4: K-resident dot-product GEMV --------------------------------------
+// ---- M <= 2: K-resident dot-product GEMV --------------------------------------
 //
 // A lane owns CH fixed 32-element K chunks (chunk c = lane + 64*i: bytes
 // [16c, 16c+16) of every weight row, so a wave reads 1 KB contiguous per row

@@ -1,6 +1,6 @@
 // W8A8 int8 GEMM on v_mfma_i32_32x32x32_i8 (gfx950), exact int32 accumulation.
 //
-// Tile: 128 x 128 outputs, BK = 64 bytes, 256 threads = 4 waves (2 x 2), each
+// Tile: 128 x 128 outputs, BK = 128 bytes (64 when K is not a multiple of 128), 256 threads = 4 waves (2 x 2), each
 // wave 64 x 64 = 2 x 2 MFMA tiles. Both operands are K-contiguous int8 rows
 // staged through LDS with a register prefetch of the next k-tile.
 // Epilogues: bf16(f32(acc) * a_scale[m] * w_scale[n]) or int32 acc + bias[n].
@@ -11,25 +11,27 @@ namespace {
 
 constexpr int BM = 128;
 constexpr int BN = 128;
-constexpr int BK = 64;
 constexpr int NTHREADS = 256;
-constexpr int LDS_LD = BK + 16;  // bytes per LDS row
 
+// BK bytes of K per step; rows padded by 16 bytes against bank aliasing.
+template <int BK>
 struct I8Tile {
-  int8_t a[BM][LDS_LD];
-  int8_t b[BN][LDS_LD];
+  int8_t a[BM][BK + 16];
+  int8_t b[BN][BK + 16];
 };
 
 enum class Epi { kBf16Scaled, kI32Bias };
 
-template <Epi E>
+template <Epi E, int BK>
 __global__ __launch_bounds__(NTHREADS) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t lda, int M,
                                                            const int8_t* __restrict__ w, int64_t ldw, int N, int K,
                                                            const float* __restrict__ a_scales,
                                                            const float* __restrict__ w_scales,
                                                            const int32_t* __restrict__ bias, void* __restrict__ out,
                                                            int64_t ldo, int mblocks) {
-  __shared__ I8Tile t;
+  __shared__ I8Tile<BK> t;
+  constexpr int CPR = BK / 16;                 // 16-byte chunks per row
+  constexpr int NCH = BM * CPR / NTHREADS;     // chunks per thread per operand
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -39,18 +41,19 @@ __global__ __launch_bounds__(NTHREADS) void i8_gemm_kernel(const int8_t* __restr
   const int m0 = (bid % mblocks) * BM;
   const int n0 = (bid / mblocks) * BN;
 
-  // Staging: chunk c = tid + 256*i (i = 0,1) covers row c/4, bytes (c%4)*16.
-  const int8_t* ap[2];
-  const int8_t* wp[2];
-  int srow[2], scol[2];
+  // Staging: chunk c = tid + 256*i covers row c/CPR, bytes (c%CPR)*16. Rows
+  // past the end read a clamped valid row; their outputs are never stored.
+  const int8_t* ap[NCH];
+  const int8_t* wp[NCH];
+  int srow[NCH], scol[NCH];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     const int c = tid + NTHREADS * i;
-    srow[i] = c >> 2;
-    scol[i] = (c & 3) * 16;
+    srow[i] = c / CPR;
+    scol[i] = (c % CPR) * 16;
     const int m = m0 + srow[i];
     const int n = n0 + srow[i];
-    ap[i] = m < M ? a + (int64_t)m * lda + scol[i] : nullptr;
+    ap[i] = a + (int64_t)(m < M ? m : M - 1) * lda + scol[i];
     wp[i] = w + (int64_t)(n < N ? n : N - 1) * ldw + scol[i];
   }
 
@@ -63,23 +66,23 @@ __global__ __launch_bounds__(NTHREADS) void i8_gemm_kernel(const int8_t* __restr
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
 
   const int nk = K / BK;
-  u32x4 ar[2], wr[2];
+  u32x4 ar[NCH], wr[NCH];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    ar[i] = ap[i] ? load16(ap[i]) : u32x4{0, 0, 0, 0};
+  for (int i = 0; i < NCH; ++i) {
+    ar[i] = load16(ap[i]);
     wr[i] = load16(wp[i]);
   }
   for (int kt = 0; kt < nk; ++kt) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       *reinterpret_cast<u32x4*>(&t.a[srow[i]][scol[i]]) = ar[i];
       *reinterpret_cast<u32x4*>(&t.b[srow[i]][scol[i]]) = wr[i];
     }
     __syncthreads();
     if (kt + 1 < nk) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        ar[i] = ap[i] ? load16(ap[i] + (int64_t)(kt + 1) * BK) : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < NCH; ++i) {
+        ar[i] = load16(ap[i] + (int64_t)(kt + 1) * BK);
         wr[i] = load16(wp[i] + (int64_t)(kt + 1) * BK);
       }
     }
@@ -149,8 +152,12 @@ int launch_i8(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const float* 
   const int nblocks = (int)((N + BN - 1) / BN);
   const int64_t grid = (int64_t)mblocks * nblocks;
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
-  hipLaunchKernelGGL((i8_gemm_kernel<E>), dim3((unsigned)grid), dim3(NTHREADS), 0, (hipStream_t)stream, a, a_ld,
-                     (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
+  if (K % 128 == 0)
+    hipLaunchKernelGGL((i8_gemm_kernel<E, 128>), dim3((unsigned)grid), dim3(NTHREADS), 0, (hipStream_t)stream, a,
+                       a_ld, (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
+  else
+    hipLaunchKernelGGL((i8_gemm_kernel<E, 64>), dim3((unsigned)grid), dim3(NTHREADS), 0, (hipStream_t)stream, a,
+                       a_ld, (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
   return intent::launch_status(name);
 }
 
