@@ -48,6 +48,10 @@ def parse():
                     help="'decode' times only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--probe", choices=["traffic"], default=None,
+                    help="'traffic': only run 40 decode launches over distinct weight copies, then four 64 MiB "
+                         "device copies (run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE; the copies calibrate "
+                         "the counters)")
     return ap.parse_args()
 
 
@@ -147,6 +151,37 @@ def bench_moe(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": 1}
 
 
+def measured_traffic() -> int | None:
+    """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE profile."""
+    path = ROOT / "profiles" / "w4a16_gemv_dot_m1_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
+def traffic_probe() -> None:
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    d = inputs.to_device(inputs.config1_w4a16_decode(0, M=1))
+    art = intent.compile(intent.weight_only_int4_asym_matmul, target=intent.MI355XTarget(0))
+    sets = [(d["x"].clone(), d["packed"].clone(), d["scales"].clone(), d["zeros"].clone()) for _ in range(40)]
+    for call in [art.prepare(*s) for s in sets]:
+        call.launch()
+    torch.cuda.synchronize()
+    n = 64 << 20
+    for _ in range(4):
+        a = torch.empty(n, dtype=torch.uint8, device="cuda")
+        b = torch.empty(n, dtype=torch.uint8, device="cuda")
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """C oracle (plain-C port of the reference CPU numerics) on the headline workload."""
     import oracle
@@ -182,6 +217,9 @@ def main() -> int:
         return 1
     from intent_amd import _native
 
+    if args.probe == "traffic":
+        traffic_probe()
+        return 0
     arch = _native.device_arch(0)
     log(f"[bench] device 0: {arch}; decode M=1 steps={args.steps} warmup={args.warmup}")
     dec = bench_w4a16(1, 4096, 4096, args.steps, args.warmup)
@@ -203,7 +241,7 @@ def main() -> int:
         "config": {"workload": "w4a16 decode GEMV M=1 K=4096 N=4096 g128 asymmetric uint4 (BASELINE configs[1])",
                    "kernel": dec["entry"], "weight_copies": dec["copies"], "arch": arch},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": dec["work"].bytes, "kernel": "w4a16_gemv_kernel"},
     }
     extra = {}
