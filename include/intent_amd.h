@@ -165,7 +165,7 @@ int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_k, int64_t 
  * act f16 [num_blocks*block_size, F].
  * Replaces the first contraction + activation of moe_expert_ffn
  * (examples/kernels/ragged/moe.py:28-45) for SiLU-gated W4 experts.
- * Requires block_size == 128, H % 128 == 0, F % 64 == 0.
+ * Requires block_size 64 or 128, H % 128 == 0, F % 64 == 0.
  */
 int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_t x_ld,
                           const int32_t* sorted_route_ids, const int32_t* expert_blocks,
@@ -180,7 +180,7 @@ int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_t x_ld,
  * Wd: packed [E][H, F/2], scales/zeros [E][H, F/g]; out f32 [R, H].
  * Replaces the second contraction of moe_expert_ffn
  * (examples/kernels/ragged/moe.py:46-53).
- * Requires block_size == 128, F % 128 == 0.
+ * Requires block_size 64 or 128, F % 128 == 0.
  */
 int intent_moe_down_w4(const void* act, int64_t act_ld,
                        const int32_t* sorted_route_ids, const int32_t* expert_blocks,
@@ -206,9 +206,14 @@ int intent_moe_combine(const float* route_out, int64_t out_ld,
  * gate/up(SiLU) -> down -> combine into y (f32 [T,H], accumulated).
  * Replaces moe_expert_ffn (examples/kernels/ragged/moe.py:12-53) together
  * with its host alignment (examples/programs/composition.py:134-174).
- * `workspace` must hold intent_moe_workspace_size(...) bytes (16-byte aligned).
- * block_size is 128. If topk_ids_out / topk_weights_out are non-null the
- * routing results are also copied there ([T,top_k] each).
+ * `workspace` must hold intent_moe_workspace_size(T, top_k, E, H, F, 0) bytes
+ * (16-byte aligned). The composite picks its own alignment block (64 while
+ * experts average fewer than 256 routes, else 128) and may split the down
+ * projection's K into up to 4 partial sums, which the combine adds in split
+ * order before weighting. intent_moe_workspace_size with block_size > 0 gives
+ * the staged pipeline's buffers for that block size (no split).
+ * If topk_ids_out / topk_weights_out are non-null the routing results are
+ * also copied there ([T,top_k] each).
  */
 size_t intent_moe_workspace_size(int64_t T, int64_t top_k, int64_t E, int64_t H,
                                  int64_t F, int64_t block_size);

@@ -26,6 +26,13 @@ INTENT_DEVICE To bit_cast(From v) {
 INTENT_DEVICE u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 INTENT_DEVICE void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// v_bfi_b32: (mask & a) | (~mask & b).
+INTENT_DEVICE uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
+  return r;
+}
+
 // f16 value with bit pattern 0x6400 | q equals 1024 + q for q in 0..1023.
 // Subtracting (1024 + z) is exact for nibbles, so (q - z) comes out exact in
 // f16 and one packed multiply applies the group scale.
@@ -40,10 +47,14 @@ INTENT_DEVICE f16x8 dequant8(uint32_t w, f16x2 zoff, f16x2 scale) {
   uint32_t p1 = __builtin_amdgcn_perm(w4, w, 0x0c050c01u);
   uint32_t p2 = __builtin_amdgcn_perm(w4, w, 0x0c060c02u);
   uint32_t p3 = __builtin_amdgcn_perm(w4, w, 0x0c070c03u);
-  p0 = (p0 & 0x000F000Fu) | 0x64006400u;
-  p1 = (p1 & 0x000F000Fu) | 0x64006400u;
-  p2 = (p2 & 0x000F000Fu) | 0x64006400u;
-  p3 = (p3 & 0x000F000Fu) | 0x64006400u;
+  // (p & 0x000F000F) | 0x64006400 as one v_bfi_b32 (bitfield select); the
+  // magic word sits in a register the compiler cannot fold back into a literal.
+  uint32_t magic = 0x64006400u;
+  asm("" : "+v"(magic));
+  p0 = bfi(0x000F000Fu, p0, magic);
+  p1 = bfi(0x000F000Fu, p1, magic);
+  p2 = bfi(0x000F000Fu, p2, magic);
+  p3 = bfi(0x000F000Fu, p3, magic);
   f16x2 h0 = (bit_cast<f16x2>(p0) - zoff) * scale;
   f16x2 h1 = (bit_cast<f16x2>(p1) - zoff) * scale;
   f16x2 h2 = (bit_cast<f16x2>(p2) - zoff) * scale;

@@ -17,26 +17,27 @@ struct ClampRows {
   }
 };
 
-template <class WSrc, bool kColScale>
-__global__ __launch_bounds__(NTHREADS) void dense_gemm_kernel(DenseRows rows, WSrc w, int N, int K, f16* __restrict__ y,
-                                                              int64_t ldy, const f16* __restrict__ colscale,
-                                                              int mblocks) {
-  __shared__ SharedTile tile;
+template <class T, class WSrc, bool kColScale>
+__global__ __launch_bounds__(T::NT, 2) void dense_gemm_kernel(DenseRows rows, WSrc w, int N, int K,
+                                                                            f16* __restrict__ y, int64_t ldy,
+                                                                            const f16* __restrict__ colscale,
+                                                                            int mblocks) {
+  __shared__ typename T::Shared tile;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * BM;
-  const int n0 = (bid / mblocks) * BN;
-  f32x16 acc[2][2];
-  mainloop(rows, m0, w, ClampRows{n0, N}, K, tile, acc);
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  f32x16 acc[T::TI][T::TJ];
+  mainloop<T>(rows, m0, w, ClampRows{n0, N}, K, tile, acc);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + acc_col(j);
+  for (int j = 0; j < T::TJ; ++j) {
+    const int col = n0 + T::acc_col(j);
     if (col >= N) continue;
     const float cs = kColScale ? (float)colscale[col] : 1.0f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < T::TI; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = m0 + acc_row(i, v);
+        const int row = m0 + T::acc_row(i, v);
         if (row < rows.M) {
           const float val = kColScale ? acc[i][j][v] * cs : acc[i][j][v];
           y[(int64_t)row * ldy + col] = (f16)val;
@@ -45,16 +46,36 @@ __global__ __launch_bounds__(NTHREADS) void dense_gemm_kernel(DenseRows rows, WS
   }
 }
 
+template <class T, class WSrc, bool kColScale>
+int launch_tile(const f16* x, int64_t ldx, int M, int N, int K, const WSrc& w, f16* y, int64_t ldy,
+                const f16* colscale, hipStream_t st, const char* name) {
+  const int mblocks = (M + T::BM - 1) / T::BM;
+  const int nblocks = (N + T::BN - 1) / T::BN;
+  const int64_t grid = (int64_t)mblocks * nblocks;
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
+  hipLaunchKernelGGL((dense_gemm_kernel<T, WSrc, kColScale>), dim3((unsigned)grid), dim3(T::NT), 0, st,
+                     DenseRows{x, ldx, M}, w, N, K, y, ldy, colscale, mblocks);
+  return intent::launch_status(name);
+}
+
+#ifndef INTENT_DENSE_TILE
+#define INTENT_DENSE_TILE 1
+#endif
+
+// Tile choice: 256 x 128 (128 x 64 per wave) once M fills it, else 128 x 128.
 template <class WSrc, bool kColScale>
 int launch_dense(const f16* x, int64_t ldx, int M, int N, int K, const WSrc& w, f16* y, int64_t ldy,
                  const f16* colscale, hipStream_t st, const char* name) {
-  const int mblocks = (M + BM - 1) / BM;
-  const int nblocks = (N + BN - 1) / BN;
-  const int64_t grid = (int64_t)mblocks * nblocks;
-  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
-  hipLaunchKernelGGL((dense_gemm_kernel<WSrc, kColScale>), dim3((unsigned)grid), dim3(NTHREADS), 0, st,
-                     DenseRows{x, ldx, M}, w, N, K, y, ldy, colscale, mblocks);
-  return intent::launch_status(name);
+#if INTENT_DENSE_TILE == 0
+  return launch_tile<Tile<128, 128, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+#elif INTENT_DENSE_TILE == 1
+  if (M > 128) return launch_tile<Tile<256, 128, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+  return launch_tile<Tile<128, 128, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+#elif INTENT_DENSE_TILE == 2
+  return launch_tile<Tile<128, 256, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+#elif INTENT_DENSE_TILE == 3
+  return launch_tile<Tile<256, 256, 2, 4>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+#endif
 }
 
 }  // namespace
@@ -75,6 +96,11 @@ int w4a16_gemm_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
                       int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld, int64_t gs,
                       void* y, int64_t y_ld, void* stream) {
   if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(gs == 32 || gs % 64 == 0, INTENT_ERR_UNSUPPORTED,
+                 "the tiled GEMM needs group_size 32 or a multiple of 64, got %lld", (long long)gs);
+  INTENT_REQUIRE(intent::fits_offset(N, packed_ld) && intent::fits_offset(N, qparam_ld * 2) &&
+                     intent::fits_offset(256 + 1, x_ld * 2),
+                 INTENT_ERR_UNSUPPORTED, "w4a16_gemm: operand too large for 31-bit buffer offsets");
   W4Source w{packed, packed_ld, (const f16*)scales, zeros, qparam_ld, (int)gs};
   return launch_dense<W4Source, false>((const f16*)x, x_ld, (int)M, (int)N, (int)K, w, (f16*)y, y_ld, nullptr,
                                        (hipStream_t)stream, "w4a16_gemm");
@@ -127,6 +153,8 @@ extern "C" int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t 
   INTENT_REQUIRE(intent::aligned16(x) && intent::aligned16(w) && x_ld % 8 == 0 && w_ld % 16 == 0, INTENT_ERR_ALIGNMENT,
                  "x and w must be 16-byte aligned with 16-byte row strides");
   if (M <= 16) return intent::w8a16_gemv_launch(x, M, K, x_ld, w, N, w_ld, scales, y, y_ld, stream);
+  INTENT_REQUIRE(intent::fits_offset(N, w_ld) && intent::fits_offset(256 + 1, x_ld * 2), INTENT_ERR_UNSUPPORTED,
+                 "w8a16_matmul: operand too large for 31-bit buffer offsets");
   W8Source ws{w, w_ld};
   return launch_dense<W8Source, true>((const f16*)x, x_ld, (int)M, (int)N, (int)K, ws, (f16*)y, y_ld,
                                       (const f16*)scales, (hipStream_t)stream, "w8a16_matmul");

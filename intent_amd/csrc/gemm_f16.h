@@ -4,11 +4,13 @@
 //
 // A rows come from a RowSource (dense rows, MoE token gather, or padded MoE
 // rows); B rows are quantized weight rows decoded by a WeightSource while being
-// staged into LDS, so the MFMA loop only ever sees f16 tiles. An Epilogue
+// staged into LDS, so the MFMA loop only ever sees f16 tiles. An epilogue
 // consumes the fp32 accumulators.
 //
-// Tile: BM x BN = 128 x 128, BK = 64, 256 threads = 4 waves in a 2 x 2 grid,
-// each wave 64 x 64 = 2 x 2 tiles of v_mfma_f32_32x32x16_f16.
+// A Tile<BM, BN, WM, WN> is BM x BN outputs computed by WM x WN waves; each
+// wave owns a (BM/WM) x (BN/WN) block of 32 x 32 v_mfma_f32_32x32x16_f16 tiles.
+// BK = 64 k per LDS stage. LDS traffic per MFMA falls with the wave block:
+// a 64 x 64 wave block reads 1 KB of fragments per MFMA, 128 x 64 reads 0.75 KB.
 // Pipeline: global loads of k-tile t+1 are issued into registers before the
 // MFMAs of tile t, then decoded and written to LDS after the barrier.
 #pragma once
@@ -17,25 +19,98 @@
 
 namespace gemm {
 
-constexpr int BM = 128;
-constexpr int BN = 128;
 constexpr int BK = 64;
-constexpr int NTHREADS = 256;
 constexpr int LDS_LD = BK + 8;  // halfs per LDS row: 144 B breaks bank aliasing of the 32-row fragment reads
 
-struct SharedTile {
-  f16 a[BM][LDS_LD];
-  f16 b[BN][LDS_LD];
+template <int BM_, int BN_, int WM_, int WN_>
+struct Tile {
+  static constexpr int BM = BM_;
+  static constexpr int BN = BN_;
+  static constexpr int WM = WM_;
+  static constexpr int WN = WN_;
+  static constexpr int NT = WM * WN * 64;
+  static constexpr int TI = BM / WM / 32;  // 32-row MFMA tiles per wave
+  static constexpr int TJ = BN / WN / 32;  // 32-col MFMA tiles per wave
+  static_assert(TI >= 1 && TJ >= 1 && TI * WM * 32 == BM && TJ * WN * 32 == BN, "tile shape");
+  static_assert((BM * 8) % NT == 0, "A staging chunks must divide evenly");
+
+  struct Shared {
+    f16 a[BM][LDS_LD];
+    f16 b[BN][LDS_LD];
+  };
+
+  INTENT_DEVICE static int wave_m() { return (threadIdx.x >> 6) % WM; }
+  INTENT_DEVICE static int wave_n() { return (threadIdx.x >> 6) / WM; }
+  // Tile-local coordinates of accumulator element v of acc[i][j]; 32x32 layout:
+  // lane l holds column l%32, rows (v/4)*8 + (l/32)*4 + v%4 for v = 0..15.
+  INTENT_DEVICE static int acc_row(int i, int v) {
+    const int lane = threadIdx.x & 63;
+    return wave_m() * (BM / WM) + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+  }
+  INTENT_DEVICE static int acc_col(int j) {
+    const int lane = threadIdx.x & 63;
+    return wave_n() * (BN / WN) + j * 32 + (lane & 31);
+  }
 };
 
+// Segment tile: up to 256 rows of one MoE expert x BN columns, 2 x 2 waves.
+// Wave row wm owns the 32-row MFMA tiles 2i + wm (i < 4), so a partly filled
+// segment keeps both wave rows equally busy; 32-row tiles past the active
+// count are neither staged nor multiplied.
+template <int BN_>
+struct SegTile {
+  static constexpr int BM = 256;
+  static constexpr int BN = BN_;
+  static constexpr int WM = 2;
+  static constexpr int WN = 2;
+  static constexpr int NT = 256;
+  static constexpr int TI = 4;
+  static constexpr int TJ = BN / 64;
+  static_assert(TJ >= 1 && TJ * 64 == BN, "segment tile width");
+
+  struct Shared {
+    f16 a[BM][LDS_LD];
+    f16 b[BN][LDS_LD];
+  };
+
+  INTENT_DEVICE static int wave_m() { return (threadIdx.x >> 6) % WM; }
+  INTENT_DEVICE static int wave_n() { return (threadIdx.x >> 6) / WM; }
+  INTENT_DEVICE static int tile_index(int i) { return 2 * i + wave_m(); }
+  INTENT_DEVICE static int acc_row(int i, int v) {
+    const int lane = threadIdx.x & 63;
+    return tile_index(i) * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+  }
+  INTENT_DEVICE static int acc_col(int j) {
+    const int lane = threadIdx.x & 63;
+    return wave_n() * (BN / WN) + j * 32 + (lane & 31);
+  }
+};
+
+// ---- buffer addressing ----------------------------------------------------
+// Operands are read with buffer loads: a per-workgroup resource (base
+// pointer), a per-thread 32-bit byte offset fixed for the whole K loop and a
+// scalar byte offset that advances with k, so the loop spends no vector
+// instructions on addresses. Hosts check that every offset fits 31 bits.
+
+using Rsrc = __amdgpu_buffer_rsrc_t;
+INTENT_DEVICE Rsrc make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+INTENT_DEVICE u32x4 bload16(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+
 // ---- A row sources ------------------------------------------------------
-// row(p) returns the f16 row pointer of tile row p or nullptr for a zero row.
+// base(m0) is the tile's base pointer; off(p) the element offset of tile row
+// p from it. Rows that hold no data (past M, MoE padding) map to some valid
+// row: loads stay unpredicated and the epilogue never stores those rows.
 
 struct DenseRows {
   const f16* x;
   int64_t ld;
   int M;
-  INTENT_DEVICE const f16* row(int p) const { return p < M ? x + (int64_t)p * ld : nullptr; }
+  INTENT_DEVICE const f16* base(int m0) const { return x + (int64_t)m0 * ld; }
+  INTENT_DEVICE int off(int m0, int p) const { return (int)((p < M ? p - m0 : M - 1 - m0) * ld); }
 };
 
 // MoE gate/up: padded row p holds route sorted[p]; token = route / top_k.
@@ -45,9 +120,10 @@ struct GatherRows {
   const int32_t* sorted;
   int R;
   int top_k;
-  INTENT_DEVICE const f16* row(int p) const {
+  INTENT_DEVICE const f16* base(int) const { return x; }
+  INTENT_DEVICE int off(int, int p) const {
     const int r = sorted[p];
-    return (r >= 0 && r < R) ? x + (int64_t)(r / top_k) * ld : nullptr;
+    return (int)(((r >= 0 && r < R) ? r / top_k : 0) * ld);
   }
 };
 
@@ -55,16 +131,18 @@ struct GatherRows {
 struct PaddedRows {
   const f16* x;
   int64_t ld;
-  INTENT_DEVICE const f16* row(int p) const { return x + (int64_t)p * ld; }
+  INTENT_DEVICE const f16* base(int m0) const { return x + (int64_t)m0 * ld; }
+  INTENT_DEVICE int off(int m0, int p) const { return (int)((p - m0) * ld); }
 };
 
 // ---- Weight sources -----------------------------------------------------
-// Each thread stages a fixed set of weight rows; RowMap maps a B-tile row
-// (0..BN-1) to a weight row index. load() fetches k-tile kt into registers,
-// store() decodes it into LDS row(s).
+// Each thread stages a fixed set of 16-byte weight chunks; RowMap maps a
+// B-tile row (0..BN-1) to a weight row index. load() fetches k-tile kt into
+// registers, store() decodes it into LDS.
 
-// W4 asymmetric group quant; a thread owns one weight row and one half
-// (32 nibbles) of the 64-k tile.
+// W4 asymmetric group quant: a chunk is one half (32 nibbles) of a row's
+// 64-k tile. The group size is 32 or a multiple of 64, so the group of a
+// chunk is 2*kt + half or kt*64/gs: a scalar term plus a per-slot constant.
 struct W4Source {
   const uint8_t* q;
   int64_t ldq;  // bytes per row
@@ -75,46 +153,67 @@ struct W4Source {
 
   struct Regs {
     u32x4 w;
-    f16 s;
+    uint16_t s;
     uint8_t z;
   };
   struct Slot {
-    const uint8_t* q;
-    const f16* s;
-    const uint8_t* z;
+    uint32_t q;  // byte offsets
+    uint32_t s;
+    uint32_t z;
     int lds_row;
     int half;
   };
-  static constexpr int kSlots = 1;
+  template <class T>
+  static constexpr int slots() {
+    static_assert((T::BN * 2) % T::NT == 0, "W4 staging chunks must divide evenly");
+    return T::BN * 2 / T::NT;
+  }
 
-  template <class RowMap>
+  template <class T, class RowMap>
   INTENT_DEVICE void slot(int tid, const RowMap& rowmap, Slot* out) const {
-    const int lrow = tid >> 1;
-    const int half = tid & 1;
-    const int wrow = rowmap(lrow);
-    out[0].q = q + (int64_t)wrow * ldq + half * 16;
-    out[0].s = s + (int64_t)wrow * ldp;
-    out[0].z = z + (int64_t)wrow * ldp;
-    out[0].lds_row = lrow;
-    out[0].half = half;
-  }
-  INTENT_DEVICE void load(const Slot* sl, int kt, Regs* r) const {
-    const int g = (kt * BK + sl[0].half * 32) / gs;
-    r[0].w = load16(sl[0].q + (int64_t)kt * (BK / 2));
-    r[0].s = sl[0].s[g];
-    r[0].z = sl[0].z[g];
-  }
-  INTENT_DEVICE void store(const Slot* sl, const Regs* r, SharedTile& t) const {
-    const f16x2 zoff = splat2((f16)(float)(1024 + r[0].z));
-    const f16x2 sc = splat2(r[0].s);
-    f16* dst = &t.b[sl[0].lds_row][sl[0].half * 32];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<f16x8*>(dst + 8 * i) = dequant8(r[0].w[i], zoff, sc);
+    for (int i = 0; i < slots<T>(); ++i) {
+      const int c = tid + i * T::NT;
+      const int lrow = c >> 1;
+      const int half = c & 1;
+      const int wrow = rowmap(lrow);
+      const int extra = gs == 32 ? half : 0;
+      out[i].q = (uint32_t)(wrow * ldq + half * 16);
+      out[i].s = (uint32_t)((wrow * ldp + extra) * 2);
+      out[i].z = (uint32_t)(wrow * ldp + extra);
+      out[i].lds_row = lrow;
+      out[i].half = half;
+    }
+  }
+  struct Rsrcs {
+    Rsrc q, s, z;
+  };
+  INTENT_DEVICE Rsrcs rsrcs() const { return {make_rsrc(q), make_rsrc(s), make_rsrc(z)}; }
+  template <class T>
+  INTENT_DEVICE void load(const Rsrcs& rs, const Slot* sl, int kt, Regs* r) const {
+    const uint32_t g = gs == 32 ? 2 * kt : (kt * BK) / gs;
+#pragma unroll
+    for (int i = 0; i < slots<T>(); ++i) {
+      r[i].w = bload16(rs.q, sl[i].q, (uint32_t)kt * (BK / 2));
+      r[i].s = __builtin_amdgcn_raw_buffer_load_b16(rs.s, sl[i].s, g * 2, 0);
+      r[i].z = __builtin_amdgcn_raw_buffer_load_b8(rs.z, sl[i].z, g, 0);
+    }
+  }
+  template <class T>
+  INTENT_DEVICE void store(const Slot* sl, const Regs* r, typename T::Shared& t) const {
+#pragma unroll
+    for (int i = 0; i < slots<T>(); ++i) {
+      const f16x2 zoff = splat2((f16)(float)(1024 + r[i].z));
+      const f16x2 sc = splat2(bit_cast<f16>(r[i].s));
+      f16* dst = &t.b[sl[i].lds_row][sl[i].half * 32];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) *reinterpret_cast<f16x8*>(dst + 8 * c) = dequant8(r[i].w[c], zoff, sc);
+    }
   }
 };
 
 // W8 per-channel: int8 rows converted exactly to f16 (the channel scale is
-// applied in the epilogue). A thread owns two 16-byte chunks.
+// applied in the epilogue). A chunk is a quarter (16 bytes) of a row's 64-k tile.
 struct W8Source {
   const int8_t* q;
   int64_t ldq;
@@ -123,31 +222,41 @@ struct W8Source {
     u32x4 w;
   };
   struct Slot {
-    const int8_t* q;
+    uint32_t q;
     int lds_row;
     int quarter;
   };
-  static constexpr int kSlots = 2;
+  template <class T>
+  static constexpr int slots() {
+    static_assert((T::BN * 4) % T::NT == 0, "W8 staging chunks must divide evenly");
+    return T::BN * 4 / T::NT;
+  }
 
-  template <class RowMap>
+  template <class T, class RowMap>
   INTENT_DEVICE void slot(int tid, const RowMap& rowmap, Slot* out) const {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * NTHREADS;
+    for (int i = 0; i < slots<T>(); ++i) {
+      const int c = tid + i * T::NT;
       const int lrow = c >> 2;
       const int quarter = c & 3;
-      out[i].q = q + (int64_t)rowmap(lrow) * ldq + quarter * 16;
+      out[i].q = (uint32_t)(rowmap(lrow) * ldq + quarter * 16);
       out[i].lds_row = lrow;
       out[i].quarter = quarter;
     }
   }
-  INTENT_DEVICE void load(const Slot* sl, int kt, Regs* r) const {
+  struct Rsrcs {
+    Rsrc q;
+  };
+  INTENT_DEVICE Rsrcs rsrcs() const { return {make_rsrc(q)}; }
+  template <class T>
+  INTENT_DEVICE void load(const Rsrcs& rs, const Slot* sl, int kt, Regs* r) const {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) r[i].w = load16(sl[i].q + (int64_t)kt * BK);
+    for (int i = 0; i < slots<T>(); ++i) r[i].w = bload16(rs.q, sl[i].q, (uint32_t)kt * BK);
   }
-  INTENT_DEVICE void store(const Slot* sl, const Regs* r, SharedTile& t) const {
+  template <class T>
+  INTENT_DEVICE void store(const Slot* sl, const Regs* r, typename T::Shared& t) const {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < slots<T>(); ++i) {
       f16* dst = &t.b[sl[i].lds_row][sl[i].quarter * 16];
       *reinterpret_cast<f16x8*>(dst) = int8x8_to_f16(r[i].w[0], r[i].w[1]);
       *reinterpret_cast<f16x8*>(dst + 8) = int8x8_to_f16(r[i].w[2], r[i].w[3]);
@@ -156,81 +265,154 @@ struct W8Source {
 };
 
 // ---- Main loop ------------------------------------------------------------
-// acc[i][j]: wave tile rows wm*64 + i*32, cols wn*64 + j*32; 32x32 layout:
-// lane l holds column l%32, rows (v/4)*8 + (l/32)*4 + v%4 for v = 0..15.
+// acc[i][j]: wave block rows wave_m*(BM/WM) + i*32, cols wave_n*(BN/WN) + j*32.
 
-template <class Rows, class WSrc, class RowMap>
-INTENT_DEVICE void mainloop(const Rows& rows, int m0, const WSrc& wsrc, const RowMap& rowmap, int K, SharedTile& t,
-                            f32x16 (&acc)[2][2]) {
+template <class T, class Rows, class WSrc, class RowMap>
+INTENT_DEVICE void mainloop(const Rows& rows, int m0, const WSrc& wsrc, const RowMap& rowmap, int K,
+                            typename T::Shared& t, f32x16 (&acc)[T::TI][T::TJ]) {
+  constexpr int NA = T::BM * 8 / T::NT;  // 16-byte A chunks per thread
+  constexpr int NW = WSrc::template slots<T>();
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave & 1;
-  const int wn = wave >> 1;
+  const int wm = T::wave_m();
+  const int wn = T::wave_n();
 
-  // A staging: thread owns rows tid/8 + 32*i, column chunk (tid%8)*8.
-  const f16* arow[4];
+  // A staging: chunk c = tid + NT*i covers row c/8, halfs (c%8)*8.
+  const Rsrc ars = make_rsrc(rows.base(m0));
+  uint32_t aoff[NA];
+  int a_r[NA];
   const int acol = (tid & 7) * 8;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f16* p = rows.row(m0 + (tid >> 3) + 32 * i);
-    arow[i] = p ? p + acol : nullptr;
+  for (int i = 0; i < NA; ++i) {
+    a_r[i] = (tid + T::NT * i) >> 3;
+    aoff[i] = (uint32_t)(rows.off(m0, m0 + a_r[i]) + acol) * 2;
   }
-  typename WSrc::Slot slots[WSrc::kSlots];
-  wsrc.slot(tid, rowmap, slots);
+  typename WSrc::Slot slots[NW];
+  wsrc.template slot<T>(tid, rowmap, slots);
+  const typename WSrc::Rsrcs wrs = wsrc.rsrcs();
 
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < T::TI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   const int nk = K / BK;
-  u32x4 areg[4];
-  typename WSrc::Regs wreg[WSrc::kSlots];
+  u32x4 areg[NA];
+  typename WSrc::Regs wreg[NW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) areg[i] = arow[i] ? load16(arow[i]) : u32x4{0, 0, 0, 0};
-  wsrc.load(slots, 0, wreg);
+  for (int i = 0; i < NA; ++i) areg[i] = bload16(ars, aoff[i], 0);
+  wsrc.template load<T>(wrs, slots, 0, wreg);
 
   for (int kt = 0; kt < nk; ++kt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(&t.a[(tid >> 3) + 32 * i][acol]) = areg[i];
-    wsrc.store(slots, wreg, t);
+    for (int i = 0; i < NA; ++i) *reinterpret_cast<u32x4*>(&t.a[a_r[i]][acol]) = areg[i];
+    wsrc.template store<T>(slots, wreg, t);
     __syncthreads();
     if (kt + 1 < nk) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        areg[i] = arow[i] ? load16(arow[i] + (int64_t)(kt + 1) * BK) : u32x4{0, 0, 0, 0};
-      wsrc.load(slots, kt + 1, wreg);
+      for (int i = 0; i < NA; ++i) areg[i] = bload16(ars, aoff[i], (uint32_t)(kt + 1) * BK * 2);
+      wsrc.template load<T>(wrs, slots, kt + 1, wreg);
     }
+#ifndef INTENT_SETPRIO
+#define INTENT_SETPRIO 0
+#endif
+    if (INTENT_SETPRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      f16x8 af[2], bf[2];
+      f16x8 af[T::TI], bf[T::TJ];
       const int kof = kk * 16 + (lane >> 5) * 8;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const f16x8*>(&t.a[wm * 64 + i * 32 + (lane & 31)][kof]);
+      for (int i = 0; i < T::TI; ++i)
+        af[i] = *reinterpret_cast<const f16x8*>(&t.a[wm * (T::BM / T::WM) + i * 32 + (lane & 31)][kof]);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const f16x8*>(&t.b[wn * 64 + j * 32 + (lane & 31)][kof]);
+      for (int j = 0; j < T::TJ; ++j)
+        bf[j] = *reinterpret_cast<const f16x8*>(&t.b[wn * (T::BN / T::WN) + j * 32 + (lane & 31)][kof]);
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < T::TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < T::TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
+    if (INTENT_SETPRIO) __builtin_amdgcn_s_setprio(0);
     __syncthreads();
   }
 }
 
-// Tile-local coordinates of accumulator element v of acc[i][j].
-INTENT_DEVICE int acc_row(int i, int v) {
-  const int lane = threadIdx.x & 63;
-  const int wm = (threadIdx.x >> 6) & 1;
-  return wm * 64 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-}
-INTENT_DEVICE int acc_col(int j) {
-  const int lane = threadIdx.x & 63;
-  const int wn = threadIdx.x >> 7;
-  return wn * 64 + j * 32 + (lane & 31);
+// Segment main loop: `nact` (1..8) active 32-row tiles starting at tile row
+// m0. A chunk i of a thread is row (tid/8) + 32*i, i.e. it lies in 32-row
+// tile i, so "chunk active" is uniform across the workgroup.
+template <class T, class Rows, class WSrc, class RowMap>
+INTENT_DEVICE void seg_mainloop(const Rows& rows, int m0, int nact, const WSrc& wsrc, const RowMap& rowmap, int K,
+                                typename T::Shared& t, f32x16 (&acc)[T::TI][T::TJ]) {
+  constexpr int NA = T::BM * 8 / T::NT;
+  constexpr int NW = WSrc::template slots<T>();
+  static_assert(NA == 8, "one A chunk per 32-row tile");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wn = T::wave_n();
+
+  const Rsrc ars = make_rsrc(rows.base(m0));
+  uint32_t aoff[NA];
+  const int acol = (tid & 7) * 8;
+  const int arow_in_tile = tid >> 3;
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+    aoff[i] = (uint32_t)(rows.off(m0, m0 + arow_in_tile + 32 * (i < nact ? i : 0)) + acol) * 2;
+  typename WSrc::Slot slots[NW];
+  wsrc.template slot<T>(tid, rowmap, slots);
+  const typename WSrc::Rsrcs wrs = wsrc.rsrcs();
+
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  bool live[T::TI];
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) live[i] = T::tile_index(i) < nact;
+
+  const int nk = K / BK;
+  u32x4 areg[NA];
+  typename WSrc::Regs wreg[NW];
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+    if (i < nact) areg[i] = bload16(ars, aoff[i], 0);
+  wsrc.template load<T>(wrs, slots, 0, wreg);
+
+  for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+      if (i < nact) *reinterpret_cast<u32x4*>(&t.a[arow_in_tile + 32 * i][acol]) = areg[i];
+    wsrc.template store<T>(slots, wreg, t);
+    __syncthreads();
+    if (kt + 1 < nk) {
+#pragma unroll
+      for (int i = 0; i < NA; ++i)
+        if (i < nact) areg[i] = bload16(ars, aoff[i], (uint32_t)(kt + 1) * BK * 2);
+      wsrc.template load<T>(wrs, slots, kt + 1, wreg);
+    }
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      f16x8 af[T::TI], bf[T::TJ];
+      const int kof = kk * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j)
+        bf[j] = *reinterpret_cast<const f16x8*>(&t.b[wn * (T::BN / T::WN) + j * 32 + (lane & 31)][kof]);
+#pragma unroll
+      for (int i = 0; i < T::TI; ++i) {
+        if (!live[i]) continue;
+        af[i] = *reinterpret_cast<const f16x8*>(&t.a[T::tile_index(i) * 32 + (lane & 31)][kof]);
+#pragma unroll
+        for (int j = 0; j < T::TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
 }
 
 }  // namespace gemm

@@ -16,6 +16,13 @@ void clear_error();
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// rows * stride_bytes stays below 2^31: the byte offsets of buffer loads are
+// 32-bit and the kernels keep them non-negative ints.
+inline bool fits_offset(int64_t rows, int64_t stride_bytes) {
+  return rows >= 0 && stride_bytes >= 0 && (rows == 0 || stride_bytes <= ((int64_t)1 << 31) / rows) &&
+         rows * stride_bytes < ((int64_t)1 << 31);
+}
+
 // Checks hipGetLastError() after a launch.
 int launch_status(const char* kernel);
 

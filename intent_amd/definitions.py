@@ -284,7 +284,7 @@ def _ffn_check(env: dict) -> None:
 
 def _ffn_workspace(env: dict) -> int:
     lib = _native.library()
-    return int(lib.intent_moe_workspace_size(env["T"], env["TOP_K"], env["E"], env["H"], env["F"], 128))
+    return int(lib.intent_moe_workspace_size(env["T"], env["TOP_K"], env["E"], env["H"], env["F"], 0))
 
 
 def _ffn_launch(v: dict, env: dict, stream: int, workspace) -> str:

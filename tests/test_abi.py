@@ -85,12 +85,14 @@ def test_moe_checks():
     assert "needs" in _native.last_error()
     assert status("intent_moe_align", FAKE, 16, 2, 1000, 128, FAKE, 10 ** 6, FAKE, 10 ** 4, FAKE, FAKE, None) == \
         errors.INTENT_ERR_UNSUPPORTED
-    assert status("intent_moe_gate_up_w4", FAKE, 4, 256, 256, FAKE, FAKE, 2, 64, 2, FAKE, FAKE, FAKE, 2, 128, 128,
-                  FAKE, 128, None) == errors.INTENT_ERR_UNSUPPORTED  # block size 64
+    assert status("intent_moe_gate_up_w4", FAKE, 4, 256, 256, FAKE, FAKE, 2, 32, 2, FAKE, FAKE, FAKE, 2, 128, 128,
+                  FAKE, 128, None) == errors.INTENT_ERR_UNSUPPORTED  # block size 32
     assert status("intent_moe_down_w4", FAKE, 96, FAKE, FAKE, 2, 128, 8, FAKE, FAKE, FAKE, 2, 256, 96, 32,
                   FAKE, 256, None) == errors.INTENT_ERR_UNSUPPORTED  # F % 128
-    need = _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 128)
-    assert need >= 16 * 128 * 14336 * 2 + 1024 * 4096 * 4  # padded activations + route outputs
+    assert _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 128) >= \
+        16 * 128 * 14336 * 2 + 1024 * 4096 * 4  # block 128: padded activations + route outputs
+    need = _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 0)  # composite plan
+    assert need >= (1024 + 8 * 31) * 14336 * 2 + 1024 * 4096 * 4  # 32-row alignment
     assert status("intent_moe_expert_ffn_w4", FAKE, FAKE, 512, 4096, 8, 2, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
                   14336, 128, FAKE, FAKE, need - 1, None, None, None) == errors.INTENT_ERR_WORKSPACE
     assert _native.library().intent_moe_workspace_size(-1, 2, 8, 64, 64, 128) == 0

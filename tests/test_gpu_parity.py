@@ -76,7 +76,8 @@ def test_w4a16_gemv_shapes(gpu, threads, M, K, N, group):
 
 
 @pytest.mark.parametrize("M,K,N,group", [(16, 4096, 4096, 128), (17, 512, 200, 128), (130, 256, 64, 64),
-                                         (256, 1024, 384, 128), (1, 128, 128, 32)])
+                                         (256, 1024, 384, 128), (1, 128, 128, 32), (40, 512, 256, 32),
+                                         (300, 384, 130, 192)])
 def test_w4a16_gemm_shapes(gpu, threads, M, K, N, group):
     x, q, s, z = w4_case(2, M, K, N, group)
     y = art(intent.weight_only_int4_asym_matmul, KERNEL="gemm").run(dev(x), dev(q), dev(s), dev(z))
@@ -183,7 +184,8 @@ def run_ffn(d, y0, renorm=True):
     return host(y)
 
 
-@pytest.mark.parametrize("T,H,E,k,F", [(64, 256, 4, 2, 512), (37, 512, 8, 2, 256), (5, 128, 3, 1, 128)])
+@pytest.mark.parametrize("T,H,E,k,F", [(64, 256, 4, 2, 512), (37, 512, 8, 2, 256), (5, 128, 3, 1, 128),
+                                       (600, 256, 2, 1, 256)])
 def test_moe_ffn_small(gpu, threads, T, H, E, k, F):
     d = moe_small(3, T, H, E, k, F)
     y0 = np.random.default_rng(1).standard_normal((T, H), dtype=np.float32)
@@ -192,6 +194,16 @@ def test_moe_ffn_small(gpu, threads, T, H, E, k, F):
     ref = oracle.moe_ffn_w4(d["x"], ids, wts, d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"],
                             y=y0.copy(), threads=threads)
     assert_close_rms(got - y0, ref - y0, what="moe ffn delta")
+
+
+@pytest.mark.parametrize("group", [32, 64])
+def test_moe_ffn_group_sizes(gpu, threads, group):
+    T, H, E, k, F = 70, 256, 4, 2, 384
+    d = moe_small(5, T, H, E, k, F, group=group)
+    got = run_ffn(d, np.zeros((T, H), np.float32))
+    ids, wts = oracle.moe_route(d["logits"], k, True)
+    ref = oracle.moe_ffn_w4(d["x"], ids, wts, d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"], threads=threads)
+    assert_close_rms(got, ref, what=f"moe ffn group {group}")
 
 
 def test_moe_ffn_config4(gpu, threads):
@@ -224,14 +236,16 @@ def test_moe_ffn_config4(gpu, threads):
     assert_close_rms(got, y.cpu().numpy(), what="moe config4 vs f64")
 
 
-def test_moe_stage_entries(gpu, threads):
-    T, H, E, k, F = 48, 256, 4, 2, 256
+@pytest.mark.parametrize("B,T,F", [(128, 48, 256), (64, 48, 256), (64, 100, 384)])
+def test_moe_stage_entries(gpu, threads, B, T, F):
+    H, E, k = 256, 4, 2
     d = moe_small(9, T, H, E, k, F)
     ids, wts = art(intent.moe_route_topk, TOP_K=k).run(dev(d["logits"]))
-    sorted_ids, blocks, offsets, total = art(intent.moe_align_block_size, EXPERTS=E).run(ids)
-    act = art(intent.moe_gate_up_w4, TOP_K=k).run(dev(d["x"]), sorted_ids, blocks, dev(d["wgu"]), dev(d["sgu"]),
-                                                 dev(d["zgu"]))
-    ro = art(intent.moe_down_w4, ROUTES=T * k).run(act, sorted_ids, blocks, dev(d["wd"]), dev(d["sd"]), dev(d["zd"]))
+    sorted_ids, blocks, offsets, total = art(intent.moe_align_block_size, EXPERTS=E, BLOCK_SIZE=B).run(ids)
+    act = art(intent.moe_gate_up_w4, TOP_K=k, BLOCK_SIZE=B).run(dev(d["x"]), sorted_ids, blocks, dev(d["wgu"]),
+                                                               dev(d["sgu"]), dev(d["zgu"]))
+    ro = art(intent.moe_down_w4, ROUTES=T * k, BLOCK_SIZE=B).run(act, sorted_ids, blocks, dev(d["wd"]), dev(d["sd"]),
+                                                                 dev(d["zd"]))
     y = torch.zeros(T, H, dtype=torch.float32, device="cuda")
     art(intent.moe_combine).run(ro, wts, y)
     ref = oracle.moe_ffn_w4(d["x"], host(ids), host(wts), d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"],
