@@ -207,11 +207,9 @@ int intent_moe_combine(const float* route_out, int64_t out_ld,
  * Replaces moe_expert_ffn (examples/kernels/ragged/moe.py:12-53) together
  * with its host alignment (examples/programs/composition.py:134-174).
  * `workspace` must hold intent_moe_workspace_size(T, top_k, E, H, F, 0) bytes
- * (16-byte aligned). The composite picks its own alignment block (64 while
- * experts average fewer than 256 routes, else 128) and may split the down
- * projection's K into up to 4 partial sums, which the combine adds in split
- * order before weighting. intent_moe_workspace_size with block_size > 0 gives
- * the staged pipeline's buffers for that block size (no split).
+ * (16-byte aligned); the composite aligns routes to 128-row blocks.
+ * intent_moe_workspace_size with block_size > 0 gives the staged pipeline's
+ * buffers for that block size (block_size <= 0 means the composite's 128).
  * If topk_ids_out / topk_weights_out are non-null the routing results are
  * also copied there ([T,top_k] each).
  */

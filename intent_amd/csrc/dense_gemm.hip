@@ -18,10 +18,9 @@ struct ClampRows {
 };
 
 template <class T, class WSrc, bool kColScale>
-__global__ __launch_bounds__(T::NT, 2) void dense_gemm_kernel(DenseRows rows, WSrc w, int N, int K,
-                                                                            f16* __restrict__ y, int64_t ldy,
-                                                                            const f16* __restrict__ colscale,
-                                                                            int mblocks) {
+__global__ __launch_bounds__(T::NT, 2) void dense_gemm_kernel(DenseRows rows, WSrc w, int N, int K, f16* __restrict__ y,
+                                                           int64_t ldy, const f16* __restrict__ colscale,
+                                                           int mblocks) {
   __shared__ typename T::Shared tile;
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   const int m0 = (bid % mblocks) * T::BM;
@@ -58,24 +57,12 @@ int launch_tile(const f16* x, int64_t ldx, int M, int N, int K, const WSrc& w, f
   return intent::launch_status(name);
 }
 
-#ifndef INTENT_DENSE_TILE
-#define INTENT_DENSE_TILE 1
-#endif
-
 // Tile choice: 256 x 128 (128 x 64 per wave) once M fills it, else 128 x 128.
 template <class WSrc, bool kColScale>
 int launch_dense(const f16* x, int64_t ldx, int M, int N, int K, const WSrc& w, f16* y, int64_t ldy,
                  const f16* colscale, hipStream_t st, const char* name) {
-#if INTENT_DENSE_TILE == 0
-  return launch_tile<Tile<128, 128, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
-#elif INTENT_DENSE_TILE == 1
   if (M > 128) return launch_tile<Tile<256, 128, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
   return launch_tile<Tile<128, 128, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
-#elif INTENT_DENSE_TILE == 2
-  return launch_tile<Tile<128, 256, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
-#elif INTENT_DENSE_TILE == 3
-  return launch_tile<Tile<256, 256, 2, 4>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
-#endif
 }
 
 }  // namespace

@@ -12,7 +12,8 @@
 // BK = 64 k per LDS stage. LDS traffic per MFMA falls with the wave block:
 // a 64 x 64 wave block reads 1 KB of fragments per MFMA, 128 x 64 reads 0.75 KB.
 // Pipeline: global loads of k-tile t+1 are issued into registers before the
-// MFMAs of tile t, then decoded and written to LDS after the barrier.
+// MFMAs of tile t, then decoded and written to LDS after the barrier; the
+// fragments of 16-k step kk+1 are read before the MFMAs of step kk.
 #pragma once
 
 #include "common.h"
@@ -46,39 +47,6 @@ struct Tile {
   INTENT_DEVICE static int acc_row(int i, int v) {
     const int lane = threadIdx.x & 63;
     return wave_m() * (BM / WM) + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-  }
-  INTENT_DEVICE static int acc_col(int j) {
-    const int lane = threadIdx.x & 63;
-    return wave_n() * (BN / WN) + j * 32 + (lane & 31);
-  }
-};
-
-// Segment tile: up to 256 rows of one MoE expert x BN columns, 2 x 2 waves.
-// Wave row wm owns the 32-row MFMA tiles 2i + wm (i < 4), so a partly filled
-// segment keeps both wave rows equally busy; 32-row tiles past the active
-// count are neither staged nor multiplied.
-template <int BN_>
-struct SegTile {
-  static constexpr int BM = 256;
-  static constexpr int BN = BN_;
-  static constexpr int WM = 2;
-  static constexpr int WN = 2;
-  static constexpr int NT = 256;
-  static constexpr int TI = 4;
-  static constexpr int TJ = BN / 64;
-  static_assert(TJ >= 1 && TJ * 64 == BN, "segment tile width");
-
-  struct Shared {
-    f16 a[BM][LDS_LD];
-    f16 b[BN][LDS_LD];
-  };
-
-  INTENT_DEVICE static int wave_m() { return (threadIdx.x >> 6) % WM; }
-  INTENT_DEVICE static int wave_n() { return (threadIdx.x >> 6) / WM; }
-  INTENT_DEVICE static int tile_index(int i) { return 2 * i + wave_m(); }
-  INTENT_DEVICE static int acc_row(int i, int v) {
-    const int lane = threadIdx.x & 63;
-    return tile_index(i) * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
   }
   INTENT_DEVICE static int acc_col(int j) {
     const int lane = threadIdx.x & 63;
@@ -315,101 +283,30 @@ INTENT_DEVICE void mainloop(const Rows& rows, int m0, const WSrc& wsrc, const Ro
       for (int i = 0; i < NA; ++i) areg[i] = bload16(ars, aoff[i], (uint32_t)(kt + 1) * BK * 2);
       wsrc.template load<T>(wrs, slots, kt + 1, wreg);
     }
-#ifndef INTENT_SETPRIO
-#define INTENT_SETPRIO 0
-#endif
-    if (INTENT_SETPRIO) __builtin_amdgcn_s_setprio(1);
+    // Fragments of 16-k step kk+1 are read before the MFMAs of step kk.
+    f16x8 af[2][T::TI], bf[2][T::TJ];
+    const int arow0 = wm * (T::BM / T::WM) + (lane & 31);
+    const int brow0 = wn * (T::BN / T::WN) + (lane & 31);
+    const int khalf = (lane >> 5) * 8;
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i) af[0][i] = *reinterpret_cast<const f16x8*>(&t.a[arow0 + i * 32][khalf]);
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j) bf[0][j] = *reinterpret_cast<const f16x8*>(&t.b[brow0 + j * 32][khalf]);
 #pragma unroll
     for (int kk = 0; kk < BK / 16; ++kk) {
-      f16x8 af[T::TI], bf[T::TJ];
-      const int kof = kk * 16 + (lane >> 5) * 8;
+      const int cb = kk & 1;
+      if (kk + 1 < BK / 16) {
+        const int kof = (kk + 1) * 16 + khalf;
 #pragma unroll
-      for (int i = 0; i < T::TI; ++i)
-        af[i] = *reinterpret_cast<const f16x8*>(&t.a[wm * (T::BM / T::WM) + i * 32 + (lane & 31)][kof]);
+        for (int i = 0; i < T::TI; ++i) af[cb ^ 1][i] = *reinterpret_cast<const f16x8*>(&t.a[arow0 + i * 32][kof]);
 #pragma unroll
-      for (int j = 0; j < T::TJ; ++j)
-        bf[j] = *reinterpret_cast<const f16x8*>(&t.b[wn * (T::BN / T::WN) + j * 32 + (lane & 31)][kof]);
-#pragma unroll
-      for (int i = 0; i < T::TI; ++i)
-#pragma unroll
-        for (int j = 0; j < T::TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    if (INTENT_SETPRIO) __builtin_amdgcn_s_setprio(0);
-    __syncthreads();
-  }
-}
-
-// Segment main loop: `nact` (1..8) active 32-row tiles starting at tile row
-// m0. A chunk i of a thread is row (tid/8) + 32*i, i.e. it lies in 32-row
-// tile i, so "chunk active" is uniform across the workgroup.
-template <class T, class Rows, class WSrc, class RowMap>
-INTENT_DEVICE void seg_mainloop(const Rows& rows, int m0, int nact, const WSrc& wsrc, const RowMap& rowmap, int K,
-                                typename T::Shared& t, f32x16 (&acc)[T::TI][T::TJ]) {
-  constexpr int NA = T::BM * 8 / T::NT;
-  constexpr int NW = WSrc::template slots<T>();
-  static_assert(NA == 8, "one A chunk per 32-row tile");
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wn = T::wave_n();
-
-  const Rsrc ars = make_rsrc(rows.base(m0));
-  uint32_t aoff[NA];
-  const int acol = (tid & 7) * 8;
-  const int arow_in_tile = tid >> 3;
-#pragma unroll
-  for (int i = 0; i < NA; ++i)
-    aoff[i] = (uint32_t)(rows.off(m0, m0 + arow_in_tile + 32 * (i < nact ? i : 0)) + acol) * 2;
-  typename WSrc::Slot slots[NW];
-  wsrc.template slot<T>(tid, rowmap, slots);
-  const typename WSrc::Rsrcs wrs = wsrc.rsrcs();
-
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i)
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  bool live[T::TI];
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i) live[i] = T::tile_index(i) < nact;
-
-  const int nk = K / BK;
-  u32x4 areg[NA];
-  typename WSrc::Regs wreg[NW];
-#pragma unroll
-  for (int i = 0; i < NA; ++i)
-    if (i < nact) areg[i] = bload16(ars, aoff[i], 0);
-  wsrc.template load<T>(wrs, slots, 0, wreg);
-
-  for (int kt = 0; kt < nk; ++kt) {
-#pragma unroll
-    for (int i = 0; i < NA; ++i)
-      if (i < nact) *reinterpret_cast<u32x4*>(&t.a[arow_in_tile + 32 * i][acol]) = areg[i];
-    wsrc.template store<T>(slots, wreg, t);
-    __syncthreads();
-    if (kt + 1 < nk) {
-#pragma unroll
-      for (int i = 0; i < NA; ++i)
-        if (i < nact) areg[i] = bload16(ars, aoff[i], (uint32_t)(kt + 1) * BK * 2);
-      wsrc.template load<T>(wrs, slots, kt + 1, wreg);
-    }
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      f16x8 af[T::TI], bf[T::TJ];
-      const int kof = kk * 16 + (lane >> 5) * 8;
-#pragma unroll
-      for (int j = 0; j < T::TJ; ++j)
-        bf[j] = *reinterpret_cast<const f16x8*>(&t.b[wn * (T::BN / T::WN) + j * 32 + (lane & 31)][kof]);
-#pragma unroll
-      for (int i = 0; i < T::TI; ++i) {
-        if (!live[i]) continue;
-        af[i] = *reinterpret_cast<const f16x8*>(&t.a[T::tile_index(i) * 32 + (lane & 31)][kof]);
-#pragma unroll
-        for (int j = 0; j < T::TJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < T::TJ; ++j) bf[cb ^ 1][j] = *reinterpret_cast<const f16x8*>(&t.b[brow0 + j * 32][kof]);
       }
+#pragma unroll
+      for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+        for (int j = 0; j < T::TJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cb][i], bf[cb][j], acc[i][j], 0, 0, 0);
     }
     __syncthreads();
   }

@@ -2,8 +2,6 @@
 // gate/up (+SiLU) and down projections, fixed-order weighted combine.
 #include <math.h>
 
-#include <algorithm>
-
 #include "common.h"
 #include "gemm_f16.h"
 #include "internal.h"
@@ -19,11 +17,7 @@ template <int B>
 struct MoeTiles;
 template <>
 struct MoeTiles<128> {
-#ifdef INTENT_GU128
-  using GateUp = Tile<128, 128, 2, 2>;
-#else
   using GateUp = Tile<128, 256, 2, 2>;  // waves of 64 x 128
-#endif
   using Down = Tile<128, 128, 2, 2>;    // waves of 64 x 64
 };
 template <>
@@ -82,9 +76,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t*
                                                                   int32_t* __restrict__ sorted, int capacity,
                                                                   int32_t* __restrict__ blocks, int nblocks,
                                                                   int32_t* __restrict__ offsets,
-                                                                  int32_t* __restrict__ total,
-                                                                  int32_t* __restrict__ segs, int max_segs,
-                                                                  int seg_rows) {
+                                                                  int32_t* __restrict__ total) {
   __shared__ int cnt[kMaxAlignExperts];
   __shared__ int off[kMaxAlignExperts + 1];
   __shared__ int base[kMaxAlignExperts];
@@ -111,24 +103,6 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t*
       off[e + 1] = acc;
     }
     total[0] = acc;
-    // Optional expert segments {expert, first padded row, rows, 0}: each
-    // expert's padded rows cut into pieces of at most seg_rows.
-    if (segs) {
-      int n = 0;
-      for (int e = 0; e < E; ++e)
-        for (int p = off[e]; p < off[e + 1] && n < max_segs; p += seg_rows, ++n) {
-          segs[4 * n] = e;
-          segs[4 * n + 1] = p;
-          segs[4 * n + 2] = min(seg_rows, off[e + 1] - p);
-          segs[4 * n + 3] = 0;
-        }
-      for (; n < max_segs; ++n) {
-        segs[4 * n] = -1;
-        segs[4 * n + 1] = 0;
-        segs[4 * n + 2] = 0;
-        segs[4 * n + 3] = 0;
-      }
-    }
   }
   __syncthreads();
   for (int e = tid; e <= E; e += kAlignThreads) offsets[e] = off[e];
@@ -253,31 +227,25 @@ __global__ __launch_bounds__(MoeTiles<B>::GateUp::NT, 2) void moe_gate_up_kernel
   }
 }
 
-// Split-K down projection: grid = mblocks x ntiles x splits; split s covers
-// k in [s*kc, (s+1)*kc) and writes its partial sums to out + s*split_stride.
+// Down projection: grid = mblocks x ntiles; fp32 rows scattered to routes.
 template <int B>
 __global__ __launch_bounds__(MoeTiles<B>::Down::NT, 2) void moe_down_kernel(
     const f16* __restrict__ act, int64_t ld_act, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ blocks, int mblocks, int ntiles, int R, const uint8_t* __restrict__ wq,
-    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int H, int F, int gs, int kc,
-    float* __restrict__ out, int64_t ldo, int64_t split_stride) {
+    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int H, int F, int gs, float* __restrict__ out,
+    int64_t ldo) {
   using T = typename MoeTiles<B>::Down;
   __shared__ typename T::Shared tile;
   const int mb = blockIdx.x % mblocks;
-  const int nt = (blockIdx.x / mblocks) % ntiles;
-  const int split = blockIdx.x / (mblocks * ntiles);
-  const int n0 = nt * T::BN;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
   const int e = blocks[mb];
   if (e < 0) return;
-  const int k0 = split * kc;
   const int64_t ldq = F / 2;
   const int64_t ldp = F / gs;
-  W4Source w{wq + (int64_t)e * H * ldq + k0 / 2, ldq, ws + (int64_t)e * H * ldp + k0 / gs,
-             wz + (int64_t)e * H * ldp + k0 / gs, ldp, gs};
+  W4Source w{wq + (int64_t)e * H * ldq, ldq, ws + (int64_t)e * H * ldp, wz + (int64_t)e * H * ldp, ldp, gs};
   const int m0 = mb * B;
   f32x16 acc[T::TI][T::TJ];
-  mainloop<T>(PaddedRows{act + k0, ld_act}, m0, w, ClampRows{n0, H}, kc, tile, acc);
-  float* dst = out + split * split_stride;
+  mainloop<T>(PaddedRows{act, ld_act}, m0, w, ClampRows{n0, H}, F, tile, acc);
 #pragma unroll
   for (int j = 0; j < T::TJ; ++j) {
     const int col = n0 + T::acc_col(j);
@@ -287,110 +255,15 @@ __global__ __launch_bounds__(MoeTiles<B>::Down::NT, 2) void moe_down_kernel(
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = sorted[m0 + T::acc_row(i, v)];
-        if (r >= 0 && r < R) dst[(int64_t)r * ldo + col] = acc[i][j][v];
+        if (r >= 0 && r < R) out[(int64_t)r * ldo + col] = acc[i][j][v];
       }
-  }
-}
-
-// ---- expert-segment projections (composite path) ------------------------------
-// A workgroup owns one expert segment (up to 256 padded rows of one expert,
-// 32-row aligned) and one output tile, so every weight tile is fetched and
-// decoded once per segment instead of once per alignment block.
-
-constexpr int kSegRows = 256;
-using SegGateUpT = SegTile<128>;  // 64 features (gate + up rows) per tile
-using SegDownT = SegTile<128>;
-
-__global__ __launch_bounds__(SegGateUpT::NT, 2) void moe_gate_up_seg_kernel(
-    const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
-    const int32_t* __restrict__ segs, int ntiles, int R, int top_k, const uint8_t* __restrict__ wq,
-    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int F, int gs, f16* __restrict__ act,
-    int64_t ld_act) {
-  using T = SegGateUpT;
-  __shared__ T::Shared tile;
-  const int id = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int sg = id / ntiles;
-  const int e = segs[4 * sg];
-  if (e < 0) return;
-  const int m0 = segs[4 * sg + 1];
-  const int nact = segs[4 * sg + 2] >> 5;
-  const int f0 = (id % ntiles) * (T::BN / 2);
-  const int64_t ldq = H / 2;
-  const int64_t ldp = H / gs;
-  W4Source w{wq + (int64_t)e * 2 * F * ldq, ldq, ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs};
-  f32x16 acc[T::TI][T::TJ];
-  seg_mainloop<T>(GatherRows{x, ldx, sorted, R, top_k}, m0, nact, w, GateUpRowMap<T>{f0, F}, H, tile, acc);
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int p = 0; p < T::TJ / 2; ++p) {
-    const int f = f0 + GateUpRowMap<T>::feature_offset(T::wave_n(), p) + (lane & 31);
-    if (f >= F) continue;
-#pragma unroll
-    for (int i = 0; i < T::TI; ++i) {
-      if (T::tile_index(i) >= nact) continue;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + T::acc_row(i, v);
-        const int r = sorted[row];
-        f16 out = (f16)0.f;
-        if (r >= 0 && r < R) {
-          const float g = acc[i][2 * p][v];
-          const float u = acc[i][2 * p + 1][v];
-          const float silu = g / (1.0f + expf(-g));
-          out = (f16)(silu * u);
-        }
-        act[(int64_t)row * ld_act + f] = out;
-      }
-    }
-  }
-}
-
-// grid = max_segs x ntiles x splits; split s covers k in [s*kc, (s+1)*kc).
-__global__ __launch_bounds__(SegDownT::NT, 2) void moe_down_seg_kernel(
-    const f16* __restrict__ act, int64_t ld_act, const int32_t* __restrict__ sorted,
-    const int32_t* __restrict__ segs, int max_segs, int ntiles, int R, const uint8_t* __restrict__ wq,
-    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int H, int F, int gs, int kc,
-    float* __restrict__ out, int64_t ldo, int64_t split_stride) {
-  using T = SegDownT;
-  __shared__ T::Shared tile;
-  const int id = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int nt = id % ntiles;
-  const int sg = (id / ntiles) % max_segs;
-  const int split = id / (ntiles * max_segs);
-  const int e = segs[4 * sg];
-  if (e < 0) return;
-  const int m0 = segs[4 * sg + 1];
-  const int nact = segs[4 * sg + 2] >> 5;
-  const int n0 = nt * T::BN;
-  const int k0 = split * kc;
-  const int64_t ldq = F / 2;
-  const int64_t ldp = F / gs;
-  W4Source w{wq + (int64_t)e * H * ldq + k0 / 2, ldq, ws + (int64_t)e * H * ldp + k0 / gs,
-             wz + (int64_t)e * H * ldp + k0 / gs, ldp, gs};
-  f32x16 acc[T::TI][T::TJ];
-  seg_mainloop<T>(PaddedRows{act + k0, ld_act}, m0, nact, w, ClampRows{n0, H}, kc, tile, acc);
-  float* dst = out + split * split_stride;
-#pragma unroll
-  for (int j = 0; j < T::TJ; ++j) {
-    const int col = n0 + T::acc_col(j);
-    if (col >= H) continue;
-#pragma unroll
-    for (int i = 0; i < T::TI; ++i) {
-      if (T::tile_index(i) >= nact) continue;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = sorted[m0 + T::acc_row(i, v)];
-        if (r >= 0 && r < R) dst[(int64_t)r * ldo + col] = acc[i][j][v];
-      }
-    }
   }
 }
 
 // y[t, d] += w[t, s] * out[t*k + s, d], slot by slot (mul then add, no fma).
-// With splits > 1, out[r, d] is the sum of the split partials in split order.
 __global__ void moe_combine_kernel(const float* __restrict__ route_out, int64_t ldo,
                                    const float* __restrict__ weights, int T, int top_k, float* __restrict__ y, int H,
-                                   int64_t ldy, int splits, int64_t split_stride) {
+                                   int64_t ldy) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)T * H;
   if (i >= total) return;
@@ -398,10 +271,7 @@ __global__ void moe_combine_kernel(const float* __restrict__ route_out, int64_t 
   const int d = (int)(i % H);
   float acc = y[(int64_t)t * ldy + d];
   for (int s = 0; s < top_k; ++s) {
-    const float* ro = route_out + ((int64_t)t * top_k + s) * ldo + d;
-    float v = ro[0];
-    for (int p = 1; p < splits; ++p) v = __fadd_rn(v, ro[p * split_stride]);
-    const float prod = __fmul_rn(weights[(int64_t)t * top_k + s], v);
+    const float prod = __fmul_rn(weights[(int64_t)t * top_k + s], route_out[((int64_t)t * top_k + s) * ldo + d]);
     acc = __fadd_rn(acc, prod);
   }
   y[(int64_t)t * ldy + d] = acc;
@@ -449,7 +319,7 @@ extern "C" int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_
                  INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, (hipStream_t)stream, topk_ids, (int)R, (int)E,
                      (int)block_size, sorted_route_ids, (int)capacity, expert_blocks, (int)num_blocks,
-                     expert_offsets, total_padded, nullptr, 0, 0);
+                     expert_offsets, total_padded);
   return intent::launch_status("moe_align");
 }
 
@@ -472,24 +342,24 @@ int gate_up_launch(const void* x, int64_t T, int64_t H, int64_t x_ld, const int3
 template <int B>
 int down_launch(const void* act, int64_t act_ld, const int32_t* sorted, const int32_t* blocks, int64_t num_blocks,
                 int64_t R, const uint8_t* wq, const void* ws, const uint8_t* wz, int64_t H, int64_t F, int64_t gs,
-                int splits, float* out, int64_t out_ld, int64_t split_stride, void* stream) {
+                float* out, int64_t out_ld, void* stream) {
   using Tl = typename MoeTiles<B>::Down;
   const int64_t ntiles = (H + Tl::BN - 1) / Tl::BN;
-  const int64_t grid = num_blocks * ntiles * splits;
+  const int64_t grid = num_blocks * ntiles;
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
   hipLaunchKernelGGL((moe_down_kernel<B>), dim3((unsigned)grid), dim3(Tl::NT), 0, (hipStream_t)stream,
                      (const f16*)act, act_ld, sorted, blocks, (int)num_blocks, (int)ntiles, (int)R, wq,
-                     (const f16*)ws, wz, (int)H, (int)F, (int)gs, (int)(F / splits), out, out_ld, split_stride);
+                     (const f16*)ws, wz, (int)H, (int)F, (int)gs, out, out_ld);
   return intent::launch_status("moe_down_w4");
 }
 
 int combine_launch(const float* route_out, int64_t out_ld, const float* topk_weights, int64_t T, int64_t top_k,
-                   float* y, int64_t H, int64_t y_ld, int splits, int64_t split_stride, void* stream) {
+                   float* y, int64_t H, int64_t y_ld, void* stream) {
   const int threads = 256;
   const int64_t blocks = (T * H + threads - 1) / threads;
   INTENT_REQUIRE(blocks < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, route_out,
-                     out_ld, topk_weights, (int)T, (int)top_k, y, (int)H, y_ld, splits, split_stride);
+                     out_ld, topk_weights, (int)T, (int)top_k, y, (int)H, y_ld);
   return intent::launch_status("moe_combine");
 }
 
@@ -553,12 +423,10 @@ int down_check(const void* act, int64_t act_ld, const int32_t* sorted_route_ids,
 
 int down_dispatch(const void* act, int64_t act_ld, const int32_t* sorted, const int32_t* blocks, int64_t num_blocks,
                   int64_t block_size, int64_t R, const uint8_t* wq, const void* ws, const uint8_t* wz, int64_t H,
-                  int64_t F, int64_t gs, int splits, float* out, int64_t out_ld, int64_t split_stride, void* stream) {
+                  int64_t F, int64_t gs, float* out, int64_t out_ld, void* stream) {
   if (block_size == 64)
-    return down_launch<64>(act, act_ld, sorted, blocks, num_blocks, R, wq, ws, wz, H, F, gs, splits, out, out_ld,
-                           split_stride, stream);
-  return down_launch<128>(act, act_ld, sorted, blocks, num_blocks, R, wq, ws, wz, H, F, gs, splits, out, out_ld,
-                          split_stride, stream);
+    return down_launch<64>(act, act_ld, sorted, blocks, num_blocks, R, wq, ws, wz, H, F, gs, out, out_ld, stream);
+  return down_launch<128>(act, act_ld, sorted, blocks, num_blocks, R, wq, ws, wz, H, F, gs, out, out_ld, stream);
 }
 
 }  // namespace
@@ -572,7 +440,7 @@ extern "C" int intent_moe_down_w4(const void* act, int64_t act_ld, const int32_t
                       w_zeros, E, H, F, group_size, out, out_ld);
   if (st != INTENT_OK || num_blocks == 0 || R == 0) return st;
   return down_dispatch(act, act_ld, sorted_route_ids, expert_blocks, num_blocks, block_size, R, w_packed, w_scales,
-                       w_zeros, H, F, group_size, 1, out, out_ld, 0, stream);
+                       w_zeros, H, F, group_size, out, out_ld, stream);
 }
 
 extern "C" int intent_moe_combine(const float* route_out, int64_t out_ld, const float* topk_weights, int64_t T,
@@ -582,29 +450,23 @@ extern "C" int intent_moe_combine(const float* route_out, int64_t out_ld, const 
   if (T == 0 || H == 0) return INTENT_OK;
   INTENT_REQUIRE(route_out && topk_weights && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(out_ld >= H && y_ld >= H, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
-  return combine_launch(route_out, out_ld, topk_weights, T, top_k, y, H, y_ld, 1, 0, stream);
+  return combine_launch(route_out, out_ld, topk_weights, T, top_k, y, H, y_ld, stream);
 }
 
 namespace {
 
 struct MoEWorkspace {
-  size_t ids, weights, sorted, blocks, offsets, total, segs, act, out, bytes;
-  int64_t block, splits, capacity, nblocks, max_segs;
+  size_t ids, weights, sorted, blocks, offsets, total, act, out, bytes;
+  int64_t capacity, nblocks;
 };
 
 size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Buffers of one MoE call. With segments (composite), alignment is 32-row and
-// the segment list bounds sum_e ceil(padded_e / 256) <= (R + 31E)/256 + E.
-MoEWorkspace moe_layout(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t F, int64_t B, int64_t S,
-                        bool segments) {
+MoEWorkspace moe_layout(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t F, int64_t B) {
   MoEWorkspace w{};
   const int64_t R = T * top_k;
-  w.block = B;
-  w.splits = S;
   w.capacity = align_capacity(R, E, B);
   w.nblocks = (w.capacity + B - 1) / B;
-  w.max_segs = segments ? w.capacity / kSegRows + E + 1 : 0;
   size_t o = 0;
   w.ids = o;     o = round256(o + sizeof(int32_t) * R);
   w.weights = o; o = round256(o + sizeof(float) * R);
@@ -612,45 +474,24 @@ MoEWorkspace moe_layout(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t 
   w.blocks = o;  o = round256(o + sizeof(int32_t) * w.nblocks);
   w.offsets = o; o = round256(o + sizeof(int32_t) * (E + 1));
   w.total = o;   o = round256(o + sizeof(int32_t));
-  w.segs = o;    o = round256(o + sizeof(int32_t) * 4 * w.max_segs);
   w.act = o;     o = round256(o + sizeof(uint16_t) * (size_t)(w.nblocks * B) * F);
-  w.out = o;     o = round256(o + sizeof(float) * (size_t)S * R * H);
+  w.out = o;     o = round256(o + sizeof(float) * (size_t)R * H);
   w.bytes = o;
   return w;
 }
 
-#ifndef INTENT_MOE_SEG
-#define INTENT_MOE_SEG 0
-#endif
-#ifndef INTENT_MOE_MAXS
-#define INTENT_MOE_MAXS 1
-#endif
-
-// Composite plan. Block mode: 128-row alignment blocks, one M tile each.
-// Segment mode: 32-row alignment cut into expert segments of up to 256 rows.
-// The down projection may split K (each split a whole number of 64-k tiles)
-// until about 1024 workgroups are busy. The workspace is sized for this split
-// count; a group size that does not divide the split length lowers it at
-// launch (fewer partial buffers are used).
-MoEWorkspace moe_plan(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t F) {
-  const int64_t R = T * top_k;
-  const bool seg = INTENT_MOE_SEG;
-  const int64_t B = seg ? 32 : 128;
-  const int64_t units = seg ? std::min<int64_t>(R / kSegRows + E, align_capacity(R, E, 32) / kSegRows + E + 1)
-                            : std::min<int64_t>(R / B + E, align_capacity(R, E, B) / B + 1);
-  const int64_t busy = units * ((H + 127) / 128);
-  int64_t S = 1;
-  while (S < INTENT_MOE_MAXS && busy * S < 1024 && F % (2 * S * 64) == 0) S *= 2;
-  return moe_layout(T, top_k, E, H, F, B, S, seg);
-}
+// The composite aligns to 128-row blocks: measured on config 4, 64-row
+// blocks and 256-row expert segments were both slower (the W4 decode per
+// MFMA grows as the tile's row count falls), and a split-K down projection
+// did not help either.
+constexpr int64_t kCompositeBlock = 128;
 
 }  // namespace
 
 extern "C" size_t intent_moe_workspace_size(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t F,
                                             int64_t block_size) {
   if (T < 0 || top_k < 1 || E < 1 || H < 0 || F < 0) return 0;
-  if (block_size <= 0) return moe_plan(T, top_k, E, H, F).bytes;
-  return moe_layout(T, top_k, E, H, F, block_size, 1, false).bytes;
+  return moe_layout(T, top_k, E, H, F, block_size > 0 ? block_size : kCompositeBlock).bytes;
 }
 
 extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* x, int64_t T, int64_t H, int64_t E,
@@ -660,28 +501,14 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
                                         int64_t group_size, float* y, void* workspace, size_t workspace_bytes,
                                         int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
   intent::clear_error();
+  const int64_t B = kCompositeBlock;
   INTENT_REQUIRE(T >= 0 && top_k >= 1 && E >= 1 && H > 0 && F > 0, INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   if (T == 0) return INTENT_OK;
-  INTENT_REQUIRE(H % 128 == 0 && H <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "H must be a positive multiple of 128");
-  INTENT_REQUIRE(F % 128 == 0 && F <= INT32_MAX / 2, INTENT_ERR_UNSUPPORTED, "F must be a positive multiple of 128");
-  INTENT_REQUIRE(group_size > 0 && (group_size == 32 || group_size % 64 == 0) && H % group_size == 0 &&
-                     F % group_size == 0,
-                 INTENT_ERR_UNSUPPORTED, "group_size must be 32 or a multiple of 64 dividing H and F");
-  INTENT_REQUIRE(intent::fits_offset(2 * F, H / 2) && intent::fits_offset(2 * F, H / group_size * 2) &&
-                     intent::fits_offset(H, F / 2) && intent::fits_offset(T, H * 2) &&
-                     intent::fits_offset(256 + 1, F * 2),
-                 INTENT_ERR_UNSUPPORTED, "moe_expert_ffn_w4: operand too large for 31-bit buffer offsets");
-  INTENT_REQUIRE(E <= kMaxRouteExperts, INTENT_ERR_UNSUPPORTED, "experts must be in [1, %d]", kMaxRouteExperts);
-  const MoEWorkspace L = moe_plan(T, top_k, E, H, F);
+  const MoEWorkspace L = moe_layout(T, top_k, E, H, F, B);
   INTENT_REQUIRE(workspace && workspace_bytes >= L.bytes, INTENT_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
                  L.bytes, workspace_bytes);
   INTENT_REQUIRE(intent::aligned16(workspace), INTENT_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
-  INTENT_REQUIRE(x && y && router_logits && wgu_packed && wgu_scales && wgu_zeros && wd_packed && wd_scales && wd_zeros,
-                 INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
-  INTENT_REQUIRE(intent::aligned16(x) && intent::aligned16(wgu_packed) && intent::aligned16(wd_packed),
-                 INTENT_ERR_ALIGNMENT, "x and weights must be 16-byte aligned");
-  int64_t splits = L.splits;
-  while (splits > 1 && (F / splits) % group_size != 0) splits /= 2;
+  INTENT_REQUIRE(y, INTENT_ERR_INVALID_ARGUMENT, "null output");
   char* ws = (char*)workspace;
   int32_t* ids = topk_ids_out ? topk_ids_out : (int32_t*)(ws + L.ids);
   float* wts = topk_weights_out ? topk_weights_out : (float*)(ws + L.weights);
@@ -689,43 +516,17 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
   int32_t* blocks = (int32_t*)(ws + L.blocks);
   int32_t* offsets = (int32_t*)(ws + L.offsets);
   int32_t* total = (int32_t*)(ws + L.total);
-  int32_t* segs = (int32_t*)(ws + L.segs);
-  f16* act = (f16*)(ws + L.act);
+  void* act = ws + L.act;
   float* out = (float*)(ws + L.out);
-  const int64_t R = T * top_k;
-  hipStream_t st = (hipStream_t)stream;
-  int rc = intent_moe_route(router_logits, T, E, top_k, renormalize, ids, wts, stream);
-  if (rc != INTENT_OK) return rc;
-  INTENT_REQUIRE(R <= (1ll << 30), INTENT_ERR_INVALID_ARGUMENT, "too many routes");
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, st, ids, (int)R, (int)E, (int)L.block, sorted,
-                     (int)L.capacity, blocks, (int)L.nblocks, offsets, total, L.max_segs ? segs : nullptr,
-                     (int)L.max_segs, kSegRows);
-  rc = intent::launch_status("moe_align");
-  if (rc != INTENT_OK) return rc;
-  if (L.max_segs == 0) {
-    rc = intent_moe_gate_up_w4(x, T, H, H, sorted, blocks, L.nblocks, L.block, top_k, wgu_packed, wgu_scales, wgu_zeros,
-                               E, F, group_size, act, F, stream);
-    if (rc != INTENT_OK) return rc;
-    rc = down_dispatch(act, F, sorted, blocks, L.nblocks, L.block, R, wd_packed, wd_scales, wd_zeros, H, F, group_size,
-                       (int)splits, out, H, R * H, stream);
-    if (rc != INTENT_OK) return rc;
-    return combine_launch(out, H, wts, T, top_k, y, H, H, (int)splits, R * H, stream);
-  }
-  const int64_t gu_tiles = (F + SegGateUpT::BN / 2 - 1) / (SegGateUpT::BN / 2);
-  const int64_t gu_grid = L.max_segs * gu_tiles;
-  INTENT_REQUIRE(gu_grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL(moe_gate_up_seg_kernel, dim3((unsigned)gu_grid), dim3(SegGateUpT::NT), 0, st, (const f16*)x, H,
-                     (int)H, sorted, segs, (int)gu_tiles, (int)R, (int)top_k, wgu_packed, (const f16*)wgu_scales,
-                     wgu_zeros, (int)F, (int)group_size, act, F);
-  rc = intent::launch_status("moe_gate_up_w4");
-  if (rc != INTENT_OK) return rc;
-  const int64_t dn_tiles = (H + SegDownT::BN - 1) / SegDownT::BN;
-  const int64_t dn_grid = L.max_segs * dn_tiles * splits;
-  INTENT_REQUIRE(dn_grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL(moe_down_seg_kernel, dim3((unsigned)dn_grid), dim3(SegDownT::NT), 0, st, act, F, sorted, segs,
-                     (int)L.max_segs, (int)dn_tiles, (int)R, wd_packed, (const f16*)wd_scales, wd_zeros, (int)H,
-                     (int)F, (int)group_size, (int)(F / splits), out, H, R * H);
-  rc = intent::launch_status("moe_down_w4");
-  if (rc != INTENT_OK) return rc;
-  return combine_launch(out, H, wts, T, top_k, y, H, H, (int)splits, R * H, stream);
+  int st = intent_moe_route(router_logits, T, E, top_k, renormalize, ids, wts, stream);
+  if (st != INTENT_OK) return st;
+  st = intent_moe_align(ids, T, top_k, E, B, sorted, L.capacity, blocks, L.nblocks, offsets, total, stream);
+  if (st != INTENT_OK) return st;
+  st = intent_moe_gate_up_w4(x, T, H, H, sorted, blocks, L.nblocks, B, top_k, wgu_packed, wgu_scales, wgu_zeros, E, F,
+                             group_size, act, F, stream);
+  if (st != INTENT_OK) return st;
+  st = intent_moe_down_w4(act, F, sorted, blocks, L.nblocks, B, T * top_k, wd_packed, wd_scales, wd_zeros, E, H, F,
+                          group_size, out, H, stream);
+  if (st != INTENT_OK) return st;
+  return intent_moe_combine(out, H, wts, T, top_k, y, H, H, stream);
 }
