@@ -1,68 +1,125 @@
 // Dense weight-only contractions on the shared f16 MFMA tile GEMM:
 //   W4A16 (asymmetric group-quant nibbles) and W8A16 (per-channel int8).
 #include "common.h"
-#include "gemm_f16.h"
 #include "internal.h"
+#include "mfma_pipe.h"
 
 namespace {
 
-using namespace gemm;
-
+// Weight row of B-tile row c; tail rows read the last valid row and their
+// outputs are dropped.
 struct ClampRows {
   int n0;
   int N;
   INTENT_DEVICE int operator()(int c) const {
     const int n = n0 + c;
-    return n < N ? n : N - 1;  // tail rows read a valid row; their outputs are dropped
+    return n < N ? n : N - 1;
   }
 };
 
-template <class T, class WSrc, bool kColScale>
-__global__ __launch_bounds__(T::NT, 2) void dense_gemm_kernel(DenseRows rows, WSrc w, int N, int K, f16* __restrict__ y,
-                                                           int64_t ldy, const f16* __restrict__ colscale,
-                                                           int mblocks) {
-  __shared__ typename T::Shared tile;
+struct W4Args {
+  const uint8_t* q;
+  int64_t ldq;
+  const f16* s;
+  const uint8_t* z;
+  int64_t ldp;
+  int gs;
+};
+struct W8Args {
+  const int8_t* q;
+  int64_t ldq;
+};
+
+template <class T, class WArgs>
+struct WeightOp;
+template <class T>
+struct WeightOp<T, W4Args> {
+  using Op = mp::W4Operand<T::BN>;
+  INTENT_DEVICE static void init(Op& op, const W4Args& w, int n0, int N) {
+    op.init(w.q, w.ldq, w.s, w.z, w.ldp, w.gs, ClampRows{n0, N});
+  }
+};
+template <class T>
+struct WeightOp<T, W8Args> {
+  using Op = mp::W8Operand<T::BN>;
+  INTENT_DEVICE static void init(Op& op, const W8Args& w, int n0, int N) { op.init(w.q, w.ldq, ClampRows{n0, N}); }
+};
+
+// y[m, n] = f16(sum_k x[m, k] * deq(W)[n, k] (* colscale[n])).
+template <class T, class WArgs, bool kColScale>
+__global__ __launch_bounds__(mp::NTHREADS, 1) void dense_gemm_kernel(const f16* __restrict__ x, int64_t ldx, int M,
+                                                                   WArgs w, int N, int K, f16* __restrict__ y,
+                                                                   int64_t ldy, const f16* __restrict__ colscale,
+                                                                   int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   const int m0 = (bid % mblocks) * T::BM;
   const int n0 = (bid / mblocks) * T::BN;
+  mp::RegRowsOperand<T::BM, mp::DenseRows> aop;
+  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave());
+  typename WeightOp<T, WArgs>::Op bop;
+  WeightOp<T, WArgs>::init(bop, w, n0, N);
   f32x16 acc[T::TI][T::TJ];
-  mainloop<T>(rows, m0, w, ClampRows{n0, N}, K, tile, acc);
+  mp::mainloop<T, mp::F16Math>(aop, bop, K / 64, buf0, buf1, acc);
+
+  // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
+  const bool vec = (ldy & 3) == 0 && (((uintptr_t)y) & 7) == 0;
 #pragma unroll
-  for (int j = 0; j < T::TJ; ++j) {
-    const int col = n0 + T::acc_col(j);
-    if (col >= N) continue;
-    const float cs = kColScale ? (float)colscale[col] : 1.0f;
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
 #pragma unroll
-    for (int i = 0; i < T::TI; ++i)
+    for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + T::acc_row(i, v);
-        if (row < rows.M) {
-          const float val = kColScale ? acc[i][j][v] * cs : acc[i][j][v];
-          y[(int64_t)row * ldy + col] = (f16)val;
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        f16* o = y + (int64_t)m * ldy + n;
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          v[c] = acc[i][j][4 * g + c];
+          if (kColScale && n + c < N) v[c] *= (float)colscale[n + c];
+        }
+        if (vec && n + 3 < N) {
+          f16x2 lo, hi;
+          lo[0] = (f16)v[0];
+          lo[1] = (f16)v[1];
+          hi[0] = (f16)v[2];
+          hi[1] = (f16)v[3];
+          *reinterpret_cast<u32x2*>(o) = u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (n + c < N) o[c] = (f16)v[c];
         }
       }
   }
 }
 
-template <class T, class WSrc, bool kColScale>
-int launch_tile(const f16* x, int64_t ldx, int M, int N, int K, const WSrc& w, f16* y, int64_t ldy,
+template <class T, class WArgs, bool kColScale>
+int launch_tile(const f16* x, int64_t ldx, int M, int N, int K, const WArgs& w, f16* y, int64_t ldy,
                 const f16* colscale, hipStream_t st, const char* name) {
   const int mblocks = (M + T::BM - 1) / T::BM;
   const int nblocks = (N + T::BN - 1) / T::BN;
   const int64_t grid = (int64_t)mblocks * nblocks;
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
-  hipLaunchKernelGGL((dense_gemm_kernel<T, WSrc, kColScale>), dim3((unsigned)grid), dim3(T::NT), 0, st,
-                     DenseRows{x, ldx, M}, w, N, K, y, ldy, colscale, mblocks);
+  INTENT_REQUIRE(intent::fits_offset(M, ldx * 2), INTENT_ERR_UNSUPPORTED,
+                 "%s: activations too large for 31-bit buffer offsets", name);
+  hipLaunchKernelGGL((dense_gemm_kernel<T, WArgs, kColScale>), dim3((unsigned)grid), dim3(mp::NTHREADS), 0, st, x, ldx,
+                     M, w, N, K, y, ldy, colscale, mblocks);
   return intent::launch_status(name);
 }
 
-// Tile choice: 256 x 128 (128 x 64 per wave) once M fills it, else 128 x 128.
-template <class WSrc, bool kColScale>
-int launch_dense(const f16* x, int64_t ldx, int M, int N, int K, const WSrc& w, f16* y, int64_t ldy,
+// Tiles: 256 x 192 (128 x 96 per wave) once M fills it, else 128 x 128.
+// 192 columns: N = 11008 gives 58 column tiles; with 8 row tiles that is 464
+// workgroups, 1.8 rounds of 256 CUs (256-wide tiles would give 344, 1.34).
+template <class WArgs, bool kColScale>
+int launch_dense(const f16* x, int64_t ldx, int M, int N, int K, const WArgs& w, f16* y, int64_t ldy,
                  const f16* colscale, hipStream_t st, const char* name) {
-  if (M > 128) return launch_tile<Tile<256, 128, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
-  return launch_tile<Tile<128, 128, 2, 2>, WSrc, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+  if (M > 128)
+    return launch_tile<mp::Tile<256, 192, 2, 2>, WArgs, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+  return launch_tile<mp::Tile<128, 128, 2, 2>, WArgs, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
 }
 
 }  // namespace
@@ -88,8 +145,8 @@ int w4a16_gemm_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
   INTENT_REQUIRE(intent::fits_offset(N, packed_ld) && intent::fits_offset(N, qparam_ld * 2) &&
                      intent::fits_offset(256 + 1, x_ld * 2),
                  INTENT_ERR_UNSUPPORTED, "w4a16_gemm: operand too large for 31-bit buffer offsets");
-  W4Source w{packed, packed_ld, (const f16*)scales, zeros, qparam_ld, (int)gs};
-  return launch_dense<W4Source, false>((const f16*)x, x_ld, (int)M, (int)N, (int)K, w, (f16*)y, y_ld, nullptr,
+  W4Args w{packed, packed_ld, (const f16*)scales, zeros, qparam_ld, (int)gs};
+  return launch_dense<W4Args, false>((const f16*)x, x_ld, (int)M, (int)N, (int)K, w, (f16*)y, y_ld, nullptr,
                                        (hipStream_t)stream, "w4a16_gemm");
 }
 
@@ -142,7 +199,7 @@ extern "C" int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t 
   if (M <= 16) return intent::w8a16_gemv_launch(x, M, K, x_ld, w, N, w_ld, scales, y, y_ld, stream);
   INTENT_REQUIRE(intent::fits_offset(N, w_ld) && intent::fits_offset(256 + 1, x_ld * 2), INTENT_ERR_UNSUPPORTED,
                  "w8a16_matmul: operand too large for 31-bit buffer offsets");
-  W8Source ws{w, w_ld};
-  return launch_dense<W8Source, true>((const f16*)x, x_ld, (int)M, (int)N, (int)K, ws, (f16*)y, y_ld,
+  W8Args ws{w, w_ld};
+  return launch_dense<W8Args, true>((const f16*)x, x_ld, (int)M, (int)N, (int)K, ws, (f16*)y, y_ld,
                                       (const f16*)scales, (hipStream_t)stream, "w8a16_matmul");
 }

@@ -1,0 +1,449 @@
+// Software-pipelined MFMA GEMM core for gfx950 (f16 and int8 operands).
+//
+//   acc[m, n] = sum_k A[m, k] * B[n, k]          (A rows: activations, B rows: weights)
+//
+// Both operands are staged through LDS one k-stage at a time. A stage holds
+// 128 bytes of every tile row: 64 k of f16 or 128 k of int8. Operands go
+// global -> VGPR (buffer loads) -> LDS (ds_write_b128); quantized weights are
+// decoded to f16 on the way. Two register sets and two LDS buffers keep two
+// stages in flight per workgroup (128 KB for a 256 x 256 int8 tile), which is
+// what the L2/MALL latency under a full-chip load needs to stay hidden.
+//
+// LDS layout of a stage row: eight 16-byte chunks; chunk c of row r sits in
+// slot c ^ ((r >> 1) & 7). Sixteen consecutive rows reading the same chunk then
+// hit sixteen distinct (bank half, slot) pairs, so the 32-row fragment reads of
+// v_mfma_*_32x32x* are conflict-free.
+//
+// Pipeline, one barrier per stage (step kt computes on LDS buffer kt % 2):
+//   top:    buffer loads of stage kt+2 into register set kt % 2;
+//   middle: MFMAs of stage kt, fragment reads of step kk+1 interleaved with
+//           the MFMAs of step kk;
+//   end:    stage kt+1 (register set (kt+1) % 2, loaded one step earlier)
+//           written to the other LDS buffer; lgkmcnt wait; barrier.
+//
+// Each wave owns a (BM/WM) x (BN/WN) block of 32 x 32 MFMA tiles. The MFMA
+// is issued as mfma(Bfrag, Afrag), so a lane's accumulator holds one m and
+// four consecutive n per 4-register group:
+//   m = wave_m*(BM/WM) + i*32 + lane%32
+//   n = wave_n*(BN/WN) + j*32 + (v/4)*8 + (lane/32)*4 + v%4
+// which lets epilogues store 4 (f16/bf16) or 4 (f32/i32) adjacent outputs.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+
+namespace mp {
+
+constexpr int ROWB = 128;  // bytes per tile row per stage
+constexpr int NTHREADS = 256;
+
+typedef __attribute__((address_space(3))) void lds_t;
+
+INTENT_DEVICE constexpr int swz(int row) { return (row >> 1) & 7; }
+
+using Rsrc = __amdgpu_buffer_rsrc_t;
+INTENT_DEVICE Rsrc make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
+// s_waitcnt with only vmcnt constrained (expcnt 7, lgkmcnt 15 = no wait).
+template <int N>
+INTENT_DEVICE void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// s_waitcnt vmcnt(N) lgkmcnt(0), then a workgroup barrier.
+template <int N>
+INTENT_DEVICE void wait_vm_lgkm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+  __builtin_amdgcn_s_barrier();
+}
+
+template <int BM_, int BN_, int WM_, int WN_>
+struct Tile {
+  static constexpr int BM = BM_;
+  static constexpr int BN = BN_;
+  static constexpr int WM = WM_;
+  static constexpr int WN = WN_;
+  static_assert(WM * WN * 64 == NTHREADS, "four waves");
+  static constexpr int WTM = BM / WM;
+  static constexpr int WTN = BN / WN;
+  static constexpr int TI = WTM / 32;
+  static constexpr int TJ = WTN / 32;
+  static_assert(TI * 32 * WM == BM && TJ * 32 * WN == BN, "tile shape");
+  static constexpr int A_BYTES = BM * ROWB;
+  static constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+
+  INTENT_DEVICE static int wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+  INTENT_DEVICE static int wave_m() { return wave() % WM; }
+  INTENT_DEVICE static int wave_n() { return wave() / WM; }
+  // Tile-local output coordinates of accumulator acc[i][j], register group g (0..3).
+  INTENT_DEVICE static int row(int i) { return wave_m() * WTM + i * 32 + (threadIdx.x & 31); }
+  INTENT_DEVICE static int col(int j, int g) { return wave_n() * WTN + j * 32 + g * 8 + ((threadIdx.x >> 5) & 1) * 4; }
+};
+
+struct F16Math {
+  using Acc = f32x16;
+  using Frag = f16x8;
+  INTENT_DEVICE static Acc mfma(Frag b, Frag a, Acc c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, c, 0, 0, 0); }
+};
+struct I8Math {
+  using Acc = i32x16;
+  using Frag = i32x4;
+  INTENT_DEVICE static Acc mfma(Frag b, Frag a, Acc c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(b, a, c, 0, 0, 0); }
+};
+
+// ---- row sources: byte offset of tile row p from a per-tile base --------------
+// Rows that hold no data map to some valid row; loads stay unpredicated and
+// epilogues never store those rows.
+
+struct DenseRows {  // rows m0.. of a row-major matrix; rows >= M clamp to M-1
+  const void* base;
+  int64_t ld_bytes;
+  int M;
+  INTENT_DEVICE const void* tile_base(int m0) const { return (const char*)base + (int64_t)m0 * ld_bytes; }
+  INTENT_DEVICE uint32_t off(int m0, int p) const {
+    const int m = m0 + p;
+    return (uint32_t)((m < M ? p : M - 1 - m0) * ld_bytes);
+  }
+};
+
+struct GatherRows {  // MoE gate/up: padded row p holds route sorted[p]; token = route / top_k
+  const void* base;
+  int64_t ld_bytes;
+  const int32_t* sorted;
+  int R;
+  int top_k;
+  INTENT_DEVICE const void* tile_base(int) const { return base; }
+  INTENT_DEVICE uint32_t off(int m0, int p) const {
+    const int r = sorted[m0 + p];
+    return (uint32_t)(((r >= 0 && r < R) ? r / top_k : 0) * ld_bytes);
+  }
+};
+
+// ---- operand staging ----------------------------------------------------------
+
+// Raw rows (f16 activations, int8 operands): lane i of instruction j holds
+// 16 bytes of tile row (4j + wave) * 8 + i/8 and writes LDS slot i % 8 of that
+// row, so it fetches chunk (i % 8) ^ swz(row). A half stage (64 bytes, int8
+// with K % 128 == 64) re-reads chunks 0..3 instead of running past the row.
+template <int ROWS, class Rows, bool kHalf = false>
+struct RegRowsOperand {
+  static constexpr int N_INST = ROWS / 32;
+  static_assert(N_INST * 32 == ROWS, "rows per tile must be a multiple of 32");
+  static constexpr int NVM = N_INST;
+  static constexpr int NDS = N_INST;  // LDS writes per stage
+  Rsrc rs;
+  uint32_t voff[N_INST];
+  uint32_t lds_off[N_INST];
+  int half_kt;        // stage index that is a half stage, or -1
+  uint32_t half_adj;  // 64 if this lane fetches a chunk in 4..7, else 0
+  struct Regs {
+    u32x4 v[N_INST];
+  };
+  INTENT_DEVICE void init(const Rows& rows, int m0, int wave, int half_stage = -1) {
+    rs = make_rsrc(rows.tile_base(m0));
+    half_kt = half_stage;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) {
+      const int r = (j * 4 + wave) * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ swz(r);
+      voff[j] = rows.off(m0, r) + chunk * 16;
+      lds_off[j] = (uint32_t)(r * ROWB + (lane & 7) * 16);
+    }
+    // swz(row) does not depend on j, so neither does the fetched chunk.
+    half_adj = (((lane & 7) ^ swz((wave * 8) + (lane >> 3))) >= 4) ? 64u : 0u;
+  }
+  INTENT_DEVICE void load(int kt, Regs& r) const {
+    const uint32_t adj = (kHalf && kt == half_kt) ? half_adj : 0u;
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) r.v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[j] - adj, (uint32_t)kt * ROWB, 0);
+  }
+  INTENT_DEVICE void store(const Regs& r, char* lds_region) const {
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) *reinterpret_cast<u32x4*>(lds_region + lds_off[j]) = r.v[j];
+  }
+};
+
+// Asymmetric group-quantized 4-bit weight rows (packed two per byte, low nibble
+// = even k), decoded to f16 (q - z) * s. A stage is 64 k = 32 packed bytes per
+// row, read as P = 2 pieces of 16 bytes (32 k each) or 4 pieces of 8 bytes.
+template <int ROWS>
+struct W4Operand {
+  static constexpr int PIECE = (ROWS * 2) % NTHREADS == 0 ? 16 : 8;  // bytes per load
+  static constexpr int P = 32 / PIECE;                                 // pieces per row per stage
+  static constexpr int NS = ROWS * P / NTHREADS;                       // loads per thread per stage
+  static_assert(NS * NTHREADS == ROWS * P, "W4 staging must divide evenly");
+  static constexpr int NVM = 3 * NS;  // vector memory instructions per stage
+  static constexpr int NDS = NS * (PIECE / 4);  // LDS writes per stage
+  typedef uint32_t Piece __attribute__((ext_vector_type(PIECE / 4)));
+
+  Rsrc rq, rs, rz;
+  uint32_t qoff[NS], soff[NS], zoff[NS];
+  int lrow[NS], part[NS];
+  int gs;  // 32 or a multiple of 64
+
+  struct Regs {
+    Piece w[NS];
+    uint16_t s[NS];
+    uint8_t z[NS];
+  };
+
+  // wrow(c): weight row of B-tile row c; ldq bytes per packed row; ldp groups per row.
+  template <class RowMap>
+  INTENT_DEVICE void init(const uint8_t* q, int64_t ldq, const f16* s, const uint8_t* z, int64_t ldp, int gsize,
+                          const RowMap& wrow) {
+    rq = make_rsrc(q);
+    rs = make_rsrc(s);
+    rz = make_rsrc(z);
+    gs = gsize;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int c = threadIdx.x + i * NTHREADS;
+      lrow[i] = c / P;
+      part[i] = c % P;
+      const int64_t w = wrow(lrow[i]);
+      // gs == 32: a stage spans two groups; piece p starts at k = p * PIECE * 2.
+      const int extra = gsize == 32 ? (part[i] * PIECE * 2) / 32 : 0;
+      qoff[i] = (uint32_t)(w * ldq + part[i] * PIECE);
+      soff[i] = (uint32_t)((w * ldp + extra) * 2);
+      zoff[i] = (uint32_t)(w * ldp + extra);
+    }
+  }
+  INTENT_DEVICE void load(int kt, Regs& r) const {
+    const uint32_t g = gs == 32 ? 2 * kt : (kt * 64) / gs;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      if constexpr (PIECE == 16)
+        r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[i], (uint32_t)kt * 32, 0);
+      else
+        r.w[i] = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff[i], (uint32_t)kt * 32, 0);
+      r.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[i], g * 2, 0);
+      r.z[i] = __builtin_amdgcn_raw_buffer_load_b8(rz, zoff[i], g, 0);
+    }
+  }
+  // Decode into the B region of a stage buffer.
+  INTENT_DEVICE void store(const Regs& r, char* lds_b) const {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const f16x2 zo = splat2((f16)(float)(1024 + r.z[i]));
+      const f16x2 sc = splat2(bit_cast<f16>(r.s[i]));
+      char* row = lds_b + lrow[i] * ROWB;
+      const int sw = swz(lrow[i]);
+#pragma unroll
+      for (int d = 0; d < PIECE / 4; ++d) {
+        const int chunk = part[i] * (PIECE / 4) + d;  // each dword = 8 k = one 16-byte f16 chunk
+        *reinterpret_cast<f16x8*>(row + ((chunk ^ sw) << 4)) = dequant8(r.w[i][d], zo, sc);
+      }
+    }
+  }
+};
+
+// Per-channel int8 weight rows converted exactly to f16 (scale applied in the
+// epilogue). A stage is 64 k = 64 bytes per row, loaded as 16-byte pieces.
+template <int ROWS>
+struct W8Operand {
+  static constexpr int P = 4;
+  static constexpr int NS = ROWS * P / NTHREADS;
+  static_assert(NS * NTHREADS == ROWS * P, "W8 staging must divide evenly");
+  static constexpr int NVM = NS;
+  static constexpr int NDS = 2 * NS;
+  Rsrc rq;
+  uint32_t qoff[NS];
+  int lrow[NS], part[NS];
+  struct Regs {
+    u32x4 w[NS];
+  };
+  template <class RowMap>
+  INTENT_DEVICE void init(const int8_t* q, int64_t ldq, const RowMap& wrow) {
+    rq = make_rsrc(q);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int c = threadIdx.x + i * NTHREADS;
+      lrow[i] = c / P;
+      part[i] = c % P;
+      qoff[i] = (uint32_t)((int64_t)wrow(lrow[i]) * ldq + part[i] * 16);
+    }
+  }
+  INTENT_DEVICE void load(int kt, Regs& r) const {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[i], (uint32_t)kt * 64, 0);
+  }
+  INTENT_DEVICE void store(const Regs& r, char* lds_b) const {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      char* row = lds_b + lrow[i] * ROWB;
+      const int sw = swz(lrow[i]);
+      const int c0 = part[i] * 2;
+      *reinterpret_cast<f16x8*>(row + ((c0 ^ sw) << 4)) = int8x8_to_f16(r.w[i][0], r.w[i][1]);
+      *reinterpret_cast<f16x8*>(row + (((c0 + 1) ^ sw) << 4)) = int8x8_to_f16(r.w[i][2], r.w[i][3]);
+    }
+  }
+};
+
+// ---- main loop ------------------------------------------------------------------
+
+// Fragment reads and MFMAs of one stage (KK steps of 32 bytes of k). The reads
+// of step kk+1 are interleaved one-for-one with the MFMAs of step kk.
+template <class T, class Math, int KK = 4, bool kSched = true>
+INTENT_DEVICE void compute_stage(const char* buf, const uint32_t (&aaddr)[4], const uint32_t (&baddr)[4],
+                                 typename Math::Acc (&acc)[T::TI][T::TJ]) {
+  using Frag = typename Math::Frag;
+  constexpr int NR = T::TI + T::TJ;
+  constexpr int NM = T::TI * T::TJ;
+  Frag af[2][T::TI], bf[2][T::TJ];
+  const char* a = buf;
+  const char* b = buf + T::A_BYTES;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) af[0][i] = *reinterpret_cast<const Frag*>(a + aaddr[0] + i * 32 * ROWB);
+#pragma unroll
+  for (int j = 0; j < T::TJ; ++j) bf[0][j] = *reinterpret_cast<const Frag*>(b + baddr[0] + j * 32 * ROWB);
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) {
+    const int cb = kk & 1;
+    if (kk + 1 < KK) {
+#pragma unroll
+      for (int i = 0; i < T::TI; ++i)
+        af[cb ^ 1][i] = *reinterpret_cast<const Frag*>(a + aaddr[kk + 1] + i * 32 * ROWB);
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j)
+        bf[cb ^ 1][j] = *reinterpret_cast<const Frag*>(b + baddr[kk + 1] + j * 32 * ROWB);
+    }
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) acc[i][j] = Math::mfma(bf[cb][j], af[cb][i], acc[i][j]);
+  }
+  if constexpr (kSched) {
+    // Standalone stage (no loads or stores around it): the first step's
+    // reads, then MFMA/read pairs while reads of the next step remain.
+    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if (kk + 1 < KK) {
+        constexpr int PAIRS = NR < NM ? NR : NM;
+#pragma unroll
+        for (int x = 0; x < PAIRS; ++x) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if (NR > NM) __builtin_amdgcn_sched_group_barrier(0x100, NR - NM, 0);
+        if (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+      }
+    }
+  }
+}
+
+// Instruction schedule of one pipelined step: 4*NM MFMA slots. The fragment
+// reads of step kk+1 ride on the first NR slots of step kk; NV buffer loads
+// are spread over the first half of the slots and NW LDS writes over the
+// second half (sched_group_barrier masks: 0x008 MFMA, 0x020 VMEM read,
+// 0x100 DS read, 0x200 DS write).
+constexpr int spread(int s, int n, int slots) { return (s + 1) * n / slots - s * n / slots; }
+
+template <int NM, int NR, int NV, int NW, int S>
+INTENT_DEVICE void sched_slots() {
+  if constexpr (S < 4 * NM) {
+    constexpr int kk = S / NM;
+    constexpr int x = S % NM;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if constexpr (kk < 3 && x < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    if constexpr (S < 2 * NM && spread(S, NV, 2 * NM) > 0)
+      __builtin_amdgcn_sched_group_barrier(0x020, spread(S, NV, 2 * NM), 0);
+    if constexpr (S >= 2 * NM && spread(S - 2 * NM, NW, 2 * NM) > 0)
+      __builtin_amdgcn_sched_group_barrier(0x200, spread(S - 2 * NM, NW, 2 * NM), 0);
+    sched_slots<NM, NR, NV, NW, S + 1>();
+  }
+}
+template <int NM, int NR, int NV, int NW>
+INTENT_DEVICE void sched_step() {
+  __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+  sched_slots<NM, NR, NV, NW, 0>();
+}
+
+// buf0/buf1: the two LDS stage buffers, each STAGE_BYTES: A rows then B rows.
+// nk: number of stages; half_last: the last stage carries 64 bytes of k
+// (its loads must already re-read chunks 0..3, see RegRowsOperand).
+template <class T, class Math, class AOp, class BOp>
+INTENT_DEVICE void mainloop(const AOp& aop, const BOp& bop, int nk, char* buf0, char* buf1,
+                            typename Math::Acc (&acc)[T::TI][T::TJ], bool half_last = false, int k_rot = 0) {
+  // Stage order: full stages start at k_rot and wrap; a half stage stays last.
+  const int nfull = half_last ? nk - 1 : nk;
+  const int rot = nfull > 0 ? k_rot % nfull : 0;
+  auto kidx = [&](int kt) {
+    if (kt >= nfull) return kt;
+    const int r = kt + rot;
+    return r >= nfull ? r - nfull : r;
+  };
+  const int lane = threadIdx.x & 63;
+  // Fragment addresses: row (lane % 32) of each 32-row tile, chunk 2*kk + lane/32.
+  uint32_t aaddr[4], baddr[4];
+  {
+    const int r = lane & 31;
+    const int x = (lane >> 5) ^ swz(r);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint32_t s = (uint32_t)(((2 * kk) ^ x) << 4);
+      aaddr[kk] = (uint32_t)((T::wave_m() * T::WTM + r) * ROWB) + s;
+      baddr[kk] = (uint32_t)((T::wave_n() * T::WTN + r) * ROWB) + s;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+  if (nk <= 0) return;
+
+  typename AOp::Regs ra0, ra1;
+  typename BOp::Regs rb0, rb1;
+  aop.load(kidx(0), ra0);
+  bop.load(kidx(0), rb0);
+  if (nk > 1) {
+    aop.load(kidx(1), ra1);
+    bop.load(kidx(1), rb1);
+  }
+  aop.store(ra0, buf0);
+  bop.store(rb0, buf0 + T::A_BYTES);
+  wait_vm_lgkm_barrier<AOp::NVM + BOp::NVM>();
+
+  // Step kt: rn holds stage kt+1, rf receives stage kt+2.
+  // The step body is one basic block: the stage-kt+2 load is clamped to the
+  // last stage (the last step re-loads it and never stores it), so the whole
+  // step can be scheduled as one interleaved stream.
+  auto step = [&](int kt, char* cur, char* nxt, typename AOp::Regs& ran, typename BOp::Regs& rbn,
+                  typename AOp::Regs& raf, typename BOp::Regs& rbf) {
+    const int kn = kidx(kt + 2 < nk ? kt + 2 : nk - 1);
+    aop.load(kn, raf);
+    bop.load(kn, rbf);
+    compute_stage<T, Math, 4, false>(cur, aaddr, baddr, acc);
+    aop.store(ran, nxt);
+    bop.store(rbn, nxt + T::A_BYTES);
+    sched_step<T::TI * T::TJ, T::TI + T::TJ, AOp::NVM + BOp::NVM, AOp::NDS + BOp::NDS>();
+    wait_vm_lgkm_barrier<AOp::NVM + BOp::NVM>();
+  };
+  // Every stage but the last runs a full step; the last stage is peeled so
+  // that it can be a half stage and issues no loads or stores.
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    step(kt, buf0, buf1, ra1, rb1, ra0, rb0);
+    step(kt + 1, buf1, buf0, ra0, rb0, ra1, rb1);
+  }
+  if (kt + 1 < nk) {
+    step(kt, buf0, buf1, ra1, rb1, ra0, rb0);
+    ++kt;
+  }
+  char* last = (kt & 1) ? buf1 : buf0;
+  if (half_last)
+    compute_stage<T, Math, 2>(last, aaddr, baddr, acc);
+  else
+    compute_stage<T, Math, 4>(last, aaddr, baddr, acc);
+}
+
+}  // namespace mp

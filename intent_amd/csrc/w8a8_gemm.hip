@@ -1,130 +1,78 @@
 // W8A8 int8 GEMM on v_mfma_i32_32x32x32_i8 (gfx950), exact int32 accumulation.
 //
-// Tile: 128 x 128 outputs, BK = 128 bytes (64 when K is not a multiple of 128), 256 threads = 4 waves (2 x 2), each
-// wave 64 x 64 = 2 x 2 MFMA tiles. Both operands are K-contiguous int8 rows
-// staged through LDS with a register prefetch of the next k-tile.
+// Tiles of 256 x 256 (or 128 x 128 for small problems), 4 waves in 2 x 2, on
+// the pipelined core in mfma_pipe.h: both K-contiguous int8 operands are
+// staged global -> VGPR -> LDS, 128 k per stage, two stages in flight.
 // Epilogues: bf16(f32(acc) * a_scale[m] * w_scale[n]) or int32 acc + bias[n].
 #include "common.h"
 #include "internal.h"
+#include "mfma_pipe.h"
 
+#ifndef KROT
+#define KROT 0
+#endif
 namespace {
 
-constexpr int BM = 128;
-constexpr int BN = 128;
-constexpr int NTHREADS = 256;
-
-// BK bytes of K per step; rows padded by 16 bytes against bank aliasing.
-template <int BK>
-struct I8Tile {
-  int8_t a[BM][BK + 16];
-  int8_t b[BN][BK + 16];
-};
+using T256 = mp::Tile<256, 256, 2, 2>;  // 128 x 128 per wave: 16 MFMA tiles of 32 x 32
+using T128 = mp::Tile<128, 128, 2, 2>;  // small problems: more workgroups
 
 enum class Epi { kBf16Scaled, kI32Bias };
 
-template <Epi E, int BK>
-__global__ __launch_bounds__(NTHREADS) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t lda, int M,
-                                                           const int8_t* __restrict__ w, int64_t ldw, int N, int K,
-                                                           const float* __restrict__ a_scales,
-                                                           const float* __restrict__ w_scales,
-                                                           const int32_t* __restrict__ bias, void* __restrict__ out,
-                                                           int64_t ldo, int mblocks) {
-  __shared__ I8Tile<BK> t;
-  constexpr int CPR = BK / 16;                 // 16-byte chunks per row
-  constexpr int NCH = BM * CPR / NTHREADS;     // chunks per thread per operand
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave & 1;
-  const int wn = wave >> 1;
+// One workgroup per output tile; 128 k per LDS stage, the last one possibly 64.
+template <class T, Epi E, bool kHalf>
+__global__ __launch_bounds__(mp::NTHREADS, 1) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t lda, int M,
+                                                                const int8_t* __restrict__ w, int64_t ldw, int N,
+                                                                int K, const float* __restrict__ a_scales,
+                                                                const float* __restrict__ w_scales,
+                                                                const int32_t* __restrict__ bias,
+                                                                void* __restrict__ out, int64_t ldo, int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * BM;
-  const int n0 = (bid / mblocks) * BN;
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  const int wave = T::wave();
+  const int nk = (K + mp::ROWB - 1) / mp::ROWB;
+  const bool half = kHalf;
+  mp::RegRowsOperand<T::BM, mp::DenseRows, kHalf> aop;
+  mp::RegRowsOperand<T::BN, mp::DenseRows, kHalf> bop;
+  aop.init(mp::DenseRows{a, lda, M}, m0, wave, half ? nk - 1 : -1);
+  bop.init(mp::DenseRows{w, ldw, N}, n0, wave, half ? nk - 1 : -1);
+  i32x16 acc[T::TI][T::TJ];
+  mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc, half, KROT);
 
-  // Staging: chunk c = tid + 256*i covers row c/CPR, bytes (c%CPR)*16. Rows
-  // past the end read a clamped valid row; their outputs are never stored.
-  const int8_t* ap[NCH];
-  const int8_t* wp[NCH];
-  int srow[NCH], scol[NCH];
+  // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    const int c = tid + NTHREADS * i;
-    srow[i] = c / CPR;
-    scol[i] = (c % CPR) * 16;
-    const int m = m0 + srow[i];
-    const int n = n0 + srow[i];
-    ap[i] = a + (int64_t)(m < M ? m : M - 1) * lda + scol[i];
-    wp[i] = w + (int64_t)(n < N ? n : N - 1) * ldw + scol[i];
-  }
-
-  i32x16 acc[2][2];
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+    const float sa = E == Epi::kBf16Scaled ? a_scales[m] : 0.f;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
-
-  const int nk = K / BK;
-  u32x4 ar[NCH], wr[NCH];
-#pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    ar[i] = load16(ap[i]);
-    wr[i] = load16(wp[i]);
-  }
-  for (int kt = 0; kt < nk; ++kt) {
-#pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-      *reinterpret_cast<u32x4*>(&t.a[srow[i]][scol[i]]) = ar[i];
-      *reinterpret_cast<u32x4*>(&t.b[srow[i]][scol[i]]) = wr[i];
-    }
-    __syncthreads();
-    if (kt + 1 < nk) {
-#pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        ar[i] = load16(ap[i] + (int64_t)(kt + 1) * BK);
-        wr[i] = load16(wp[i] + (int64_t)(kt + 1) * BK);
-      }
-    }
-#pragma unroll
-    for (int kk = 0; kk < BK / 32; ++kk) {
-      i32x4 af[2], bf[2];
-      const int kof = kk * 32 + (lane >> 5) * 16;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = *reinterpret_cast<const i32x4*>(&t.a[wm * 64 + i * 32 + (lane & 31)][kof]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = *reinterpret_cast<const i32x4*>(&t.b[wn * 64 + j * 32 + (lane & 31)][kof]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-
-  // 32x32 layout: lane l holds column l%32, rows (v/4)*8 + (l/32)*4 + v%4.
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-    if (col >= N) continue;
-    float ws = 0.f;
-    int32_t bs = 0;
-    if (E == Epi::kBf16Scaled) ws = w_scales[col];
-    if (E == Epi::kI32Bias && bias) bs = bias[col];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * 64 + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (row >= M) continue;
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
         if (E == Epi::kBf16Scaled) {
-          float f = (float)acc[i][j][v];
-          f = f * a_scales[row];
-          f = f * ws;
-          reinterpret_cast<uint16_t*>(out)[(int64_t)row * ldo + col] = f32_to_bf16_rne(f);
+          uint16_t* o = reinterpret_cast<uint16_t*>(out) + (int64_t)m * ldo + n;
+          if (vec && n + 3 < N) {
+            const f32x4 ws = *reinterpret_cast<const f32x4*>(w_scales + n);
+            uint32_t lo = 0, hi = 0;
+            lo = f32_to_bf16_rne(((float)acc[i][j][4 * g] * sa) * ws[0]) |
+                 ((uint32_t)f32_to_bf16_rne(((float)acc[i][j][4 * g + 1] * sa) * ws[1]) << 16);
+            hi = f32_to_bf16_rne(((float)acc[i][j][4 * g + 2] * sa) * ws[2]) |
+                 ((uint32_t)f32_to_bf16_rne(((float)acc[i][j][4 * g + 3] * sa) * ws[3]) << 16);
+            *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
+          } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              if (n + c < N) o[c] = f32_to_bf16_rne(((float)acc[i][j][4 * g + c] * sa) * w_scales[n + c]);
+          }
         } else {
-          reinterpret_cast<int32_t*>(out)[(int64_t)row * ldo + col] =
-              (int32_t)((uint32_t)acc[i][j][v] + (uint32_t)bs);
+          int32_t* o = reinterpret_cast<int32_t*>(out) + (int64_t)m * ldo + n;
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (n + c < N) o[c] = (int32_t)((uint32_t)acc[i][j][4 * g + c] + (uint32_t)(bias ? bias[n + c] : 0));
         }
       }
   }
@@ -144,21 +92,34 @@ int check_i8(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const int8_t* 
   return INTENT_OK;
 }
 
+template <class T, Epi E>
+int launch_tile(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const float* sa, const int8_t* w, int64_t N,
+                int64_t w_ld, const float* sw, const int32_t* bias, void* out, int64_t out_ld, void* stream,
+                const char* name) {
+  const int mblocks = (int)((M + T::BM - 1) / T::BM);
+  const int nblocks = (int)((N + T::BN - 1) / T::BN);
+  const int64_t grid = (int64_t)mblocks * nblocks;
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, w_ld), INTENT_ERR_UNSUPPORTED,
+                 "%s: operand too large for 31-bit buffer offsets", name);
+  if (K % mp::ROWB == 0)
+    hipLaunchKernelGGL((i8_gemm_kernel<T, E, false>), dim3((unsigned)grid), dim3(mp::NTHREADS), 0,
+                       (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
+  else
+    hipLaunchKernelGGL((i8_gemm_kernel<T, E, true>), dim3((unsigned)grid), dim3(mp::NTHREADS), 0,
+                       (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
+  return intent::launch_status(name);
+}
+
+// 256 x 256 tiles once the problem has enough of them to fill the chip.
 template <Epi E>
 int launch_i8(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const float* sa, const int8_t* w, int64_t N,
               int64_t w_ld, const float* sw, const int32_t* bias, void* out, int64_t out_ld, void* stream,
               const char* name) {
-  const int mblocks = (int)((M + BM - 1) / BM);
-  const int nblocks = (int)((N + BN - 1) / BN);
-  const int64_t grid = (int64_t)mblocks * nblocks;
-  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
-  if (K % 128 == 0)
-    hipLaunchKernelGGL((i8_gemm_kernel<E, 128>), dim3((unsigned)grid), dim3(NTHREADS), 0, (hipStream_t)stream, a,
-                       a_ld, (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
-  else
-    hipLaunchKernelGGL((i8_gemm_kernel<E, 64>), dim3((unsigned)grid), dim3(NTHREADS), 0, (hipStream_t)stream, a,
-                       a_ld, (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
-  return intent::launch_status(name);
+  const int64_t big = ((M + 255) / 256) * ((N + 255) / 256);
+  if (big >= 256)
+    return launch_tile<T256, E>(a, M, K, a_ld, sa, w, N, w_ld, sw, bias, out, out_ld, stream, name);
+  return launch_tile<T128, E>(a, M, K, a_ld, sa, w, N, w_ld, sw, bias, out, out_ld, stream, name);
 }
 
 }  // namespace
