@@ -34,20 +34,20 @@ template <class T, class WArgs>
 struct WeightOp;
 template <class T>
 struct WeightOp<T, W4Args> {
-  using Op = mp::W4Operand<T::BN>;
+  using Op = mp::W4Operand<T::BN, T::NT>;
   INTENT_DEVICE static void init(Op& op, const W4Args& w, int n0, int N) {
     op.init(w.q, w.ldq, w.s, w.z, w.ldp, w.gs, ClampRows{n0, N});
   }
 };
 template <class T>
 struct WeightOp<T, W8Args> {
-  using Op = mp::W8Operand<T::BN>;
+  using Op = mp::W8Operand<T::BN, T::NT>;
   INTENT_DEVICE static void init(Op& op, const W8Args& w, int n0, int N) { op.init(w.q, w.ldq, ClampRows{n0, N}); }
 };
 
 // y[m, n] = f16(sum_k x[m, k] * deq(W)[n, k] (* colscale[n])).
 template <class T, class WArgs, bool kColScale>
-__global__ __launch_bounds__(mp::NTHREADS, 1) void dense_gemm_kernel(const f16* __restrict__ x, int64_t ldx, int M,
+__global__ __launch_bounds__(T::NT, 1) void dense_gemm_kernel(const f16* __restrict__ x, int64_t ldx, int M,
                                                                    WArgs w, int N, int K, f16* __restrict__ y,
                                                                    int64_t ldy, const f16* __restrict__ colscale,
                                                                    int mblocks) {
@@ -56,12 +56,12 @@ __global__ __launch_bounds__(mp::NTHREADS, 1) void dense_gemm_kernel(const f16* 
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   const int m0 = (bid % mblocks) * T::BM;
   const int n0 = (bid / mblocks) * T::BN;
-  mp::RegRowsOperand<T::BM, mp::DenseRows> aop;
-  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave());
   typename WeightOp<T, WArgs>::Op bop;
   WeightOp<T, WArgs>::init(bop, w, n0, N);
   f32x16 acc[T::TI][T::TJ];
-  mp::mainloop<T, mp::F16Math>(aop, bop, K / 64, buf0, buf1, acc);
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave());
+  mp::mainloop_dma_a<T, mp::F16Math>(aop, bop, K / 64, buf0, buf1, acc);
 
   // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
   const bool vec = (ldy & 3) == 0 && (((uintptr_t)y) & 7) == 0;
@@ -106,19 +106,22 @@ int launch_tile(const f16* x, int64_t ldx, int M, int N, int K, const WArgs& w, 
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
   INTENT_REQUIRE(intent::fits_offset(M, ldx * 2), INTENT_ERR_UNSUPPORTED,
                  "%s: activations too large for 31-bit buffer offsets", name);
-  hipLaunchKernelGGL((dense_gemm_kernel<T, WArgs, kColScale>), dim3((unsigned)grid), dim3(mp::NTHREADS), 0, st, x, ldx,
+  hipLaunchKernelGGL((dense_gemm_kernel<T, WArgs, kColScale>), dim3((unsigned)grid), dim3(T::NT), 0, st, x, ldx,
                      M, w, N, K, y, ldy, colscale, mblocks);
   return intent::launch_status(name);
 }
 
-// Tiles: 256 x 192 (128 x 96 per wave) once M fills it, else 128 x 128.
-// 192 columns: N = 11008 gives 58 column tiles; with 8 row tiles that is 464
-// workgroups, 1.8 rounds of 256 CUs (256-wide tiles would give 344, 1.34).
+// Tiles: 256 x 192 with 8 waves (64 x 96 each, two waves per SIMD so that one
+// wave's weight decode overlaps the other's MFMAs) once M fills it, else
+// 128 x 128 with 4 waves. 192 columns: N = 11008 gives 58 column tiles; with
+// 8 row tiles that is 464 workgroups, 1.8 rounds of 256 CUs (256-wide tiles
+// would give 344, 1.34). Activations go global -> LDS by DMA, weights through
+// VGPRs with the decode.
 template <class WArgs, bool kColScale>
 int launch_dense(const f16* x, int64_t ldx, int M, int N, int K, const WArgs& w, f16* y, int64_t ldy,
                  const f16* colscale, hipStream_t st, const char* name) {
   if (M > 128)
-    return launch_tile<mp::Tile<256, 192, 2, 2>, WArgs, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+    return launch_tile<mp::Tile<256, 192, 4, 2>, WArgs, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
   return launch_tile<mp::Tile<128, 128, 2, 2>, WArgs, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
 }
 

@@ -36,7 +36,7 @@
 namespace mp {
 
 constexpr int ROWB = 128;  // bytes per tile row per stage
-constexpr int NTHREADS = 256;
+constexpr int NTHREADS = 256;  // default workgroup: 4 waves
 
 typedef __attribute__((address_space(3))) void lds_t;
 
@@ -67,7 +67,9 @@ struct Tile {
   static constexpr int BN = BN_;
   static constexpr int WM = WM_;
   static constexpr int WN = WN_;
-  static_assert(WM * WN * 64 == NTHREADS, "four waves");
+  static constexpr int NW = WM * WN;  // waves: 4 (one per SIMD) or 8 (two per SIMD)
+  static constexpr int NT = NW * 64;
+  static_assert(NW == 4 || NW == 8, "four or eight waves");
   static constexpr int WTM = BM / WM;
   static constexpr int WTN = BN / WN;
   static constexpr int TI = WTM / 32;
@@ -126,13 +128,13 @@ struct GatherRows {  // MoE gate/up: padded row p holds route sorted[p]; token =
 // ---- operand staging ----------------------------------------------------------
 
 // Raw rows (f16 activations, int8 operands): lane i of instruction j holds
-// 16 bytes of tile row (4j + wave) * 8 + i/8 and writes LDS slot i % 8 of that
+// 16 bytes of tile row (NW*j + wave) * 8 + i/8 and writes LDS slot i % 8 of that
 // row, so it fetches chunk (i % 8) ^ swz(row). A half stage (64 bytes, int8
 // with K % 128 == 64) re-reads chunks 0..3 instead of running past the row.
-template <int ROWS, class Rows, bool kHalf = false>
+template <int ROWS, class Rows, bool kHalf = false, int NW = 4>
 struct RegRowsOperand {
-  static constexpr int N_INST = ROWS / 32;
-  static_assert(N_INST * 32 == ROWS, "rows per tile must be a multiple of 32");
+  static constexpr int N_INST = ROWS / (8 * NW);
+  static_assert(N_INST * 8 * NW == ROWS, "tile rows must be a multiple of 8 per wave");
   static constexpr int NVM = N_INST;
   static constexpr int NDS = N_INST;  // LDS writes per stage
   Rsrc rs;
@@ -149,7 +151,7 @@ struct RegRowsOperand {
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < N_INST; ++j) {
-      const int r = (j * 4 + wave) * 8 + (lane >> 3);
+      const int r = (j * NW + wave) * 8 + (lane >> 3);
       const int chunk = (lane & 7) ^ swz(r);
       voff[j] = rows.off(m0, r) + chunk * 16;
       lds_off[j] = (uint32_t)(r * ROWB + (lane & 7) * 16);
@@ -168,28 +170,60 @@ struct RegRowsOperand {
   }
 };
 
+// Raw rows copied global -> LDS by DMA (buffer_load ... lds): no VGPRs and
+// no ds_write issue slots. Each wave instruction moves 8 rows x 128 bytes;
+// lane i writes slot i%8 of row i/8, fetching chunk slot ^ swz(row).
+template <int ROWS, class Rows, int NW = 4>
+struct DmaRowsOperand {
+  static constexpr int N_INST = ROWS / (8 * NW);
+  static_assert(N_INST * 8 * NW == ROWS, "tile rows must be a multiple of 8 per wave");
+  static constexpr int NVM = N_INST;
+  Rsrc rs;
+  uint32_t voff[N_INST];
+  int lds_row0[N_INST];
+  INTENT_DEVICE void init(const Rows& rows, int m0, int wave) {
+    rs = make_rsrc(rows.tile_base(m0));
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) {
+      const int r0 = (j * NW + wave) * 8;
+      const int r = r0 + (lane >> 3);
+      voff[j] = rows.off(m0, r) + (((lane & 7) ^ swz(r)) << 4);
+      lds_row0[j] = r0;
+    }
+  }
+  INTENT_DEVICE void issue(char* lds_region, int kt) const {
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_t*)(lds_region + lds_row0[j] * ROWB), 16, voff[j],
+                                               (uint32_t)kt * ROWB, 0, 0);
+  }
+};
+
 // Asymmetric group-quantized 4-bit weight rows (packed two per byte, low nibble
 // = even k), decoded to f16 (q - z) * s. A stage is 64 k = 32 packed bytes per
 // row, read as P = 2 pieces of 16 bytes (32 k each) or 4 pieces of 8 bytes.
-template <int ROWS>
+template <int ROWS, int NT = NTHREADS>
 struct W4Operand {
-  static constexpr int PIECE = (ROWS * 2) % NTHREADS == 0 ? 16 : 8;  // bytes per load
-  static constexpr int P = 32 / PIECE;                                 // pieces per row per stage
-  static constexpr int NS = ROWS * P / NTHREADS;                       // loads per thread per stage
-  static_assert(NS * NTHREADS == ROWS * P, "W4 staging must divide evenly");
-  static constexpr int NVM = 3 * NS;  // vector memory instructions per stage
+  static constexpr int PIECE = (ROWS * 2) % NT == 0 ? 16 : (ROWS * 4) % NT == 0 ? 8 : 4;  // bytes per load
+  static constexpr int P = 32 / PIECE;                                                     // pieces per row per stage
+  static constexpr int NS = ROWS * P / NT;                                                 // loads per thread per stage
+  static_assert(NS * NT == ROWS * P, "W4 staging must divide evenly");
+  static constexpr int NVM = 3 * NS;            // vector memory instructions per stage
   static constexpr int NDS = NS * (PIECE / 4);  // LDS writes per stage
-  typedef uint32_t Piece __attribute__((ext_vector_type(PIECE / 4)));
+  typedef uint32_t Piece __attribute__((ext_vector_type(PIECE / 4 > 1 ? PIECE / 4 : 2)));
 
   Rsrc rq, rs, rz;
   uint32_t qoff[NS], soff[NS], zoff[NS];
   int lrow[NS], part[NS];
   int gs;  // 32 or a multiple of 64
 
+  // Scales and zeros stay in 32-bit registers: packing two 16-bit loads
+  // into one VGPR would force a wait right after they are issued.
   struct Regs {
     Piece w[NS];
-    uint16_t s[NS];
-    uint8_t z[NS];
+    uint32_t s[NS];
+    uint32_t z[NS];
   };
 
   // wrow(c): weight row of B-tile row c; ldq bytes per packed row; ldp groups per row.
@@ -202,7 +236,7 @@ struct W4Operand {
     gs = gsize;
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const int c = threadIdx.x + i * NTHREADS;
+      const int c = threadIdx.x + i * NT;
       lrow[i] = c / P;
       part[i] = c % P;
       const int64_t w = wrow(lrow[i]);
@@ -219,10 +253,12 @@ struct W4Operand {
     for (int i = 0; i < NS; ++i) {
       if constexpr (PIECE == 16)
         r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[i], (uint32_t)kt * 32, 0);
-      else
+      else if constexpr (PIECE == 8)
         r.w[i] = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff[i], (uint32_t)kt * 32, 0);
-      r.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, soff[i], g * 2, 0);
-      r.z[i] = __builtin_amdgcn_raw_buffer_load_b8(rz, zoff[i], g, 0);
+      else
+        r.w[i][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, qoff[i], (uint32_t)kt * 32, 0);
+      r.s[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, soff[i], g * 2, 0);
+      r.z[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rz, zoff[i], g, 0);
     }
   }
   // Decode into the B region of a stage buffer.
@@ -230,7 +266,7 @@ struct W4Operand {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const f16x2 zo = splat2((f16)(float)(1024 + r.z[i]));
-      const f16x2 sc = splat2(bit_cast<f16>(r.s[i]));
+      const f16x2 sc = splat2(bit_cast<f16>((uint16_t)r.s[i]));
       char* row = lds_b + lrow[i] * ROWB;
       const int sw = swz(lrow[i]);
 #pragma unroll
@@ -243,14 +279,17 @@ struct W4Operand {
 };
 
 // Per-channel int8 weight rows converted exactly to f16 (scale applied in the
-// epilogue). A stage is 64 k = 64 bytes per row, loaded as 16-byte pieces.
-template <int ROWS>
+// epilogue). A stage is 64 k = 64 bytes per row, loaded as 16-byte pieces
+// (two f16 chunks) or 8-byte pieces (one chunk) so that every thread gets the
+// same number of pieces.
+template <int ROWS, int NT = NTHREADS>
 struct W8Operand {
-  static constexpr int P = 4;
-  static constexpr int NS = ROWS * P / NTHREADS;
-  static_assert(NS * NTHREADS == ROWS * P, "W8 staging must divide evenly");
+  static constexpr int PIECE = (ROWS * 4) % NT == 0 ? 16 : 8;
+  static constexpr int P = 64 / PIECE;
+  static constexpr int NS = ROWS * P / NT;
+  static_assert(NS * NT == ROWS * P, "W8 staging must divide evenly");
   static constexpr int NVM = NS;
-  static constexpr int NDS = 2 * NS;
+  static constexpr int NDS = NS * PIECE / 8;
   Rsrc rq;
   uint32_t qoff[NS];
   int lrow[NS], part[NS];
@@ -262,24 +301,32 @@ struct W8Operand {
     rq = make_rsrc(q);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const int c = threadIdx.x + i * NTHREADS;
+      const int c = threadIdx.x + i * NT;
       lrow[i] = c / P;
       part[i] = c % P;
-      qoff[i] = (uint32_t)((int64_t)wrow(lrow[i]) * ldq + part[i] * 16);
+      qoff[i] = (uint32_t)((int64_t)wrow(lrow[i]) * ldq + part[i] * PIECE);
     }
   }
   INTENT_DEVICE void load(int kt, Regs& r) const {
 #pragma unroll
-    for (int i = 0; i < NS; ++i) r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[i], (uint32_t)kt * 64, 0);
+    for (int i = 0; i < NS; ++i) {
+      if constexpr (PIECE == 16) {
+        r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[i], (uint32_t)kt * 64, 0);
+      } else {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff[i], (uint32_t)kt * 64, 0);
+        r.w[i] = u32x4{v[0], v[1], 0u, 0u};
+      }
+    }
   }
   INTENT_DEVICE void store(const Regs& r, char* lds_b) const {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       char* row = lds_b + lrow[i] * ROWB;
       const int sw = swz(lrow[i]);
-      const int c0 = part[i] * 2;
+      const int c0 = part[i] * (PIECE / 8);
       *reinterpret_cast<f16x8*>(row + ((c0 ^ sw) << 4)) = int8x8_to_f16(r.w[i][0], r.w[i][1]);
-      *reinterpret_cast<f16x8*>(row + (((c0 + 1) ^ sw) << 4)) = int8x8_to_f16(r.w[i][2], r.w[i][3]);
+      if constexpr (PIECE == 16)
+        *reinterpret_cast<f16x8*>(row + (((c0 + 1) ^ sw) << 4)) = int8x8_to_f16(r.w[i][2], r.w[i][3]);
     }
   }
 };
@@ -343,7 +390,7 @@ INTENT_DEVICE void compute_stage(const char* buf, const uint32_t (&aaddr)[4], co
 // reads of step kk+1 ride on the first NR slots of step kk; NV buffer loads
 // are spread over the first half of the slots and NW LDS writes over the
 // second half (sched_group_barrier masks: 0x008 MFMA, 0x020 VMEM read,
-// 0x100 DS read, 0x200 DS write).
+// 0x100 DS read, 0x200 DS write). Decode VALU is left to the compiler.
 constexpr int spread(int s, int n, int slots) { return (s + 1) * n / slots - s * n / slots; }
 
 template <int NM, int NR, int NV, int NW, int S>
@@ -444,6 +491,59 @@ INTENT_DEVICE void mainloop(const AOp& aop, const BOp& bop, int nk, char* buf0, 
     compute_stage<T, Math, 2>(last, aaddr, baddr, acc);
   else
     compute_stage<T, Math, 4>(last, aaddr, baddr, acc);
+}
+
+// Variant with the A operand copied by DMA one stage ahead (B through VGPRs,
+// two stages ahead). At the loop header no DMA is in flight: the DMA of a
+// step is older than its B loads, so the step-end vmcnt wait retires it.
+template <class T, class Math, int NWA, class Rows, class BOp>
+INTENT_DEVICE void mainloop_dma_a(const DmaRowsOperand<T::BM, Rows, NWA>& aop, const BOp& bop, int nk, char* buf0,
+                                  char* buf1, typename Math::Acc (&acc)[T::TI][T::TJ]) {
+  const int lane = threadIdx.x & 63;
+  uint32_t aaddr[4], baddr[4];
+  {
+    const int r = lane & 31;
+    const int x = (lane >> 5) ^ swz(r);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint32_t s = (uint32_t)(((2 * kk) ^ x) << 4);
+      aaddr[kk] = (uint32_t)((T::wave_m() * T::WTM + r) * ROWB) + s;
+      baddr[kk] = (uint32_t)((T::wave_n() * T::WTN + r) * ROWB) + s;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+  if (nk <= 0) return;
+  using ADma = DmaRowsOperand<T::BM, Rows, NWA>;
+  typename BOp::Regs rb0, rb1;
+  bop.load(0, rb0);
+  if (nk > 1) bop.load(1, rb1);
+  aop.issue(buf0, 0);
+  bop.store(rb0, buf0 + T::A_BYTES);
+  wait_vm_lgkm_barrier<0>();
+  auto step = [&](int kt, char* cur, char* nxt, typename BOp::Regs& rbn, typename BOp::Regs& rbf) {
+    aop.issue(nxt, kt + 1);
+    const int kn = kt + 2 < nk ? kt + 2 : nk - 1;
+    bop.load(kn, rbf);
+    compute_stage<T, Math, 4, false>(cur, aaddr, baddr, acc);
+    bop.store(rbn, nxt + T::A_BYTES);
+    sched_step<T::TI * T::TJ, T::TI + T::TJ, ADma::NVM + BOp::NVM, BOp::NDS>();
+    wait_vm_lgkm_barrier<BOp::NVM>();
+  };
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    step(kt, buf0, buf1, rb1, rb0);
+    step(kt + 1, buf1, buf0, rb0, rb1);
+  }
+  if (kt + 1 < nk) {
+    step(kt, buf0, buf1, rb1, rb0);
+    ++kt;
+  }
+  compute_stage<T, Math, 4>((kt & 1) ? buf1 : buf0, aaddr, baddr, acc);
 }
 
 }  // namespace mp

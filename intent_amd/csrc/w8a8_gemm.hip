@@ -20,7 +20,7 @@ enum class Epi { kBf16Scaled, kI32Bias };
 
 // One workgroup per output tile; 128 k per LDS stage, the last one possibly 64.
 template <class T, Epi E, bool kHalf>
-__global__ __launch_bounds__(mp::NTHREADS, 1) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t lda, int M,
+__global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t lda, int M,
                                                                 const int8_t* __restrict__ w, int64_t ldw, int N,
                                                                 int K, const float* __restrict__ a_scales,
                                                                 const float* __restrict__ w_scales,
@@ -34,8 +34,8 @@ __global__ __launch_bounds__(mp::NTHREADS, 1) void i8_gemm_kernel(const int8_t* 
   const int wave = T::wave();
   const int nk = (K + mp::ROWB - 1) / mp::ROWB;
   const bool half = kHalf;
-  mp::RegRowsOperand<T::BM, mp::DenseRows, kHalf> aop;
-  mp::RegRowsOperand<T::BN, mp::DenseRows, kHalf> bop;
+  mp::RegRowsOperand<T::BM, mp::DenseRows, kHalf, T::NW> aop;
+  mp::RegRowsOperand<T::BN, mp::DenseRows, kHalf, T::NW> bop;
   aop.init(mp::DenseRows{a, lda, M}, m0, wave, half ? nk - 1 : -1);
   bop.init(mp::DenseRows{w, ldw, N}, n0, wave, half ? nk - 1 : -1);
   i32x16 acc[T::TI][T::TJ];
@@ -103,10 +103,10 @@ int launch_tile(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const float
   INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, w_ld), INTENT_ERR_UNSUPPORTED,
                  "%s: operand too large for 31-bit buffer offsets", name);
   if (K % mp::ROWB == 0)
-    hipLaunchKernelGGL((i8_gemm_kernel<T, E, false>), dim3((unsigned)grid), dim3(mp::NTHREADS), 0,
+    hipLaunchKernelGGL((i8_gemm_kernel<T, E, false>), dim3((unsigned)grid), dim3(T::NT), 0,
                        (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
   else
-    hipLaunchKernelGGL((i8_gemm_kernel<T, E, true>), dim3((unsigned)grid), dim3(mp::NTHREADS), 0,
+    hipLaunchKernelGGL((i8_gemm_kernel<T, E, true>), dim3((unsigned)grid), dim3(T::NT), 0,
                        (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, sa, sw, bias, out, out_ld, mblocks);
   return intent::launch_status(name);
 }
