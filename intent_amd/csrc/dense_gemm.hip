@@ -34,7 +34,7 @@ template <class T, class WArgs>
 struct WeightOp;
 template <class T>
 struct WeightOp<T, W4Args> {
-  using Op = mp::W4Operand<T::BN, T::NT>;
+  using Op = mp::W4Operand<T::BN, T::NT>;  // staged by the NT producer threads
   INTENT_DEVICE static void init(Op& op, const W4Args& w, int n0, int N) {
     op.init(w.q, w.ldq, w.s, w.z, w.ldp, w.gs, ClampRows{n0, N});
   }
@@ -47,7 +47,7 @@ struct WeightOp<T, W8Args> {
 
 // y[m, n] = f16(sum_k x[m, k] * deq(W)[n, k] (* colscale[n])).
 template <class T, class WArgs, bool kColScale>
-__global__ __launch_bounds__(T::NT, 1) void dense_gemm_kernel(const f16* __restrict__ x, int64_t ldx, int M,
+__global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __restrict__ x, int64_t ldx, int M,
                                                                    WArgs w, int N, int K, f16* __restrict__ y,
                                                                    int64_t ldy, const f16* __restrict__ colscale,
                                                                    int mblocks) {
@@ -60,8 +60,8 @@ __global__ __launch_bounds__(T::NT, 1) void dense_gemm_kernel(const f16* __restr
   WeightOp<T, WArgs>::init(bop, w, n0, N);
   f32x16 acc[T::TI][T::TJ];
   mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
-  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave());
-  mp::mainloop_dma_a<T, mp::F16Math>(aop, bop, K / 64, buf0, buf1, acc);
+  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave() % T::NW);
+  if (!mp::mainloop_ws<T, mp::F16Math>(aop, bop, K / 64, buf0, buf1, acc)) return;
 
   // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
   const bool vec = (ldy & 3) == 0 && (((uintptr_t)y) & 7) == 0;
@@ -106,22 +106,21 @@ int launch_tile(const f16* x, int64_t ldx, int M, int N, int K, const WArgs& w, 
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
   INTENT_REQUIRE(intent::fits_offset(M, ldx * 2), INTENT_ERR_UNSUPPORTED,
                  "%s: activations too large for 31-bit buffer offsets", name);
-  hipLaunchKernelGGL((dense_gemm_kernel<T, WArgs, kColScale>), dim3((unsigned)grid), dim3(T::NT), 0, st, x, ldx,
+  hipLaunchKernelGGL((dense_gemm_kernel<T, WArgs, kColScale>), dim3((unsigned)grid), dim3(T::NT_WS), 0, st, x, ldx,
                      M, w, N, K, y, ldy, colscale, mblocks);
   return intent::launch_status(name);
 }
 
-// Tiles: 256 x 192 with 8 waves (64 x 96 each, two waves per SIMD so that one
-// wave's weight decode overlaps the other's MFMAs) once M fills it, else
-// 128 x 128 with 4 waves. 192 columns: N = 11008 gives 58 column tiles; with
-// 8 row tiles that is 464 workgroups, 1.8 rounds of 256 CUs (256-wide tiles
-// would give 344, 1.34). Activations go global -> LDS by DMA, weights through
-// VGPRs with the decode.
+// Tiles: 256 x 192 (4 consumer waves of 128 x 96) once M fills it, else
+// 128 x 128 (consumers of 64 x 64); each with 4 producer waves that copy the
+// activations by LDS DMA and decode the weights (mainloop_ws). 192 columns:
+// N = 11008 gives 58 column tiles; with 8 row tiles that is 464 workgroups,
+// 1.8 rounds of 256 CUs (256-wide tiles would give 344, 1.34).
 template <class WArgs, bool kColScale>
 int launch_dense(const f16* x, int64_t ldx, int M, int N, int K, const WArgs& w, f16* y, int64_t ldy,
                  const f16* colscale, hipStream_t st, const char* name) {
   if (M > 128)
-    return launch_tile<mp::Tile<256, 192, 4, 2>, WArgs, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
+    return launch_tile<mp::Tile<256, 192, 2, 2>, WArgs, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
   return launch_tile<mp::Tile<128, 128, 2, 2>, WArgs, kColScale>(x, ldx, M, N, K, w, y, ldy, colscale, st, name);
 }
 

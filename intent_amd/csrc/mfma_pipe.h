@@ -70,6 +70,9 @@ struct Tile {
   static constexpr int NW = WM * WN;  // waves: 4 (one per SIMD) or 8 (two per SIMD)
   static constexpr int NT = NW * 64;
   static_assert(NW == 4 || NW == 8, "four or eight waves");
+  // Producer/consumer workgroups (mainloop_ws): NW consumer waves plus NW
+  // producer waves, one of each per SIMD.
+  static constexpr int NT_WS = 2 * NT;
   static constexpr int WTM = BM / WM;
   static constexpr int WTN = BN / WN;
   static constexpr int TI = WTM / 32;
@@ -236,7 +239,7 @@ struct W4Operand {
     gs = gsize;
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const int c = threadIdx.x + i * NT;
+      const int c = (int)(threadIdx.x % NT) + i * NT;
       lrow[i] = c / P;
       part[i] = c % P;
       const int64_t w = wrow(lrow[i]);
@@ -301,7 +304,7 @@ struct W8Operand {
     rq = make_rsrc(q);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const int c = threadIdx.x + i * NT;
+      const int c = (int)(threadIdx.x % NT) + i * NT;
       lrow[i] = c / P;
       part[i] = c % P;
       qoff[i] = (uint32_t)((int64_t)wrow(lrow[i]) * ldq + part[i] * PIECE);
@@ -493,12 +496,58 @@ INTENT_DEVICE void mainloop(const AOp& aop, const BOp& bop, int nk, char* buf0, 
     compute_stage<T, Math, 4>(last, aaddr, baddr, acc);
 }
 
-// Variant with the A operand copied by DMA one stage ahead (B through VGPRs,
-// two stages ahead). At the loop header no DMA is in flight: the DMA of a
-// step is older than its B loads, so the step-end vmcnt wait retires it.
-template <class T, class Math, int NWA, class Rows, class BOp>
-INTENT_DEVICE void mainloop_dma_a(const DmaRowsOperand<T::BM, Rows, NWA>& aop, const BOp& bop, int nk, char* buf0,
-                                  char* buf1, typename Math::Acc (&acc)[T::TI][T::TJ]) {
+// Producer/consumer variant. Waves 0..NW-1 (consumers) only read fragments
+// and issue MFMAs; waves NW..2NW-1 (producers, one per SIMD beside a
+// consumer) issue the A DMA one stage ahead, load the weights two stages
+// ahead and decode them into LDS. A wave's MFMAs do not co-issue with its own
+// VALU decode, but they do with the other wave of the SIMD. Both roles meet at
+// one barrier per stage. Operands must be built with NT = T::NT (producer
+// thread index = threadIdx.x % NT) and the producer wave index. Returns true
+// in consumer waves, which then hold acc.
+template <class T, class Math, class Rows, class BOp>
+INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, const BOp& bop, int nk, char* buf0,
+                               char* buf1, typename Math::Acc (&acc)[T::TI][T::TJ]) {
+  const bool consumer = T::wave() < T::NW;
+  if (nk <= 0) {
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+    return consumer;
+  }
+  if (!consumer) {
+    typename BOp::Regs rb0, rb1;
+    bop.load(0, rb0);
+    if (nk > 1) bop.load(1, rb1);
+    aop.issue(buf0, 0);
+    bop.store(rb0, buf0 + T::A_BYTES);
+    wait_vm_lgkm_barrier<0>();
+    // The barrier that ends a step must see this step's DMA complete. vmcnt
+    // counts in issue order, so the DMA is pinned ahead of the weight loads
+    // (sched_barrier) and the wait leaves exactly those NVM loads in flight.
+    // The loop's clamped loads are always live (the next step or the tail
+    // consumes them); the tail step issues none and waits for everything.
+    auto step = [&](int kt, char* nxt, typename BOp::Regs& rbn, typename BOp::Regs& rbf) {
+      aop.issue(nxt, kt + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      bop.load(kt + 2 < nk ? kt + 2 : nk - 1, rbf);
+      bop.store(rbn, nxt + T::A_BYTES);
+      wait_vm_lgkm_barrier<BOp::NVM>();
+    };
+    int kt = 0;
+    for (; kt + 2 < nk; kt += 2) {
+      step(kt, buf1, rb1, rb0);
+      step(kt + 1, buf0, rb0, rb1);
+    }
+    if (kt + 1 < nk) {
+      aop.issue(buf1, kt + 1);
+      bop.store(rb1, buf1 + T::A_BYTES);
+      wait_vm_lgkm_barrier<0>();
+    }
+    return false;
+  }
   const int lane = threadIdx.x & 63;
   uint32_t aaddr[4], baddr[4];
   {
@@ -517,33 +566,21 @@ INTENT_DEVICE void mainloop_dma_a(const DmaRowsOperand<T::BM, Rows, NWA>& aop, c
     for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
-  if (nk <= 0) return;
-  using ADma = DmaRowsOperand<T::BM, Rows, NWA>;
-  typename BOp::Regs rb0, rb1;
-  bop.load(0, rb0);
-  if (nk > 1) bop.load(1, rb1);
-  aop.issue(buf0, 0);
-  bop.store(rb0, buf0 + T::A_BYTES);
   wait_vm_lgkm_barrier<0>();
-  auto step = [&](int kt, char* cur, char* nxt, typename BOp::Regs& rbn, typename BOp::Regs& rbf) {
-    aop.issue(nxt, kt + 1);
-    const int kn = kt + 2 < nk ? kt + 2 : nk - 1;
-    bop.load(kn, rbf);
-    compute_stage<T, Math, 4, false>(cur, aaddr, baddr, acc);
-    bop.store(rbn, nxt + T::A_BYTES);
-    sched_step<T::TI * T::TJ, T::TI + T::TJ, ADma::NVM + BOp::NVM, BOp::NDS>();
-    wait_vm_lgkm_barrier<BOp::NVM>();
-  };
   int kt = 0;
   for (; kt + 2 < nk; kt += 2) {
-    step(kt, buf0, buf1, rb1, rb0);
-    step(kt + 1, buf1, buf0, rb0, rb1);
+    compute_stage<T, Math>(buf0, aaddr, baddr, acc);
+    wait_vm_lgkm_barrier<0>();
+    compute_stage<T, Math>(buf1, aaddr, baddr, acc);
+    wait_vm_lgkm_barrier<0>();
   }
   if (kt + 1 < nk) {
-    step(kt, buf0, buf1, rb1, rb0);
+    compute_stage<T, Math>(buf0, aaddr, baddr, acc);
+    wait_vm_lgkm_barrier<0>();
     ++kt;
   }
-  compute_stage<T, Math, 4>((kt & 1) ? buf1 : buf0, aaddr, baddr, acc);
+  compute_stage<T, Math>((kt & 1) ? buf1 : buf0, aaddr, baddr, acc);
+  return true;
 }
 
 }  // namespace mp

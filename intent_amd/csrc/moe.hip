@@ -3,28 +3,10 @@
 #include <math.h>
 
 #include "common.h"
-#include "gemm_f16.h"
 #include "internal.h"
+#include "mfma_pipe.h"
 
 namespace {
-
-using namespace gemm;
-
-// Grouped-projection tiles per alignment block size B (one M tile = one
-// expert block). gate/up tiles hold 256 weight rows = 128 output features;
-// down tiles 128 output columns.
-template <int B>
-struct MoeTiles;
-template <>
-struct MoeTiles<128> {
-  using GateUp = Tile<128, 256, 2, 2>;  // waves of 64 x 128
-  using Down = Tile<128, 128, 2, 2>;    // waves of 64 x 64
-};
-template <>
-struct MoeTiles<64> {
-  using GateUp = Tile<64, 256, 1, 4>;  // waves of 64 x 64
-  using Down = Tile<64, 128, 1, 2>;    // waves of 64 x 64
-};
 
 constexpr int kMaxTopK = 8;
 constexpr int kMaxRouteExperts = 256;
@@ -157,23 +139,43 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t*
 }
 
 // ---- grouped projections ------------------------------------------------------
+// Tile GEMMs on the pipelined core (mfma_pipe.h) over 128- or 64-row blocks
+// of the aligned route order; the block's expert comes from the block map
+// and selects the weight base pointers. Token rows reach LDS by DMA through
+// the route ids; weights go through VGPRs with the W4 decode.
 
-// B-tile row c of a gate/up tile. Each wave owns BN/WN consecutive rows in
-// groups of 64: 32 gate rows then the 32 up rows of the same features, so
-// MFMA tiles 2p and 2p+1 of a lane hold gate and up of one output element.
+// Tiles per alignment block size B: gate/up covers 256 weight rows (128
+// features, gate and up), down 128 output columns. Producer/consumer
+// workgroups (mainloop_ws): 4 consumer waves + 4 producer waves.
+template <int B>
+struct MoeTiles;
+template <>
+struct MoeTiles<128> {
+  using GateUp = mp::Tile<128, 256, 2, 2>;  // consumers of 64 x 128
+  using Down = mp::Tile<128, 128, 2, 2>;    // consumers of 64 x 64
+};
+template <>
+struct MoeTiles<64> {
+  using GateUp = mp::Tile<64, 256, 2, 2>;  // consumers of 32 x 128
+  using Down = mp::Tile<64, 128, 2, 2>;    // consumers of 32 x 64
+};
+
+// B-tile row c of a gate/up tile. Wave column block w (BN/WN rows) holds
+// WTN/2 gate rows then the WTN/2 up rows of the same features, so a lane's
+// accumulators j and j + TJ/2 hold gate and up of one output element.
 // Features past F read row F-1 and are never stored.
 template <class T>
 struct GateUpRowMap {
   int f0;
   int F;
-  static constexpr int kWaveRows = T::BN / T::WN;
-  INTENT_DEVICE static int feature_offset(int w, int p) { return w * (kWaveRows / 2) + p * 32; }
+  static constexpr int kHalf = T::WTN / 2;
+  INTENT_DEVICE static int feature(int w, int u) { return w * kHalf + u; }
   INTENT_DEVICE int operator()(int c) const {
-    const int w = c / kWaveRows;
-    const int u = c % kWaveRows;
-    int f = f0 + feature_offset(w, u >> 6) + (u & 31);
+    const int w = c / T::WTN;
+    const int u = c % T::WTN;
+    int f = f0 + feature(w, u % kHalf);
     f = f < F ? f : F - 1;
-    return ((u >> 5) & 1) ? F + f : f;
+    return u >= kHalf ? F + f : f;
   }
 };
 
@@ -187,75 +189,108 @@ struct ClampRows {
 };
 
 template <int B>
-__global__ __launch_bounds__(MoeTiles<B>::GateUp::NT, 2) void moe_gate_up_kernel(
+__global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_kernel(
     const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ blocks, int mblocks, int R, int top_k, const uint8_t* __restrict__ wq,
     const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int F, int gs, f16* __restrict__ act,
     int64_t ld_act) {
   using T = typename MoeTiles<B>::GateUp;
-  __shared__ typename T::Shared tile;
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   const int mb = blockIdx.x % mblocks;
   const int f0 = (blockIdx.x / mblocks) * (T::BN / 2);
   const int e = blocks[mb];
   if (e < 0) return;
   const int64_t ldq = H / 2;
   const int64_t ldp = H / gs;
-  W4Source w{wq + (int64_t)e * 2 * F * ldq, ldq, ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs};
   const int m0 = mb * B;
+  mp::DmaRowsOperand<T::BM, mp::GatherRows, T::NW> aop;
+  aop.init(mp::GatherRows{x, ldx * 2, sorted, R, top_k}, m0, T::wave() % T::NW);
+  mp::W4Operand<T::BN, T::NT> bop;
+  bop.init(wq + (int64_t)e * 2 * F * ldq, ldq, ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs,
+           GateUpRowMap<T>{f0, F});
   f32x16 acc[T::TI][T::TJ];
-  mainloop<T>(GatherRows{x, ldx, sorted, R, top_k}, m0, w, GateUpRowMap<T>{f0, F}, H, tile, acc);
-  const int lane = threadIdx.x & 63;
+  if (!mp::mainloop_ws<T, mp::F16Math>(aop, bop, H / 64, buf0, buf1, acc)) return;
+
+  // acc[i][j][4g + c]: row(i), feature f0 + feature(wave_n, j*32 + g*8 + h*4 + c).
+  const bool vec = (ld_act & 3) == 0 && (F & 3) == 0;
 #pragma unroll
-  for (int p = 0; p < T::TJ / 2; ++p) {
-    const int f = f0 + GateUpRowMap<T>::feature_offset(T::wave_n(), p) + (lane & 31);
-    if (f >= F) continue;
+  for (int i = 0; i < T::TI; ++i) {
+    const int row = m0 + T::row(i);
+    const int r = sorted[row];
+    const bool valid = r >= 0 && r < R;
 #pragma unroll
-    for (int i = 0; i < T::TI; ++i)
+    for (int j = 0; j < T::TJ / 2; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + T::acc_row(i, v);
-        const int r = sorted[row];
-        f16 out = (f16)0.f;
-        if (r >= 0 && r < R) {
-          const float g = acc[i][2 * p][v];
-          const float u = acc[i][2 * p + 1][v];
-          const float silu = g / (1.0f + expf(-g));
-          out = (f16)(silu * u);
+      for (int g = 0; g < 4; ++g) {
+        const int f = f0 + GateUpRowMap<T>::feature(T::wave_n(), T::col(j, g) - T::wave_n() * T::WTN);
+        f16 o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float gt = acc[i][j][4 * g + c];
+          const float up = acc[i][j + T::TJ / 2][4 * g + c];
+          o[c] = valid ? (f16)((gt / (1.0f + expf(-gt))) * up) : (f16)0.f;
         }
-        act[(int64_t)row * ld_act + f] = out;
+        f16* dst = act + (int64_t)row * ld_act + f;
+        if (vec && f + 3 < F) {
+          f16x2 lo, hi;
+          lo[0] = o[0];
+          lo[1] = o[1];
+          hi[0] = o[2];
+          hi[1] = o[3];
+          *reinterpret_cast<u32x2*>(dst) = u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (f + c < F) dst[c] = o[c];
+        }
       }
   }
 }
 
 // Down projection: grid = mblocks x ntiles; fp32 rows scattered to routes.
 template <int B>
-__global__ __launch_bounds__(MoeTiles<B>::Down::NT, 2) void moe_down_kernel(
+__global__ __launch_bounds__(MoeTiles<B>::Down::NT_WS, 1) void moe_down_kernel(
     const f16* __restrict__ act, int64_t ld_act, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ blocks, int mblocks, int ntiles, int R, const uint8_t* __restrict__ wq,
     const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int H, int F, int gs, float* __restrict__ out,
     int64_t ldo) {
   using T = typename MoeTiles<B>::Down;
-  __shared__ typename T::Shared tile;
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   const int mb = blockIdx.x % mblocks;
   const int n0 = (blockIdx.x / mblocks) * T::BN;
   const int e = blocks[mb];
   if (e < 0) return;
   const int64_t ldq = F / 2;
   const int64_t ldp = F / gs;
-  W4Source w{wq + (int64_t)e * H * ldq, ldq, ws + (int64_t)e * H * ldp, wz + (int64_t)e * H * ldp, ldp, gs};
   const int m0 = mb * B;
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{act, ld_act * 2, m0 + T::BM}, m0, T::wave() % T::NW);
+  mp::W4Operand<T::BN, T::NT> bop;
+  bop.init(wq + (int64_t)e * H * ldq, ldq, ws + (int64_t)e * H * ldp, wz + (int64_t)e * H * ldp, ldp, gs,
+           ClampRows{n0, H});
   f32x16 acc[T::TI][T::TJ];
-  mainloop<T>(PaddedRows{act, ld_act}, m0, w, ClampRows{n0, H}, F, tile, acc);
+  if (!mp::mainloop_ws<T, mp::F16Math>(aop, bop, F / 64, buf0, buf1, acc)) return;
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
 #pragma unroll
-  for (int j = 0; j < T::TJ; ++j) {
-    const int col = n0 + T::acc_col(j);
-    if (col >= H) continue;
+  for (int i = 0; i < T::TI; ++i) {
+    const int r = sorted[m0 + T::row(i)];
+    if (r < 0 || r >= R) continue;
 #pragma unroll
-    for (int i = 0; i < T::TI; ++i)
+    for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = sorted[m0 + T::acc_row(i, v)];
-        if (r >= 0 && r < R) out[(int64_t)r * ldo + col] = acc[i][j][v];
+      for (int g = 0; g < 4; ++g) {
+        const int col = n0 + T::col(j, g);
+        float* dst = out + (int64_t)r * ldo + col;
+        if (vec && col + 3 < H) {
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (col + c < H) dst[c] = acc[i][j][4 * g + c];
+        }
       }
   }
 }
@@ -333,7 +368,7 @@ int gate_up_launch(const void* x, int64_t T, int64_t H, int64_t x_ld, const int3
   const int64_t ftile = Tl::BN / 2;
   const int64_t grid = num_blocks * ((F + ftile - 1) / ftile);
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL((moe_gate_up_kernel<B>), dim3((unsigned)grid), dim3(Tl::NT), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL((moe_gate_up_kernel<B>), dim3((unsigned)grid), dim3(Tl::NT_WS), 0, (hipStream_t)stream,
                      (const f16*)x, x_ld, (int)H, sorted, blocks, (int)num_blocks, (int)(T * top_k), (int)top_k, wq,
                      (const f16*)ws, wz, (int)F, (int)gs, (f16*)act, act_ld);
   return intent::launch_status("moe_gate_up_w4");
@@ -347,7 +382,7 @@ int down_launch(const void* act, int64_t act_ld, const int32_t* sorted, const in
   const int64_t ntiles = (H + Tl::BN - 1) / Tl::BN;
   const int64_t grid = num_blocks * ntiles;
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL((moe_down_kernel<B>), dim3((unsigned)grid), dim3(Tl::NT), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL((moe_down_kernel<B>), dim3((unsigned)grid), dim3(Tl::NT_WS), 0, (hipStream_t)stream,
                      (const f16*)act, act_ld, sorted, blocks, (int)num_blocks, (int)ntiles, (int)R, wq,
                      (const f16*)ws, wz, (int)H, (int)F, (int)gs, out, out_ld);
   return intent::launch_status("moe_down_w4");

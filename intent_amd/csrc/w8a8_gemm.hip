@@ -1,19 +1,16 @@
 // W8A8 int8 GEMM on v_mfma_i32_32x32x32_i8 (gfx950), exact int32 accumulation.
 //
-// Tiles of 256 x 256 (or 128 x 128 for small problems), 4 waves in 2 x 2, on
-// the pipelined core in mfma_pipe.h: both K-contiguous int8 operands are
+// Tiles of 256 x 256 with 8 waves in 4 x 2 (or 128 x 128 with 4 waves for
+// small problems) on the pipelined core in mfma_pipe.h: both K-contiguous int8 operands are
 // staged global -> VGPR -> LDS, 128 k per stage, two stages in flight.
 // Epilogues: bf16(f32(acc) * a_scale[m] * w_scale[n]) or int32 acc + bias[n].
 #include "common.h"
 #include "internal.h"
 #include "mfma_pipe.h"
 
-#ifndef KROT
-#define KROT 0
-#endif
 namespace {
 
-using T256 = mp::Tile<256, 256, 2, 2>;  // 128 x 128 per wave: 16 MFMA tiles of 32 x 32
+using T256 = mp::Tile<256, 256, 4, 2>;  // 8 waves of 64 x 128 (two per SIMD)
 using T128 = mp::Tile<128, 128, 2, 2>;  // small problems: more workgroups
 
 enum class Epi { kBf16Scaled, kI32Bias };
@@ -34,12 +31,12 @@ __global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restr
   const int wave = T::wave();
   const int nk = (K + mp::ROWB - 1) / mp::ROWB;
   const bool half = kHalf;
-  mp::RegRowsOperand<T::BM, mp::DenseRows, kHalf, T::NW> aop;
   mp::RegRowsOperand<T::BN, mp::DenseRows, kHalf, T::NW> bop;
-  aop.init(mp::DenseRows{a, lda, M}, m0, wave, half ? nk - 1 : -1);
   bop.init(mp::DenseRows{w, ldw, N}, n0, wave, half ? nk - 1 : -1);
   i32x16 acc[T::TI][T::TJ];
-  mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc, half, KROT);
+  mp::RegRowsOperand<T::BM, mp::DenseRows, kHalf, T::NW> aop;
+  aop.init(mp::DenseRows{a, lda, M}, m0, wave, half ? nk - 1 : -1);
+  mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc, half);
 
   // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
   const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
