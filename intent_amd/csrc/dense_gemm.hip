@@ -53,6 +53,7 @@ __global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __re
                                                                    int mblocks) {
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  char* const bufs[2] = {buf0, buf1};
   const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
   const int m0 = (bid % mblocks) * T::BM;
   const int n0 = (bid / mblocks) * T::BN;
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __re
   f32x16 acc[T::TI][T::TJ];
   mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
   aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave() % T::NW);
-  if (!mp::mainloop_ws<T, mp::F16Math>(aop, bop, K / 64, buf0, buf1, acc)) return;
+  if (!mp::mainloop_ws<T, mp::F16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
 
   // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
   const bool vec = (ldy & 3) == 0 && (((uintptr_t)y) & 7) == 0;

@@ -61,6 +61,16 @@ INTENT_DEVICE void wait_vm_lgkm_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
+// ds_write_b128 that the compiler does not see as an LDS access. Producer
+// waves write decoded weights into a stage buffer while LDS DMAs into other
+// buffers are in flight; a visible LDS store there would make the compiler's
+// wait-count pass wait for those DMAs. The caller waits lgkmcnt before the
+// barrier that publishes the stage.
+INTENT_DEVICE void lds_store16(char* p, u32x4 v) {
+  const uint32_t a = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)p;
+  asm volatile("ds_write_b128 %0, %1" : : "v"(a), "v"(v) : "memory");
+}
+
 template <int BM_, int BN_, int WM_, int WN_>
 struct Tile {
   static constexpr int BM = BM_;
@@ -264,7 +274,8 @@ struct W4Operand {
       r.z[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rz, zoff[i], g, 0);
     }
   }
-  // Decode into the B region of a stage buffer.
+  // Decode into the B region of a stage buffer (kAsm: see lds_store16).
+  template <bool kAsm = false>
   INTENT_DEVICE void store(const Regs& r, char* lds_b) const {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
@@ -275,7 +286,11 @@ struct W4Operand {
 #pragma unroll
       for (int d = 0; d < PIECE / 4; ++d) {
         const int chunk = part[i] * (PIECE / 4) + d;  // each dword = 8 k = one 16-byte f16 chunk
-        *reinterpret_cast<f16x8*>(row + ((chunk ^ sw) << 4)) = dequant8(r.w[i][d], zo, sc);
+        const f16x8 v = dequant8(r.w[i][d], zo, sc);
+        if constexpr (kAsm)
+          lds_store16(row + ((chunk ^ sw) << 4), bit_cast<u32x4>(v));
+        else
+          *reinterpret_cast<f16x8*>(row + ((chunk ^ sw) << 4)) = v;
       }
     }
   }
@@ -321,15 +336,25 @@ struct W8Operand {
       }
     }
   }
+  template <bool kAsm = false>
   INTENT_DEVICE void store(const Regs& r, char* lds_b) const {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       char* row = lds_b + lrow[i] * ROWB;
       const int sw = swz(lrow[i]);
       const int c0 = part[i] * (PIECE / 8);
-      *reinterpret_cast<f16x8*>(row + ((c0 ^ sw) << 4)) = int8x8_to_f16(r.w[i][0], r.w[i][1]);
-      if constexpr (PIECE == 16)
-        *reinterpret_cast<f16x8*>(row + (((c0 + 1) ^ sw) << 4)) = int8x8_to_f16(r.w[i][2], r.w[i][3]);
+      const f16x8 v0 = int8x8_to_f16(r.w[i][0], r.w[i][1]);
+      if constexpr (kAsm)
+        lds_store16(row + ((c0 ^ sw) << 4), bit_cast<u32x4>(v0));
+      else
+        *reinterpret_cast<f16x8*>(row + ((c0 ^ sw) << 4)) = v0;
+      if constexpr (PIECE == 16) {
+        const f16x8 v1 = int8x8_to_f16(r.w[i][2], r.w[i][3]);
+        if constexpr (kAsm)
+          lds_store16(row + (((c0 + 1) ^ sw) << 4), bit_cast<u32x4>(v1));
+        else
+          *reinterpret_cast<f16x8*>(row + (((c0 + 1) ^ sw) << 4)) = v1;
+      }
     }
   }
 };
@@ -498,53 +523,63 @@ INTENT_DEVICE void mainloop(const AOp& aop, const BOp& bop, int nk, char* buf0, 
 
 // Producer/consumer variant. Waves 0..NW-1 (consumers) only read fragments
 // and issue MFMAs; waves NW..2NW-1 (producers, one per SIMD beside a
-// consumer) issue the A DMA one stage ahead, load the weights two stages
-// ahead and decode them into LDS. A wave's MFMAs do not co-issue with its own
-// VALU decode, but they do with the other wave of the SIMD. Both roles meet at
-// one barrier per stage. Operands must be built with NT = T::NT (producer
-// thread index = threadIdx.x % NT) and the producer wave index. Returns true
-// in consumer waves, which then hold acc.
-template <class T, class Math, class Rows, class BOp>
-INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, const BOp& bop, int nk, char* buf0,
-                               char* buf1, typename Math::Acc (&acc)[T::TI][T::TJ]) {
+// consumer) copy the A rows by LDS DMA NB-1 stages ahead, load the weights NB
+// stages ahead into a ring of NB register sets and decode them into LDS one
+// stage ahead. A wave's MFMAs do not co-issue with its own VALU decode, but
+// they do with the other wave of the SIMD. Both roles meet at one barrier per
+// stage. bufs: NB stage buffers (distinct __shared__ objects, STAGE_BYTES
+// each). Operands must be built with NT = T::NT (producer thread index =
+// threadIdx.x % NT) and the producer wave index. Returns true in consumer
+// waves, which then hold acc.
+template <class T, class Math, int NB, class Rows, class BOp>
+INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, const BOp& bop, int nk,
+                               char* const (&bufs)[NB], typename Math::Acc (&acc)[T::TI][T::TJ]) {
+  static_assert(NB == 2 || NB == 3, "two or three stage buffers");
+  using ADma = DmaRowsOperand<T::BM, Rows, T::NW>;
   const bool consumer = T::wave() < T::NW;
-  if (nk <= 0) {
 #pragma unroll
-    for (int i = 0; i < T::TI; ++i)
+  for (int i = 0; i < T::TI; ++i)
 #pragma unroll
-      for (int j = 0; j < T::TJ; ++j)
+    for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
-    return consumer;
-  }
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+  if (nk <= 0) return consumer;
   if (!consumer) {
-    typename BOp::Regs rb0, rb1;
-    bop.load(0, rb0);
-    if (nk > 1) bop.load(1, rb1);
-    aop.issue(buf0, 0);
-    bop.store(rb0, buf0 + T::A_BYTES);
+    typename BOp::Regs rb[NB];
+#pragma unroll
+    for (int s = 0; s < NB - 1; ++s)
+      if (s < nk) aop.issue(bufs[s], s);
+#pragma unroll
+    for (int s = 0; s < NB; ++s)
+      if (s < nk) bop.load(s, rb[s]);
+    bop.template store<true>(rb[0], bufs[0] + T::A_BYTES);
     wait_vm_lgkm_barrier<0>();
-    // The barrier that ends a step must see this step's DMA complete. vmcnt
-    // counts in issue order, so the DMA is pinned ahead of the weight loads
-    // (sched_barrier) and the wait leaves exactly those NVM loads in flight.
-    // The loop's clamped loads are always live (the next step or the tail
-    // consumes them); the tail step issues none and waits for everything.
-    auto step = [&](int kt, char* nxt, typename BOp::Regs& rbn, typename BOp::Regs& rbf) {
-      aop.issue(nxt, kt + 1);
+    // Step kt publishes stage kt+1. Its DMA was issued NB-2 steps earlier;
+    // vmcnt counts in issue order, so the wait leaves exactly the operations
+    // issued after it in flight (sched_barrier pins the DMA ahead of the
+    // loads). Near the end some are skipped and the wait drains everything.
+    // The DMA and the loads are unconditional, with stage indices clamped to
+    // the last stage (a conditional load would make the compiler wait for it
+    // where the paths join); near the end the extra copies land in buffers
+    // and registers that nobody reads any more, and those steps drain.
+    constexpr int kAfter = (NB - 2) * (ADma::NVM + BOp::NVM) + BOp::NVM;
+    auto step = [&](auto J, int kt) {
+      constexpr int j = decltype(J)::value;  // kt % NB
+      const bool full = kt + NB < nk;
+      aop.issue(bufs[(j + NB - 1) % NB], kt + NB - 1 < nk ? kt + NB - 1 : nk - 1);
       __builtin_amdgcn_sched_barrier(0);
-      bop.load(kt + 2 < nk ? kt + 2 : nk - 1, rbf);
-      bop.store(rbn, nxt + T::A_BYTES);
-      wait_vm_lgkm_barrier<BOp::NVM>();
+      bop.load(full ? kt + NB : nk - 1, rb[j]);
+      bop.template store<true>(rb[(j + 1) % NB], bufs[(j + 1) % NB] + T::A_BYTES);
+      if (full)
+        wait_vm_lgkm_barrier<kAfter>();
+      else
+        wait_vm_lgkm_barrier<0>();
     };
-    int kt = 0;
-    for (; kt + 2 < nk; kt += 2) {
-      step(kt, buf1, rb1, rb0);
-      step(kt + 1, buf0, rb0, rb1);
-    }
-    if (kt + 1 < nk) {
-      aop.issue(buf1, kt + 1);
-      bop.store(rb1, buf1 + T::A_BYTES);
-      wait_vm_lgkm_barrier<0>();
+    for (int kt = 0; kt < nk - 1; kt += NB) {
+      step(std::integral_constant<int, 0>{}, kt);
+      if (kt + 1 < nk - 1) step(std::integral_constant<int, 1>{}, kt + 1);
+      if constexpr (NB > 2)
+        if (kt + 2 < nk - 1) step(std::integral_constant<int, 2 % NB>{}, kt + 2);
     }
     return false;
   }
@@ -560,26 +595,16 @@ INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, co
       baddr[kk] = (uint32_t)((T::wave_n() * T::WTN + r) * ROWB) + s;
     }
   }
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i)
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
   wait_vm_lgkm_barrier<0>();
-  int kt = 0;
-  for (; kt + 2 < nk; kt += 2) {
-    compute_stage<T, Math>(buf0, aaddr, baddr, acc);
-    wait_vm_lgkm_barrier<0>();
-    compute_stage<T, Math>(buf1, aaddr, baddr, acc);
-    wait_vm_lgkm_barrier<0>();
+  for (int kt = 0; kt < nk; kt += NB) {
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      if (kt + j < nk) {
+        compute_stage<T, Math>(bufs[j], aaddr, baddr, acc);
+        if (kt + j < nk - 1) wait_vm_lgkm_barrier<0>();
+      }
+    }
   }
-  if (kt + 1 < nk) {
-    compute_stage<T, Math>(buf0, aaddr, baddr, acc);
-    wait_vm_lgkm_barrier<0>();
-    ++kt;
-  }
-  compute_stage<T, Math>((kt & 1) ? buf1 : buf0, aaddr, baddr, acc);
   return true;
 }
 

@@ -197,6 +197,8 @@ __global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_ker
   using T = typename MoeTiles<B>::GateUp;
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf2[T::STAGE_BYTES];
+  char* const bufs[3] = {buf0, buf1, buf2};
   const int mb = blockIdx.x % mblocks;
   const int f0 = (blockIdx.x / mblocks) * (T::BN / 2);
   const int e = blocks[mb];
@@ -210,7 +212,7 @@ __global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_ker
   bop.init(wq + (int64_t)e * 2 * F * ldq, ldq, ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs,
            GateUpRowMap<T>{f0, F});
   f32x16 acc[T::TI][T::TJ];
-  if (!mp::mainloop_ws<T, mp::F16Math>(aop, bop, H / 64, buf0, buf1, acc)) return;
+  if (!mp::mainloop_ws<T, mp::F16Math, 3>(aop, bop, H / 64, bufs, acc)) return;
 
   // acc[i][j][4g + c]: row(i), feature f0 + feature(wave_n, j*32 + g*8 + h*4 + c).
   const bool vec = (ld_act & 3) == 0 && (F & 3) == 0;
@@ -258,6 +260,8 @@ __global__ __launch_bounds__(MoeTiles<B>::Down::NT_WS, 1) void moe_down_kernel(
   using T = typename MoeTiles<B>::Down;
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf2[T::STAGE_BYTES];
+  char* const bufs[3] = {buf0, buf1, buf2};
   const int mb = blockIdx.x % mblocks;
   const int n0 = (blockIdx.x / mblocks) * T::BN;
   const int e = blocks[mb];
@@ -271,7 +275,7 @@ __global__ __launch_bounds__(MoeTiles<B>::Down::NT_WS, 1) void moe_down_kernel(
   bop.init(wq + (int64_t)e * H * ldq, ldq, ws + (int64_t)e * H * ldp, wz + (int64_t)e * H * ldp, ldp, gs,
            ClampRows{n0, H});
   f32x16 acc[T::TI][T::TJ];
-  if (!mp::mainloop_ws<T, mp::F16Math>(aop, bop, F / 64, buf0, buf1, acc)) return;
+  if (!mp::mainloop_ws<T, mp::F16Math, 3>(aop, bop, F / 64, bufs, acc)) return;
   const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
