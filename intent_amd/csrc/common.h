@@ -22,16 +22,19 @@ INTENT_DEVICE To bit_cast(From v) {
   return __builtin_bit_cast(To, v);
 }
 
+// Buffer resource over [base, base + 2 GiB): raw buffer loads then take a
+// 32-bit lane offset plus a wave-uniform offset.
+INTENT_DEVICE __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+
 // 16-byte global load (global_load_dwordx4).
 INTENT_DEVICE u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 INTENT_DEVICE void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 // v_bfi_b32: (mask & a) | (~mask & b).
-INTENT_DEVICE uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
-  uint32_t r;
-  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "s"(mask), "v"(a), "v"(b));
-  return r;
-}
+// The compiler matches this pattern (no inline asm, so no hazard padding).
+INTENT_DEVICE uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) { return (mask & a) | (~mask & b); }
 
 // f16 value with bit pattern 0x6400 | q equals 1024 + q for q in 0..1023.
 // Subtracting (1024 + z) is exact for nibbles, so (q - z) comes out exact in
@@ -100,3 +103,50 @@ INTENT_DEVICE int xcd_swizzle(int bid, int nblocks) {
   const int per_xcd = full >> 3;
   return (bid & 7) * per_xcd + (bid >> 3);
 }
+
+// ---- wave-wide reduction of V per-lane partial sums (no LDS) -----------------
+// Reduce-scatter over the 64 lanes: v_permlane32_swap pairs value i with
+// value i + V/2 across the two half-waves, v_permlane16_swap does the same
+// across 16-lane rows, DPP row rotations finish inside each row. Afterwards
+// every lane of row R (lanes 16R..16R+15) holds the wave totals of the values
+// listed by wave_reduce_index(R, j), j < V / 4 (for V < 4 a row holds all V).
+// The summation order is fixed, so results are deterministic.
+template <int CTRL>
+INTENT_DEVICE float dpp_f32(float v) {
+  return bit_cast<float>(__builtin_amdgcn_update_dpp(0u, bit_cast<uint32_t>(v), CTRL, 0xf, 0xf, false));
+}
+template <int V>
+struct WaveReduce {
+  static constexpr int S32 = V >= 2 && V % 2 == 0;           // stage 1 scatters
+  static constexpr int V1 = S32 ? V / 2 : V;
+  static constexpr int S16 = V1 >= 2 && V1 % 2 == 0;         // stage 2 scatters
+  static constexpr int OUT = S16 ? V1 / 2 : V1;              // values left per lane
+  // Original index of output j in row R.
+  INTENT_DEVICE static constexpr int index(int R, int j) {
+    const int h = R >> 1, rr = R & 1;
+    const int j1 = S16 ? j + rr * OUT : j;
+    return S32 ? j1 + h * V1 : j1;
+  }
+  INTENT_DEVICE static void run(const float (&in)[V], float (&out)[OUT]) {
+    float a[V1];
+#pragma unroll
+    for (int i = 0; i < V1; ++i) {
+      const uint32_t x = bit_cast<uint32_t>(in[i]);
+      const uint32_t y = bit_cast<uint32_t>(S32 ? in[i + V1] : in[i]);
+      const auto r = __builtin_amdgcn_permlane32_swap(x, y, false, false);
+      a[i] = bit_cast<float>(r[0]) + bit_cast<float>(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < OUT; ++i) {
+      const uint32_t x = bit_cast<uint32_t>(a[i]);
+      const uint32_t y = bit_cast<uint32_t>(S16 ? a[i + OUT] : a[i]);
+      const auto r = __builtin_amdgcn_permlane16_swap(x, y, false, false);
+      float s = bit_cast<float>(r[0]) + bit_cast<float>(r[1]);
+      s += dpp_f32<0x128>(s);  // row_ror:8
+      s += dpp_f32<0x124>(s);  // row_ror:4
+      s += dpp_f32<0x4E>(s);   // quad_perm [2,3,0,1]
+      s += dpp_f32<0xB1>(s);   // quad_perm [1,0,3,2]
+      out[i] = s;
+    }
+  }
+};

@@ -43,9 +43,6 @@ typedef __attribute__((address_space(3))) void lds_t;
 INTENT_DEVICE constexpr int swz(int row) { return (row >> 1) & 7; }
 
 using Rsrc = __amdgpu_buffer_rsrc_t;
-INTENT_DEVICE Rsrc make_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
-}
 
 // s_waitcnt with only vmcnt constrained (expcnt 7, lgkmcnt 15 = no wait).
 template <int N>

@@ -138,59 +138,70 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
 // where xs1 / xs16 are the activation sums over the x1 / x16 positions; the
 // result is scaled by s once per chunk. Lane partials are reduced across the
 // wave with cross-lane shuffles in a fixed order.
-template <int M, int CH, int RW>
-__global__ __launch_bounds__(256) void w4a16_gemv_dot_kernel(const f16* __restrict__ x, int64_t ldx, int K,
+template <int M, int CH, int RW, int WPB = 4>
+__global__ __launch_bounds__(64 * WPB) void w4a16_gemv_dot_kernel(const f16* __restrict__ x, int64_t ldx, int K,
                                                              const uint8_t* __restrict__ wq, int64_t ldw,
                                                              const f16* __restrict__ sc,
                                                              const uint8_t* __restrict__ zp, int64_t ldq, int gs,
                                                              f16* __restrict__ y, int64_t ldy, int N) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int row0 = (blockIdx.x * 4 + wave) * RW;
+  const int row0 = (blockIdx.x * WPB + __builtin_amdgcn_readfirstlane(wave)) * RW;
   if (row0 >= N) return;  // wave-uniform
   const int nchunks = K >> 5;
 
   // Every load is unconditional (chunks past K are clamped to a valid address
   // and zeroed later through their scale) and raw values are converted only
   // where they are consumed, so all loads of the wave are in flight together.
+  // Issue order: activations (mostly L2 hits, needed first), then per weight
+  // row its chunks, scales and zeros; vmcnt retires in order, so row r can be
+  // consumed while later rows are still arriving.
   int cc[CH];
   bool cvalid[CH];
-  int grp[CH];
+  uint32_t grp[CH];
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int c = lane + 64 * i;
     cvalid[i] = c < nchunks;
     cc[i] = cvalid[i] ? c : nchunks - 1;
-    grp[i] = (cc[i] << 5) / gs;
+    grp[i] = (uint32_t)((cc[i] << 5) / gs);
   }
-  u32x4 wv[RW][CH];
-  f16 sraw[RW][CH];
-  uint8_t zraw[RW][CH];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int n = row0 + r < N ? row0 + r : N - 1;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) wv[r][i] = load16(wq + (int64_t)n * ldw + (int64_t)cc[i] * 16);
-  }
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int n = row0 + r < N ? row0 + r : N - 1;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      sraw[r][i] = sc[(int64_t)n * ldq + grp[i]];
-      zraw[r][i] = zp[(int64_t)n * ldq + grp[i]];
-    }
-  }
+  // Buffer loads: the row bases are wave-uniform and live in scalar
+  // registers; lanes add only their 32-bit chunk offsets.
   u32x4 xraw[M][CH][4];
 #pragma unroll
-  for (int m = 0; m < M; ++m)
+  for (int m = 0; m < M; ++m) {
+    const auto xr = make_rsrc(x + (int64_t)m * ldx);
 #pragma unroll
     for (int i = 0; i < CH; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xraw[m][i][j] = load16(x + (int64_t)m * ldx + (int64_t)cc[i] * 32 + j * 8);
+      for (int j = 0; j < 4; ++j) xraw[m][i][j] = __builtin_amdgcn_raw_buffer_load_b128(xr, cc[i] * 64, j * 16, 0);
+  }
+  u32x4 wv[RW][CH];
+  uint32_t sraw[RW][CH];
+  uint32_t zraw[RW][CH];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = row0 + r < N ? row0 + r : N - 1;
+    const auto wr = make_rsrc(wq + (int64_t)n * ldw);
+    const auto sr = make_rsrc(sc + (int64_t)n * ldq);
+    const auto zr = make_rsrc(zp + (int64_t)n * ldq);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) wv[r][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, cc[i] * 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      sraw[r][i] = __builtin_amdgcn_raw_buffer_load_b16(sr, grp[i] * 2, 0, 0);
+      zraw[r][i] = __builtin_amdgcn_raw_buffer_load_b8(zr, grp[i], 0, 0);
+    }
+  }
+  // Keep every load above this point: the scheduler would otherwise sink some
+  // of them below the first wait to save registers, adding a round trip.
+  __builtin_amdgcn_sched_barrier(0);
 
   // Activation pairs: for weight dword j of chunk i, a1 = (x0,x4), b1 = (x2,x6)
   // meet the x1 nibble pairs, a16 = (x1,x5), b16 = (x3,x7) the x16 pairs.
+  // Their sums come from v_dot2 against (1, 1).
+  const f16x2 ones = splat2((f16)1.0f);
   f16x2 xa1[M][CH][4], xb1[M][CH][4], xa16[M][CH][4], xb16[M][CH][4];
   float c0[M][CH], c1[M][CH];
 #pragma unroll
@@ -201,23 +212,22 @@ __global__ __launch_bounds__(256) void w4a16_gemv_dot_kernel(const f16* __restri
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const u32x4 v = xraw[m][i][j];
-        const uint32_t a1 = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
-        const uint32_t a16 = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
-        const uint32_t b1 = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
-        const uint32_t b16 = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
-        xa1[m][i][j] = bit_cast<f16x2>(a1);
-        xa16[m][i][j] = bit_cast<f16x2>(a16);
-        xb1[m][i][j] = bit_cast<f16x2>(b1);
-        xb16[m][i][j] = bit_cast<f16x2>(b16);
-        s1 += (float)xa1[m][i][j][0] + (float)xa1[m][i][j][1] + (float)xb1[m][i][j][0] + (float)xb1[m][i][j][1];
-        s16 += (float)xa16[m][i][j][0] + (float)xa16[m][i][j][1] + (float)xb16[m][i][j][0] +
-               (float)xb16[m][i][j][1];
+        xa1[m][i][j] = bit_cast<f16x2>(__builtin_amdgcn_perm(v[2], v[0], 0x05040100u));
+        xa16[m][i][j] = bit_cast<f16x2>(__builtin_amdgcn_perm(v[2], v[0], 0x07060302u));
+        xb1[m][i][j] = bit_cast<f16x2>(__builtin_amdgcn_perm(v[3], v[1], 0x05040100u));
+        xb16[m][i][j] = bit_cast<f16x2>(__builtin_amdgcn_perm(v[3], v[1], 0x07060302u));
+        s1 = __builtin_amdgcn_fdot2(xa1[m][i][j], ones, s1, false);
+        s1 = __builtin_amdgcn_fdot2(xb1[m][i][j], ones, s1, false);
+        s16 = __builtin_amdgcn_fdot2(xa16[m][i][j], ones, s16, false);
+        s16 = __builtin_amdgcn_fdot2(xb16[m][i][j], ones, s16, false);
       }
       c0[m][i] = 1024.f * s1 + 64.f * s16;
       c1[m][i] = s1 + s16;
     }
   }
 
+  uint32_t magic = 0x64006400u;
+  asm("" : "+v"(magic));  // keep the constant in a register for v_bfi_b32
   float part[M][RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
@@ -232,10 +242,10 @@ __global__ __launch_bounds__(256) void w4a16_gemv_dot_kernel(const f16* __restri
       for (int j = 0; j < 4; ++j) {
         const uint32_t d = wv[r][i][j];
         const uint32_t d8 = d >> 8;
-        const f16x2 lo = bit_cast<f16x2>((d & 0x000F000Fu) | 0x64006400u);
-        const f16x2 hi = bit_cast<f16x2>((d & 0x00F000F0u) | 0x64006400u);
-        const f16x2 lo8 = bit_cast<f16x2>((d8 & 0x000F000Fu) | 0x64006400u);
-        const f16x2 hi8 = bit_cast<f16x2>((d8 & 0x00F000F0u) | 0x64006400u);
+        const f16x2 lo = bit_cast<f16x2>(bfi(0x000F000Fu, d, magic));
+        const f16x2 hi = bit_cast<f16x2>(bfi(0x00F000F0u, d, magic));
+        const f16x2 lo8 = bit_cast<f16x2>(bfi(0x000F000Fu, d8, magic));
+        const f16x2 hi8 = bit_cast<f16x2>(bfi(0x00F000F0u, d8, magic));
 #pragma unroll
         for (int m = 0; m < M; ++m) {
           acc1[m] = __builtin_amdgcn_fdot2(lo, xa1[m][i][j], acc1[m], false);
@@ -244,7 +254,7 @@ __global__ __launch_bounds__(256) void w4a16_gemv_dot_kernel(const f16* __restri
           acc16[m] = __builtin_amdgcn_fdot2(hi8, xb16[m][i][j], acc16[m], false);
         }
       }
-      const float sv = (float)sraw[r][i] * (cvalid[i] ? 1.f : 0.f);
+      const float sv = (float)bit_cast<f16>((uint16_t)sraw[r][i]) * (cvalid[i] ? 1.f : 0.f);
       const float zv = (float)zraw[r][i];
 #pragma unroll
       for (int m = 0; m < M; ++m) {
@@ -254,31 +264,31 @@ __global__ __launch_bounds__(256) void w4a16_gemv_dot_kernel(const f16* __restri
     }
   }
 
-  // Butterfly reduction over the 64 lanes; every lane ends with the total.
+  // Wave totals without LDS; lane 16R of row R writes the values it holds.
+  using Red = WaveReduce<M * RW>;
+  float flat[M * RW];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
+  for (int m = 0; m < M; ++m)
 #pragma unroll
-    for (int m = 0; m < M; ++m)
+    for (int r = 0; r < RW; ++r) flat[m * RW + r] = part[m][r];
+  float tot[Red::OUT];
+  Red::run(flat, tot);
+  const int R = lane >> 4;
+  const bool writer = (lane & 15) == 0 && (Red::S16 || (R & 1) == 0) && (Red::S32 || R < 2);
+  if (writer) {
 #pragma unroll
-      for (int r = 0; r < RW; ++r) part[m][r] += __shfl_xor(part[m][r], off);
-  }
-  if (lane < M * RW) {
-    const int m = lane / RW;
-    const int r = lane % RW;
-    float v = 0.f;
-#pragma unroll
-    for (int mm = 0; mm < M; ++mm)
-#pragma unroll
-      for (int rr = 0; rr < RW; ++rr)
-        if (mm == m && rr == r) v = part[mm][rr];
-    if (row0 + r < N) y[(int64_t)m * ldy + row0 + r] = (f16)v;
+    for (int j = 0; j < Red::OUT; ++j) {
+      const int idx = Red::index(R, j);
+      const int m = idx / RW, r = idx % RW;
+      if (row0 + r < N) y[(int64_t)m * ldy + row0 + r] = (f16)tot[j];
+    }
   }
 }
 
 template <int M, int CH>
 void launch_dot(const f16* x, int64_t ldx, int K, const uint8_t* wq, int64_t ldw, const f16* sc, const uint8_t* zp,
                 int64_t ldq, int gs, f16* y, int64_t ldy, int N, hipStream_t st) {
-  constexpr int RW = CH >= 8 ? 1 : 8 / CH;
+  constexpr int RW = CH >= 8 ? 1 : 8 / CH;  // eight 16-byte weight loads per lane
   const int waves = (N + RW - 1) / RW;
   const int blocks = (waves + 3) / 4;
   hipLaunchKernelGGL((w4a16_gemv_dot_kernel<M, CH, RW>), dim3(blocks), dim3(256), 0, st, x, ldx, K, wq, ldw, sc, zp,
