@@ -25,9 +25,9 @@ __global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restr
                                                                 void* __restrict__ out, int64_t ldo, int mblocks) {
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
+  // Plain dispatch order (m fastest): measured faster here than the XCD-grouped order.
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
   const int wave = T::wave();
   const int nk = (K + mp::ROWB - 1) / mp::ROWB;
   const bool half = kHalf;
