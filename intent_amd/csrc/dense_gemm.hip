@@ -45,26 +45,10 @@ struct WeightOp<T, W8Args> {
   INTENT_DEVICE static void init(Op& op, const W8Args& w, int n0, int N) { op.init(w.q, w.ldq, ClampRows{n0, N}); }
 };
 
-// y[m, n] = f16(sum_k x[m, k] * deq(W)[n, k] (* colscale[n])).
-template <class T, class WArgs, bool kColScale>
-__global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __restrict__ x, int64_t ldx, int M,
-                                                                   WArgs w, int N, int K, f16* __restrict__ y,
-                                                                   int64_t ldy, const f16* __restrict__ colscale,
-                                                                   int mblocks) {
-  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  char* const bufs[2] = {buf0, buf1};
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
-  typename WeightOp<T, WArgs>::Op bop;
-  WeightOp<T, WArgs>::init(bop, w, n0, N);
-  f32x16 acc[T::TI][T::TJ];
-  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
-  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave() % T::NW);
-  if (!mp::mainloop_ws<T, mp::F16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
-
-  // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
+// Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
+template <class T, bool kColScale>
+INTENT_DEVICE void store_dense(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N, f16* __restrict__ y,
+                               int64_t ldy, const f16* __restrict__ colscale) {
   const bool vec = (ldy & 3) == 0 && (((uintptr_t)y) & 7) == 0;
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
@@ -96,6 +80,29 @@ __global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __re
         }
       }
   }
+
+}
+
+// y[m, n] = f16(sum_k x[m, k] * deq(W)[n, k] (* colscale[n])).
+template <class T, class WArgs, bool kColScale>
+__global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __restrict__ x, int64_t ldx, int M,
+                                                                   WArgs w, int N, int K, f16* __restrict__ y,
+                                                                   int64_t ldy, const f16* __restrict__ colscale,
+                                                                   int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  char* const bufs[2] = {buf0, buf1};
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  typename WeightOp<T, WArgs>::Op bop;
+  WeightOp<T, WArgs>::init(bop, w, n0, N);
+  f32x16 acc[T::TI][T::TJ];
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave() % T::NW);
+  if (!mp::mainloop_ws<T, mp::F16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
+
+  store_dense<T, kColScale>(acc, m0, n0, M, N, y, ldy, colscale);
 }
 
 template <class T, class WArgs, bool kColScale>

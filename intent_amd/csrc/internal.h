@@ -15,6 +15,7 @@ int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 void clear_error();
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
 // rows * stride_bytes stays below 2^31: the byte offsets of buffer loads are
 // 32-bit and the kernels keep them non-negative ints.

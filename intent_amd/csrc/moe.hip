@@ -5,6 +5,7 @@
 #include "common.h"
 #include "internal.h"
 #include "mfma_pipe.h"
+#include "w4pk.h"
 
 namespace {
 
@@ -188,33 +189,11 @@ struct ClampRows {
   }
 };
 
-template <int B>
-__global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_kernel(
-    const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
-    const int32_t* __restrict__ blocks, int mblocks, int R, int top_k, const uint8_t* __restrict__ wq,
-    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int F, int gs, f16* __restrict__ act,
-    int64_t ld_act) {
-  using T = typename MoeTiles<B>::GateUp;
-  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char buf2[T::STAGE_BYTES];
-  char* const bufs[3] = {buf0, buf1, buf2};
-  const int mb = blockIdx.x % mblocks;
-  const int f0 = (blockIdx.x / mblocks) * (T::BN / 2);
-  const int e = blocks[mb];
-  if (e < 0) return;
-  const int64_t ldq = H / 2;
-  const int64_t ldp = H / gs;
-  const int m0 = mb * B;
-  mp::DmaRowsOperand<T::BM, mp::GatherRows, T::NW> aop;
-  aop.init(mp::GatherRows{x, ldx * 2, sorted, R, top_k}, m0, T::wave() % T::NW);
-  mp::W4Operand<T::BN, T::NT> bop;
-  bop.init(wq + (int64_t)e * 2 * F * ldq, ldq, ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs,
-           GateUpRowMap<T>{f0, F});
-  f32x16 acc[T::TI][T::TJ];
-  if (!mp::mainloop_ws<T, mp::F16Math, 3>(aop, bop, H / 64, bufs, acc)) return;
-
-  // acc[i][j][4g + c]: row(i), feature f0 + feature(wave_n, j*32 + g*8 + h*4 + c).
+// acc[i][j][4g + c]: row(i), feature f0 + feature(wave_n, j*32 + g*8 + h*4 + c);
+// j < TJ/2 are gate columns, j + TJ/2 the up columns of the same features.
+template <class T>
+INTENT_DEVICE void store_gate_up(const f32x16 (&acc)[T::TI][T::TJ], int m0, int f0, int F,
+                                 const int32_t* __restrict__ sorted, int R, f16* __restrict__ act, int64_t ld_act) {
   const bool vec = (ld_act & 3) == 0 && (F & 3) == 0;
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
@@ -248,6 +227,105 @@ __global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_ker
         }
       }
   }
+
+}
+
+template <int B>
+__global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_kernel(
+    const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ blocks, int mblocks, int R, int top_k, const uint8_t* __restrict__ wq,
+    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int F, int gs, f16* __restrict__ act,
+    int64_t ld_act) {
+  using T = typename MoeTiles<B>::GateUp;
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf2[T::STAGE_BYTES];
+  char* const bufs[3] = {buf0, buf1, buf2};
+  const int mb = blockIdx.x % mblocks;
+  const int f0 = (blockIdx.x / mblocks) * (T::BN / 2);
+  const int e = blocks[mb];
+  if (e < 0) return;
+  const int64_t ldq = H / 2;
+  const int64_t ldp = H / gs;
+  const int m0 = mb * B;
+  mp::DmaRowsOperand<T::BM, mp::GatherRows, T::NW> aop;
+  aop.init(mp::GatherRows{x, ldx * 2, sorted, R, top_k}, m0, T::wave() % T::NW);
+  mp::W4Operand<T::BN, T::NT> bop;
+  bop.init(wq + (int64_t)e * 2 * F * ldq, ldq, ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs,
+           GateUpRowMap<T>{f0, F});
+  f32x16 acc[T::TI][T::TJ];
+  if (!mp::mainloop_ws<T, mp::F16Math, 3>(aop, bop, H / 64, bufs, acc)) return;
+
+  store_gate_up<T>(acc, m0, f0, F, sorted, R, act, ld_act);
+}
+
+// Gate/up on the packed-weight core (w4pk.h): 128-row blocks x 128 features
+// (256 weight rows), four waves of 128 x 64 (32 gate + 32 up columns), each
+// decoding its own weight fragments; a three-stage DMA ring (78 KB of LDS)
+// leaves room for two workgroups per CU, whose independent barriers hide
+// each other's stalls. Measured on config 4: 613 us with the producer/
+// consumer kernel below, 618 us with this core at one 8-wave workgroup per
+// CU, 519 us at two 4-wave workgroups per CU.
+using GateUpPk = mp::Tile<128, 256, 1, 4>;
+constexpr int kGateUpPkStages = 3;
+
+__global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
+    const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ blocks, int mblocks, int R, int top_k, const uint8_t* __restrict__ wq,
+    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int F, int gs, f16* __restrict__ act,
+    int64_t ld_act) {
+  using T = GateUpPk;
+  constexpr int NB = kGateUpPkStages;
+  __shared__ __attribute__((aligned(16))) char smem[NB][mp::stage_bytes_pk<T>()];
+  char* bufs[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) bufs[b] = smem[b];
+  const int mb = blockIdx.x % mblocks;
+  const int f0 = (blockIdx.x / mblocks) * (T::BN / 2);
+  const int e = blocks[mb];
+  if (e < 0) return;
+  const int64_t ldq = H / 2;
+  const int64_t ldp = H / gs;
+  const int m0 = mb * T::BM;
+  const int wave = T::wave();
+  const GateUpRowMap<T> rows{f0, F};
+  mp::DmaRowsOperand<T::BM, mp::GatherRows, T::NW> aop;
+  aop.init(mp::GatherRows{x, ldx * 2, sorted, R, top_k}, m0, wave);
+  mp::PackedRowsDma<T::BN, T::NW> bop;
+  bop.init(wq + (int64_t)e * 2 * F * ldq, ldq, rows, wave);
+  mp::GroupParamsDma<T::BN, T::NW> pop;
+  pop.init(ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs, rows, wave);
+  f32x16 acc[T::TI][T::TJ];
+  mp::mainloop_pk<T, NB>(aop, bop, pop, H / 64, bufs, acc);
+  store_gate_up<T>(acc, m0, f0, F, sorted, R, act, ld_act);
+}
+
+// fp32 rows of the down projection scattered to their routes.
+template <class T>
+INTENT_DEVICE void store_down(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int H,
+                              const int32_t* __restrict__ sorted, int R, float* __restrict__ out, int64_t ldo) {
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int r = sorted[m0 + T::row(i)];
+    if (r < 0 || r >= R) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int col = n0 + T::col(j, g);
+        float* dst = out + (int64_t)r * ldo + col;
+        if (vec && col + 3 < H) {
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (col + c < H) dst[c] = acc[i][j][4 * g + c];
+        }
+      }
+  }
+
 }
 
 // Down projection: grid = mblocks x ntiles; fp32 rows scattered to routes.
@@ -276,27 +354,7 @@ __global__ __launch_bounds__(MoeTiles<B>::Down::NT_WS, 1) void moe_down_kernel(
            ClampRows{n0, H});
   f32x16 acc[T::TI][T::TJ];
   if (!mp::mainloop_ws<T, mp::F16Math, 3>(aop, bop, F / 64, bufs, acc)) return;
-  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
-    const int r = sorted[m0 + T::row(i)];
-    if (r < 0 || r >= R) continue;
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int col = n0 + T::col(j, g);
-        float* dst = out + (int64_t)r * ldo + col;
-        if (vec && col + 3 < H) {
-          *reinterpret_cast<f32x4*>(dst) =
-              f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-        } else {
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (col + c < H) dst[c] = acc[i][j][4 * g + c];
-        }
-      }
-  }
+  store_down<T>(acc, m0, n0, H, sorted, R, out, ldo);
 }
 
 // y[t, d] += w[t, s] * out[t*k + s, d], slot by slot (mul then add, no fma).
@@ -364,10 +422,20 @@ extern "C" int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_
 
 namespace {
 
+
 template <int B>
 int gate_up_launch(const void* x, int64_t T, int64_t H, int64_t x_ld, const int32_t* sorted, const int32_t* blocks,
                    int64_t num_blocks, int64_t top_k, const uint8_t* wq, const void* ws, const uint8_t* wz,
                    int64_t F, int64_t gs, void* act, int64_t act_ld, void* stream) {
+  const int64_t ldp = H / gs;
+  if (B == GateUpPk::BM && ldp % 4 == 0 && intent::aligned4(ws) && intent::aligned4(wz)) {
+    const int64_t grid = num_blocks * ((F + GateUpPk::BN / 2 - 1) / (GateUpPk::BN / 2));
+    INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+    hipLaunchKernelGGL(moe_gate_up_pk_kernel, dim3((unsigned)grid), dim3(GateUpPk::NT), 0, (hipStream_t)stream,
+                       (const f16*)x, x_ld, (int)H, sorted, blocks, (int)num_blocks, (int)(T * top_k), (int)top_k, wq,
+                       (const f16*)ws, wz, (int)F, (int)gs, (f16*)act, act_ld);
+    return intent::launch_status("moe_gate_up_w4");
+  }
   using Tl = typename MoeTiles<B>::GateUp;
   const int64_t ftile = Tl::BN / 2;
   const int64_t grid = num_blocks * ((F + ftile - 1) / ftile);
