@@ -242,7 +242,7 @@ def main() -> int:
                    "kernel": dec["entry"], "weight_copies": dec["copies"], "arch": arch},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "bytes_per_launch": dec["work"].bytes, "kernel": "w4a16_gemv_dot_kernel<1,2,4>"},
+                     "bytes_per_launch": dec["work"].bytes, "kernel": "w4a16_gemv_dot_kernel<1,2,4,4>"},
     }
     extra = {}
     if args.only == "all":
