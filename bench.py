@@ -151,6 +151,25 @@ def bench_moe(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": 1}
 
 
+def bench_q4k(steps: int, warmup: int) -> dict:
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    d = inputs.kquant_projection(0, N=4096, K=4096)
+    work = inputs.kquant_work(4096, 4096)
+    art = intent.compile(intent.quantized_projection, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes)
+    w = torch.from_numpy(d["w"]).cuda()
+    x = torch.from_numpy(d["x"]).cuda()
+    calls = [art.prepare(w.clone(), x.clone()) for _ in range(n)]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE profile."""
     path = ROOT / "profiles" / "w4a16_gemv_dot_m1_traffic.md"
@@ -266,6 +285,9 @@ def main() -> int:
         log("[bench] w8a16 M=16")
         r = bench_w8a16(args.steps, args.warmup)
         extra["w8a16_m16"] = _hbm_entry(r)
+        log("[bench] q4_k projection N=K=4096")
+        r = bench_q4k(args.steps, args.warmup)
+        extra["q4k_projection_n4096"] = _hbm_entry(r)
     line["extra"] = extra
     if not args.no_cpu:
         log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s budget)")

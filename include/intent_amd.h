@@ -226,6 +226,47 @@ int intent_moe_expert_ffn_w4(const float* router_logits, const void* x, int64_t 
                              int32_t* topk_ids_out, float* topk_weights_out,
                              void* stream);
 
+/*
+ * GGUF K-quant records (doc/dsl/quantized-operations.en.md:11-70).
+ * Q4_K record: 144 bytes (f16 d, f16 dmin, 6-bit sc[8]/m[8] in bytes 4..15,
+ * 256 nibbles in bytes 16..143). Q8_K record: 292 bytes (f32 ds, 256 x i8,
+ * 16 x i16 bsum). Little-endian, no padding.
+ *
+ * intent_q8k_quantize: f32 x [G, 256] (row stride x_ld elements, 16-byte
+ * aligned, x_ld % 4 == 0) -> G Q8_K records (row stride records_ld bytes,
+ * 4-byte aligned). Replaces I.quantize(values, format=I.quant.q8_k)
+ * (quantized-operations.en.md:5-10,62-70; RVV baseline quantize_row,
+ * experiments/cpu/baselines/weft/tianchenrv/contraction/q4_k_projection/
+ * q4_k_projection.py:29-48). Bit-exact: IEEE division for the inverse and
+ * ds, one f32 multiply per value, round half to even, saturation to i8.
+ */
+int intent_q8k_quantize(const float* x, int64_t G, int64_t x_ld,
+                        uint8_t* records, int64_t records_ld, void* stream);
+
+/*
+ * y[n] = quantized_dot(W[n, 0..G), Xq[0..G)) for N rows of G Q4_K records
+ * (row stride w_ld bytes, 16-byte aligned) and one vector of G Q8_K records
+ * (contiguous, 4-byte aligned); y f32 [N]. Replaces I.quantized_dot(...,
+ * lhs_format=q4_k, rhs_format=q8_k, acc_dtype=f32)
+ * (quantized-operations.en.md:38-58; baseline compute, q4_k_projection.py:
+ * 56-72) applied per row as in quantized_projection
+ * (examples/kernels/quantization/quantized_projection.py:15-19).
+ * Bit-exact: integer sub-sums, one rounding per f32 operation, records
+ * added in increasing order starting from +0. G == 0 gives +0 per row.
+ */
+int intent_q4k_q8k_gemv(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld,
+                        const uint8_t* xq, float* y, void* stream);
+
+/*
+ * Whole quantized_projection (examples/kernels/quantization/
+ * quantized_projection.py:5-19): quantize x (f32 [G, 256]) into xq_records
+ * (caller-provided, G * 292 bytes, 4-byte aligned; left holding the Q8_K
+ * records) and run intent_q4k_q8k_gemv into y f32 [N].
+ */
+int intent_q4k_projection(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld,
+                          const float* x, int64_t x_ld, uint8_t* xq_records,
+                          float* y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -24,6 +24,9 @@ from .definitions import (
     moe_expert_ffn_w4,
     moe_gate_up_w4,
     moe_route_topk,
+    q4_k_q8_k_dot,
+    q8_k_quantize,
+    quantized_projection,
     w8a8_scaled_matmul,
     weight_only_int4_asym_matmul,
     weight_only_int8_matmul,
@@ -43,6 +46,7 @@ __all__ = [
     "ALL_DEFINITIONS", "CompilationStageError", "CompileOptions", "CompiledArtifact", "DType", "KernelDefinition",
     "LanguageUseError", "MI355XTarget", "NativeLibraryError", "PublicInterface", "ScalarParameter", "ViewKind",
     "ViewParameter", "compile", "gemm_i8_nt", "kernel", "moe_align_block_size", "moe_combine", "moe_down_w4",
-    "moe_expert_ffn_w4", "moe_gate_up_w4", "moe_route_topk", "w8a8_scaled_matmul", "weight_only_int4_asym_matmul",
+    "moe_expert_ffn_w4", "moe_gate_up_w4", "moe_route_topk", "q4_k_q8_k_dot", "q8_k_quantize",
+    "quantized_projection", "w8a8_scaled_matmul", "weight_only_int4_asym_matmul",
     "weight_only_int8_matmul",
 ]

@@ -1,0 +1,208 @@
+// GGUF K-quant records on gfx950: Q8_K quantization of f32 activations and the
+// Q4_K x Q8_K dot product, composed into the quantized projection
+//   y[n] = quantized_dot(W[n], quantize(x)).
+//
+// Record formats and numerics follow doc/dsl/quantized-operations.en.md:11-70:
+//   Q4_K (144 B): f16 d, f16 dmin, 12 bytes of 6-bit sub-block scales sc[8]
+//                 and mins m[8], 128 bytes of nibbles;
+//   Q8_K (292 B): f32 ds, 256 x i8, 16 x i16 bsum (sums of 16 values).
+// Per record pair: S = sum_s sc[s] * dot32_s (int32, exact), T = sum_s m[s] *
+// (bsum[2s] + bsum[2s+1]) (int32, exact), v = ds * (d*S - dmin*T) with every
+// f32 operation rounded once (no contraction: built with -ffp-contract=off),
+// and the row result is the f32 sum of v in increasing record order starting
+// from +0. The kernels reproduce that order exactly, so results are bit-equal
+// to a sequential CPU evaluation.
+#include "common.h"
+#include "internal.h"
+
+namespace {
+
+constexpr int kQ4Bytes = 144;
+constexpr int kQ8Bytes = 292;
+
+// ---- Q8_K quantization: one wave per 256-value record --------------------------
+// Lane l holds values 4l..4l+3. Extremes reduce exactly across the wave; the
+// record's inverse and ds use IEEE division; q = saturate(rne(v * inverse)).
+__global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restrict__ x, int64_t ldx, int G,
+                                                           uint8_t* __restrict__ out, int64_t ld_out) {
+  const int lane = threadIdx.x & 63;
+  const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= G) return;  // wave-uniform
+  const f32x4 v = *reinterpret_cast<const f32x4*>(x + (int64_t)g * ldx + 4 * lane);
+  float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+  float mn = fminf(fminf(v[0], v[1]), fminf(v[2], v[3]));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off));
+    mn = fminf(mn, __shfl_xor(mn, off));
+  }
+  const float extreme = fabsf(mx) > fabsf(mn) ? mx : mn;  // ties pick the minimum
+  float inverse = 0.f, ds = 0.f;
+  int q[4] = {0, 0, 0, 0};
+  if (extreme != 0.f) {
+    inverse = __fdiv_rn(-127.0f, extreme);
+    ds = __fdiv_rn(1.0f, inverse);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t = rintf(__fmul_rn(v[i], inverse));
+      q[i] = t > 127.f ? 127 : t < -128.f ? -128 : (int)t;
+    }
+  }
+  uint8_t* rec = out + (int64_t)g * ld_out;
+  const uint32_t packed = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
+                          ((uint32_t)(q[3] & 255) << 24);
+  *reinterpret_cast<uint32_t*>(rec + 4 + 4 * lane) = packed;
+  // bsum[j] covers lanes 4j..4j+3.
+  int s = q[0] + q[1] + q[2] + q[3];
+  s += __shfl_xor(s, 1);
+  s += __shfl_xor(s, 2);
+  if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(rec + 260 + 2 * (lane >> 2)) = (int16_t)s;
+  if (lane == 0) *reinterpret_cast<float*>(rec) = ds;
+}
+
+// ---- Q4_K x Q8_K GEMV ------------------------------------------------------------
+// A wave owns RW weight rows. Records go 16 at a time: lane l takes record
+// c0 + l/4 and quarter u = l%4 of it, i.e. sub-blocks 2u (low nibbles of
+// packed group u) and 2u+1 (high nibbles), 64 elements. The integer dots use
+// v_dot4_i32_i8 (nibbles are non-negative, so signed bytes are exact); S and T
+// are summed over the record's four lanes (integer, exact); lane 4b computes
+// v_b and the wave adds v_b one record at a time into the row total.
+__device__ __forceinline__ int q4k_field(const u32x4 hdr, int r, int i) {
+  // Bytes 4..15 of the record are hdr dwords 1..3; byte k is (hdr[k/4] >> 8(k%4)).
+  auto byte = [&](int k) { return (int)((hdr[k >> 2] >> (8 * (k & 3))) & 255u); };
+  if (i < 4) return byte(4 + 4 * r + i) & 63;
+  const int t = i - 4;
+  return ((byte(12 + t) >> (4 * r)) & 15) | ((byte(4 + 4 * r + t) >> 6) << 4);
+}
+
+template <int RW>
+__global__ __launch_bounds__(256) void q4k_gemv_kernel(const uint8_t* __restrict__ w, int64_t ldw, int N, int G,
+                                                       const uint8_t* __restrict__ xq, float* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * RW;
+  if (row0 >= N) return;  // wave-uniform
+  const int u = lane & 3;
+  const auto xr = make_rsrc(xq);
+  float total[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) total[r] = 0.f;
+
+  for (int c0 = 0; c0 < G; c0 += 16) {
+    const int b = c0 + (lane >> 2) < G ? c0 + (lane >> 2) : G - 1;
+    // Activation fragment: 64 i8 (elements 64u..64u+63), bsum[4u..4u+3], ds.
+    const uint32_t xo = (uint32_t)b * kQ8Bytes;
+    uint32_t xqv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xqv[i] = __builtin_amdgcn_raw_buffer_load_b32(xr, xo + 4 + 64 * u + 4 * i, 0, 0);
+    const uint32_t bs01 = __builtin_amdgcn_raw_buffer_load_b32(xr, xo + 260 + 8 * u, 0, 0);
+    const uint32_t bs23 = __builtin_amdgcn_raw_buffer_load_b32(xr, xo + 264 + 8 * u, 0, 0);
+    const float ds = bit_cast<float>(__builtin_amdgcn_raw_buffer_load_b32(xr, xo, 0, 0));
+    const int bsum_lo = (int)(int16_t)(bs01 & 0xFFFFu) + (int)(int16_t)(bs01 >> 16);
+    const int bsum_hi = (int)(int16_t)(bs23 & 0xFFFFu) + (int)(int16_t)(bs23 >> 16);
+
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int n = row0 + r < N ? row0 + r : N - 1;
+      const uint8_t* rec = w + (int64_t)n * ldw + (int64_t)b * kQ4Bytes;
+      const u32x4 hdr = *reinterpret_cast<const u32x4*>(rec);
+      const u32x4 q0 = *reinterpret_cast<const u32x4*>(rec + 16 + 32 * u);
+      const u32x4 q1 = *reinterpret_cast<const u32x4*>(rec + 32 + 32 * u);
+      const uint32_t qw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+      int dlo = 0, dhi = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dlo = __builtin_amdgcn_sdot4((int)(qw[i] & 0x0F0F0F0Fu), (int)xqv[i], dlo, false);
+        dhi = __builtin_amdgcn_sdot4((int)((qw[i] >> 4) & 0x0F0F0F0Fu), (int)xqv[8 + i], dhi, false);
+      }
+      int S = q4k_field(hdr, 0, 2 * u) * dlo + q4k_field(hdr, 0, 2 * u + 1) * dhi;
+      int T = q4k_field(hdr, 1, 2 * u) * bsum_lo + q4k_field(hdr, 1, 2 * u + 1) * bsum_hi;
+      S += __shfl_xor(S, 1);
+      S += __shfl_xor(S, 2);
+      T += __shfl_xor(T, 1);
+      T += __shfl_xor(T, 2);
+      const float d = (float)bit_cast<f16>((uint16_t)(hdr[0] & 0xFFFFu));
+      const float dmin = (float)bit_cast<f16>((uint16_t)(hdr[0] >> 16));
+      const float p = __fmul_rn(d, (float)S);
+      const float nn = __fmul_rn(dmin, (float)T);
+      const float v = __fmul_rn(ds, __fsub_rn(p, nn));
+      // Record order: lane 4k holds record c0 + k.
+      const int cnt = G - c0 < 16 ? G - c0 : 16;
+      float t = total[r];
+      for (int k = 0; k < cnt; ++k)
+        t = __fadd_rn(t, bit_cast<float>(__builtin_amdgcn_readlane(bit_cast<int>(v), 4 * k)));
+      total[r] = t;
+    }
+  }
+  if (lane < RW) {
+    float out = 0.f;
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+      if (r == lane) out = total[r];
+    if (row0 + lane < N) y[row0 + lane] = out;
+  }
+}
+
+constexpr int kRows = 4;
+
+__global__ void zero_fill_kernel(float* __restrict__ y, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = 0.f;
+}
+
+int quantize_check(const float* x, int64_t G, int64_t x_ld, const uint8_t* out, int64_t out_ld) {
+  INTENT_REQUIRE(G >= 0 && G <= INT32_MAX / 4, INTENT_ERR_INVALID_ARGUMENT, "bad record count %lld", (long long)G);
+  if (G == 0) return INTENT_OK;
+  INTENT_REQUIRE(x && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(x_ld >= 256 && out_ld >= kQ8Bytes, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(x) && x_ld % 4 == 0 && intent::aligned4(out) && out_ld % 4 == 0,
+                 INTENT_ERR_ALIGNMENT, "x must be 16-byte aligned (row stride a multiple of 4), records 4-byte aligned");
+  return INTENT_OK;
+}
+
+}  // namespace
+
+extern "C" int intent_q8k_quantize(const float* x, int64_t G, int64_t x_ld, uint8_t* records, int64_t records_ld,
+                                   void* stream) {
+  intent::clear_error();
+  int st = quantize_check(x, G, x_ld, records, records_ld);
+  if (st != INTENT_OK || G == 0) return st;
+  hipLaunchKernelGGL(q8k_quantize_kernel, dim3((unsigned)((G + 3) / 4)), dim3(256), 0, (hipStream_t)stream, x, x_ld,
+                     (int)G, records, records_ld);
+  return intent::launch_status("q8k_quantize");
+}
+
+extern "C" int intent_q4k_q8k_gemv(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld, const uint8_t* xq,
+                                   float* y, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(N >= 0 && G >= 0 && N <= INT32_MAX && G <= INT32_MAX / kQ8Bytes, INTENT_ERR_INVALID_ARGUMENT,
+                 "bad extents (N=%lld G=%lld)", (long long)N, (long long)G);
+  if (N == 0) return INTENT_OK;
+  INTENT_REQUIRE(y, INTENT_ERR_INVALID_ARGUMENT, "null output");
+  if (G == 0) {  // empty dot: +0 for every row, no reads (a fill kernel, not a memset node)
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, (hipStream_t)stream, y,
+                       (int)N);
+    return intent::launch_status("q4k_q8k_gemv");
+  }
+  INTENT_REQUIRE(w && xq, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(w_ld >= G * kQ4Bytes, INTENT_ERR_INVALID_ARGUMENT, "weight row stride smaller than G records");
+  INTENT_REQUIRE(intent::aligned16(w) && w_ld % 16 == 0 && intent::aligned4(xq), INTENT_ERR_ALIGNMENT,
+                 "weights must be 16-byte aligned with 16-byte row strides; Q8_K records 4-byte aligned");
+  const int64_t waves = (N + kRows - 1) / kRows;
+  hipLaunchKernelGGL((q4k_gemv_kernel<kRows>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                     w, w_ld, (int)N, (int)G, xq, y);
+  return intent::launch_status("q4k_q8k_gemv");
+}
+
+extern "C" int intent_q4k_projection(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld, const float* x,
+                                     int64_t x_ld, uint8_t* xq_records, float* y, void* stream) {
+  intent::clear_error();
+  int st = quantize_check(x, G, x_ld, xq_records, kQ8Bytes);
+  if (st != INTENT_OK) return st;
+  if (G > 0) {
+    hipLaunchKernelGGL(q8k_quantize_kernel, dim3((unsigned)((G + 3) / 4)), dim3(256), 0, (hipStream_t)stream, x,
+                       x_ld, (int)G, xq_records, (int64_t)kQ8Bytes);
+    st = intent::launch_status("q8k_quantize");
+    if (st != INTENT_OK) return st;
+  }
+  return intent_q4k_q8k_gemv(w, N, G, w_ld, xq_records, y, stream);
+}

@@ -411,7 +411,76 @@ moe_combine = KernelDefinition(
 )
 
 
+# ---- GGUF K-quant records --------------------------------------------------------
+
+Q4K_RECORD = 144
+Q8K_RECORD = 292
+
+
+def _q8k_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    x, r = v["values"], v["records"]
+    _native.call("intent_q8k_quantize", _ptr(x), env["G"], _ld(x), _ptr(r), _ld(r), stream)
+    return "intent_q8k_quantize"
+
+
+q8_k_quantize = KernelDefinition(
+    name="q8_k_quantize",
+    params=(
+        Param("values", "f32", ("G", 256), leading_stride=True),
+        Param("records", "u8", ("G", Q8K_RECORD), OUT, leading_stride=True),
+    ),
+    launch=_q8k_launch,
+    reference="doc/dsl/quantized-operations.en.md:5-10,62-70 (I.quantize(values, format=I.quant.q8_k))",
+    doc="f32 [G,256] -> Q8_K records u8 [G,292] (ds, i8 q, i16 bsum)",
+)
+
+
+def _qdot_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    w, xq, y = v["weights"], v["records"], v["output"]
+    _native.call("intent_q4k_q8k_gemv", _ptr(w), env["N"], env["G"], w.stride(0), _ptr(xq), _ptr(y), stream)
+    return "intent_q4k_q8k_gemv"
+
+
+q4_k_q8_k_dot = KernelDefinition(
+    name="q4_k_q8_k_dot",
+    params=(
+        Param("weights", "u8", ("N", "G", Q4K_RECORD)),
+        Param("records", "u8", ("G", Q8K_RECORD)),
+        Param("output", "f32", ("N",), OUT),
+    ),
+    launch=_qdot_launch,
+    reference="doc/dsl/quantized-operations.en.md:38-58 (I.quantized_dot, lhs q4_k, rhs q8_k, acc f32) per row",
+    doc="output[n] = quantized_dot(weights[n], records), records added in increasing order from +0",
+)
+
+
+def _qproj_workspace(env: dict) -> int:
+    return env["G"] * Q8K_RECORD
+
+
+def _qproj_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    w, x, y = v["weights"], v["activation"], v["output"]
+    _native.call("intent_q4k_projection", _ptr(w), env["N"], env["G"], w.stride(0), _ptr(x), _ld(x),
+                 workspace.data_ptr(), _ptr(y), stream)
+    return "intent_q4k_projection"
+
+
+quantized_projection = KernelDefinition(
+    name="quantized_projection",
+    params=(
+        Param("weights", "u8", ("N", "G", Q4K_RECORD)),
+        Param("activation", "f32", ("G", 256), leading_stride=True),
+        Param("output", "f32", ("N",), OUT),
+    ),
+    launch=_qproj_launch,
+    workspace=_qproj_workspace,
+    reference="examples/kernels/quantization/quantized_projection.py:5-19",
+    doc="output[n] = quantized_dot(weights[n], quantize(activation, q8_k)), Q4_K x Q8_K",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
+    q8_k_quantize, q4_k_q8_k_dot, quantized_projection,
 )

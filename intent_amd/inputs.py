@@ -82,6 +82,28 @@ def config4_moe(seed: int = 0, T: int = 512, H: int = 4096, E: int = 8, top_k: i
             "wd": wd, "sd": sd, "zd": zd}
 
 
+def q4k_records(rng: np.random.Generator, shape, d_range=(0.0005, 0.005)) -> np.ndarray:
+    """Random Q4_K records uint8 [*shape, 144]: f16 d and dmin drawn from d_range;
+    every other byte (6-bit sc/m fields, nibbles) uniform, which is always a
+    legal record (doc/dsl/quantized-operations.en.md:21-36)."""
+    shape = tuple(shape)
+    rec = rng.integers(0, 256, size=shape + (144,), dtype=np.uint8)
+    d = rng.uniform(d_range[0], d_range[1], size=shape + (2,)).astype(np.float32).astype(np.float16)
+    rec[..., 0:4] = d.view(np.uint8).reshape(shape + (4,))
+    return rec
+
+
+def kquant_projection(seed: int = 0, N: int = 4096, K: int = 4096) -> dict:
+    """quantized_projection inputs (examples/kernels/quantization/quantized_projection.py):
+    Q4_K weight records [N, K/256, 144] and f32 activations [K/256, 256] ~ N(0,1)."""
+    if K % 256:
+        raise ValueError("K must be a multiple of 256")
+    rng = np.random.default_rng(seed)
+    w = q4k_records(rng, (N, K // 256))
+    x = rng.standard_normal((K // 256, 256), dtype=np.float32)
+    return {"w": w, "x": x}
+
+
 def to_device(arrays: dict, device="cuda") -> dict:
     import torch
 
@@ -111,6 +133,13 @@ def w8a16_work(M: int, K: int, N: int) -> Workload:
 
 def w8a8_work(M: int, K: int, N: int) -> Workload:
     return Workload(f"w8a8 M{M} K{K} N{N}", 2 * M * N * K, M * K + N * K + M * 4 + N * 4 + M * N * 2)
+
+
+def kquant_work(N: int, K: int) -> Workload:
+    """Q4_K weights (144 B per 256) + f32 activations + Q8_K records written and
+    read once + f32 outputs; flops count one multiply-add per weight."""
+    G = K // 256
+    return Workload(f"q4k projection N{N} K{K}", 2 * N * K, N * G * 144 + K * 4 + 2 * G * 292 + N * 4)
 
 
 def moe_work(T: int, H: int, E: int, top_k: int, F: int, group: int = 128) -> Workload:

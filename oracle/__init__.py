@@ -61,8 +61,12 @@ def lib():
         _lib.orc_moe_route.argtypes = [p, i64, i64, i64, ci, p, p]
         _lib.orc_moe_align.argtypes = [p, i64, i64, i64, i64, p, i64, p, i64, p, p]
         _lib.orc_moe_ffn_w4.argtypes = [p, i64, i64, p, p, i64, i64, p, p, p, p, p, p, i64, i64, p, ci]
+        _lib.orc_q8k_quantize.argtypes = [p, i64, p]
+        _lib.orc_q4k_q8k_dot.argtypes = [p, p, i64]
+        _lib.orc_q4k_q8k_dot.restype = ctypes.c_float
+        _lib.orc_q4k_gemv.argtypes = [p, i64, i64, i64, p, p, ci]
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
-                     "orc_moe_ffn_w4"):
+                     "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
             getattr(_lib, name).restype = None
     return _lib
 
@@ -165,7 +169,82 @@ def moe_ffn_w4(x, ids, weights, wgu, sgu, zgu, wd, sd, zd, y=None, threads: int 
     return y
 
 
+Q4K_BYTES = 144
+Q8K_BYTES = 292
+
+
+def q8k_quantize(x) -> np.ndarray:
+    """f32 [G, 256] -> Q8_K records uint8 [G, 292]."""
+    x = _c(x, np.float32)
+    G = x.shape[0]
+    assert x.shape == (G, 256)
+    out = np.empty((G, Q8K_BYTES), np.uint8)
+    lib().orc_q8k_quantize(_ptr(x), G, _ptr(out))
+    return out
+
+
+def q4k_q8k_dot(w, xq) -> np.float32:
+    """Q4_K records [G, 144] . Q8_K records [G, 292] -> f32."""
+    w, xq = _c(w, np.uint8), _c(xq, np.uint8)
+    G = w.shape[0]
+    assert w.shape == (G, Q4K_BYTES) and xq.shape == (G, Q8K_BYTES)
+    return np.float32(lib().orc_q4k_q8k_dot(_ptr(w), _ptr(xq), G))
+
+
+def q4k_gemv(w, xq, threads: int = 1) -> np.ndarray:
+    """Rows of Q4_K records [N, G, 144] against one Q8_K vector [G, 292] -> f32 [N]."""
+    w, xq = _c(w, np.uint8), _c(xq, np.uint8)
+    N, G, _ = w.shape
+    y = np.empty(N, np.float32)
+    lib().orc_q4k_gemv(_ptr(w), N, G, G * Q4K_BYTES, _ptr(xq), _ptr(y), threads)
+    return y
+
+
 # ---- independent numpy restatements (used to pin the C oracle) ------------------
+
+def q4k_pack(d, dmin, sc, m, q) -> np.ndarray:
+    """Build Q4_K records from fields (the inverse of the spec's unpacking,
+    doc/dsl/quantized-operations.en.md:28-36): d, dmin f16 [G]; sc, m 6-bit [G, 8];
+    q 4-bit [G, 256]."""
+    d = np.asarray(d, np.float16).reshape(-1)
+    G = d.size
+    sc, m, q = (np.asarray(a, np.int64) for a in (sc, m, q))
+    rec = np.zeros((G, Q4K_BYTES), np.uint8)
+    rec[:, 0:2] = d.view(np.uint8).reshape(G, 2)
+    rec[:, 2:4] = np.asarray(dmin, np.float16).reshape(-1).view(np.uint8).reshape(G, 2)
+    for r, f in enumerate((sc, m)):
+        for i in range(4):
+            rec[:, 4 + 4 * r + i] |= (f[:, i] & 63).astype(np.uint8)
+            rec[:, 4 + 4 * r + i] |= ((f[:, 4 + i] >> 4) << 6).astype(np.uint8)
+            rec[:, 12 + i] |= ((f[:, 4 + i] & 15) << (4 * r)).astype(np.uint8)
+    for g in range(4):  # 64 elements per 32-byte group: low nibbles then high nibbles
+        lo = q[:, 64 * g:64 * g + 32]
+        hi = q[:, 64 * g + 32:64 * g + 64]
+        rec[:, 16 + 32 * g:48 + 32 * g] = (lo | (hi << 4)).astype(np.uint8)
+    return rec
+
+
+def q8k_fields(xq):
+    """Q8_K records [G, 292] -> ds f32 [G], q int64 [G, 256], bsum int64 [G, 16]."""
+    xq = np.asarray(xq, np.uint8)
+    ds = xq[:, 0:4].copy().view(np.float32).reshape(-1)
+    q = xq[:, 4:260].view(np.int8).astype(np.int64)
+    bsum = xq[:, 260:292].copy().view(np.int16).astype(np.int64)
+    return ds, q, bsum
+
+
+def q4k_q8k_dot_f64(wfields, xq) -> float:
+    """float64 dot of the dequantised vectors: sum_i (d*sc*q - dmin*m) * (ds*q8).
+    Equal to the record formula up to f32 rounding (bsum replaces sum(q8))."""
+    d, dmin, sc, m, q = wfields
+    ds, q8, _ = q8k_fields(xq)
+    sub = np.repeat(np.arange(8), 32)
+    w = (np.asarray(d, np.float16).astype(np.float64)[:, None] * sc[:, sub] * q
+         - np.asarray(dmin, np.float16).astype(np.float64)[:, None] * m[:, sub])
+    return float(np.sum(w * (ds.astype(np.float64)[:, None] * q8)))
+
+
+
 
 def unpack_nibbles(packed: np.ndarray) -> np.ndarray:
     """[N, K/2] uint8 -> [N, K] uint8; even k = low nibble."""

@@ -311,3 +311,99 @@ void orc_moe_ffn_w4(const uint16_t* x, int64_t T, int64_t H, const int32_t* ids,
   free(out);
   free(act);
 }
+
+/* ---- K-quant records: Q8_K quantize and Q4_K x Q8_K dot --------------------
+ * Record formats and numerics: doc/dsl/quantized-operations.en.md:11-70
+ * (Q4_K 144 bytes: f16 d, f16 dmin, 12 bytes of 6-bit sc/m, 128 bytes of
+ * nibbles; Q8_K 292 bytes: f32 ds, 256 i8, 16 i16 bsum). The same algorithm
+ * appears as the reference's RVV baseline,
+ * experiments/cpu/baselines/weft/tianchenrv/contraction/q4_k_projection/
+ * q4_k_projection.py:29-72 (quantize_row, compute), whose result starts from
+ * +0.0 and adds the records in increasing order. */
+
+static float orc_ld_f32(const uint8_t* p) {
+  float f;
+  memcpy(&f, p, 4);
+  return f;
+}
+
+/* quantized-operations.en.md:62-70. */
+void orc_q8k_quantize(const float* x, int64_t G, uint8_t* out) {
+  for (int64_t g = 0; g < G; ++g) {
+    const float* v = x + g * 256;
+    uint8_t* r = out + g * 292;
+    float mx = v[0], mn = v[0];
+    for (int i = 1; i < 256; ++i) {
+      if (v[i] > mx) mx = v[i];
+      if (v[i] < mn) mn = v[i];
+    }
+    const float extreme = fabsf(mx) > fabsf(mn) ? mx : mn; /* ties pick the minimum */
+    float inverse = 0.0f, ds = 0.0f;
+    int8_t q[256];
+    if (extreme != 0.0f) {
+      inverse = -127.0f / extreme;
+      ds = 1.0f / inverse;
+      for (int i = 0; i < 256; ++i) {
+        const float t = rintf(v[i] * inverse); /* round half to even (default mode) */
+        q[i] = (int8_t)(t > 127.0f ? 127 : t < -128.0f ? -128 : (int)t);
+      }
+    } else {
+      memset(q, 0, sizeof q);
+    }
+    memcpy(r, &ds, 4);
+    memcpy(r + 4, q, 256);
+    for (int j = 0; j < 16; ++j) {
+      int s = 0;
+      for (int i = 0; i < 16; ++i) s += q[16 * j + i];
+      const int16_t b = (int16_t)s;
+      memcpy(r + 260 + 2 * j, &b, 2);
+    }
+  }
+}
+
+/* Field r (0 = sc, 1 = m) of a Q4_K record: quantized-operations.en.md:28-36. */
+static int orc_q4k_field(const uint8_t* a, int r, int i) {
+  if (i < 4) return a[4 + 4 * r + i] & 63;
+  const int t = i - 4;
+  return ((a[12 + t] >> (4 * r)) & 15) | ((a[4 + 4 * r + t] >> 6) << 4);
+}
+
+/* v_b of one record pair: quantized-operations.en.md:44-54. */
+static float orc_q4k_q8k_record(const uint8_t* w, const uint8_t* x) {
+  int32_t S = 0, T = 0;
+  for (int s = 0; s < 8; ++s) {
+    int32_t dot = 0;
+    for (int i = 0; i < 32; ++i) {
+      const int e = 32 * s + i;
+      const int packed = w[16 + 32 * (e / 64) + (e % 32)];
+      const int q = (packed >> ((e % 64) < 32 ? 0 : 4)) & 15;
+      dot += q * (int32_t)(int8_t)x[4 + e];
+    }
+    S += orc_q4k_field(w, 0, s) * dot;
+    int16_t b0, b1;
+    memcpy(&b0, x + 260 + 2 * (2 * s), 2);
+    memcpy(&b1, x + 260 + 2 * (2 * s + 1), 2);
+    T += orc_q4k_field(w, 1, s) * ((int32_t)b0 + (int32_t)b1);
+  }
+  uint16_t dh, mh;
+  memcpy(&dh, w, 2);
+  memcpy(&mh, w + 2, 2);
+  const float p = orc_f16_to_f32(dh) * (float)S;
+  const float n = orc_f16_to_f32(mh) * (float)T;
+  const float diff = p - n;
+  return orc_ld_f32(x) * diff;
+}
+
+float orc_q4k_q8k_dot(const uint8_t* w, const uint8_t* x, int64_t G) {
+  float result = 0.0f;
+  for (int64_t g = 0; g < G; ++g) result = result + orc_q4k_q8k_record(w + 144 * g, x + 292 * g);
+  return result;
+}
+
+/* quantized_projection (examples/kernels/quantization/quantized_projection.py:5-19):
+ * y[n] = quantized_dot(w[n], quantize(x)). */
+void orc_q4k_gemv(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld, const uint8_t* xq, float* y, int threads) {
+  (void)threads;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t n = 0; n < N; ++n) y[n] = orc_q4k_q8k_dot(w + n * w_ld, xq, G);
+}

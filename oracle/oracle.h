@@ -26,4 +26,8 @@ void orc_moe_ffn_w4(const uint16_t* x, int64_t T, int64_t H, const int32_t* ids,
                     int64_t E, const uint8_t* wgu, const uint16_t* sgu, const uint8_t* zgu, const uint8_t* wd,
                     const uint16_t* sd, const uint8_t* zd, int64_t F, int64_t gs, float* y, int threads);
 
+void orc_q8k_quantize(const float* x, int64_t G, uint8_t* out);
+float orc_q4k_q8k_dot(const uint8_t* w, const uint8_t* x, int64_t G);
+void orc_q4k_gemv(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld, const uint8_t* xq, float* y, int threads);
+
 #endif

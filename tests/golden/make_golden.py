@@ -57,6 +57,14 @@ def main() -> None:
     assert np.array_equal(acc.astype(np.int64), oracle.i8_gemm_i64(d["a"], d["w"], bias))
     np.savez(HERE / "w8a8_m9_k256_n20.npz", a=d["a"], a_scales=d["a_scales"], w=d["w"], w_scales=d["w_scales"],
              out_bf16_bits=out, bias=bias, acc_i32=acc)
+    # K-quant projection: Q4_K rows x Q8_K records (bit-exact f32), with the
+    # float64 dequantised dot as the generation-time cross-check.
+    d = inputs.kquant_projection(14, N=7, K=768)
+    xq = oracle.q8k_quantize(d["x"])
+    y = oracle.q4k_gemv(d["w"], xq)
+    ds, q8, bsum = oracle.q8k_fields(xq)
+    assert np.array_equal(bsum, q8.reshape(-1, 16, 16).sum(-1))
+    np.savez(HERE / "q4k_n7_g3.npz", w=d["w"], x=d["x"], xq=xq, y=y)
     # MoE routing + alignment (exact) and a tiny expert FFN
     m = inputs.config4_moe(14, T=24, H=128, E=4, top_k=2, F=128)
     ids, wts = oracle.moe_route(m["logits"], 2, True)

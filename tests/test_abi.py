@@ -98,6 +98,22 @@ def test_moe_checks():
     assert _native.library().intent_moe_workspace_size(-1, 2, 8, 64, 64, 128) == 0
 
 
+def test_kquant_checks():
+    # Q8_K: x must be 16-byte aligned; rows of at least 256 values / 292 bytes
+    assert status("intent_q8k_quantize", FAKE + 4, 3, 256, FAKE, 292, None) == errors.INTENT_ERR_ALIGNMENT
+    assert status("intent_q8k_quantize", FAKE, 3, 128, FAKE, 292, None) == errors.INTENT_ERR_INVALID_ARGUMENT
+    assert status("intent_q8k_quantize", FAKE, 3, 256, FAKE, 291, None) == errors.INTENT_ERR_INVALID_ARGUMENT
+    assert status("intent_q8k_quantize", None, 0, 256, None, 292, None) == 0  # G = 0: nothing to do
+    # Q4_K rows: stride below G records, misaligned rows, null inputs
+    assert status("intent_q4k_q8k_gemv", FAKE, 4, 3, 400, FAKE, FAKE, None) == errors.INTENT_ERR_INVALID_ARGUMENT
+    assert status("intent_q4k_q8k_gemv", FAKE, 4, 3, 440, FAKE, FAKE, None) == errors.INTENT_ERR_ALIGNMENT
+    assert status("intent_q4k_q8k_gemv", FAKE, 4, 3, 432, FAKE + 2, FAKE, None) == errors.INTENT_ERR_ALIGNMENT
+    assert status("intent_q4k_q8k_gemv", None, 4, 3, 432, FAKE, FAKE, None) == errors.INTENT_ERR_INVALID_ARGUMENT
+    assert status("intent_q4k_q8k_gemv", FAKE, 0, 3, 432, FAKE, FAKE, None) == 0  # N = 0
+    assert status("intent_q4k_projection", FAKE, 4, 3, 432, FAKE + 8, 256, FAKE, FAKE, None) == \
+        errors.INTENT_ERR_ALIGNMENT
+
+
 def test_status_mapping():
     assert isinstance(errors.status_error(-1, "e", "m"), ValueError)
     assert isinstance(errors.status_error(-2, "e", "m"), ValueError)

@@ -314,3 +314,53 @@ def test_golden_moe(gpu):
     art(intent.moe_expert_ffn_w4, TOP_K=2)(dev(g["logits"]), dev(g["x"]), dev(g["wgu"]), dev(g["sgu"]),
                                            dev(g["zgu"]), dev(g["wd"]), dev(g["sd"]), dev(g["zd"]), y)
     assert_close_rms(host(y), g["y_f64"], what="moe golden")
+
+
+# ---- K-quant records: bit-exact against the oracle ---------------------------------
+
+def _bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def _kquant_x(seed, G):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((G, 256)) * rng.uniform(0.001, 1000.0, (G, 1))).astype(np.float32)
+    if G >= 4:
+        x[1] = 0.0                                  # all-zero block
+        x[2, :] = 0.25
+        x[2, 7], x[2, 9] = 3.0, -3.0                # tie: the minimum is the extreme
+        x[3, 0] = -127.0                            # inverse 1: exact half-way products
+        x[3, 1:6] = [0.5, 1.5, 2.5, -0.5, -1.5]
+        x[3, 6:] = -0.0
+    return x
+
+
+@pytest.mark.parametrize("G", [1, 4, 5, 64, 333])
+def test_q8k_quantize_bit_exact(gpu, G):
+    x = _kquant_x(20 + G, G)
+    rec = art(intent.q8_k_quantize).run(dev(x))
+    assert np.array_equal(host(rec), oracle.q8k_quantize(x))
+
+
+@pytest.mark.parametrize("N,G", [(1, 1), (7, 3), (100, 16), (33, 17), (5, 40), (4, 0)])
+def test_q4k_q8k_dot_bit_exact(gpu, N, G):
+    rng = np.random.default_rng(N * 100 + G)
+    w = inputs.q4k_records(rng, (N, G))
+    xq = oracle.q8k_quantize(_kquant_x(N + G, G)) if G else np.zeros((0, 292), np.uint8)
+    y = art(intent.q4_k_q8_k_dot).run(dev(w), dev(xq))
+    ref = oracle.q4k_gemv(w, xq) if G else np.zeros(N, np.float32)
+    assert np.array_equal(_bits(host(y)), _bits(ref))
+
+
+def test_quantized_projection_full_size_bit_exact(gpu, threads):
+    d = inputs.kquant_projection(0, N=4096, K=4096)
+    y = art(intent.quantized_projection).run(dev(d["w"]), dev(d["x"]))
+    ref = oracle.q4k_gemv(d["w"], oracle.q8k_quantize(d["x"]), threads)
+    assert np.array_equal(_bits(host(y)), _bits(ref))
+
+
+def test_golden_kquant(gpu):
+    g = np.load(GOLDEN / "q4k_n7_g3.npz")
+    assert np.array_equal(host(art(intent.q8_k_quantize).run(dev(g["x"]))), g["xq"])
+    y = art(intent.quantized_projection).run(dev(g["w"]), dev(g["x"]))
+    assert np.array_equal(_bits(host(y)), _bits(g["y"]))

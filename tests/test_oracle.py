@@ -254,3 +254,137 @@ def test_moe_ffn_accumulates_in_slot_order():
     y = oracle.moe_ffn_w4(m["x"], ids1, w1, m["wgu"], m["sgu"], m["zgu"], m["wd"], m["sd"], m["zd"])
     y64 = oracle.moe_ffn_f64(m["x"], ids1, w1, m["wgu"], m["sgu"], m["zgu"], m["wd"], m["sd"], m["zd"])
     assert np.max(np.abs(y - y64)) <= 1e-2 * rms(y64)
+
+
+# ---- K-quant records (doc/dsl/quantized-operations.en.md:11-70) -------------------
+
+def _q4k_fields(rng, G):
+    d = rng.uniform(0.001, 0.05, G).astype(np.float16)
+    dmin = rng.uniform(0.001, 0.05, G).astype(np.float16)
+    sc = rng.integers(0, 64, (G, 8))
+    m = rng.integers(0, 64, (G, 8))
+    q = rng.integers(0, 16, (G, 256))
+    return d, dmin, sc, m, q
+
+
+def _q8k_record(ds, q8):
+    """Q8_K records from ds f32 [G] and q int [G,256] (bsum = exact sums)."""
+    q8 = np.asarray(q8, np.int64)
+    G = q8.shape[0]
+    rec = np.zeros((G, oracle.Q8K_BYTES), np.uint8)
+    rec[:, 0:4] = np.asarray(ds, np.float32).reshape(G, 1).view(np.uint8)
+    rec[:, 4:260] = q8.astype(np.int8).view(np.uint8)
+    rec[:, 260:292] = q8.reshape(G, 16, 16).sum(-1).astype(np.int16).view(np.uint8).reshape(G, 32)
+    return rec
+
+
+def test_q4k_nibble_and_field_layout_known_answers():
+    # One nonzero weight at element e, one nonzero activation at the same e:
+    # the dot is d * sc[e // 32] * q * x exactly, which pins the nibble placement
+    # (quantized-operations.en.md:31-36) and the 6-bit field unpacking.
+    for e in (0, 1, 31, 32, 33, 63, 64, 100, 127, 128, 191, 200, 255):
+        for s_val in (1, 5, 63):
+            sc = np.zeros((1, 8), np.int64)
+            sc[0, e // 32] = s_val
+            q = np.zeros((1, 256), np.int64)
+            q[0, e] = 11
+            w = oracle.q4k_pack(np.float16(0.5), np.float16(0.0), sc, np.zeros((1, 8)), q)
+            q8 = np.zeros((1, 256), np.int64)
+            q8[0, e] = -3
+            xq = _q8k_record(np.float32(2.0), q8)
+            assert oracle.q4k_q8k_dot(w, xq) == np.float32(0.5 * s_val * 11 * -3 * 2.0)
+            q8[0, e] = 0
+            q8[0, e ^ 1] = 7  # a neighbouring element contributes nothing
+            assert oracle.q4k_q8k_dot(w, _q8k_record(np.float32(2.0), q8)) == 0.0
+
+
+def test_q4k_min_term_uses_bsum_pairs():
+    # d = 0: the result is -ds * dmin * sum_s m[s] * (bsum[2s] + bsum[2s+1]).
+    rng = np.random.default_rng(5)
+    m = rng.integers(0, 64, (1, 8))
+    q8 = rng.integers(-127, 128, (1, 256))
+    w = oracle.q4k_pack(np.float16(0.0), np.float16(0.25), np.zeros((1, 8)), m, np.zeros((1, 256)))
+    xq = _q8k_record(np.float32(0.125), q8)
+    T = int(sum(m[0, s] * q8[0, 64 * s // 2:64 * s // 2 + 32].sum() for s in range(8)))
+    assert oracle.q4k_q8k_dot(w, xq) == np.float32(-0.125 * np.float32(0.25 * T))
+
+
+def test_q4k_zero_records_are_zero():
+    # examples/programs/matrix.py:48-52: a zero-filled record has zero scales.
+    xq = oracle.q8k_quantize(np.random.default_rng(1).standard_normal((3, 256)).astype(np.float32))
+    r = oracle.q4k_q8k_dot(np.zeros((3, 144), np.uint8), xq)
+    assert r == 0.0 and not np.signbit(r)
+    assert oracle.q4k_q8k_dot(np.zeros((0, 144), np.uint8), np.zeros((0, 292), np.uint8)) == 0.0
+
+
+def test_q4k_dot_matches_float64_dequantised_dot():
+    rng = np.random.default_rng(7)
+    for G in (1, 2, 5, 16):
+        f = _q4k_fields(rng, G)
+        w = oracle.q4k_pack(*f)
+        xq = oracle.q8k_quantize(rng.standard_normal((G, 256)).astype(np.float32))
+        got = float(oracle.q4k_q8k_dot(w, xq))
+        ref = oracle.q4k_q8k_dot_f64(f, xq)
+        assert abs(got - ref) <= 1e-5 * max(1.0, abs(ref)), (G, got, ref)
+
+
+def test_q4k_record_order_and_rounding():
+    # The result is ((+0 + v0) + v1) + ... in f32: per-record values from
+    # single-record calls, summed in order with numpy f32, give the same bits.
+    rng = np.random.default_rng(9)
+    G = 11
+    w = oracle.q4k_pack(*_q4k_fields(rng, G))
+    xq = oracle.q8k_quantize((rng.standard_normal((G, 256)) * 10).astype(np.float32))
+    acc = np.float32(0.0)
+    for b in range(G):
+        acc = np.float32(acc + oracle.q4k_q8k_dot(w[b:b + 1], xq[b:b + 1]))
+    assert oracle.q4k_q8k_dot(w, xq).view(np.uint32) == acc.view(np.uint32)
+
+
+def test_q4k_gemv_rows_match_single_dots():
+    rng = np.random.default_rng(3)
+    w = rng.integers(0, 256, (6, 4, 144), dtype=np.uint8)
+    w[..., 0:4] = rng.uniform(0.001, 0.01, (6, 4, 2)).astype(np.float16).view(np.uint8).reshape(6, 4, 4)
+    xq = oracle.q8k_quantize(rng.standard_normal((4, 256)).astype(np.float32))
+    y = oracle.q4k_gemv(w, xq, threads=2)
+    assert all(y[n].view(np.uint32) == oracle.q4k_q8k_dot(w[n], xq).view(np.uint32) for n in range(6))
+
+
+def test_q8k_quantize_properties():
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((64, 256)) * rng.uniform(0.01, 100, (64, 1))).astype(np.float32)
+    xq = oracle.q8k_quantize(x)
+    ds, q, bsum = oracle.q8k_fields(xq)
+    assert np.array_equal(bsum, q.reshape(64, 16, 16).sum(-1))
+    # The extreme value maps to -127 (its sign flips through the negative inverse).
+    ext = np.where(np.abs(x.max(1)) > np.abs(x.min(1)), x.max(1), x.min(1))
+    idx = np.argmax(x == ext[:, None], axis=1)
+    assert np.all(q[np.arange(64), idx] == -127)
+    # Reconstruction error is at most half a step.
+    err = np.abs(ds[:, None].astype(np.float64) * q - x)
+    assert np.all(err <= 0.5 * np.abs(ds[:, None]) * (1 + 1e-5))
+    # ds is exactly 1 / inverse with inverse = -127 / extreme (two f32 divisions).
+    inv = np.float32(-127.0) / ext.astype(np.float32)
+    assert np.array_equal(ds, (np.float32(1.0) / inv).astype(np.float32))
+
+
+def test_q8k_quantize_ties_zero_block_and_rounding():
+    x = np.zeros((3, 256), np.float32)
+    x[0, 3], x[0, 9] = 2.0, -2.0  # |max| == |min|: the minimum is the extreme
+    x[2, :] = np.linspace(-1, 1, 256, dtype=np.float32)
+    xq = oracle.q8k_quantize(x)
+    ds, q, bsum = oracle.q8k_fields(xq)
+    assert q[0, 9] == -127 and q[0, 3] == 127 and ds[0] > 0
+    assert not xq[1].any()  # all-zero block: ds=+0, q=0, bsum=0
+    # Half-way products round to even: x = k + 0.5 steps.
+    y = np.zeros((1, 256), np.float32)
+    y[0, 0] = -127.0  # inverse = 1, ds = 1
+    y[0, 1:6] = [0.5, 1.5, 2.5, -0.5, -1.5]
+    _, q1, _ = oracle.q8k_fields(oracle.q8k_quantize(y))
+    assert list(q1[0, :6]) == [-127, 0, 2, 2, 0, -2]
+
+
+def test_kquant_golden():
+    g = np.load(GOLDEN / "q4k_n7_g3.npz")
+    assert np.array_equal(oracle.q8k_quantize(g["x"]), g["xq"])
+    assert np.array_equal(oracle.q4k_gemv(g["w"], g["xq"]).view(np.uint32), g["y"].view(np.uint32))
