@@ -267,6 +267,21 @@ int intent_q4k_projection(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld,
                           const float* x, int64_t x_ld, uint8_t* xq_records,
                           float* y, void* stream);
 
+/*
+ * Groupwise FP8 activation quantizer, bit-exact: for each row and group of
+ * 128 columns, scale = max(absmax, eps) / 448 (eps = 1e-12 for bf16 input,
+ * 1e-4 for f32), q = E4M3FN(min(max(x / scale, -448), 448)) rounded to
+ * nearest even. x is f32 or bf16 (x_is_bf16) [M, N] with row stride x_ld
+ * elements; q E4M3FN bytes [M, N] (row stride q_ld); scales f32 [M, G]
+ * (G >= ceil(N/128); groups past N get eps / 448). Replaces
+ * bf16_groupwise_fp8_quantize / f32_groupwise_fp8_quantize
+ * (examples/kernels/quantization/fp8.py:11-69; CPU side
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:142-147). N % 4 == 0.
+ */
+int intent_fp8_groupwise_quantize(const void* x, int x_is_bf16, int64_t M, int64_t N,
+                                  int64_t x_ld, uint8_t* q, int64_t q_ld, float* scales,
+                                  int64_t G, int64_t scales_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

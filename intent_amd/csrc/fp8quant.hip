@@ -1,0 +1,94 @@
+// Groupwise FP8 (OCP E4M3FN) activation quantizers for gfx950, bit-exact:
+//   scale = max(absmax over a group of 128 columns, eps) / 448
+//   q     = e4m3fn(min(max(x / scale, -448), 448)), round to nearest even
+// (examples/kernels/quantization/fp8.py:11-69; eps 1e-12 for bf16 input,
+// 1e-4 for f32 input). Every division is IEEE f32; the E4M3FN rounding is done
+// in integer arithmetic, so the bytes equal a CPU evaluation of the formula.
+#include "common.h"
+#include "internal.h"
+
+namespace {
+
+// f32 -> E4M3FN bits, round half to even; |f| >= 448 saturates to 448, NaN -> NaN.
+INTENT_DEVICE uint32_t f32_to_e4m3fn(float f) {
+  const uint32_t u = bit_cast<uint32_t>(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  const float mag = bit_cast<float>(a);
+  if (mag >= 448.0f) return sign | 0x7eu;
+  if (mag < 0.015625f) return sign | (uint32_t)rintf(mag * 512.0f);  // subnormal step 2^-9
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  return sign | ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+}
+
+// Thread t of a 32-lane half-wave holds columns 4t..4t+3 of its group.
+template <bool kBf16>
+__global__ __launch_bounds__(256) void fp8_groupwise_kernel(const void* __restrict__ xv, int64_t ldx, int M, int N,
+                                                            int G, float eps, uint8_t* __restrict__ q, int64_t ldq,
+                                                            float* __restrict__ scales, int64_t lds) {
+  const int pair = blockIdx.x * 8 + (threadIdx.x >> 5);
+  const bool active = pair < M * G;
+  const int row = active ? pair / G : 0;
+  const int g = active ? pair % G : 0;
+  const int c = g * 128 + (threadIdx.x & 31) * 4;
+  const bool has = active && c < N;  // N % 4 == 0: all four columns or none
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (has) {
+    if constexpr (kBf16) {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(xv) + (int64_t)row * ldx + c);
+      v[0] = bit_cast<float>(w[0] << 16);
+      v[1] = bit_cast<float>(w[0] & 0xffff0000u);
+      v[2] = bit_cast<float>(w[1] << 16);
+      v[3] = bit_cast<float>(w[1] & 0xffff0000u);
+    } else {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(xv) + (int64_t)row * ldx + c);
+      v[0] = w[0], v[1] = w[1], v[2] = w[2], v[3] = w[3];
+    }
+  }
+  float amax = has ? fmaxf(fmaxf(fmaxf(v[0], -v[0]), fmaxf(v[1], -v[1])), fmaxf(fmaxf(v[2], -v[2]), fmaxf(v[3], -v[3])))
+                   : -INFINITY;
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  const float scale = __fdiv_rn(fmaxf(amax, eps), 448.0f);
+  if (has) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float t = fminf(fmaxf(__fdiv_rn(v[i], scale), -448.0f), 448.0f);
+      packed |= f32_to_e4m3fn(t) << (8 * i);
+    }
+    *reinterpret_cast<uint32_t*>(q + (int64_t)row * ldq + c) = packed;
+  }
+  if (active && (threadIdx.x & 31) == 0) scales[(int64_t)row * lds + g] = scale;
+}
+
+}  // namespace
+
+extern "C" int intent_fp8_groupwise_quantize(const void* x, int x_is_bf16, int64_t M, int64_t N, int64_t x_ld,
+                                             uint8_t* q, int64_t q_ld, float* scales, int64_t G, int64_t scales_ld,
+                                             void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && G >= 0 && M <= INT32_MAX && N <= INT32_MAX && M * G <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents (M=%lld N=%lld G=%lld)", (long long)M, (long long)N,
+                 (long long)G);
+  INTENT_REQUIRE(G * 128 >= N, INTENT_ERR_INVALID_ARGUMENT, "%lld groups of 128 do not cover N=%lld", (long long)G,
+                 (long long)N);
+  INTENT_REQUIRE(N % 4 == 0, INTENT_ERR_UNSUPPORTED, "N must be a multiple of 4, got %lld", (long long)N);
+  if (M == 0 || G == 0) return INTENT_OK;
+  INTENT_REQUIRE(x && q && scales, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(x_ld >= N && q_ld >= N && scales_ld >= G, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  const uintptr_t xa = reinterpret_cast<uintptr_t>(x);
+  INTENT_REQUIRE((x_is_bf16 ? (xa & 7) == 0 : (xa & 15) == 0) && x_ld % 4 == 0 && intent::aligned4(q) &&
+                     q_ld % 4 == 0,
+                 INTENT_ERR_ALIGNMENT, "x must be 8 (bf16) / 16 (f32) byte aligned with x_ld %% 4 == 0; q 4-byte aligned");
+  const unsigned blocks = (unsigned)((M * G + 7) / 8);
+  if (x_is_bf16)
+    hipLaunchKernelGGL((fp8_groupwise_kernel<true>), dim3(blocks), dim3(256), 0, (hipStream_t)stream, x, x_ld, (int)M,
+                       (int)N, (int)G, 1.0e-12f, q, q_ld, scales, scales_ld);
+  else
+    hipLaunchKernelGGL((fp8_groupwise_kernel<false>), dim3(blocks), dim3(256), 0, (hipStream_t)stream, x, x_ld,
+                       (int)M, (int)N, (int)G, 1.0e-4f, q, q_ld, scales, scales_ld);
+  return intent::launch_status("fp8_groupwise_quantize");
+}

@@ -479,8 +479,43 @@ quantized_projection = KernelDefinition(
 )
 
 
+# ---- groupwise FP8 activation quantizers -----------------------------------------
+
+def _fp8q_check(env: dict) -> None:
+    if env["G"] * 128 < env["N"]:
+        raise ValueError(f"scales.shape[1] ({env['G']}) groups of 128 do not cover N ({env['N']})")
+
+
+def _fp8q_launch(bf16: bool):
+    def launch(v: dict, env: dict, stream: int, workspace) -> str:
+        x, q, sc = v["x"], v["quantized"], v["scales"]
+        _native.call("intent_fp8_groupwise_quantize", _ptr(x), int(bf16), env["M"], env["N"], _ld(x), _ptr(q), _ld(q),
+                     _ptr(sc), env["G"], _ld(sc), stream)
+        return "intent_fp8_groupwise_quantize"
+    return launch
+
+
+def _fp8q_definition(name: str, src: str, lines: str) -> KernelDefinition:
+    return KernelDefinition(
+        name=name,
+        params=(
+            Param("x", src, ("M", "N"), leading_stride=True),
+            Param("quantized", "f8e4m3fn", ("M", "N"), OUT, leading_stride=True),
+            Param("scales", "f32", ("M", "G"), INOUT, leading_stride=True),
+        ),
+        launch=_fp8q_launch(src == "bf16"),
+        check=_fp8q_check,
+        reference=f"examples/kernels/quantization/fp8.py:{lines}",
+        doc="scale = max(absmax of 128 columns, eps) / 448; quantized = e4m3fn(clamp(x / scale, +-448))",
+    )
+
+
+bf16_groupwise_fp8_quantize = _fp8q_definition("bf16_groupwise_fp8_quantize", "bf16", "11-39")
+f32_groupwise_fp8_quantize = _fp8q_definition("f32_groupwise_fp8_quantize", "f32", "42-69")
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
-    q8_k_quantize, q4_k_q8_k_dot, quantized_projection,
+    q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
 )

@@ -42,6 +42,7 @@ DTYPES = {
     "i32": DType("i32", 32, "signed"),
     "i64": DType("i64", 64, "signed"),
     "bool": DType("bool", 8, "bool"),
+    "f8e4m3fn": DType("f8e4m3fn", 8, "float"),
 }
 
 
@@ -56,7 +57,8 @@ def torch_dtype(element: DType):
     import torch
 
     return {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32, "i8": torch.int8,
-            "u8": torch.uint8, "i32": torch.int32, "i64": torch.int64, "bool": torch.bool}[element.name]
+            "u8": torch.uint8, "i32": torch.int32, "i64": torch.int64, "bool": torch.bool,
+            "f8e4m3fn": torch.float8_e4m3fn}[element.name]
 
 
 @dataclass(frozen=True, slots=True)

@@ -65,6 +65,10 @@ def lib():
         _lib.orc_q4k_q8k_dot.argtypes = [p, p, i64]
         _lib.orc_q4k_q8k_dot.restype = ctypes.c_float
         _lib.orc_q4k_gemv.argtypes = [p, i64, i64, i64, p, p, ci]
+        _lib.orc_f32_to_e4m3fn.argtypes = [ctypes.c_float]
+        _lib.orc_f32_to_e4m3fn.restype = ctypes.c_uint8
+        _lib.orc_fp8_groupwise_quantize.argtypes = [p, i64, i64, i64, i64, ctypes.c_float, p, i64, p, i64]
+        _lib.orc_fp8_groupwise_quantize.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
             getattr(_lib, name).restype = None
@@ -198,6 +202,26 @@ def q4k_gemv(w, xq, threads: int = 1) -> np.ndarray:
     y = np.empty(N, np.float32)
     lib().orc_q4k_gemv(_ptr(w), N, G, G * Q4K_BYTES, _ptr(xq), _ptr(y), threads)
     return y
+
+
+FP8_EPS = {"bf16": 1.0e-12, "f32": 1.0e-4}  # examples/kernels/quantization/fp8.py:33,63
+
+
+def fp8_groupwise_quantize(x, groups: int | None = None, source: str = "f32"):
+    """[M, N] values (f32, or bf16 widened exactly to f32) -> (E4M3FN bits uint8 [M, N],
+    scales f32 [M, groups]); groups defaults to ceil(N / 128)."""
+    x = _c(x, np.float32)
+    M, N = x.shape
+    G = groups if groups is not None else (N + 127) // 128
+    q = np.empty((M, N), np.uint8)
+    sc = np.empty((M, G), np.float32)
+    lib().orc_fp8_groupwise_quantize(_ptr(x), M, N, N, G, FP8_EPS[source], _ptr(q), N, _ptr(sc), G)
+    return q, sc
+
+
+def f32_to_e4m3fn(values) -> np.ndarray:
+    v = np.asarray(values, np.float32).reshape(-1)
+    return np.array([lib().orc_f32_to_e4m3fn(float(f)) for f in v], np.uint8)
 
 
 # ---- independent numpy restatements (used to pin the C oracle) ------------------

@@ -407,3 +407,54 @@ void orc_q4k_gemv(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld, const ui
 #pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
   for (int64_t n = 0; n < N; ++n) y[n] = orc_q4k_q8k_dot(w + n * w_ld, xq, G);
 }
+
+/* ---- groupwise FP8 (E4M3FN) activation quantizers ---------------------------
+ * examples/kernels/quantization/fp8.py:11-69 (bf16_groupwise_fp8_quantize,
+ * f32_groupwise_fp8_quantize), the same as the reference's CPU comparison
+ * side experiments/cpu/baselines/pytorch/cpu_runtime.py:142-147:
+ *   scale = max(absmax(group of 128), eps) / 448      (eps 1e-12 bf16, 1e-4 f32)
+ *   q     = e4m3fn(min(max(x / scale, -448), 448))    (round to nearest even)
+ * Columns past N belong to no group element (masked out of the max). */
+
+/* f32 -> OCP E4M3FN bits (bias 7, no infinities, NaN = S.1111.111), round to
+ * nearest even. Inputs of magnitude above 448 saturate to 448 (callers clamp
+ * first, so this never triggers for the quantizers). */
+uint8_t orc_f32_to_e4m3fn(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7f); /* NaN */
+  float mag;
+  memcpy(&mag, &a, 4);
+  if (mag >= 448.0f) return (uint8_t)(sign | 0x7e);
+  if (mag < 0.015625f) { /* below 2^-6: subnormal step 2^-9 */
+    const float m = rintf(mag * 512.0f); /* exact scaling, then round half even */
+    return (uint8_t)(sign | (uint8_t)m);  /* m == 8 is the smallest normal, 0x08 */
+  }
+  /* normal: keep 3 mantissa bits, round half to even on the 20 dropped bits */
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  const uint32_t e = (r >> 23) - 127 + 7;
+  const uint32_t m = (r >> 20) & 7u;
+  return (uint8_t)(sign | (e << 3) | m);
+}
+
+void orc_fp8_groupwise_quantize(const float* x, int64_t M, int64_t N, int64_t ldx, int64_t G, float eps,
+                                uint8_t* q, int64_t ldq, float* scales, int64_t lds_) {
+  for (int64_t r = 0; r < M; ++r) {
+    for (int64_t g = 0; g < G; ++g) {
+      float amax = -INFINITY;
+      for (int64_t c = g * 128; c < g * 128 + 128 && c < N; ++c) {
+        const float v = x[r * ldx + c];
+        const float av = fmaxf(v, -v);
+        if (av > amax) amax = av;
+      }
+      const float scale = fmaxf(amax, eps) / 448.0f;
+      scales[r * lds_ + g] = scale;
+      for (int64_t c = g * 128; c < g * 128 + 128 && c < N; ++c) {
+        const float t = x[r * ldx + c] / scale;
+        q[r * ldq + c] = orc_f32_to_e4m3fn(fminf(fmaxf(t, -448.0f), 448.0f));
+      }
+    }
+  }
+}

@@ -29,5 +29,8 @@ void orc_moe_ffn_w4(const uint16_t* x, int64_t T, int64_t H, const int32_t* ids,
 void orc_q8k_quantize(const float* x, int64_t G, uint8_t* out);
 float orc_q4k_q8k_dot(const uint8_t* w, const uint8_t* x, int64_t G);
 void orc_q4k_gemv(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld, const uint8_t* xq, float* y, int threads);
+uint8_t orc_f32_to_e4m3fn(float f);
+void orc_fp8_groupwise_quantize(const float* x, int64_t M, int64_t N, int64_t ldx, int64_t G, float eps,
+                                uint8_t* q, int64_t ldq, float* scales, int64_t lds_);
 
 #endif

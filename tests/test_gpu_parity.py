@@ -364,3 +364,26 @@ def test_golden_kquant(gpu):
     assert np.array_equal(host(art(intent.q8_k_quantize).run(dev(g["x"]))), g["xq"])
     y = art(intent.quantized_projection).run(dev(g["w"]), dev(g["x"]))
     assert np.array_equal(_bits(host(y)), _bits(g["y"]))
+
+
+# ---- groupwise FP8 quantizers: bit-exact against the oracle ----------------------
+
+@pytest.mark.parametrize("src", ["f32", "bf16"])
+@pytest.mark.parametrize("M,N,G", [(1, 128, 1), (3, 300, 3), (17, 4096, 32), (2, 256, 4), (64, 8192, 64)])
+def test_fp8_groupwise_quantize_bit_exact(gpu, src, M, N, G):
+    rng = np.random.default_rng(M * 7 + N)
+    x = (rng.standard_normal((M, N)) * rng.uniform(1e-6, 1e4, (M, 1))).astype(np.float32)
+    x[0, :5] = [0.0, -0.0, 1e-30, -448.0, 3.0]
+    x[-1, : min(N, 128)] = 0.0  # an all-zero group takes the eps floor
+    if src == "bf16":
+        xt = torch.from_numpy(x).to(torch.bfloat16)
+        x = xt.float().numpy()  # exact widening: the oracle sees the same values
+        defn = intent.bf16_groupwise_fp8_quantize
+    else:
+        xt = torch.from_numpy(x)
+        defn = intent.f32_groupwise_fp8_quantize
+    scales = torch.zeros(M, G, dtype=torch.float32, device="cuda")
+    q = art(defn).run(xt.cuda(), scales)
+    ref_q, ref_s = oracle.fp8_groupwise_quantize(x, groups=G, source=src)
+    assert np.array_equal(host(q.view(torch.uint8)), ref_q)
+    assert np.array_equal(host(scales).view(np.uint32), ref_s.view(np.uint32))

@@ -388,3 +388,45 @@ def test_kquant_golden():
     g = np.load(GOLDEN / "q4k_n7_g3.npz")
     assert np.array_equal(oracle.q8k_quantize(g["x"]), g["xq"])
     assert np.array_equal(oracle.q4k_gemv(g["w"], g["xq"]).view(np.uint32), g["y"].view(np.uint32))
+
+
+# ---- groupwise FP8 quantizers (examples/kernels/quantization/fp8.py:11-69) ---------
+
+def test_e4m3fn_conversion_matches_torch():
+    # torch's float8_e4m3fn cast (round to nearest even) is an independent routine.
+    rng = np.random.default_rng(2)
+    grid = np.concatenate([
+        np.linspace(-448, 448, 20001, dtype=np.float32),
+        (rng.standard_normal(20000) * np.exp2(rng.uniform(-12, 8, 20000))).astype(np.float32),
+        np.float32([0.0, -0.0, 2.0 ** -9, 2.0 ** -10, 3 * 2.0 ** -11, 2.0 ** -6, 448.0, -448.0, 1.0625, 1.1875]),
+    ])
+    grid = np.clip(grid, -448, 448).astype(np.float32)
+    want = torch.from_numpy(grid).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.f32_to_e4m3fn(grid), want)
+
+
+@pytest.mark.parametrize("M,N", [(3, 256), (5, 300), (2, 129)])
+def test_fp8_groupwise_matches_reference_cpu_formula(M, N):
+    # experiments/cpu/baselines/pytorch/cpu_runtime.py:142-147 restated with torch
+    # (padding the last group with zeros leaves its max unchanged for |x| >= 0).
+    rng = np.random.default_rng(M * N)
+    x = (rng.standard_normal((M, N)) * rng.uniform(1e-6, 1e3, (M, 1))).astype(np.float32)
+    x[0, :7] = 0.0
+    q, sc = oracle.fp8_groupwise_quantize(x)
+    G = (N + 127) // 128
+    t = torch.zeros(M, G * 128)
+    t[:, :N] = torch.from_numpy(x)
+    v = t.reshape(M, G, 128)
+    scale = v.abs().amax(dim=-1).clamp_min(1e-4) / 448.0
+    ref = (v / scale[:, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).reshape(M, -1)[:, :N]
+    assert np.array_equal(sc, scale.numpy())
+    assert np.array_equal(q, ref.view(torch.uint8).numpy())
+
+
+def test_fp8_groupwise_bf16_eps_and_zero_group():
+    x = np.zeros((1, 256), np.float32)
+    q, sc = oracle.fp8_groupwise_quantize(x, source="bf16")
+    assert not q.any() and np.all(sc == np.float32(np.float32(1e-12) / np.float32(448.0)))
+    x[0, 130] = -3.5  # group 1's extreme maps to -448 exactly
+    q, sc = oracle.fp8_groupwise_quantize(x, source="bf16")
+    assert q[0, 130] == 0xFE and sc[0, 1] == np.float32(3.5) / np.float32(448.0)
