@@ -170,6 +170,27 @@ def bench_q4k(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": n}
 
 
+def bench_w4a8(steps: int, warmup: int) -> dict:
+    """The reference's W4A8 case (experiments/cpu/providers/mojo/contraction.py:201-206)."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    rng = np.random.default_rng(0)
+    M, K, N = 4096, 4096, 14336
+    a = torch.from_numpy(rng.integers(-128, 128, (M, K), dtype=np.int8)).cuda()
+    p = torch.from_numpy(rng.integers(0, 256, (N, K // 2), dtype=np.uint8)).cuda()
+    work = inputs.Workload(f"w4a8 M{M} K{K} N{N}", 2 * M * N * K, M * K + N * K // 2 + M * N * 4)
+    art = intent.compile(intent.w4a8_packed_matmul, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes, minimum=2)
+    calls = [art.prepare(a.clone(), p.clone()) for _ in range(n)]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE profile."""
     path = ROOT / "profiles" / "w4a16_gemv_dot_m1_traffic.md"
@@ -285,6 +306,9 @@ def main() -> int:
         log("[bench] w8a16 M=16")
         r = bench_w8a16(args.steps, args.warmup)
         extra["w8a16_m16"] = _hbm_entry(r)
+        log("[bench] w4a8 M=4096 K=4096 N=14336")
+        r = bench_w4a8(steps, warm)
+        extra["w4a8_m4096_n14336"] = _flop_entry(r, I8_PEAK_TOPS, "TOP/s")
         log("[bench] q4_k projection N=K=4096")
         r = bench_q4k(args.steps, args.warmup)
         extra["q4k_projection_n4096"] = _hbm_entry(r)

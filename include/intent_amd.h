@@ -282,6 +282,28 @@ int intent_fp8_groupwise_quantize(const void* x, int x_is_bf16, int64_t M, int64
                                   int64_t x_ld, uint8_t* q, int64_t q_ld, float* scales,
                                   int64_t G, int64_t scales_ld, void* stream);
 
+/*
+ * Low-bit weight x int8 activation GEMMs, exact int32 (modulo 2^32).
+ * a: int8 [M, K] (row stride a_ld, 16-byte aligned rows); K % 128 == 0.
+ *
+ * intent_w4a8_gemm: w_packed u8 [N, K/2] (row stride w_ld bytes, 8-byte
+ * aligned), two's-complement nibbles, low nibble = even k;
+ * out[n, m] = sum_k w[n, k] * a[m, k], out int32 [N, M] (row stride out_ld).
+ * Replaces w4a8_packed_matmul (examples/kernels/contraction/
+ * weight_only_int4.py:54-91).
+ *
+ * intent_bitnet_int2_gemm: w_packed u8 [N, K/4] (row stride w_ld bytes,
+ * 4-byte aligned), values 0..3 interleaved: k in byte (k/16)*4 + k%4 at bit
+ * 2*((k/4)%4); out[m, n] = sum_k a[m, k] * w[n, k], out int32 [M, N].
+ * Replaces bitnet_int2_matmul (weight_only_int4.py:94-124).
+ */
+int intent_w4a8_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                     const uint8_t* w_packed, int64_t N, int64_t w_ld,
+                     int32_t* out, int64_t out_ld, void* stream);
+int intent_bitnet_int2_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                            const uint8_t* w_packed, int64_t N, int64_t w_ld,
+                            int32_t* out, int64_t out_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

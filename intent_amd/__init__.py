@@ -17,6 +17,7 @@ from .compiler import CompileOptions, MI355XTarget, compile
 from .definitions import (
     ALL_DEFINITIONS,
     KernelDefinition,
+    bitnet_int2_matmul,
     bf16_groupwise_fp8_quantize,
     f32_groupwise_fp8_quantize,
     gemm_i8_nt,
@@ -29,6 +30,7 @@ from .definitions import (
     q4_k_q8_k_dot,
     q8_k_quantize,
     quantized_projection,
+    w4a8_packed_matmul,
     w8a8_scaled_matmul,
     weight_only_int4_asym_matmul,
     weight_only_int8_matmul,
@@ -45,7 +47,7 @@ def kernel(function=None):
 
 
 __all__ = [
-    "ALL_DEFINITIONS", "CompilationStageError", "bf16_groupwise_fp8_quantize", "f32_groupwise_fp8_quantize", "CompileOptions", "CompiledArtifact", "DType", "KernelDefinition",
+    "ALL_DEFINITIONS", "CompilationStageError", "bitnet_int2_matmul", "w4a8_packed_matmul", "bf16_groupwise_fp8_quantize", "f32_groupwise_fp8_quantize", "CompileOptions", "CompiledArtifact", "DType", "KernelDefinition",
     "LanguageUseError", "MI355XTarget", "NativeLibraryError", "PublicInterface", "ScalarParameter", "ViewKind",
     "ViewParameter", "compile", "gemm_i8_nt", "kernel", "moe_align_block_size", "moe_combine", "moe_down_w4",
     "moe_expert_ffn_w4", "moe_gate_up_w4", "moe_route_topk", "q4_k_q8_k_dot", "q8_k_quantize",

@@ -180,6 +180,78 @@ struct RegRowsOperand {
   }
 };
 
+// Packed low-bit weight rows decoded to int8 on the way to LDS, for the int8
+// MFMA path. Same row / slot assignment as RegRowsOperand (lane i of
+// instruction j: tile row (NW*j + wave)*8 + i/8, LDS slot i%8 holding 16-k
+// chunk (i%8) ^ swz(row)); a lane loads only the packed bytes of its chunk.
+//   kSignedNibble: two 4-bit values per byte, low nibble = even k, decoded
+//     as two's complement (n - 2*(n & 8)) (weight_only_int4.py:54-91);
+//   kInt2: four 2-bit values (0..3) per byte, interleaved: k lives in byte
+//     (k/16)*4 + k%4 at bit 2*((k/4)%4) (weight_only_int4.py:94-124), so the
+//     16-k chunk c is packed dword c and output dword a is (d >> 2a) & 3s.
+enum class LowBit { kSignedNibble, kInt2 };
+
+template <int ROWS, LowBit F, int NW = 4>
+struct LowBitRowsOperand {
+  static constexpr int N_INST = ROWS / (8 * NW);
+  static_assert(N_INST * 8 * NW == ROWS, "tile rows must be a multiple of 8 per wave");
+  static constexpr int NVM = N_INST;
+  static constexpr int NDS = N_INST;
+  static constexpr int CHUNK_BYTES = F == LowBit::kSignedNibble ? 8 : 4;  // packed bytes per 16 k
+  static constexpr int STAGE_BYTES = 8 * CHUNK_BYTES;                     // per row per 128-k stage
+  Rsrc rs;
+  uint32_t voff[N_INST];
+  uint32_t lds_off[N_INST];
+  struct Regs {
+    u32x2 v[N_INST];
+  };
+  // rows: packed rows (row stride ld_bytes); tile rows past M read row M-1.
+  INTENT_DEVICE void init(const uint8_t* base, int64_t ld_bytes, int M, int m0, int wave) {
+    rs = make_rsrc(base + (int64_t)m0 * ld_bytes);
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) {
+      const int r = (j * NW + wave) * 8 + (lane >> 3);
+      const int chunk = (lane & 7) ^ swz(r);
+      const int rr = m0 + r < M ? r : M - 1 - m0;
+      voff[j] = (uint32_t)(rr * ld_bytes + chunk * CHUNK_BYTES);
+      lds_off[j] = (uint32_t)(r * ROWB + (lane & 7) * 16);
+    }
+  }
+  INTENT_DEVICE void load(int kt, Regs& r) const {
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) {
+      if constexpr (F == LowBit::kSignedNibble) {
+        r.v[j] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff[j], (uint32_t)kt * STAGE_BYTES, 0);
+      } else {
+        r.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff[j], (uint32_t)kt * STAGE_BYTES, 0);
+        r.v[j][1] = 0u;
+      }
+    }
+  }
+  INTENT_DEVICE static u32x4 decode(u32x2 v) {
+    if constexpr (F == LowBit::kSignedNibble) {
+      u32x4 out;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t lo = v[h] & 0x0F0F0F0Fu, hi = (v[h] >> 4) & 0x0F0F0F0Fu;
+        lo |= ((lo >> 3) & 0x01010101u) * 0xF0u;  // sign-extend each nibble into its byte
+        hi |= ((hi >> 3) & 0x01010101u) * 0xF0u;
+        out[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);      // k = 0, 1, 2, 3 of the dword
+        out[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // k = 4, 5, 6, 7
+      }
+      return out;
+    } else {
+      const uint32_t d = v[0];
+      return u32x4{d & 0x03030303u, (d >> 2) & 0x03030303u, (d >> 4) & 0x03030303u, (d >> 6) & 0x03030303u};
+    }
+  }
+  INTENT_DEVICE void store(const Regs& r, char* lds_region) const {
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) *reinterpret_cast<u32x4*>(lds_region + lds_off[j]) = decode(r.v[j]);
+  }
+};
+
 // Raw rows copied global -> LDS by DMA (buffer_load ... lds): no VGPRs and
 // no ds_write issue slots. Each wave instruction moves 8 rows x 128 bytes;
 // lane i writes slot i%8 of row i/8, fetching chunk slot ^ swz(row).

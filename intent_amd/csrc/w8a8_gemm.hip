@@ -15,30 +15,11 @@ using T128 = mp::Tile<128, 128, 2, 2>;  // small problems: more workgroups
 
 enum class Epi { kBf16Scaled, kI32Bias };
 
-// One workgroup per output tile; 128 k per LDS stage, the last one possibly 64.
-template <class T, Epi E, bool kHalf>
-__global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t lda, int M,
-                                                                const int8_t* __restrict__ w, int64_t ldw, int N,
-                                                                int K, const float* __restrict__ a_scales,
-                                                                const float* __restrict__ w_scales,
-                                                                const int32_t* __restrict__ bias,
-                                                                void* __restrict__ out, int64_t ldo, int mblocks) {
-  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  // Plain dispatch order (m fastest): measured faster here than the XCD-grouped order.
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
-  const int wave = T::wave();
-  const int nk = (K + mp::ROWB - 1) / mp::ROWB;
-  const bool half = kHalf;
-  mp::RegRowsOperand<T::BN, mp::DenseRows, kHalf, T::NW> bop;
-  bop.init(mp::DenseRows{w, ldw, N}, n0, wave, half ? nk - 1 : -1);
-  i32x16 acc[T::TI][T::TJ];
-  mp::RegRowsOperand<T::BM, mp::DenseRows, kHalf, T::NW> aop;
-  aop.init(mp::DenseRows{a, lda, M}, m0, wave, half ? nk - 1 : -1);
-  mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc, half);
-
-  // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
+// Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
+template <class T, Epi E>
+INTENT_DEVICE void store_tile(const i32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N,
+                              const float* __restrict__ a_scales, const float* __restrict__ w_scales,
+                              const int32_t* __restrict__ bias, void* __restrict__ out, int64_t ldo) {
   const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
@@ -73,6 +54,72 @@ __global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restr
         }
       }
   }
+
+}
+
+// One workgroup per output tile; 128 k per LDS stage, the last one possibly 64.
+template <class T, Epi E, bool kHalf>
+__global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restrict__ a, int64_t lda, int M,
+                                                                const int8_t* __restrict__ w, int64_t ldw, int N,
+                                                                int K, const float* __restrict__ a_scales,
+                                                                const float* __restrict__ w_scales,
+                                                                const int32_t* __restrict__ bias,
+                                                                void* __restrict__ out, int64_t ldo, int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  // Plain dispatch order (m fastest): measured faster here than the XCD-grouped order.
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  const int wave = T::wave();
+  const int nk = (K + mp::ROWB - 1) / mp::ROWB;
+  const bool half = kHalf;
+  mp::RegRowsOperand<T::BN, mp::DenseRows, kHalf, T::NW> bop;
+  bop.init(mp::DenseRows{w, ldw, N}, n0, wave, half ? nk - 1 : -1);
+  i32x16 acc[T::TI][T::TJ];
+  mp::RegRowsOperand<T::BM, mp::DenseRows, kHalf, T::NW> aop;
+  aop.init(mp::DenseRows{a, lda, M}, m0, wave, half ? nk - 1 : -1);
+  mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc, half);
+
+  store_tile<T, E>(acc, m0, n0, M, N, a_scales, w_scales, bias, out, ldo);
+}
+
+// Low-bit weight x int8 activation contractions with exact int32 outputs.
+// W4A8 (weight_only_int4.py:54-91): out[n, m] = sum_k sext4(W[n, k]) * a[m, k],
+//   so the weight rows are the tile's M side and the output is [N, M].
+// BitNet int2 (weight_only_int4.py:94-124): out[m, n] = sum_k a[m, k] * W2[n, k]
+//   with weights 0..3 in the interleaved 2-bit packing.
+// The packed weights are decoded to int8 while staged into LDS; the rest is
+// the int8 pipeline above (128 k per stage, K % 128 == 0).
+template <class T, bool kBitNet>
+__global__ __launch_bounds__(T::NT, 1) void lowbit_gemm_kernel(const int8_t* __restrict__ act, int64_t ld_act,
+                                                               int M, const uint8_t* __restrict__ wq,
+                                                               int64_t ld_w, int N, int K,
+                                                               int32_t* __restrict__ out, int64_t ldo,
+                                                               int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  // Tile rows come from the side that is the output's row dimension.
+  const int rows = kBitNet ? M : N;
+  const int cols = kBitNet ? N : M;
+  const int r0 = (blockIdx.x % mblocks) * T::BM;
+  const int c0 = (blockIdx.x / mblocks) * T::BN;
+  const int wave = T::wave();
+  const int nk = K / mp::ROWB;
+  i32x16 acc[T::TI][T::TJ];
+  if constexpr (kBitNet) {
+    mp::RegRowsOperand<T::BM, mp::DenseRows, false, T::NW> aop;
+    aop.init(mp::DenseRows{act, ld_act, M}, r0, wave);
+    mp::LowBitRowsOperand<T::BN, mp::LowBit::kInt2, T::NW> bop;
+    bop.init(wq, ld_w, N, c0, wave);
+    mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc);
+  } else {
+    mp::LowBitRowsOperand<T::BM, mp::LowBit::kSignedNibble, T::NW> aop;
+    aop.init(wq, ld_w, N, r0, wave);
+    mp::RegRowsOperand<T::BN, mp::DenseRows, false, T::NW> bop;
+    bop.init(mp::DenseRows{act, ld_act, M}, c0, wave);
+    mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc);
+  }
+  store_tile<T, Epi::kI32Bias>(acc, r0, c0, rows, cols, nullptr, nullptr, nullptr, out, ldo);
 }
 
 int check_i8(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const int8_t* w, int64_t N, int64_t w_ld,
@@ -138,4 +185,55 @@ extern "C" int intent_i8_gemm_i32(const int8_t* a, int64_t M, int64_t K, int64_t
   int st = check_i8(a, M, K, a_ld, w, N, w_ld, c, c_ld);
   if (st != INTENT_OK || M == 0 || N == 0) return st;
   return launch_i8<Epi::kI32Bias>(a, M, K, a_ld, nullptr, w, N, w_ld, nullptr, bias, c, c_ld, stream, "i8_gemm_i32");
+}
+
+namespace {
+
+template <class T, bool kBitNet>
+int launch_lowbit(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* w, int64_t N, int64_t w_ld,
+                  int32_t* out, int64_t out_ld, void* stream, const char* name) {
+  const int64_t rows = kBitNet ? M : N, cols = kBitNet ? N : M;
+  const int mblocks = (int)((rows + T::BM - 1) / T::BM);
+  const int64_t grid = (int64_t)mblocks * ((cols + T::BN - 1) / T::BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
+  hipLaunchKernelGGL((lowbit_gemm_kernel<T, kBitNet>), dim3((unsigned)grid), dim3(T::NT), 0, (hipStream_t)stream, a,
+                     a_ld, (int)M, w, w_ld, (int)N, (int)K, out, out_ld, mblocks);
+  return intent::launch_status(name);
+}
+
+template <bool kBitNet>
+int lowbit_entry(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* w, int64_t N, int64_t w_ld,
+                 int32_t* out, int64_t out_ld, void* stream, const char* name) {
+  intent::clear_error();
+  const int per_byte = kBitNet ? 4 : 2;
+  const int align = kBitNet ? 4 : 8;
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "%s: bad extents", name);
+  INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "%s: K must be a multiple of 128, got %lld", name,
+                 (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(a && w && out, INTENT_ERR_INVALID_ARGUMENT, "%s: null pointer argument", name);
+  INTENT_REQUIRE(a_ld >= K && w_ld >= K / per_byte && out_ld >= (kBitNet ? N : M), INTENT_ERR_INVALID_ARGUMENT,
+                 "%s: leading stride smaller than the row", name);
+  INTENT_REQUIRE(intent::aligned16(a) && a_ld % 16 == 0 && (reinterpret_cast<uintptr_t>(w) % align) == 0 &&
+                     w_ld % align == 0,
+                 INTENT_ERR_ALIGNMENT, "%s: activations 16-byte aligned rows, packed weights %d-byte aligned rows",
+                 name, align);
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, w_ld), INTENT_ERR_UNSUPPORTED,
+                 "%s: operand too large for 31-bit buffer offsets", name);
+  const int64_t big = ((M + 255) / 256) * ((N + 255) / 256);
+  if (big >= 256) return launch_lowbit<T256, kBitNet>(a, M, K, a_ld, w, N, w_ld, out, out_ld, stream, name);
+  return launch_lowbit<T128, kBitNet>(a, M, K, a_ld, w, N, w_ld, out, out_ld, stream, name);
+}
+
+}  // namespace
+
+extern "C" int intent_w4a8_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* w_packed,
+                                int64_t N, int64_t w_ld, int32_t* out, int64_t out_ld, void* stream) {
+  return lowbit_entry<false>(a, M, K, a_ld, w_packed, N, w_ld, out, out_ld, stream, "w4a8_gemm");
+}
+
+extern "C" int intent_bitnet_int2_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* w_packed,
+                                       int64_t N, int64_t w_ld, int32_t* out, int64_t out_ld, void* stream) {
+  return lowbit_entry<true>(a, M, K, a_ld, w_packed, N, w_ld, out, out_ld, stream, "bitnet_int2_gemm");
 }

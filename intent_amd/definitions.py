@@ -514,8 +514,60 @@ bf16_groupwise_fp8_quantize = _fp8q_definition("bf16_groupwise_fp8_quantize", "b
 f32_groupwise_fp8_quantize = _fp8q_definition("f32_groupwise_fp8_quantize", "f32", "42-69")
 
 
+# ---- low-bit weight x int8 activation (exact int32) ---------------------------------
+
+def _lowbit_check(per_byte: int):
+    def check(env: dict) -> None:
+        if env["P"] * per_byte != env["K"]:
+            raise ValueError(f"packed_weight.shape[1] ({env['P']}) must be K/{per_byte} ({env['K']}/{per_byte})")
+    return check
+
+
+def _w4a8_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    a, w, out = v["activation"], v["packed_weight"], v["output"]
+    _native.call("intent_w4a8_gemm", _ptr(a), env["M"], env["K"], _ld(a), _ptr(w), env["N"], _ld(w), _ptr(out),
+                 _ld(out), stream)
+    return "intent_w4a8_gemm"
+
+
+w4a8_packed_matmul = KernelDefinition(
+    name="w4a8_packed_matmul",
+    params=(
+        Param("activation", "i8", ("M", "K"), leading_stride=True),
+        Param("packed_weight", "u8", ("N", "P"), leading_stride=True),
+        Param("output", "i32", ("N", "M"), OUT, leading_stride=True),
+    ),
+    launch=_w4a8_launch,
+    check=_lowbit_check(2),
+    reference="examples/kernels/contraction/weight_only_int4.py:54-91",
+    doc="output[n, m] = sum_k sext4(packed nibble k of row n) * activation[m, k], int32",
+)
+
+
+def _bitnet_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    a, w, out = v["activation"], v["packed_weight"], v["output"]
+    _native.call("intent_bitnet_int2_gemm", _ptr(a), env["M"], env["K"], _ld(a), _ptr(w), env["N"], _ld(w),
+                 _ptr(out), _ld(out), stream)
+    return "intent_bitnet_int2_gemm"
+
+
+bitnet_int2_matmul = KernelDefinition(
+    name="bitnet_int2_matmul",
+    params=(
+        Param("activation", "i8", ("M", "K"), leading_stride=True),
+        Param("packed_weight", "u8", ("N", "P"), leading_stride=True),
+        Param("output", "i32", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_bitnet_launch,
+    check=_lowbit_check(4),
+    reference="examples/kernels/contraction/weight_only_int4.py:94-124",
+    doc="output[m, n] = sum_k activation[m, k] * int2 value k of row n (interleaved packing), int32",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
+    w4a8_packed_matmul, bitnet_int2_matmul,
 )

@@ -69,6 +69,10 @@ def lib():
         _lib.orc_f32_to_e4m3fn.restype = ctypes.c_uint8
         _lib.orc_fp8_groupwise_quantize.argtypes = [p, i64, i64, i64, i64, ctypes.c_float, p, i64, p, i64]
         _lib.orc_fp8_groupwise_quantize.restype = None
+        _lib.orc_w4a8.argtypes = [p, i64, i64, p, i64, p, ci]
+        _lib.orc_bitnet_int2.argtypes = [p, i64, i64, p, i64, p, ci]
+        _lib.orc_w4a8.restype = None
+        _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
             getattr(_lib, name).restype = None
@@ -224,7 +228,43 @@ def f32_to_e4m3fn(values) -> np.ndarray:
     return np.array([lib().orc_f32_to_e4m3fn(float(f)) for f in v], np.uint8)
 
 
+def w4a8(a, packed, threads: int = 1) -> np.ndarray:
+    """int8 a [M, K] x signed-nibble weights [N, K/2] -> int32 [N, M]."""
+    a, packed = _c(a, np.int8), _c(packed, np.uint8)
+    M, K = a.shape
+    N = packed.shape[0]
+    out = np.empty((N, M), np.int32)
+    lib().orc_w4a8(_ptr(a), M, K, _ptr(packed), N, _ptr(out), threads)
+    return out
+
+
+def bitnet_int2(a, packed, threads: int = 1) -> np.ndarray:
+    """int8 a [M, K] x interleaved 2-bit weights [N, K/4] -> int32 [M, N]."""
+    a, packed = _c(a, np.int8), _c(packed, np.uint8)
+    M, K = a.shape
+    N = packed.shape[0]
+    out = np.empty((M, N), np.int32)
+    lib().orc_bitnet_int2(_ptr(a), M, K, _ptr(packed), N, _ptr(out), threads)
+    return out
+
+
 # ---- independent numpy restatements (used to pin the C oracle) ------------------
+
+def w4a8_int64(a, packed) -> np.ndarray:
+    """The reference's CPU formula (cpu_runtime.py:105-108) in int64 numpy."""
+    p = np.asarray(packed, np.int64)
+    nib = np.stack((p & 15, p >> 4), axis=-1).reshape(p.shape[0], -1)
+    signed = nib - ((nib & 8) << 1)
+    return signed @ np.asarray(a, np.int64).T
+
+
+def bitnet_int2_int64(a, packed) -> np.ndarray:
+    """The reference's CPU formula (cpu_runtime.py:111-114) in int64 numpy."""
+    p = np.asarray(packed, np.int64)
+    groups = p.reshape(p.shape[0], -1, 4)
+    logical = np.stack(tuple((groups >> (lane * 2)) & 3 for lane in range(4)), axis=2).reshape(p.shape[0], -1)
+    return np.asarray(a, np.int64) @ logical.T
+
 
 def q4k_pack(d, dmin, sc, m, q) -> np.ndarray:
     """Build Q4_K records from fields (the inverse of the spec's unpacking,

@@ -458,3 +458,41 @@ void orc_fp8_groupwise_quantize(const float* x, int64_t M, int64_t N, int64_t ld
     }
   }
 }
+
+/* ---- low-bit weight x int8 activation, exact int32 ---------------------------
+ * w4a8_packed_matmul (examples/kernels/contraction/weight_only_int4.py:54-91):
+ *   nibble k of row n = (packed[n, k/2] >> 4*(k%2)) & 15, signed = n - ((n & 8) << 1),
+ *   out[n, m] = sum_k signed[n, k] * a[m, k]          (output [N, M]).
+ * bitnet_int2_matmul (weight_only_int4.py:94-124):
+ *   value k of row n = (packed[n, (k/16)*4 + k%4] >> 2*((k/4)%4)) & 3,
+ *   out[m, n] = sum_k a[m, k] * value[n, k]            (output [M, N]).
+ * int32 accumulation, modulo 2^32 (types-numerics-and-effects.en.md:40). */
+void orc_w4a8(const int8_t* a, int64_t M, int64_t K, const uint8_t* packed, int64_t N, int32_t* out, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    for (int64_t m = 0; m < M; ++m) {
+      uint32_t acc = 0;
+      for (int64_t k = 0; k < K; ++k) {
+        const int nib = (packed[n * (K / 2) + k / 2] >> (4 * (k % 2))) & 15;
+        const int w = nib - ((nib & 8) << 1);
+        acc += (uint32_t)(w * (int32_t)a[m * K + k]);
+      }
+      out[n * M + m] = (int32_t)acc;
+    }
+  }
+}
+
+void orc_bitnet_int2(const int8_t* a, int64_t M, int64_t K, const uint8_t* packed, int64_t N, int32_t* out,
+                     int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      uint32_t acc = 0;
+      for (int64_t k = 0; k < K; ++k) {
+        const int v = (packed[n * (K / 4) + (k / 16) * 4 + k % 4] >> (2 * ((k / 4) % 4))) & 3;
+        acc += (uint32_t)((int32_t)a[m * K + k] * v);
+      }
+      out[m * N + n] = (int32_t)acc;
+    }
+  }
+}

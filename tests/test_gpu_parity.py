@@ -387,3 +387,31 @@ def test_fp8_groupwise_quantize_bit_exact(gpu, src, M, N, G):
     ref_q, ref_s = oracle.fp8_groupwise_quantize(x, groups=G, source=src)
     assert np.array_equal(host(q.view(torch.uint8)), ref_q)
     assert np.array_equal(host(scales).view(np.uint32), ref_s.view(np.uint32))
+
+
+# ---- W4A8 and BitNet int2: exact int32 ----------------------------------------------
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 1), (37, 256, 100), (300, 384, 130), (512, 2048, 1024)])
+def test_w4a8_and_bitnet_exact(gpu, threads, M, K, N):
+    rng = np.random.default_rng(M + 3 * N)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    p4 = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    p2 = rng.integers(0, 256, (N, K // 4), dtype=np.uint8)
+    got = art(intent.w4a8_packed_matmul).run(dev(a), dev(p4))
+    assert np.array_equal(host(got), oracle.w4a8(a, p4, threads))
+    got = art(intent.bitnet_int2_matmul).run(dev(a), dev(p2))
+    assert np.array_equal(host(got), oracle.bitnet_int2(a, p2, threads))
+
+
+def test_w4a8_full_size_exact(gpu):
+    # The reference's W4A8 case: a [4096, 4096], packed [14336, 2048] -> int32 [14336, 4096]
+    # (experiments/cpu/providers/mojo/contraction.py:201-206), checked on the GPU
+    # against an exact float64 restatement (|products| sum below 2^53).
+    rng = np.random.default_rng(99)
+    a = torch.from_numpy(rng.integers(-128, 128, (4096, 4096), dtype=np.int8)).cuda()
+    p = torch.from_numpy(rng.integers(0, 256, (14336, 2048), dtype=np.uint8)).cuda()
+    got = art(intent.w4a8_packed_matmul).run(a, p)
+    nib = torch.stack((p & 15, p >> 4), dim=-1).reshape(14336, -1).to(torch.int32)
+    signed = (nib - ((nib & 8) << 1)).to(torch.float64)
+    ref = (signed @ a.to(torch.float64).T)
+    assert torch.equal(got.to(torch.float64), ref)

@@ -430,3 +430,33 @@ def test_fp8_groupwise_bf16_eps_and_zero_group():
     x[0, 130] = -3.5  # group 1's extreme maps to -448 exactly
     q, sc = oracle.fp8_groupwise_quantize(x, source="bf16")
     assert q[0, 130] == 0xFE and sc[0, 1] == np.float32(3.5) / np.float32(448.0)
+
+
+# ---- W4A8 and BitNet int2 (examples/kernels/contraction/weight_only_int4.py:54-124) -
+
+@pytest.mark.parametrize("M,K,N", [(3, 64, 5), (16, 256, 33), (1, 512, 7)])
+def test_w4a8_and_bitnet_match_reference_formulas(M, K, N):
+    rng = np.random.default_rng(M + K + N)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    p4 = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    p2 = rng.integers(0, 256, (N, K // 4), dtype=np.uint8)
+    assert np.array_equal(oracle.w4a8(a, p4).astype(np.int64), oracle.w4a8_int64(a, p4))
+    assert np.array_equal(oracle.bitnet_int2(a, p2).astype(np.int64), oracle.bitnet_int2_int64(a, p2))
+
+
+def test_w4a8_and_bitnet_known_answers():
+    # Nibble 0x8 is -8, 0xF is -1, 0x7 is +7; low nibble = even k.
+    a = np.zeros((1, 4), np.int8)
+    a[0] = [1, 10, 100, -1]
+    p4 = np.array([[0x8F, 0x07]], np.uint8)  # k0 = 0xF (-1), k1 = 0x8 (-8), k2 = 7, k3 = 0
+    assert oracle.w4a8(a, p4)[0, 0] == -1 * 1 + -8 * 10 + 7 * 100
+    # int2 interleaving: k = 16c + 4a + b lives in byte 4c + b at bits 2a.
+    K = 32
+    for k in (0, 1, 3, 4, 5, 15, 16, 21, 31):
+        p2 = np.zeros((1, K // 4), np.uint8)
+        p2[0, (k // 16) * 4 + k % 4] = 3 << (2 * ((k // 4) % 4))
+        act = np.zeros((1, K), np.int8)
+        act[0, k] = 5
+        assert oracle.bitnet_int2(act, p2)[0, 0] == 15
+        act[0, k], act[0, (k + 1) % K] = 0, 5
+        assert oracle.bitnet_int2(act, p2)[0, 0] == 0
