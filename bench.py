@@ -191,6 +191,38 @@ def bench_w4a8(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": n}
 
 
+def bench_mxfp8(steps: int, warmup: int) -> dict:
+    """The reference's mxfp8_gemm case (experiments/cpu/providers/mojo/contraction.py:285-305):
+    M=4096, K=4096, N=14336, E4M3FN with E8M0 scales per 32, rhs given as the [KB, 32, N]
+    view of [N, K] rows."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    M, K, N = 4096, 4096, 14336
+    rng = np.random.default_rng(0)
+
+    def operand(rows):
+        v = rng.integers(0, 256, (rows, K), dtype=np.uint8)
+        v[(v & 0x7F) == 0x7F] = 0x38
+        return torch.from_numpy(v).cuda().view(torch.float8_e4m3fn)
+
+    a, b = operand(M), operand(N)
+    sa = torch.from_numpy(rng.integers(120, 134, (M, K // 32), dtype=np.uint8)).cuda()
+    sb = torch.from_numpy(rng.integers(120, 134, (N, K // 32), dtype=np.uint8)).cuda()
+    work = inputs.Workload(f"mxfp8 M{M} K{K} N{N}", 2 * M * N * K, M * K + N * K + (M + N) * K // 32 + M * N * 4)
+    art = intent.compile(intent.block_scaled_matmul, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes, minimum=2)
+    sets = [(a.clone().view(M, K // 32, 32), sa.clone(), b.clone().T.view(K // 32, 32, N), sb.clone().T)
+            for _ in range(n)]
+    calls = [art.prepare(*s) for s in sets]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls, sets
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
 def measured_traffic() -> int | None:
     """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE profile."""
     path = ROOT / "profiles" / "w4a16_gemv_dot_m1_traffic.md"
@@ -309,6 +341,9 @@ def main() -> int:
         log("[bench] w4a8 M=4096 K=4096 N=14336")
         r = bench_w4a8(steps, warm)
         extra["w4a8_m4096_n14336"] = _flop_entry(r, I8_PEAK_TOPS, "TOP/s")
+        log("[bench] mxfp8 M=4096 K=4096 N=14336")
+        r = bench_mxfp8(steps, warm)
+        extra["mxfp8_m4096_n14336"] = _flop_entry(r, 5033.2, "TFLOP/s")
         log("[bench] q4_k projection N=K=4096")
         r = bench_q4k(args.steps, args.warmup)
         extra["q4k_projection_n4096"] = _hbm_entry(r)

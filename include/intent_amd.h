@@ -304,6 +304,24 @@ int intent_bitnet_int2_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
                             const uint8_t* w_packed, int64_t N, int64_t w_ld,
                             int32_t* out, int64_t out_ld, void* stream);
 
+/*
+ * MX block-scaled FP8 GEMM: out[m, n] = sum_k (a[m,k] * 2^(sa[m,k/32]-127)) *
+ * (b[n,k] * 2^(sb[n,k/32]-127)), a and b OCP E4M3FN bytes with K contiguous
+ * (row strides a_ld, b_ld bytes, 16-byte aligned), E8M0 scales u8 [M, K/32]
+ * and [N, K/32] (row strides a_scales_ld, b_scales_ld, multiples of 4), out
+ * f32 [M, N]; K % 128 == 0. f32 accumulation on v_mfma_scale_f32_32x32x64_f8f6f4.
+ * Replaces block_scaled_matmul (examples/kernels/contraction/block_scaled.py:
+ * 11-39; CPU semantics lib/Conversion/KIRToCPU/Contractions.cpp:177-259),
+ * whose rhs [KB, 32, N] is here passed as rows n with K contiguous (the
+ * layout of the reference's own benchmark view, experiments/cpu/providers/
+ * mojo/contraction.py:285-305).
+ */
+int intent_mxfp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                      const uint8_t* a_scales, int64_t a_scales_ld,
+                      const uint8_t* b, int64_t N, int64_t b_ld,
+                      const uint8_t* b_scales, int64_t b_scales_ld,
+                      float* out, int64_t out_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

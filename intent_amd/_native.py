@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_fp8_groupwise_quantize": ([P, INT, I64, I64, I64, P, I64, P, I64, I64, P], INT),
     "intent_w4a8_gemm": ([P, I64, I64, I64, P, I64, I64, P, I64, P], INT),
     "intent_bitnet_int2_gemm": ([P, I64, I64, I64, P, I64, I64, P, I64, P], INT),
+    "intent_mxfp8_gemm": ([P, I64, I64, I64, P, I64, P, I64, I64, P, I64, P, I64, P], INT),
     "intent_moe_workspace_size": ([I64, I64, I64, I64, I64, I64], SIZE),
     "intent_moe_expert_ffn_w4": ([P, P, I64, I64, I64, I64, INT, P, P, P, P, P, P, I64, I64, P, P, SIZE, P, P, P],
                                  INT),

@@ -1,0 +1,239 @@
+// MX block-scaled FP8 GEMM on gfx950's scaled MFMA (v_mfma_scale_f32_32x32x64_f8f6f4):
+//   out[m, n] = sum_k (A[m, k] * 2^(sa[m, k/32] - 127)) * (B[n, k] * 2^(sb[n, k/32] - 127))
+// with A, B OCP E4M3FN bytes (K contiguous), E8M0 scales per 32 k, f32 output.
+// Replaces block_scaled_matmul (examples/kernels/contraction/block_scaled.py:11-39;
+// CPU semantics lib/Conversion/KIRToCPU/Contractions.cpp:177-259: decode each
+// operand to f32 = value * 2^(s-127), E8M0 255 = NaN, then an f32 contraction).
+//
+// The pipeline is the int8 one (mfma_pipe.h): 128 k per LDS stage, both
+// operands through VGPRs into XOR-swizzled LDS rows, two stages in flight.
+// Each stage also carries one dword of scales per tile row (the four E8M0
+// bytes of its four 32-k groups). One scaled MFMA covers 64 k (step s). The
+// instruction reads a lane's 32 operand bytes as two 16-k halves, k 16h..16h+15
+// and 32+16h..32+16h+15 of the step (h = lane / 32), and applies lane half
+// b's scale to k 32b..32b+31; so lane half h takes LDS chunks 4s+h and
+// 4s+2+h, and its scale byte is that of group 2s+h. (Measured: with the two
+// halves read as one contiguous 32-k run, groups with different scales mix.)
+#include "common.h"
+#include "internal.h"
+#include "mfma_pipe.h"
+
+namespace {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// Data rows plus their per-stage scale dword. Lanes 8q (one per tile row of
+// an instruction) store the scale; every lane loads it (same address).
+template <int ROWS, int NW>
+struct ScaledRows {
+  using Data = mp::RegRowsOperand<ROWS, mp::DenseRows, false, NW>;
+  static constexpr int N_INST = Data::N_INST;
+  static constexpr int NVM = 2 * N_INST;
+  Data data;
+  mp::Rsrc rsc;
+  uint32_t soff[N_INST];
+  uint32_t slds[N_INST];
+  struct Regs {
+    typename Data::Regs d;
+    uint32_t s[N_INST];
+  };
+  INTENT_DEVICE void init(const uint8_t* rows, int64_t ld, int M, const uint8_t* scales, int64_t ld_scale, int m0,
+                          int wave) {
+    data.init(mp::DenseRows{rows, ld, M}, m0, wave);
+    rsc = make_rsrc(scales);
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) {
+      const int r = (j * NW + wave) * 8 + (lane >> 3);
+      const int m = m0 + r < M ? m0 + r : M - 1;
+      soff[j] = (uint32_t)(m * ld_scale);
+      slds[j] = (uint32_t)(r * 4);
+    }
+  }
+  INTENT_DEVICE void load(int kt, Regs& r) const {
+    data.load(kt, r.d);
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) r.s[j] = __builtin_amdgcn_raw_buffer_load_b32(rsc, soff[j], (uint32_t)kt * 4, 0);
+  }
+  INTENT_DEVICE void store(const Regs& r, char* lds_rows, char* lds_scales) const {
+    data.store(r.d, lds_rows);
+    if ((threadIdx.x & 7) == 0) {
+#pragma unroll
+      for (int j = 0; j < N_INST; ++j) *reinterpret_cast<uint32_t*>(lds_scales + slds[j]) = r.s[j];
+    }
+  }
+};
+
+template <class T>
+struct MxLayout {
+  static constexpr int A_SCALES = (T::BM + T::BN) * mp::ROWB;  // after A rows then B rows
+  static constexpr int B_SCALES = A_SCALES + T::BM * 4;
+  static constexpr int STAGE = B_SCALES + T::BN * 4;
+};
+
+// 32 bytes of row r: chunks c0 and c0 + 2 of a swizzled 128-byte LDS row.
+INTENT_DEVICE i32x8 read_frag(const char* rows, int r, int c0) {
+  const i32x4 lo = *reinterpret_cast<const i32x4*>(rows + r * mp::ROWB + ((c0 ^ mp::swz(r)) << 4));
+  const i32x4 hi = *reinterpret_cast<const i32x4*>(rows + r * mp::ROWB + (((c0 + 2) ^ mp::swz(r)) << 4));
+  return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+template <class T>
+INTENT_DEVICE void compute_stage_mx(const char* buf, i32x16 (&acc)[T::TI][T::TJ]) {
+  using L = MxLayout<T>;
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5;
+  const int ra = T::wave_m() * T::WTM + (lane & 31);
+  const int rb = T::wave_n() * T::WTN + (lane & 31);
+  uint32_t sa[T::TI], sb[T::TJ];
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) sa[i] = *reinterpret_cast<const uint32_t*>(buf + L::A_SCALES + (ra + 32 * i) * 4);
+#pragma unroll
+  for (int j = 0; j < T::TJ; ++j) sb[j] = *reinterpret_cast<const uint32_t*>(buf + L::B_SCALES + (rb + 32 * j) * 4);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int c0 = 4 * s + h;
+    const int sh = 8 * (2 * s + h);
+    i32x8 af[T::TI], bf[T::TJ];
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i) af[i] = read_frag(buf, ra + 32 * i, c0);
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j) bf[j] = read_frag(buf + T::A_BYTES, rb + 32 * j, c0);
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) {
+        // (B, A) order: the lane's accumulators hold one m and four adjacent n.
+        f32x16 c = bit_cast<f32x16>(acc[i][j]);
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[j], af[i], c, 0, 0, 0, (int)((sb[j] >> sh) & 255u), 0,
+                                                             (int)((sa[i] >> sh) & 255u));
+        acc[i][j] = bit_cast<i32x16>(c);
+      }
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(T::NT, 1) void mxfp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                              const uint8_t* __restrict__ sa, int64_t ld_sa,
+                                                              const uint8_t* __restrict__ b, int64_t ldb, int N,
+                                                              const uint8_t* __restrict__ sb, int64_t ld_sb, int K,
+                                                              float* __restrict__ out, int64_t ldo, int mblocks) {
+  using L = MxLayout<T>;
+  __shared__ __attribute__((aligned(16))) char buf0[L::STAGE];
+  __shared__ __attribute__((aligned(16))) char buf1[L::STAGE];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  const int wave = T::wave();
+  const int nk = K / mp::ROWB;
+  ScaledRows<T::BM, T::NW> aop;
+  aop.init(a, lda, M, sa, ld_sa, m0, wave);
+  ScaledRows<T::BN, T::NW> bop;
+  bop.init(b, ldb, N, sb, ld_sb, n0, wave);
+  i32x16 acc[T::TI][T::TJ];
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;  // the bits of +0.0f
+
+  constexpr int NV = ScaledRows<T::BM, T::NW>::NVM + ScaledRows<T::BN, T::NW>::NVM;
+  typename ScaledRows<T::BM, T::NW>::Regs ra0, ra1;
+  typename ScaledRows<T::BN, T::NW>::Regs rb0, rb1;
+  auto stage_store = [&](const auto& rra, const auto& rrb, char* buf) {
+    aop.store(rra, buf, buf + L::A_SCALES);
+    bop.store(rrb, buf + T::A_BYTES, buf + L::B_SCALES);
+  };
+  aop.load(0, ra0);
+  bop.load(0, rb0);
+  if (nk > 1) {
+    aop.load(1, ra1);
+    bop.load(1, rb1);
+  }
+  stage_store(ra0, rb0, buf0);
+  mp::wait_vm_lgkm_barrier<NV>();
+  // Step kt computes on one buffer while stage kt+1 (loaded a step earlier)
+  // goes to the other and stage kt+2 is loaded; the last step only computes.
+  auto step = [&](int kt, char* cur, char* nxt, auto& ran, auto& rbn, auto& raf, auto& rbf) {
+    const int kn = kt + 2 < nk ? kt + 2 : nk - 1;
+    aop.load(kn, raf);
+    bop.load(kn, rbf);
+    compute_stage_mx<T>(cur, acc);
+    stage_store(ran, rbn, nxt);
+    mp::wait_vm_lgkm_barrier<NV>();
+  };
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    step(kt, buf0, buf1, ra1, rb1, ra0, rb0);
+    step(kt + 1, buf1, buf0, ra0, rb0, ra1, rb1);
+  }
+  if (kt + 1 < nk) {
+    step(kt, buf0, buf1, ra1, rb1, ra0, rb0);
+    ++kt;
+  }
+  compute_stage_mx<T>((kt & 1) ? buf1 : buf0, acc);
+
+  // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        const f32x16 c = bit_cast<f32x16>(acc[i][j]);
+        float* o = out + (int64_t)m * ldo + n;
+        if (vec && n + 3 < N) {
+          *reinterpret_cast<f32x4*>(o) = f32x4{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < N) o[q] = c[4 * g + q];
+        }
+      }
+  }
+}
+
+// 128 x 128 tiles, four waves of 64 x 64 (a 256 x 256 tile does not fit the
+// registers of eight waves once the 32-byte scaled-MFMA fragments are counted).
+using TMx128 = mp::Tile<128, 128, 2, 2>;
+
+template <class T>
+int launch_mx(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* sa, int64_t sa_ld,
+              const uint8_t* b, int64_t N, int64_t b_ld, const uint8_t* sb, int64_t sb_ld, float* out, int64_t out_ld,
+              void* stream) {
+  const int mblocks = (int)((M + T::BM - 1) / T::BM);
+  const int64_t grid = (int64_t)mblocks * ((N + T::BN - 1) / T::BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "mxfp8_gemm: grid too large");
+  hipLaunchKernelGGL((mxfp8_gemm_kernel<T>), dim3((unsigned)grid), dim3(T::NT), 0, (hipStream_t)stream, a, a_ld,
+                     (int)M, sa, sa_ld, b, b_ld, (int)N, sb, sb_ld, (int)K, out, out_ld, mblocks);
+  return intent::launch_status("mxfp8_gemm");
+}
+
+}  // namespace
+
+extern "C" int intent_mxfp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* a_scales,
+                                 int64_t a_scales_ld, const uint8_t* b, int64_t N, int64_t b_ld,
+                                 const uint8_t* b_scales, int64_t b_scales_ld, float* out, int64_t out_ld,
+                                 void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 128, got %lld", (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(a && b && a_scales && b_scales && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(a_ld >= K && b_ld >= K && a_scales_ld >= K / 32 && b_scales_ld >= K / 32 && out_ld >= N,
+                 INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(b) && a_ld % 16 == 0 && b_ld % 16 == 0 &&
+                     intent::aligned4(a_scales) && intent::aligned4(b_scales) && a_scales_ld % 4 == 0 &&
+                     b_scales_ld % 4 == 0,
+                 INTENT_ERR_ALIGNMENT, "operand rows 16-byte aligned, scale rows 4-byte aligned");
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, b_ld) &&
+                     intent::fits_offset(M, a_scales_ld) && intent::fits_offset(N, b_scales_ld),
+                 INTENT_ERR_UNSUPPORTED, "mxfp8_gemm: operand too large for 31-bit buffer offsets");
+  return launch_mx<TMx128>(a, M, K, a_ld, a_scales, a_scales_ld, b, N, b_ld, b_scales, b_scales_ld, out, out_ld,
+                           stream);
+}

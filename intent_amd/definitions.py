@@ -28,6 +28,7 @@ class Param:
     dims: tuple
     access: ViewKind = IN
     leading_stride: bool = False  # 2-D views may carry a leading stride; others must be contiguous
+    free_strides: bool = False    # any strides; the definition's launch adapts the layout
 
 
 @dataclass(frozen=True)
@@ -87,7 +88,7 @@ class KernelDefinition:
                     shape.append(-1)
                     dims.append(0)
             rank = len(p.dims)
-            strides = tuple([None] * (rank - 1) + [1]) if p.leading_stride else tuple(
+            strides = (None,) * rank if p.free_strides else tuple([None] * (rank - 1) + [1]) if p.leading_stride else tuple(
                 None if i < rank - 1 else 1 for i in range(rank))
             parameters.append(ViewParameter(position, p.name, dtype(p.dtype), tuple(shape), tuple(dims), strides,
                                             p.access))
@@ -565,9 +566,51 @@ bitnet_int2_matmul = KernelDefinition(
 )
 
 
+# ---- MX block-scaled FP8 --------------------------------------------------------
+
+def _mx_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    import torch
+
+    lhs, ls, rhs, rs, out = v["lhs"], v["lhs_scale"], v["rhs"], v["rhs_scale"], v["output"]
+    M, KB, N = env["M"], env["KB"], env["N"]
+    # The kernel reads rows with K contiguous. The reference's benchmark passes
+    # rhs as such a view of [N, K] (strides (32, 1, K)); other layouts are
+    # re-laid out once here.
+    if not (rhs.stride(1) == 1 and (KB == 1 or rhs.stride(0) == 32)):
+        rhs = rhs.permute(2, 0, 1).contiguous().permute(1, 2, 0)
+    if not (N == 1 or rs.stride(0) == 1) or rs.stride(1) % 4:
+        rs = rs.t().contiguous().t()
+    b_ld = rhs.stride(2) if N > 1 else KB * 32
+    sb_ld = rs.stride(1) if N > 1 else KB
+    _native.call("intent_mxfp8_gemm", _ptr(lhs.view(torch.uint8)), M, KB * 32, KB * 32, _ptr(ls), KB,
+                 _ptr(rhs.view(torch.uint8)), N, b_ld, _ptr(rs), sb_ld, _ptr(out), _ld(out), stream)
+    return "intent_mxfp8_gemm"
+
+
+def _mx_check(env: dict) -> None:
+    if env["KB"] % 4:
+        raise NotImplementedError(f"the number of 32-element blocks ({env['KB']}) must be a multiple of 4 (K % 128)")
+
+
+block_scaled_matmul = KernelDefinition(
+    name="block_scaled_matmul",
+    params=(
+        Param("lhs", "f8e4m3fn", ("M", "KB", 32)),
+        Param("lhs_scale", "u8", ("M", "KB")),
+        Param("rhs", "f8e4m3fn", ("KB", 32, "N"), free_strides=True),
+        Param("rhs_scale", "u8", ("KB", "N"), free_strides=True),
+        Param("output", "f32", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_mx_launch,
+    check=_mx_check,
+    reference="examples/kernels/contraction/block_scaled.py:11-39 (I.scaled_matmul, e4m3 x e4m3, E8M0, group 32)",
+    doc="output = sum over k of (lhs * 2^(lhs_scale-127)) * (rhs * 2^(rhs_scale-127)), f32",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
-    w4a8_packed_matmul, bitnet_int2_matmul,
+    w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul,
 )

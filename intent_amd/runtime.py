@@ -141,7 +141,7 @@ class HIPRuntime:
         expected = torch.device("cuda", self.device)
         if t.device != expected:
             raise ValueError(f"compiled artifact is bound to {expected}, but {p.name} is on {t.device}")
-        if t.numel() == 0:
+        if t.numel() == 0 or p.free_strides:
             return
         if p.leading_stride and t.dim() == 2:
             if t.stride(1) != 1 and t.shape[1] > 1:

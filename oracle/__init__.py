@@ -72,6 +72,12 @@ def lib():
         _lib.orc_w4a8.argtypes = [p, i64, i64, p, i64, p, ci]
         _lib.orc_bitnet_int2.argtypes = [p, i64, i64, p, i64, p, ci]
         _lib.orc_w4a8.restype = None
+        _lib.orc_e4m3fn_to_f32.argtypes = [ctypes.c_uint8]
+        _lib.orc_e4m3fn_to_f32.restype = ctypes.c_float
+        _lib.orc_e8m0_to_f32.argtypes = [ctypes.c_uint8]
+        _lib.orc_e8m0_to_f32.restype = ctypes.c_float
+        _lib.orc_mxfp8_gemm.argtypes = [p, p, i64, i64, p, p, i64, p, ci]
+        _lib.orc_mxfp8_gemm.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -246,6 +252,24 @@ def bitnet_int2(a, packed, threads: int = 1) -> np.ndarray:
     out = np.empty((M, N), np.int32)
     lib().orc_bitnet_int2(_ptr(a), M, K, _ptr(packed), N, _ptr(out), threads)
     return out
+
+
+def mxfp8_gemm(a, sa, b, sb, threads: int = 1) -> np.ndarray:
+    """E4M3FN bytes a [M, K], b [N, K] with E8M0 scales [M, K/32], [N, K/32] -> f32 [M, N]."""
+    a, sa, b, sb = (_c(t, np.uint8) for t in (a, sa, b, sb))
+    M, K = a.shape
+    N = b.shape[0]
+    out = np.empty((M, N), np.float32)
+    lib().orc_mxfp8_gemm(_ptr(a), _ptr(sa), M, K, _ptr(b), _ptr(sb), N, _ptr(out), threads)
+    return out
+
+
+def e4m3fn_to_f32(bits) -> np.ndarray:
+    return np.array([lib().orc_e4m3fn_to_f32(int(v)) for v in np.asarray(bits, np.uint8).reshape(-1)], np.float32)
+
+
+def e8m0_to_f32(bits) -> np.ndarray:
+    return np.array([lib().orc_e8m0_to_f32(int(v)) for v in np.asarray(bits, np.uint8).reshape(-1)], np.float32)
 
 
 # ---- independent numpy restatements (used to pin the C oracle) ------------------

@@ -496,3 +496,41 @@ void orc_bitnet_int2(const int8_t* a, int64_t M, int64_t K, const uint8_t* packe
     }
   }
 }
+
+/* ---- MX block-scaled FP8 contraction ------------------------------------------
+ * block_scaled_matmul (examples/kernels/contraction/block_scaled.py:11-39) with
+ * the CPU semantics of lib/Conversion/KIRToCPU/Contractions.cpp:177-259: each
+ * E4M3FN element widens exactly to f32 and is multiplied by its E8M0 scale
+ * (bits e << 23; e == 0 gives 2^-127 = 0x00400000, e == 255 NaN), then
+ * out = f32 contraction with fma accumulation in k order (Contractions.cpp:12-41). */
+float orc_e4m3fn_to_f32(uint8_t v) {
+  const int sign = v >> 7, e = (v >> 3) & 15, m = v & 7;
+  float mag;
+  if (e == 15 && m == 7) mag = NAN;
+  else if (e == 0) mag = ldexpf((float)m, -9);
+  else mag = ldexpf(1.0f + (float)m / 8.0f, e - 7);
+  return sign ? -mag : mag;
+}
+
+float orc_e8m0_to_f32(uint8_t e) {
+  const uint32_t bits = e == 0 ? 0x00400000u : e == 255 ? 0x7fc00000u : (uint32_t)e << 23;
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+void orc_mxfp8_gemm(const uint8_t* a, const uint8_t* sa, int64_t M, int64_t K, const uint8_t* b, const uint8_t* sb,
+                    int64_t N, float* out, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) {
+        const float x = orc_e4m3fn_to_f32(a[m * K + k]) * orc_e8m0_to_f32(sa[m * (K / 32) + k / 32]);
+        const float y = orc_e4m3fn_to_f32(b[n * K + k]) * orc_e8m0_to_f32(sb[n * (K / 32) + k / 32]);
+        acc = fmaf(x, y, acc);
+      }
+      out[m * N + n] = acc;
+    }
+  }
+}

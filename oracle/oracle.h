@@ -35,5 +35,9 @@ void orc_fp8_groupwise_quantize(const float* x, int64_t M, int64_t N, int64_t ld
 void orc_w4a8(const int8_t* a, int64_t M, int64_t K, const uint8_t* packed, int64_t N, int32_t* out, int threads);
 void orc_bitnet_int2(const int8_t* a, int64_t M, int64_t K, const uint8_t* packed, int64_t N, int32_t* out,
                      int threads);
+float orc_e4m3fn_to_f32(uint8_t v);
+float orc_e8m0_to_f32(uint8_t e);
+void orc_mxfp8_gemm(const uint8_t* a, const uint8_t* sa, int64_t M, int64_t K, const uint8_t* b, const uint8_t* sb,
+                    int64_t N, float* out, int threads);
 
 #endif

@@ -415,3 +415,36 @@ def test_w4a8_full_size_exact(gpu):
     signed = (nib - ((nib & 8) << 1)).to(torch.float64)
     ref = (signed @ a.to(torch.float64).T)
     assert torch.equal(got.to(torch.float64), ref)
+
+
+# ---- MX block-scaled FP8 ------------------------------------------------------------
+
+def _mx_case(seed, M, K, N):
+    rng = np.random.default_rng(seed)
+    a = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    b = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    a[(a & 0x7F) == 0x7F] = 0x38  # keep NaN codes out of the data (E4M3FN 0x7F / 0xFF)
+    b[(b & 0x7F) == 0x7F] = 0x38
+    sa = rng.integers(120, 134, (M, K // 32), dtype=np.uint8)
+    sb = rng.integers(120, 134, (N, K // 32), dtype=np.uint8)
+    return a, sa, b, sb
+
+
+@pytest.mark.parametrize("M,K,N,layout", [(64, 128, 64, "view"), (130, 256, 70, "view"), (512, 768, 512, "view"),
+                                          (33, 384, 100, "contiguous")])
+def test_block_scaled_matmul(gpu, threads, M, K, N, layout):
+    a, sa, b, sb = _mx_case(M + N, M, K, N)
+    KB = K // 32
+    lhs = dev(a).view(torch.float8_e4m3fn).view(M, KB, 32)
+    bt = dev(b).view(torch.float8_e4m3fn)
+    if layout == "view":  # the reference benchmark's layout: rhs = rhs_rows.T.view(KB, 32, N)
+        rhs = bt.T.view(KB, 32, N)
+        rs = dev(sb).T
+    else:
+        rhs = bt.T.contiguous().view(KB, 32, N)
+        rs = dev(sb).T.contiguous()
+    out = art(intent.block_scaled_matmul).run(lhs, dev(sa), rhs, rs)
+    ref = oracle.mxfp8_gemm(a, sa, b, sb, threads)
+    # The scaled MFMA sums 64 products per instruction in its own order and
+    # precision (measured ~1e-4 of the largest term); the gate is the float one.
+    assert_close_rms(host(out), ref, what=f"mxfp8 {M}x{K}x{N}")

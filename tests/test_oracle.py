@@ -460,3 +460,35 @@ def test_w4a8_and_bitnet_known_answers():
         assert oracle.bitnet_int2(act, p2)[0, 0] == 15
         act[0, k], act[0, (k + 1) % K] = 0, 5
         assert oracle.bitnet_int2(act, p2)[0, 0] == 0
+
+
+# ---- MX block-scaled FP8 (examples/kernels/contraction/block_scaled.py:11-39) -------
+
+def test_e4m3fn_and_e8m0_decode():
+    bits = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(bits).view(torch.float8_e4m3fn).float().numpy()
+    got = oracle.e4m3fn_to_f32(bits)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
+    s = oracle.e8m0_to_f32(bits)
+    assert s[0] == np.float32(2.0 ** -127) and np.isnan(s[255])
+    assert np.array_equal(s[1:255], np.exp2(np.arange(1, 255) - 127.0).astype(np.float32))
+
+
+def test_mxfp8_gemm_matches_reference_formula():
+    # experiments/cpu/baselines/pytorch/cpu_runtime.py:1025-1032 restated with torch
+    # in float64 (products of e4m3 values and power-of-two scales are exact).
+    rng = np.random.default_rng(4)
+    M, K, N = 5, 128, 7
+    a = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    b = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    a[(a & 0x7F) == 0x7F] = 0x10  # no NaN codes
+    b[(b & 0x7F) == 0x7F] = 0x10
+    sa = rng.integers(118, 136, (M, K // 32), dtype=np.uint8)
+    sb = rng.integers(118, 136, (N, K // 32), dtype=np.uint8)
+    got = oracle.mxfp8_gemm(a, sa, b, sb)
+    fa = torch.from_numpy(a).view(torch.float8_e4m3fn).double() * torch.exp2(torch.from_numpy(sa).double() - 127).repeat_interleave(32, 1)
+    fb = torch.from_numpy(b).view(torch.float8_e4m3fn).double() * torch.exp2(torch.from_numpy(sb).double() - 127).repeat_interleave(32, 1)
+    ref = (fa @ fb.T).numpy()
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
