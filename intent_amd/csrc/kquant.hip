@@ -21,14 +21,15 @@ constexpr int kQ4Bytes = 144;
 constexpr int kQ8Bytes = 292;
 
 // ---- Q8_K quantization: one wave per 256-value record --------------------------
-// Lane l holds values 4l..4l+3. Extremes reduce exactly across the wave; the
+// Lane l holds values 4l..4l+3 (v). Extremes reduce exactly across the wave; the
 // record's inverse and ds use IEEE division; q = saturate(rne(v * inverse)).
-__global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restrict__ x, int64_t ldx, int G,
-                                                           uint8_t* __restrict__ out, int64_t ld_out) {
-  const int lane = threadIdx.x & 63;
-  const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (g >= G) return;  // wave-uniform
-  const f32x4 v = *reinterpret_cast<const f32x4*>(x + (int64_t)g * ldx + 4 * lane);
+struct Q8Lane {
+  float ds;         // the record's scale (every lane)
+  uint32_t packed;  // the lane's four i8 values
+  int bsum;         // sum of the lane's quad (bsum[lane / 4]; every lane of the quad)
+};
+
+INTENT_DEVICE Q8Lane quantize_lane(const f32x4 v) {
   float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
   float mn = fminf(fminf(v[0], v[1]), fminf(v[2], v[3]));
 #pragma unroll
@@ -48,16 +49,31 @@ __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restri
       q[i] = t > 127.f ? 127 : t < -128.f ? -128 : (int)t;
     }
   }
-  uint8_t* rec = out + (int64_t)g * ld_out;
-  const uint32_t packed = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
-                          ((uint32_t)(q[3] & 255) << 24);
-  *reinterpret_cast<uint32_t*>(rec + 4 + 4 * lane) = packed;
-  // bsum[j] covers lanes 4j..4j+3.
-  int s = q[0] + q[1] + q[2] + q[3];
-  s += __shfl_xor(s, 1);
-  s += __shfl_xor(s, 2);
-  if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(rec + 260 + 2 * (lane >> 2)) = (int16_t)s;
-  if (lane == 0) *reinterpret_cast<float*>(rec) = ds;
+  Q8Lane r;
+  r.ds = ds;
+  r.packed = (uint32_t)(q[0] & 255) | ((uint32_t)(q[1] & 255) << 8) | ((uint32_t)(q[2] & 255) << 16) |
+             ((uint32_t)(q[3] & 255) << 24);
+  int sum = q[0] + q[1] + q[2] + q[3];
+  sum += __shfl_xor(sum, 1);
+  sum += __shfl_xor(sum, 2);
+  r.bsum = sum;
+  return r;
+}
+
+// Writes the lane's share of a 292-byte Q8_K record.
+INTENT_DEVICE void store_q8_record(uint8_t* rec, const Q8Lane& q, int lane) {
+  *reinterpret_cast<uint32_t*>(rec + 4 + 4 * lane) = q.packed;
+  if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(rec + 260 + 2 * (lane >> 2)) = (int16_t)q.bsum;
+  if (lane == 0) *reinterpret_cast<float*>(rec) = q.ds;
+}
+
+__global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restrict__ x, int64_t ldx, int G,
+                                                           uint8_t* __restrict__ out, int64_t ld_out) {
+  const int lane = threadIdx.x & 63;
+  const int g = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= G) return;  // wave-uniform
+  const f32x4 v = *reinterpret_cast<const f32x4*>(x + (int64_t)g * ldx + 4 * lane);
+  store_q8_record(out + (int64_t)g * ld_out, quantize_lane(v), lane);
 }
 
 // ---- Q4_K x Q8_K GEMV ------------------------------------------------------------
@@ -73,6 +89,49 @@ __device__ __forceinline__ int q4k_field(const u32x4 hdr, int r, int i) {
   if (i < 4) return byte(4 + 4 * r + i) & 63;
   const int t = i - 4;
   return ((byte(12 + t) >> (4 * r)) & 15) | ((byte(4 + 4 * r + t) >> 6) << 4);
+}
+
+// v_b of the record pair a lane's quad works on (the same value in the four
+// lanes): hdr = bytes 0..15 of the Q4_K record, q0/q1 = packed group u
+// (bytes 16+32u .. 47+32u), xqv = the 64 i8 activations 64u..64u+63,
+// bsum_lo/hi = bsum[4u]+bsum[4u+1] and bsum[4u+2]+bsum[4u+3], ds its scale.
+INTENT_DEVICE float record_value(const u32x4 hdr, const u32x4 q0, const u32x4 q1, const uint32_t (&xqv)[16],
+                                 int bsum_lo, int bsum_hi, float ds, int u) {
+  const uint32_t qw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+  int dlo = 0, dhi = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    dlo = __builtin_amdgcn_sdot4((int)(qw[i] & 0x0F0F0F0Fu), (int)xqv[i], dlo, false);
+    dhi = __builtin_amdgcn_sdot4((int)((qw[i] >> 4) & 0x0F0F0F0Fu), (int)xqv[8 + i], dhi, false);
+  }
+  int S = q4k_field(hdr, 0, 2 * u) * dlo + q4k_field(hdr, 0, 2 * u + 1) * dhi;
+  int T = q4k_field(hdr, 1, 2 * u) * bsum_lo + q4k_field(hdr, 1, 2 * u + 1) * bsum_hi;
+  S += __shfl_xor(S, 1);
+  S += __shfl_xor(S, 2);
+  T += __shfl_xor(T, 1);
+  T += __shfl_xor(T, 2);
+  const float d = (float)bit_cast<f16>((uint16_t)(hdr[0] & 0xFFFFu));
+  const float dmin = (float)bit_cast<f16>((uint16_t)(hdr[0] >> 16));
+  const float p = __fmul_rn(d, (float)S);
+  const float nn = __fmul_rn(dmin, (float)T);
+  return __fmul_rn(ds, __fsub_rn(p, nn));
+}
+
+// Adds v of records c0 .. c0+cnt-1 (lane 4k holds record c0 + k) to t in order.
+INTENT_DEVICE float add_in_order(float t, float v, int cnt) {
+  for (int k = 0; k < cnt; ++k) t = __fadd_rn(t, bit_cast<float>(__builtin_amdgcn_readlane(bit_cast<int>(v), 4 * k)));
+  return t;
+}
+
+// The weight bytes a lane needs of record b of a row: header and group u.
+struct Q4Frag {
+  u32x4 hdr, q0, q1;
+};
+INTENT_DEVICE Q4Frag load_q4(__amdgpu_buffer_rsrc_t row, int b, int u) {
+  const uint32_t o = (uint32_t)(b * kQ4Bytes);
+  return Q4Frag{__builtin_amdgcn_raw_buffer_load_b128(row, o, 0, 0),
+                __builtin_amdgcn_raw_buffer_load_b128(row, o + 16 + 32 * u, 0, 0),
+                __builtin_amdgcn_raw_buffer_load_b128(row, o + 32 + 32 * u, 0, 0)};
 }
 
 template <int RW>
@@ -99,38 +158,97 @@ __global__ __launch_bounds__(256) void q4k_gemv_kernel(const uint8_t* __restrict
     const float ds = bit_cast<float>(__builtin_amdgcn_raw_buffer_load_b32(xr, xo, 0, 0));
     const int bsum_lo = (int)(int16_t)(bs01 & 0xFFFFu) + (int)(int16_t)(bs01 >> 16);
     const int bsum_hi = (int)(int16_t)(bs23 & 0xFFFFu) + (int)(int16_t)(bs23 >> 16);
-
+    const int cnt = G - c0 < 16 ? G - c0 : 16;
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
       const int n = row0 + r < N ? row0 + r : N - 1;
-      const uint8_t* rec = w + (int64_t)n * ldw + (int64_t)b * kQ4Bytes;
-      const u32x4 hdr = *reinterpret_cast<const u32x4*>(rec);
-      const u32x4 q0 = *reinterpret_cast<const u32x4*>(rec + 16 + 32 * u);
-      const u32x4 q1 = *reinterpret_cast<const u32x4*>(rec + 32 + 32 * u);
-      const uint32_t qw[8] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
-      int dlo = 0, dhi = 0;
+      const Q4Frag f = load_q4(make_rsrc(w + (int64_t)n * ldw), b, u);
+      total[r] = add_in_order(total[r], record_value(f.hdr, f.q0, f.q1, xqv, bsum_lo, bsum_hi, ds, u), cnt);
+    }
+  }
+  if (lane < RW) {
+    float out = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        dlo = __builtin_amdgcn_sdot4((int)(qw[i] & 0x0F0F0F0Fu), (int)xqv[i], dlo, false);
-        dhi = __builtin_amdgcn_sdot4((int)((qw[i] >> 4) & 0x0F0F0F0Fu), (int)xqv[8 + i], dhi, false);
+    for (int r = 0; r < RW; ++r)
+      if (r == lane) out = total[r];
+    if (row0 + lane < N) y[row0 + lane] = out;
+  }
+}
+
+// ---- fused projection: quantize into LDS, then the GEMV ------------------------
+// Every workgroup quantizes the whole activation vector (G <= kFusedMaxG
+// records, a few KB of VALU work) into LDS records padded to 304 bytes (ds at
+// 0, q at 16, bsum at 272, so fragments are 16-byte aligned); workgroup 0 also
+// writes the Q8_K records out. The activation loads are issued first, then
+// the weight loads of the first 16 records, so the weights stream in while
+// the records are being quantized. One launch instead of two.
+constexpr int kFusedMaxG = 64;
+constexpr int kLdsRec = 304;
+
+template <int RW>
+__global__ __launch_bounds__(256) void q4k_projection_kernel(const uint8_t* __restrict__ w, int64_t ldw, int N,
+                                                             int G, const float* __restrict__ x, int64_t ldx,
+                                                             uint8_t* __restrict__ xq_out, float* __restrict__ y) {
+  __shared__ __attribute__((aligned(16))) uint8_t xs[kFusedMaxG * kLdsRec];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = (blockIdx.x * 4 + wave) * RW;
+  const int u = lane & 3;
+  // Records g = wave + 4i of this wave (up to kFusedMaxG / 4).
+  constexpr int kPerWave = kFusedMaxG / 4;
+  f32x4 xv[kPerWave];
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int g = wave + 4 * i;
+    if (g < G) xv[i] = *reinterpret_cast<const f32x4*>(x + (int64_t)g * ldx + 4 * lane);
+  }
+  const int b0 = (lane >> 2) < G ? (lane >> 2) : G - 1;
+  Q4Frag f0[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int n = row0 + r < N ? row0 + r : N - 1;
+    f0[r] = load_q4(make_rsrc(w + (int64_t)n * ldw), b0, u);
+  }
+#pragma unroll
+  for (int i = 0; i < kPerWave; ++i) {
+    const int g = wave + 4 * i;
+    if (g < G) {
+      const Q8Lane q = quantize_lane(xv[i]);
+      uint8_t* r = xs + g * kLdsRec;
+      *reinterpret_cast<uint32_t*>(r + 16 + 4 * lane) = q.packed;
+      if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(r + 272 + 2 * (lane >> 2)) = (int16_t)q.bsum;
+      if (lane == 0) *reinterpret_cast<float*>(r) = q.ds;
+      if (blockIdx.x == 0) store_q8_record(xq_out + (int64_t)g * kQ8Bytes, q, lane);
+    }
+  }
+  __syncthreads();
+  if (row0 >= N) return;  // wave-uniform, after the barrier
+
+  float total[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) total[r] = 0.f;
+  for (int c0 = 0; c0 < G; c0 += 16) {
+    const int b = c0 + (lane >> 2) < G ? c0 + (lane >> 2) : G - 1;
+    const uint8_t* rec = xs + b * kLdsRec;
+    uint32_t xqv[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(rec + 16 + 64 * u + 16 * i);
+      xqv[4 * i] = v[0], xqv[4 * i + 1] = v[1], xqv[4 * i + 2] = v[2], xqv[4 * i + 3] = v[3];
+    }
+    const u32x2 bs = *reinterpret_cast<const u32x2*>(rec + 272 + 8 * u);
+    const float ds = *reinterpret_cast<const float*>(rec);
+    const int bsum_lo = (int)(int16_t)(bs[0] & 0xFFFFu) + (int)(int16_t)(bs[0] >> 16);
+    const int bsum_hi = (int)(int16_t)(bs[1] & 0xFFFFu) + (int)(int16_t)(bs[1] >> 16);
+    const int cnt = G - c0 < 16 ? G - c0 : 16;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      Q4Frag f = f0[r];
+      if (c0 > 0) {
+        const int n = row0 + r < N ? row0 + r : N - 1;
+        f = load_q4(make_rsrc(w + (int64_t)n * ldw), b, u);
       }
-      int S = q4k_field(hdr, 0, 2 * u) * dlo + q4k_field(hdr, 0, 2 * u + 1) * dhi;
-      int T = q4k_field(hdr, 1, 2 * u) * bsum_lo + q4k_field(hdr, 1, 2 * u + 1) * bsum_hi;
-      S += __shfl_xor(S, 1);
-      S += __shfl_xor(S, 2);
-      T += __shfl_xor(T, 1);
-      T += __shfl_xor(T, 2);
-      const float d = (float)bit_cast<f16>((uint16_t)(hdr[0] & 0xFFFFu));
-      const float dmin = (float)bit_cast<f16>((uint16_t)(hdr[0] >> 16));
-      const float p = __fmul_rn(d, (float)S);
-      const float nn = __fmul_rn(dmin, (float)T);
-      const float v = __fmul_rn(ds, __fsub_rn(p, nn));
-      // Record order: lane 4k holds record c0 + k.
-      const int cnt = G - c0 < 16 ? G - c0 : 16;
-      float t = total[r];
-      for (int k = 0; k < cnt; ++k)
-        t = __fadd_rn(t, bit_cast<float>(__builtin_amdgcn_readlane(bit_cast<int>(v), 4 * k)));
-      total[r] = t;
+      total[r] = add_in_order(total[r], record_value(f.hdr, f.q0, f.q1, xqv, bsum_lo, bsum_hi, ds, u), cnt);
     }
   }
   if (lane < RW) {
@@ -198,6 +316,17 @@ extern "C" int intent_q4k_projection(const uint8_t* w, int64_t N, int64_t G, int
   intent::clear_error();
   int st = quantize_check(x, G, x_ld, xq_records, kQ8Bytes);
   if (st != INTENT_OK) return st;
+  if (G > 0 && G <= kFusedMaxG && N > 0) {
+    INTENT_REQUIRE(w && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+    INTENT_REQUIRE(N <= INT32_MAX, INTENT_ERR_INVALID_ARGUMENT, "bad extent N=%lld", (long long)N);
+    INTENT_REQUIRE(w_ld >= G * kQ4Bytes, INTENT_ERR_INVALID_ARGUMENT, "weight row stride smaller than G records");
+    INTENT_REQUIRE(intent::aligned16(w) && w_ld % 16 == 0, INTENT_ERR_ALIGNMENT,
+                   "weights must be 16-byte aligned with 16-byte row strides");
+    const int64_t waves = (N + kRows - 1) / kRows;
+    hipLaunchKernelGGL((q4k_projection_kernel<kRows>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, w, w_ld, (int)N, (int)G, x, x_ld, xq_records, y);
+    return intent::launch_status("q4k_projection");
+  }
   if (G > 0) {
     hipLaunchKernelGGL(q8k_quantize_kernel, dim3((unsigned)((G + 3) / 4)), dim3(256), 0, (hipStream_t)stream, x,
                        x_ld, (int)G, xq_records, (int64_t)kQ8Bytes);

@@ -359,6 +359,25 @@ def test_quantized_projection_full_size_bit_exact(gpu, threads):
     assert np.array_equal(_bits(host(y)), _bits(ref))
 
 
+@pytest.mark.parametrize("N,G", [(1, 1), (9, 3), (100, 16), (33, 17), (64, 64), (5, 65), (70, 100)])
+def test_quantized_projection_bit_exact(gpu, N, G):
+    """Both projection paths (one fused launch for G <= 64, quantize + GEMV
+    above): the output and the Q8_K records written on the way."""
+    from intent_amd import _native
+
+    rng = np.random.default_rng(300 + N + G)
+    w = inputs.q4k_records(rng, (N, G))
+    x = _kquant_x(N * 3 + G, G)
+    wd, xd = dev(w), dev(x)
+    rec = torch.full((G, 292), 0xAB, dtype=torch.uint8, device="cuda")
+    y = torch.full((N,), float("nan"), dtype=torch.float32, device="cuda")
+    _native.call("intent_q4k_projection", wd.data_ptr(), N, G, G * 144, xd.data_ptr(), 256, rec.data_ptr(),
+                 y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    xq = oracle.q8k_quantize(x)
+    assert np.array_equal(host(rec), xq)
+    assert np.array_equal(_bits(host(y)), _bits(oracle.q4k_gemv(w, xq)))
+
+
 def test_golden_kquant(gpu):
     g = np.load(GOLDEN / "q4k_n7_g3.npz")
     assert np.array_equal(host(art(intent.q8_k_quantize).run(dev(g["x"]))), g["xq"])
