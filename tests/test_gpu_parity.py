@@ -132,7 +132,7 @@ def test_w8a8_config3(gpu, threads):
     assert torch.equal(out.view(torch.int16), f.to(torch.bfloat16).view(torch.int16)), "bf16 epilogue not exact"
 
 
-@pytest.mark.parametrize("M,K,N", [(100, 192, 77), (1, 64, 1), (129, 640, 257)])
+@pytest.mark.parametrize("M,K,N", [(100, 192, 77), (1, 64, 1), (129, 640, 257), (4000, 192, 4100), (4096, 64, 4096)])
 def test_i8_gemm_bias(gpu, threads, M, K, N):
     rng = np.random.default_rng(5)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
