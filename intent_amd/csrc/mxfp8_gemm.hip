@@ -5,10 +5,12 @@
 // CPU semantics lib/Conversion/KIRToCPU/Contractions.cpp:177-259: decode each
 // operand to f32 = value * 2^(s-127), E8M0 255 = NaN, then an f32 contraction).
 //
-// The pipeline is the int8 one (mfma_pipe.h): 128 k per LDS stage, both
-// operands through VGPRs into XOR-swizzled LDS rows, two stages in flight.
-// Each stage also carries one dword of scales per tile row (the four E8M0
-// bytes of its four 32-k groups). One scaled MFMA covers 64 k (step s). The
+// Two kernels share the stage layout: 128 k per LDS stage in XOR-swizzled
+// 128-byte rows, plus one dword of scales per tile row (the four E8M0 bytes
+// of its four 32-k groups). Problems with at least 256 tiles of 256 x 256 use
+// four waves of 128 x 128 fed by LDS DMA (mxfp8_gemm_dma_kernel); smaller
+// ones use 128 x 128 tiles on the int8 pipeline (mfma_pipe.h: operands
+// through VGPRs, two stages in flight) for more workgroups. One scaled MFMA covers 64 k (step s). The
 // instruction reads a lane's 32 operand bytes as two 16-k halves, k 16h..16h+15
 // and 32+16h..32+16h+15 of the step (h = lane / 32), and applies lane half
 // b's scale to k 32b..32b+31; so lane half h takes LDS chunks 4s+h and
@@ -16,7 +18,7 @@
 // halves read as one contiguous 32-k run, groups with different scales mix.)
 #include "common.h"
 #include "internal.h"
-#include "mfma_pipe.h"
+#include "w4pk.h"
 
 namespace {
 
@@ -112,6 +114,33 @@ INTENT_DEVICE void compute_stage_mx(const char* buf, i32x16 (&acc)[T::TI][T::TJ]
   }
 }
 
+// Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
+template <class T>
+INTENT_DEVICE void store_mx(const i32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N, float* __restrict__ out,
+                            int64_t ldo) {
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        const f32x16 c = bit_cast<f32x16>(acc[i][j]);
+        float* o = out + (int64_t)m * ldo + n;
+        if (vec && n + 3 < N) {
+          *reinterpret_cast<f32x4*>(o) = f32x4{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < N) o[q] = c[4 * g + q];
+        }
+      }
+  }
+}
+
 template <class T>
 __global__ __launch_bounds__(T::NT, 1) void mxfp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
                                                               const uint8_t* __restrict__ sa, int64_t ld_sa,
@@ -173,28 +202,182 @@ __global__ __launch_bounds__(T::NT, 1) void mxfp8_gemm_kernel(const uint8_t* __r
   }
   compute_stage_mx<T>((kt & 1) ? buf1 : buf0, acc);
 
-  // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
-  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
+  store_mx<T>(acc, m0, n0, M, N, out, ldo);
+}
+
+// ---- 256 x 256 tiles, four waves, operands and scales by LDS DMA --------------
+// Four waves of 128 x 128 (one per SIMD; the 256 accumulators live in AGPRs).
+// Operand rows and scale dwords are copied global -> LDS by DMA
+// (buffer_load ... lds), so no staging registers are needed and the 32-byte
+// fragments of both steps of a stage fit beside the accumulators. A stage is
+// 128 k: 128 bytes of every tile row (8 rows per DMA instruction, chunk c of
+// row r in slot c ^ swz(r)) plus one scale dword per row (64 rows per DMA
+// instruction). Two stage buffers; the refill of a buffer is issued right
+// after the stage's barrier, which sits after the stage's last fragment
+// reads, so the next stage's first reads overlap the last step's MFMAs.
+namespace mxdma {
+
+using Tile = mp::Tile<256, 256, 2, 2>;
+constexpr int kRowBytes = (Tile::BM + Tile::BN) * mp::ROWB;
+constexpr int kStage = kRowBytes + (Tile::BM + Tile::BN) * 4;
+
+template <int ROWS, int NW>
+struct Rows {
+  static constexpr int N_INST = ROWS / 8 / NW;  // data instructions per wave
+  static constexpr int S_INST = ROWS / 64 / NW;  // scale instructions per wave
+  static_assert(N_INST * 8 * NW == ROWS && S_INST * 64 * NW == ROWS, "tile rows must split evenly");
+  static constexpr int NVM = N_INST + S_INST;
+  mp::Rsrc rd, rs;
+  uint32_t voff[N_INST], soff[S_INST];
+  int wave;
+  INTENT_DEVICE void init(const uint8_t* rows, int64_t ld, int M, const uint8_t* scales, int64_t ld_scale, int m0,
+                          int w) {
+    wave = w;
+    rd = make_rsrc(rows + (int64_t)m0 * ld);
+    rs = make_rsrc(scales + (int64_t)m0 * ld_scale);
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
-    const int m = m0 + T::row(i);
-    if (m >= M) continue;
+    for (int j = 0; j < N_INST; ++j) {
+      const int r = (j * NW + w) * 8 + (lane >> 3);
+      const int rr = m0 + r < M ? r : M - 1 - m0;
+      voff[j] = (uint32_t)(rr * ld + (((lane & 7) ^ mp::swz(r)) << 4));
+    }
+#pragma unroll
+    for (int j = 0; j < S_INST; ++j) {
+      const int r = (j * NW + w) * 64 + lane;
+      const int rr = m0 + r < M ? r : M - 1 - m0;
+      soff[j] = (uint32_t)(rr * ld_scale);
+    }
+  }
+  // rows: this operand's row region of a stage; scl: its scale region.
+  INTENT_DEVICE void issue(char* rows, char* scl, int kt) const {
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (mp::lds_t*)(rows + (j * NW + wave) * 8 * mp::ROWB), 16, voff[j],
+                                               (uint32_t)kt * mp::ROWB, 0, 0);
+#pragma unroll
+    for (int j = 0; j < S_INST; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (mp::lds_t*)(scl + (j * NW + wave) * 64 * 4), 4, soff[j],
+                                               (uint32_t)kt * 4, 0, 0);
+  }
+};
+
+}  // namespace mxdma
+
+__global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                                const uint8_t* __restrict__ sa, int64_t ld_sa,
+                                                                const uint8_t* __restrict__ b, int64_t ldb, int N,
+                                                                const uint8_t* __restrict__ sb, int64_t ld_sb, int K,
+                                                                float* __restrict__ out, int64_t ldo, int mblocks) {
+  using T = mxdma::Tile;
+  constexpr int SB = mxdma::kStage;
+  constexpr int A_SC = mxdma::kRowBytes;
+  constexpr int B_SC = A_SC + T::BM * 4;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * SB];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  const int wave = T::wave();
+  const int nk = K / mp::ROWB;
+  mxdma::Rows<T::BM, T::NW> aop;
+  mxdma::Rows<T::BN, T::NW> bop;
+  aop.init(a, lda, M, sa, ld_sa, m0, wave);
+  bop.init(b, ldb, N, sb, ld_sb, n0, wave);
+  constexpr int NV = mxdma::Rows<T::BM, T::NW>::NVM + mxdma::Rows<T::BN, T::NW>::NVM;
+  static_assert(2 * NV < 64, "vmcnt range");
+
+  i32x16 acc[T::TI][T::TJ];
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i)
 #pragma unroll
     for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + T::col(j, g);
-        const f32x16 c = bit_cast<f32x16>(acc[i][j]);
-        float* o = out + (int64_t)m * ldo + n;
-        if (vec && n + 3 < N) {
-          *reinterpret_cast<f32x4*>(o) = f32x4{c[4 * g], c[4 * g + 1], c[4 * g + 2], c[4 * g + 3]};
-        } else {
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;  // the bits of +0.0f
+
+  const int lane = threadIdx.x & 63;
+  const int h = lane >> 5;
+  const int ra = T::wave_m() * T::WTM + (lane & 31);
+  const int rb = T::wave_n() * T::WTN + (lane & 31);
+  auto issue = [&](int slot, int kt) {
+    char* base = smem + slot * SB;
+    const int st = kt < nk ? kt : nk - 1;  // past the end: the last stage again, into a buffer nobody reads
+    aop.issue(base, base + A_SC, st);
+    bop.issue(base + T::A_BYTES, base + B_SC, st);
+  };
+  // Fragments of step s: lane half h reads chunks 4s+h and 4s+2+h; two
+  // register sets (step parity). Scales: one dword per fragment row and
+  // stage; the next stage's are read into nsa / nsb and become current at the
+  // stage's end.
+  i32x8 af[2][T::TI], bf[2][T::TJ];
+  uint32_t csa[T::TI], csb[T::TJ], nsa[T::TI], nsb[T::TJ];
+  auto read = [&](const char* base, int s, int set) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (n + q < N) o[q] = c[4 * g + q];
-        }
+    for (int i = 0; i < T::TI; ++i) af[set][i] = read_frag(base, ra + 32 * i, 4 * s + h);
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j) bf[set][j] = read_frag(base + T::A_BYTES, rb + 32 * j, 4 * s + h);
+  };
+  auto read_scales = [&](const char* base, uint32_t (&xa)[T::TI], uint32_t (&xb)[T::TJ]) {
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i) xa[i] = *reinterpret_cast<const uint32_t*>(base + A_SC + (ra + 32 * i) * 4);
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j) xb[j] = *reinterpret_cast<const uint32_t*>(base + B_SC + (rb + 32 * j) * 4);
+  };
+  auto mfmas = [&](int s) {
+    const int sh = 8 * (2 * s + h);
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) {
+        f32x16 c = bit_cast<f32x16>(acc[i][j]);
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[s][j], af[s][i], c, 0, 0, 0, (int)((csb[j] >> sh) & 255u),
+                                                             0, (int)((csa[i] >> sh) & 255u));
+        acc[i][j] = bit_cast<i32x16>(c);
       }
-  }
+  };
+  // Schedule hint: each MFMA followed by its share of NR LDS reads (0x100).
+  auto interleave = [&](auto NR) {
+    mp::static_for<0, T::TI * T::TJ>([&](auto X) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      constexpr int x = decltype(X)::value;
+      constexpr int nr = decltype(NR)::value;
+      constexpr int r = (x + 1) * nr / (T::TI * T::TJ) - x * nr / (T::TI * T::TJ);
+      if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
+    });
+  };
+
+  issue(0, 0);
+  issue(1, 1);
+  mp::wait_vm_lgkm_barrier<NV>();
+  read_scales(smem, csa, csb);
+  read(smem, 0, 0);
+
+  // The last stage is peeled off so that the loop body has no branch.
+  auto stage = [&](int kt, auto more) {
+    const int slot = kt & 1;
+    const char* base = smem + slot * SB;
+    read(base, 1, 1);
+    mfmas(0);
+    interleave(std::integral_constant<int, 2 * (T::TI + T::TJ)>{});
+    if constexpr (decltype(more)::value) {
+      mp::wait_vm_lgkm_barrier<0>();  // stage kt+1 landed everywhere; stage kt fully read
+      issue(slot, kt + 2);
+      const char* nb = smem + (slot ^ 1) * SB;
+      read_scales(nb, nsa, nsb);
+      read(nb, 0, 0);
+      mfmas(1);
+      interleave(std::integral_constant<int, 2 * (T::TI + T::TJ) + 4>{});
+#pragma unroll
+      for (int i = 0; i < T::TI; ++i) csa[i] = nsa[i];
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) csb[j] = nsb[j];
+    } else {
+      mfmas(1);
+    }
+  };
+  for (int kt = 0; kt < nk - 1; ++kt) stage(kt, std::true_type{});
+  stage(nk - 1, std::false_type{});
+  mp::wait_vm<0>();  // no DMA may still be writing LDS when the workgroup ends
+
+  store_mx<T>(acc, m0, n0, M, N, out, ldo);
 }
 
 // 128 x 128 tiles, four waves of 64 x 64 (a 256 x 256 tile does not fit the
@@ -234,6 +417,14 @@ extern "C" int intent_mxfp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t
   INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, b_ld) &&
                      intent::fits_offset(M, a_scales_ld) && intent::fits_offset(N, b_scales_ld),
                  INTENT_ERR_UNSUPPORTED, "mxfp8_gemm: operand too large for 31-bit buffer offsets");
+  const int64_t big = ((M + 255) / 256) * ((N + 255) / 256);
+  if (big >= 256) {
+    const int mblocks = (int)((M + 255) / 256);
+    INTENT_REQUIRE(big < (1ll << 31), INTENT_ERR_UNSUPPORTED, "mxfp8_gemm: grid too large");
+    hipLaunchKernelGGL(mxfp8_gemm_dma_kernel, dim3((unsigned)big), dim3(256), 0, (hipStream_t)stream, a, a_ld, (int)M,
+                       a_scales, a_scales_ld, b, b_ld, (int)N, b_scales, b_scales_ld, (int)K, out, out_ld, mblocks);
+    return intent::launch_status("mxfp8_gemm");
+  }
   return launch_mx<TMx128>(a, M, K, a_ld, a_scales, a_scales_ld, b, N, b_ld, b_scales, b_scales_ld, out, out_ld,
                            stream);
 }
