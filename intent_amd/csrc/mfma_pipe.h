@@ -246,9 +246,15 @@ struct LowBitRowsOperand {
       return u32x4{d & 0x03030303u, (d >> 2) & 0x03030303u, (d >> 4) & 0x03030303u, (d >> 6) & 0x03030303u};
     }
   }
+  template <bool kAsm = false>  // kAsm: see lds_store16
   INTENT_DEVICE void store(const Regs& r, char* lds_region) const {
 #pragma unroll
-    for (int j = 0; j < N_INST; ++j) *reinterpret_cast<u32x4*>(lds_region + lds_off[j]) = decode(r.v[j]);
+    for (int j = 0; j < N_INST; ++j) {
+      if constexpr (kAsm)
+        lds_store16(lds_region + lds_off[j], decode(r.v[j]));
+      else
+        *reinterpret_cast<u32x4*>(lds_region + lds_off[j]) = decode(r.v[j]);
+    }
   }
 };
 
@@ -432,7 +438,9 @@ struct W8Operand {
 
 // Fragment reads and MFMAs of one stage (KK steps of 32 bytes of k). The reads
 // of step kk+1 are interleaved one-for-one with the MFMAs of step kk.
-template <class T, class Math, int KK = 4, bool kSched = true>
+// kSwap: issue mfma(A, B) instead of mfma(B, A), so that a lane's
+// accumulators hold one n and four consecutive m per 4-register group.
+template <class T, class Math, int KK = 4, bool kSched = true, bool kSwap = false>
 INTENT_DEVICE void compute_stage(const char* buf, const uint32_t (&aaddr)[4], const uint32_t (&baddr)[4],
                                  typename Math::Acc (&acc)[T::TI][T::TJ]) {
   using Frag = typename Math::Frag;
@@ -459,7 +467,8 @@ INTENT_DEVICE void compute_stage(const char* buf, const uint32_t (&aaddr)[4], co
 #pragma unroll
     for (int i = 0; i < T::TI; ++i)
 #pragma unroll
-      for (int j = 0; j < T::TJ; ++j) acc[i][j] = Math::mfma(bf[cb][j], af[cb][i], acc[i][j]);
+      for (int j = 0; j < T::TJ; ++j)
+        acc[i][j] = kSwap ? Math::mfma(af[cb][i], bf[cb][j], acc[i][j]) : Math::mfma(bf[cb][j], af[cb][i], acc[i][j]);
   }
   if constexpr (kSched) {
     // Standalone stage (no loads or stores around it): the first step's
@@ -600,7 +609,7 @@ INTENT_DEVICE void mainloop(const AOp& aop, const BOp& bop, int nk, char* buf0, 
 // each). Operands must be built with NT = T::NT (producer thread index =
 // threadIdx.x % NT) and the producer wave index. Returns true in consumer
 // waves, which then hold acc.
-template <class T, class Math, int NB, class Rows, class BOp>
+template <class T, class Math, int NB, class Rows, class BOp, bool kSwap = false>
 INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, const BOp& bop, int nk,
                                char* const (&bufs)[NB], typename Math::Acc (&acc)[T::TI][T::TJ]) {
   static_assert(NB == 2 || NB == 3, "two or three stage buffers");
@@ -669,7 +678,7 @@ INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, co
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if (kt + j < nk) {
-        compute_stage<T, Math>(bufs[j], aaddr, baddr, acc);
+        compute_stage<T, Math, 4, true, kSwap>(bufs[j], aaddr, baddr, acc);
         if (kt + j < nk - 1) wait_vm_lgkm_barrier<0>();
       }
     }

@@ -122,6 +122,63 @@ __global__ __launch_bounds__(T::NT, 1) void lowbit_gemm_kernel(const int8_t* __r
   store_tile<T, Epi::kI32Bias>(acc, r0, c0, rows, cols, nullptr, nullptr, nullptr, out, ldo);
 }
 
+// Large W4A8 / BitNet problems on producer/consumer workgroups
+// (mainloop_ws): four consumer waves only read fragments and issue MFMAs;
+// four producer waves copy the int8 activation rows by LDS DMA and load,
+// decode and store the packed weight rows as int8. The activations are the
+// tile's A side (rows m), the weights its B side (rows n). For W4A8 (output
+// [N, M]) the MFMA operands are swapped so that a lane holds one weight row n
+// and four consecutive activation rows m per register group, four adjacent
+// int32 of the output; BitNet's output is [M, N], the usual lane layout.
+using TWs = mp::Tile<256, 192, 2, 2>;  // consumers of 128 x 96
+
+template <class T, bool kBitNet>
+__global__ __launch_bounds__(T::NT_WS, 1) void lowbit_ws_kernel(const int8_t* __restrict__ act, int64_t ld_act, int M,
+                                                                const uint8_t* __restrict__ wq, int64_t ld_w, int N,
+                                                                int K, int32_t* __restrict__ out, int64_t ldo,
+                                                                int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  char* const bufs[2] = {buf0, buf1};
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  const int pw = T::wave() % T::NW;
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{act, ld_act, M}, m0, pw);
+  mp::LowBitRowsOperand<T::BN, kBitNet ? mp::LowBit::kInt2 : mp::LowBit::kSignedNibble, T::NW> bop;
+  bop.init(wq, ld_w, N, n0, pw);
+  i32x16 acc[T::TI][T::TJ];
+  if (!mp::mainloop_ws<T, mp::I8Math, 2, mp::DenseRows, decltype(bop), !kBitNet>(aop, bop, K / mp::ROWB, bufs, acc))
+    return;
+  if constexpr (kBitNet) {
+    store_tile<T, Epi::kI32Bias>(acc, m0, n0, M, N, nullptr, nullptr, nullptr, out, ldo);
+    return;
+  }
+  // acc[i][j][4g + c]: n = col j, lane % 32; m = row block i, 8g + 4h + c.
+  const int lane = threadIdx.x & 63;
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
+#pragma unroll
+  for (int j = 0; j < T::TJ; ++j) {
+    const int n = n0 + T::wave_n() * T::WTN + j * 32 + (lane & 31);
+    if (n >= N) continue;
+    int32_t* row = out + (int64_t)n * ldo;
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int m = m0 + T::wave_m() * T::WTM + i * 32 + g * 8 + (lane >> 5) * 4;
+        if (vec && m + 3 < M) {
+          *reinterpret_cast<i32x4*>(row + m) =
+              i32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (m + c < M) row[m + c] = acc[i][j][4 * g + c];
+        }
+      }
+  }
+}
+
 int check_i8(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const int8_t* w, int64_t N, int64_t w_ld,
              const void* out, int64_t out_ld) {
   INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0, INTENT_ERR_INVALID_ARGUMENT, "negative extent");
@@ -222,7 +279,14 @@ int lowbit_entry(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint
   INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, w_ld), INTENT_ERR_UNSUPPORTED,
                  "%s: operand too large for 31-bit buffer offsets", name);
   const int64_t big = ((M + 255) / 256) * ((N + 255) / 256);
-  if (big >= 256) return launch_lowbit<T256, kBitNet>(a, M, K, a_ld, w, N, w_ld, out, out_ld, stream, name);
+  if (big >= 256) {
+    const int mblocks = (int)((M + TWs::BM - 1) / TWs::BM);
+    const int64_t grid = (int64_t)mblocks * ((N + TWs::BN - 1) / TWs::BN);
+    INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
+    hipLaunchKernelGGL((lowbit_ws_kernel<TWs, kBitNet>), dim3((unsigned)grid), dim3(TWs::NT_WS), 0,
+                       (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, out, out_ld, mblocks);
+    return intent::launch_status(name);
+  }
   return launch_lowbit<T128, kBitNet>(a, M, K, a_ld, w, N, w_ld, out, out_ld, stream, name);
 }
 

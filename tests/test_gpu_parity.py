@@ -410,7 +410,8 @@ def test_fp8_groupwise_quantize_bit_exact(gpu, src, M, N, G):
 
 # ---- W4A8 and BitNet int2: exact int32 ----------------------------------------------
 
-@pytest.mark.parametrize("M,K,N", [(1, 128, 1), (37, 256, 100), (300, 384, 130), (512, 2048, 1024)])
+@pytest.mark.parametrize("M,K,N", [(1, 128, 1), (37, 256, 100), (300, 384, 130), (512, 2048, 1024), (4000, 256, 4100),
+                                   (4100, 384, 3900)])
 def test_w4a8_and_bitnet_exact(gpu, threads, M, K, N):
     rng = np.random.default_rng(M + 3 * N)
     a = rng.integers(-128, 128, (M, K), dtype=np.int8)
