@@ -58,7 +58,7 @@ def w4_case(seed, M, K, N, group):
 
 # ---- W4A16 --------------------------------------------------------------------------
 
-@pytest.mark.parametrize("M", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16])
 def test_w4a16_decode_config1(gpu, threads, M):
     x, q, s, z = w4_case(0, M, 4096, 4096, 128)
     y = art(intent.weight_only_int4_asym_matmul).run(dev(x), dev(q), dev(s), dev(z))
@@ -70,7 +70,7 @@ def test_w4a16_decode_config1(gpu, threads, M):
 @pytest.mark.parametrize("M,K,N,group", [(3, 256, 100, 64), (1, 384, 48, 32), (16, 128, 17, 128),
                                          (5, 2048, 1000, 256), (1, 8192, 64, 128),
                                          (2, 8192, 33, 128), (1, 16384, 24, 128), (2, 384, 40, 128),
-                                         (1, 1024, 20, 64)])
+                                         (1, 1024, 20, 64), (3, 3072, 77, 128), (3, 8192, 40, 128)])
 def test_w4a16_gemv_shapes(gpu, threads, M, K, N, group):
     x, q, s, z = w4_case(1, M, K, N, group)
     y = art(intent.weight_only_int4_asym_matmul, KERNEL="gemv").run(dev(x), dev(q), dev(s), dev(z))
