@@ -322,6 +322,33 @@ int intent_mxfp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
                       const uint8_t* b_scales, int64_t b_scales_ld,
                       float* out, int64_t out_ld, void* stream);
 
+/* Byte-matrix transpose: dst[c * dst_ld + r] = src[r * src_ld + c] for an
+ * R x C matrix of one-byte elements (FP8). Plumbing for the contractions whose
+ * right operand the reference passes as [K, N] (N contiguous): the FP8 MFMA
+ * reads both operands K-contiguous. Replaces no reference function.
+ */
+int intent_fp8_transpose(const uint8_t* src, int64_t rows, int64_t cols, int64_t src_ld,
+                         uint8_t* dst, int64_t dst_ld, void* stream);
+
+/* Per-tensor scaled FP8 (E4M3FN) GEMM with an f16 result. Replaces
+ * scaled_fp8_matmul (examples/kernels/contraction/block_scaled.py:42-63) with
+ * splits == 1, accumulate == 0: out = f16((acc * a_scale) * b_scale), acc the
+ * f32 sum over k; and scaled_fp8_splitk_matmul (block_scaled.py:66-98) with
+ * splits == SP, accumulate == 1, where k = (it*SP + s)*256 + r (the operands'
+ * [.., IT, SP, 256] layout): for s = 0 .. SP-1 in order,
+ * out = f16(out + f16((acc_s * a_scale) * b_scale)) (the reference's CPU
+ * baseline order, experiments/cpu/baselines/pytorch/cpu_runtime.py:133-139;
+ * its GPU form adds the splits with relaxed atomics, in no fixed order).
+ * a: [M, K] (K contiguous, a_ld bytes); bt: the right operand as [N, K] rows
+ * (bt_ld bytes; use intent_fp8_transpose for a [K, N] operand); out: f16
+ * [M, N] (out_ld elements, read and written when accumulate).
+ * K % 128 == 0 (K % (256 * splits) == 0 when splits > 1).
+ */
+int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                           const uint8_t* bt, int64_t N, int64_t bt_ld,
+                           float a_scale, float b_scale, int64_t splits, int accumulate,
+                           void* out, int64_t out_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,7 @@ P = ctypes.c_void_p
 I64 = ctypes.c_int64
 INT = ctypes.c_int
 SIZE = ctypes.c_size_t
+F32 = ctypes.c_float
 
 # Entry -> (argtypes, restype). Mirrors include/intent_amd.h.
 SIGNATURES: dict[str, tuple[list, object]] = {
@@ -45,6 +46,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_w4a8_gemm": ([P, I64, I64, I64, P, I64, I64, P, I64, P], INT),
     "intent_bitnet_int2_gemm": ([P, I64, I64, I64, P, I64, I64, P, I64, P], INT),
     "intent_mxfp8_gemm": ([P, I64, I64, I64, P, I64, P, I64, I64, P, I64, P, I64, P], INT),
+    "intent_fp8_transpose": ([P, I64, I64, I64, P, I64, P], INT),
+    "intent_scaled_fp8_gemm": ([P, I64, I64, I64, P, I64, I64, F32, F32, I64, INT, P, I64, P], INT),
     "intent_moe_workspace_size": ([I64, I64, I64, I64, I64, I64], SIZE),
     "intent_moe_expert_ffn_w4": ([P, P, I64, I64, I64, I64, INT, P, P, P, P, P, P, I64, I64, P, P, SIZE, P, P, P],
                                  INT),

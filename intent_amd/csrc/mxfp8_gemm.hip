@@ -221,20 +221,28 @@ using Tile = mp::Tile<256, 256, 2, 2>;
 constexpr int kRowBytes = (Tile::BM + Tile::BN) * mp::ROWB;
 constexpr int kStage = kRowBytes + (Tile::BM + Tile::BN) * 4;
 
-template <int ROWS, int NW>
+// Byte offset of stage kt (128 k) inside a row. With SP splits of 256-k
+// chunks interleaved along k (the [.., IT, SP, 256] layout of a split-K
+// contraction), split s reads chunks it*SP + s; SP = 1 is the plain order.
+struct SplitK {
+  int sp, s;
+  INTENT_DEVICE uint32_t operator()(int kt) const { return (uint32_t)(((kt >> 1) * sp + s) * 256 + (kt & 1) * 128); }
+};
+
+template <int ROWS, int NW, bool kScales>
 struct Rows {
-  static constexpr int N_INST = ROWS / 8 / NW;  // data instructions per wave
-  static constexpr int S_INST = ROWS / 64 / NW;  // scale instructions per wave
-  static_assert(N_INST * 8 * NW == ROWS && S_INST * 64 * NW == ROWS, "tile rows must split evenly");
+  static constexpr int N_INST = ROWS / 8 / NW;                    // data instructions per wave
+  static constexpr int S_INST = kScales ? ROWS / 64 / NW : 0;     // scale instructions per wave
+  static_assert(N_INST * 8 * NW == ROWS && (!kScales || S_INST * 64 * NW == ROWS), "tile rows must split evenly");
   static constexpr int NVM = N_INST + S_INST;
   mp::Rsrc rd, rs;
-  uint32_t voff[N_INST], soff[S_INST];
+  uint32_t voff[N_INST], soff[S_INST > 0 ? S_INST : 1];
   int wave;
   INTENT_DEVICE void init(const uint8_t* rows, int64_t ld, int M, const uint8_t* scales, int64_t ld_scale, int m0,
                           int w) {
     wave = w;
     rd = make_rsrc(rows + (int64_t)m0 * ld);
-    rs = make_rsrc(scales + (int64_t)m0 * ld_scale);
+    rs = make_rsrc(kScales ? scales + (int64_t)m0 * ld_scale : rows);
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < N_INST; ++j) {
@@ -249,12 +257,13 @@ struct Rows {
       soff[j] = (uint32_t)(rr * ld_scale);
     }
   }
-  // rows: this operand's row region of a stage; scl: its scale region.
-  INTENT_DEVICE void issue(char* rows, char* scl, int kt) const {
+  // rows: this operand's row region of a stage; scl: its scale region;
+  // koff: the stage's byte offset in a row; kt: its index (scale dword).
+  INTENT_DEVICE void issue(char* rows, char* scl, uint32_t koff, int kt) const {
 #pragma unroll
     for (int j = 0; j < N_INST; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (mp::lds_t*)(rows + (j * NW + wave) * 8 * mp::ROWB), 16, voff[j],
-                                               (uint32_t)kt * mp::ROWB, 0, 0);
+                                               koff, 0, 0);
 #pragma unroll
     for (int j = 0; j < S_INST; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (mp::lds_t*)(scl + (j * NW + wave) * 64 * 4), 4, soff[j],
@@ -262,37 +271,20 @@ struct Rows {
   }
 };
 
-}  // namespace mxdma
-
-__global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
-                                                                const uint8_t* __restrict__ sa, int64_t ld_sa,
-                                                                const uint8_t* __restrict__ b, int64_t ldb, int N,
-                                                                const uint8_t* __restrict__ sb, int64_t ld_sb, int K,
-                                                                float* __restrict__ out, int64_t ldo, int mblocks) {
-  using T = mxdma::Tile;
-  constexpr int SB = mxdma::kStage;
-  constexpr int A_SC = mxdma::kRowBytes;
+// acc += A·B over nk stages (stage kt at byte offset koff(kt) of every row).
+// Without kScales every block scale is E8M0 127 (2^0): a plain FP8 product.
+// Starts with a barrier, so that it can run again on the same LDS, and ends
+// with no DMA in flight.
+template <bool kScales, class KOff>
+INTENT_DEVICE void dma_mainloop(char* smem, const Rows<Tile::BM, Tile::NW, kScales>& aop,
+                                const Rows<Tile::BN, Tile::NW, kScales>& bop, int nk, KOff koff,
+                                i32x16 (&acc)[Tile::TI][Tile::TJ]) {
+  using T = Tile;
+  constexpr int SB = kStage;
+  constexpr int A_SC = kRowBytes;
   constexpr int B_SC = A_SC + T::BM * 4;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * SB];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
-  const int wave = T::wave();
-  const int nk = K / mp::ROWB;
-  mxdma::Rows<T::BM, T::NW> aop;
-  mxdma::Rows<T::BN, T::NW> bop;
-  aop.init(a, lda, M, sa, ld_sa, m0, wave);
-  bop.init(b, ldb, N, sb, ld_sb, n0, wave);
-  constexpr int NV = mxdma::Rows<T::BM, T::NW>::NVM + mxdma::Rows<T::BN, T::NW>::NVM;
+  constexpr int NV = Rows<T::BM, T::NW, kScales>::NVM + Rows<T::BN, T::NW, kScales>::NVM;
   static_assert(2 * NV < 64, "vmcnt range");
-
-  i32x16 acc[T::TI][T::TJ];
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i)
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;  // the bits of +0.0f
-
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5;
   const int ra = T::wave_m() * T::WTM + (lane & 31);
@@ -300,8 +292,8 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
   auto issue = [&](int slot, int kt) {
     char* base = smem + slot * SB;
     const int st = kt < nk ? kt : nk - 1;  // past the end: the last stage again, into a buffer nobody reads
-    aop.issue(base, base + A_SC, st);
-    bop.issue(base + T::A_BYTES, base + B_SC, st);
+    aop.issue(base, base + A_SC, koff(st), st);
+    bop.issue(base + T::A_BYTES, base + B_SC, koff(st), st);
   };
   // Fragments of step s: lane half h reads chunks 4s+h and 4s+2+h; two
   // register sets (step parity). Scales: one dword per fragment row and
@@ -317,9 +309,11 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
   };
   auto read_scales = [&](const char* base, uint32_t (&xa)[T::TI], uint32_t (&xb)[T::TJ]) {
 #pragma unroll
-    for (int i = 0; i < T::TI; ++i) xa[i] = *reinterpret_cast<const uint32_t*>(base + A_SC + (ra + 32 * i) * 4);
+    for (int i = 0; i < T::TI; ++i)
+      xa[i] = kScales ? *reinterpret_cast<const uint32_t*>(base + A_SC + (ra + 32 * i) * 4) : 0x7F7F7F7Fu;
 #pragma unroll
-    for (int j = 0; j < T::TJ; ++j) xb[j] = *reinterpret_cast<const uint32_t*>(base + B_SC + (rb + 32 * j) * 4);
+    for (int j = 0; j < T::TJ; ++j)
+      xb[j] = kScales ? *reinterpret_cast<const uint32_t*>(base + B_SC + (rb + 32 * j) * 4) : 0x7F7F7F7Fu;
   };
   auto mfmas = [&](int s) {
     const int sh = 8 * (2 * s + h);
@@ -344,6 +338,7 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
     });
   };
 
+  __syncthreads();  // a previous pass over this LDS is fully read
   issue(0, 0);
   issue(1, 1);
   mp::wait_vm_lgkm_barrier<NV>();
@@ -364,7 +359,7 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
       read_scales(nb, nsa, nsb);
       read(nb, 0, 0);
       mfmas(1);
-      interleave(std::integral_constant<int, 2 * (T::TI + T::TJ) + 4>{});
+      interleave(std::integral_constant<int, 2 * (T::TI + T::TJ) + (kScales ? 4 : 0)>{});
 #pragma unroll
       for (int i = 0; i < T::TI; ++i) csa[i] = nsa[i];
 #pragma unroll
@@ -376,8 +371,143 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
   for (int kt = 0; kt < nk - 1; ++kt) stage(kt, std::true_type{});
   stage(nk - 1, std::false_type{});
   mp::wait_vm<0>();  // no DMA may still be writing LDS when the workgroup ends
+}
 
+INTENT_DEVICE void zero(i32x16 (&acc)[Tile::TI][Tile::TJ]) {
+#pragma unroll
+  for (int i = 0; i < Tile::TI; ++i)
+#pragma unroll
+    for (int j = 0; j < Tile::TJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;  // the bits of +0.0f
+}
+
+}  // namespace mxdma
+
+__global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                                const uint8_t* __restrict__ sa, int64_t ld_sa,
+                                                                const uint8_t* __restrict__ b, int64_t ldb, int N,
+                                                                const uint8_t* __restrict__ sb, int64_t ld_sb, int K,
+                                                                float* __restrict__ out, int64_t ldo, int mblocks) {
+  using T = mxdma::Tile;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * mxdma::kStage];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  mxdma::Rows<T::BM, T::NW, true> aop;
+  mxdma::Rows<T::BN, T::NW, true> bop;
+  aop.init(a, lda, M, sa, ld_sa, m0, T::wave());
+  bop.init(b, ldb, N, sb, ld_sb, n0, T::wave());
+  i32x16 acc[T::TI][T::TJ];
+  mxdma::zero(acc);
+  mxdma::dma_mainloop<true>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, acc);
   store_mx<T>(acc, m0, n0, M, N, out, ldo);
+}
+
+// Per-tensor scaled FP8 GEMM with an f16 result (block_scaled.py:42-63 and,
+// with splits > 1, the split-K form :66-98): for each split s in order,
+//   p = f16((acc_s * lhs_scale) * rhs_scale)   (acc_s: the f32 sum over split s)
+// and out = p (kAccum false, one split) or out = f16(out + p) (kAccum).
+// A lane holds four adjacent n of one m per register group.
+template <bool kAccum>
+INTENT_DEVICE void store_f16_scaled(const i32x16 (&acc)[mxdma::Tile::TI][mxdma::Tile::TJ], int m0, int n0, int M,
+                                    int N, float ls, float rs, f16* __restrict__ out, int64_t ldo) {
+  using T = mxdma::Tile;
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        const f32x16 c = bit_cast<f32x16>(acc[i][j]);
+        f16* o = out + (int64_t)m * ldo + n;
+        f16 v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = (f16)__fmul_rn(__fmul_rn(c[4 * g + q], ls), rs);
+        if (vec && n + 3 < N) {
+          if constexpr (kAccum) {
+            const u32x2 old = *reinterpret_cast<const u32x2*>(o);
+            const f16x2 o0 = bit_cast<f16x2>(old[0]), o1 = bit_cast<f16x2>(old[1]);
+            v[0] = (f16)__fadd_rn((float)o0[0], (float)v[0]);
+            v[1] = (f16)__fadd_rn((float)o0[1], (float)v[1]);
+            v[2] = (f16)__fadd_rn((float)o1[0], (float)v[2]);
+            v[3] = (f16)__fadd_rn((float)o1[1], (float)v[3]);
+          }
+          f16x2 lo, hi;
+          lo[0] = v[0];
+          lo[1] = v[1];
+          hi[0] = v[2];
+          hi[1] = v[3];
+          *reinterpret_cast<u32x2*>(o) = u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < N) o[q] = kAccum ? (f16)__fadd_rn((float)o[q], (float)v[q]) : v[q];
+        }
+      }
+  }
+}
+
+// bt: the right operand as [N, K] rows (K contiguous). K % (256 * splits) == 0
+// when splits > 1, K % 128 == 0 otherwise. Splits run in order inside the
+// workgroup, each on the whole tile; with kAccum the f16 output tile is read
+// back by the same lanes that wrote it.
+template <bool kAccum>
+__global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                                 const uint8_t* __restrict__ bt, int64_t ldb, int N,
+                                                                 int K, int splits, float ls, float rs,
+                                                                 f16* __restrict__ out, int64_t ldo, int mblocks) {
+  using T = mxdma::Tile;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * mxdma::kStage];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  mxdma::Rows<T::BM, T::NW, false> aop;
+  mxdma::Rows<T::BN, T::NW, false> bop;
+  aop.init(a, lda, M, nullptr, 0, m0, T::wave());
+  bop.init(bt, ldb, N, nullptr, 0, n0, T::wave());
+  const int nks = K / mp::ROWB / splits;
+  i32x16 acc[T::TI][T::TJ];
+  for (int s = 0; s < splits; ++s) {
+    mxdma::zero(acc);
+    mxdma::dma_mainloop<false>(smem, aop, bop, nks, mxdma::SplitK{splits, s}, acc);
+    store_f16_scaled<kAccum>(acc, m0, n0, M, N, ls, rs, out, ldo);
+  }
+}
+
+// Byte-matrix transpose through a 64 x 64 LDS tile: dst[c][r] = src[r][c].
+__global__ __launch_bounds__(256) void byte_transpose_kernel(const uint8_t* __restrict__ src, int R, int C,
+                                                             int64_t sld, uint8_t* __restrict__ dst, int64_t dld) {
+  __shared__ uint8_t t[64][80];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int row = threadIdx.x >> 2, seg = (threadIdx.x & 3) * 16;
+  const bool full = r0 + 64 <= R && c0 + 64 <= C;
+  if (full && ((sld | (int64_t)(uintptr_t)src) & 15) == 0) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + row) * sld + c0 + seg);
+    *reinterpret_cast<u32x4*>(&t[row][seg]) = v;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      t[row][seg + i] = (r0 + row < R && c0 + seg + i < C) ? src[(int64_t)(r0 + row) * sld + c0 + seg + i] : 0;
+  }
+  __syncthreads();
+  uint8_t v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = t[seg + i][row];
+  if (full && ((dld | (int64_t)(uintptr_t)dst) & 15) == 0) {
+    u32x4 w;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      w[d] = (uint32_t)v[4 * d] | ((uint32_t)v[4 * d + 1] << 8) | ((uint32_t)v[4 * d + 2] << 16) |
+             ((uint32_t)v[4 * d + 3] << 24);
+    *reinterpret_cast<u32x4*>(dst + (int64_t)(c0 + row) * dld + r0 + seg) = w;
+  } else if (c0 + row < C) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (r0 + seg + i < R) dst[(int64_t)(c0 + row) * dld + r0 + seg + i] = v[i];
+  }
 }
 
 // 128 x 128 tiles, four waves of 64 x 64 (a 256 x 256 tile does not fit the
@@ -427,4 +557,55 @@ extern "C" int intent_mxfp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t
   }
   return launch_mx<TMx128>(a, M, K, a_ld, a_scales, a_scales_ld, b, N, b_ld, b_scales, b_scales_ld, out, out_ld,
                            stream);
+}
+
+extern "C" int intent_fp8_transpose(const uint8_t* src, int64_t rows, int64_t cols, int64_t src_ld, uint8_t* dst,
+                                    int64_t dst_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(rows >= 0 && cols >= 0 && rows <= INT32_MAX && cols <= INT32_MAX, INTENT_ERR_INVALID_ARGUMENT,
+                 "bad extents");
+  if (rows == 0 || cols == 0) return INTENT_OK;
+  INTENT_REQUIRE(src && dst, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(src_ld >= cols && dst_ld >= rows, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
+  INTENT_REQUIRE(gx < (1ll << 31) && gy < 65536, INTENT_ERR_UNSUPPORTED, "fp8_transpose: grid too large");
+  hipLaunchKernelGGL(byte_transpose_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, (hipStream_t)stream, src,
+                     (int)rows, (int)cols, src_ld, dst, dst_ld);
+  return intent::launch_status("fp8_transpose");
+}
+
+extern "C" int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* bt,
+                                      int64_t N, int64_t bt_ld, float a_scale, float b_scale, int64_t splits,
+                                      int accumulate, void* out, int64_t out_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(splits >= 1 && splits <= 64, INTENT_ERR_INVALID_ARGUMENT, "splits must be in [1, 64], got %lld",
+                 (long long)splits);
+  INTENT_REQUIRE(splits == 1 || accumulate, INTENT_ERR_INVALID_ARGUMENT, "split-K accumulates into the output");
+  if (splits > 1)
+    INTENT_REQUIRE(K % (256 * splits) == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 256 * splits, got %lld",
+                   (long long)K);
+  else
+    INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 128, got %lld", (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "empty K");
+  INTENT_REQUIRE(a && bt && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(a_ld >= K && bt_ld >= K && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(bt) && a_ld % 16 == 0 && bt_ld % 16 == 0,
+                 INTENT_ERR_ALIGNMENT, "operand rows must be 16-byte aligned");
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, bt_ld), INTENT_ERR_UNSUPPORTED,
+                 "scaled_fp8_gemm: operand too large for 31-bit buffer offsets");
+  const int mblocks = (int)((M + 255) / 256);
+  const int64_t grid = (int64_t)mblocks * ((N + 255) / 256);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "scaled_fp8_gemm: grid too large");
+  if (accumulate)
+    hipLaunchKernelGGL(fp8_scaled_gemm_kernel<true>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a, a_ld,
+                       (int)M, bt, bt_ld, (int)N, (int)K, (int)splits, a_scale, b_scale, (f16*)out, out_ld, mblocks);
+  else
+    hipLaunchKernelGGL(fp8_scaled_gemm_kernel<false>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a,
+                       a_ld, (int)M, bt, bt_ld, (int)N, (int)K, (int)splits, a_scale, b_scale, (f16*)out, out_ld,
+                       mblocks);
+  return intent::launch_status("scaled_fp8_gemm");
 }

@@ -608,9 +608,82 @@ block_scaled_matmul = KernelDefinition(
 )
 
 
+# ---- per-tensor scaled FP8 GEMM and its split-K form ---------------------------
+
+def _fp8_rhs_rows(rhs_kn, K: int, N: int, workspace, stream: int):
+    """The [K, N] right operand transposed into the workspace as [N, K] rows."""
+    _native.call("intent_fp8_transpose", _ptr(rhs_kn), K, N, rhs_kn.stride(0), workspace.data_ptr(), K, stream)
+    return workspace.data_ptr()
+
+
+def _sfp8_workspace(env: dict) -> int:
+    return env["K"] * env["N"]
+
+
+def _sfp8_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    lhs, rhs, out = v["lhs"], v["rhs"], v["output"]
+    M, K, N = env["M"], env["K"], env["N"]
+    bt = _fp8_rhs_rows(rhs, K, N, workspace, stream)
+    _native.call("intent_scaled_fp8_gemm", _ptr(lhs), M, K, _ld(lhs), bt, N, K, float(env["lhs_scale"]),
+                 float(env["rhs_scale"]), 1, 0, _ptr(out), _ld(out), stream)
+    return "intent_scaled_fp8_gemm"
+
+
+def _sfp8_check(env: dict) -> None:
+    if env["K"] % 128:
+        raise NotImplementedError(f"K ({env['K']}) must be a multiple of 128")
+
+
+scaled_fp8_matmul = KernelDefinition(
+    name="scaled_fp8_matmul",
+    params=(
+        Param("lhs", "f8e4m3fn", ("M", "K"), leading_stride=True),
+        Param("rhs", "f8e4m3fn", ("K", "N"), leading_stride=True),
+        Param("output", "f16", ("M", "N"), OUT, leading_stride=True),
+        Scalar("lhs_scale", "f32"),
+        Scalar("rhs_scale", "f32"),
+    ),
+    launch=_sfp8_launch,
+    check=_sfp8_check,
+    workspace=_sfp8_workspace,
+    reference="examples/kernels/contraction/block_scaled.py:42-63",
+    doc="output = f16((lhs @ rhs (f32) * lhs_scale) * rhs_scale), E4M3FN operands",
+)
+
+
+def _sfp8_splitk_workspace(env: dict) -> int:
+    return env["IT"] * env["SP"] * 256 * env["N"]
+
+
+def _sfp8_splitk_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    lhs, rhs, out = v["lhs"], v["rhs"], v["output"]
+    M, N, SP = env["M"], env["N"], env["SP"]
+    K = env["IT"] * SP * 256
+    bt = _fp8_rhs_rows(rhs.view(K, N), K, N, workspace, stream)
+    _native.call("intent_scaled_fp8_gemm", _ptr(lhs), M, K, K, bt, N, K, float(env["lhs_scale"]),
+                 float(env["rhs_scale"]), SP, 1, _ptr(out), _ld(out), stream)
+    return "intent_scaled_fp8_gemm"
+
+
+scaled_fp8_splitk_matmul = KernelDefinition(
+    name="scaled_fp8_splitk_matmul",
+    params=(
+        Param("lhs", "f8e4m3fn", ("M", "IT", "SP", 256)),
+        Param("rhs", "f8e4m3fn", ("IT", "SP", 256, "N")),
+        Param("output", "f16", ("M", "N"), INOUT, leading_stride=True),
+        Scalar("lhs_scale", "f32"),
+        Scalar("rhs_scale", "f32"),
+    ),
+    launch=_sfp8_splitk_launch,
+    workspace=_sfp8_splitk_workspace,
+    reference="examples/kernels/contraction/block_scaled.py:66-98",
+    doc="for each split s in order: output = f16(output + f16((partial_s * lhs_scale) * rhs_scale))",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
-    w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul,
+    w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
 )

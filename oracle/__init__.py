@@ -78,6 +78,10 @@ def lib():
         _lib.orc_e8m0_to_f32.restype = ctypes.c_float
         _lib.orc_mxfp8_gemm.argtypes = [p, p, i64, i64, p, p, i64, p, ci]
         _lib.orc_mxfp8_gemm.restype = None
+        _lib.orc_scaled_fp8_gemm.argtypes = [p, i64, i64, p, i64, ctypes.c_float, ctypes.c_float, i64, ci, p, ci]
+        _lib.orc_scaled_fp8_gemm.restype = None
+        _lib.orc_deepgemm_fp8.argtypes = [p, p, i64, i64, p, p, i64, p, ci]
+        _lib.orc_deepgemm_fp8.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -261,6 +265,32 @@ def mxfp8_gemm(a, sa, b, sb, threads: int = 1) -> np.ndarray:
     N = b.shape[0]
     out = np.empty((M, N), np.float32)
     lib().orc_mxfp8_gemm(_ptr(a), _ptr(sa), M, K, _ptr(b), _ptr(sb), N, _ptr(out), threads)
+    return out
+
+
+def scaled_fp8_gemm(a, b, lhs_scale, rhs_scale, splits=1, out=None, threads: int = 1) -> np.ndarray:
+    """E4M3FN bytes a [M, K] and b [K, N] (N contiguous) -> f16 [M, N]:
+    f16((acc * lhs_scale) * rhs_scale) per split, added in split order into
+    out when out is given (split-K form), else the plain form."""
+    a, b = _c(a, np.uint8), _c(b, np.uint8)
+    M, K = a.shape
+    N = b.shape[1]
+    accumulate = out is not None
+    res = _c(out, np.float16).copy() if accumulate else np.zeros((M, N), np.float16)
+    lib().orc_scaled_fp8_gemm(_ptr(a), M, K, _ptr(b), N, float(lhs_scale), float(rhs_scale), int(splits),
+                              int(accumulate), _ptr(res), threads)
+    return res
+
+
+def deepgemm_fp8(a, sa, b, sb, threads: int = 1) -> np.ndarray:
+    """E4M3FN bytes a [M, KB*128], b [N, KB*128]; f32 scales sa [M, KB], sb [N/128, KB]
+    -> bf16 bits (uint16) [M, N]."""
+    a, b = _c(a, np.uint8), _c(b, np.uint8)
+    sa, sb = _c(sa, np.float32), _c(sb, np.float32)
+    M, K = a.shape
+    N = b.shape[0]
+    out = np.empty((M, N), np.uint16)
+    lib().orc_deepgemm_fp8(_ptr(a), _ptr(sa), M, K // 128, _ptr(b), _ptr(sb), N, _ptr(out), threads)
     return out
 
 

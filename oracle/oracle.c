@@ -534,3 +534,64 @@ void orc_mxfp8_gemm(const uint8_t* a, const uint8_t* sa, int64_t M, int64_t K, c
     }
   }
 }
+
+/* ---- per-tensor scaled FP8 GEMM and its split-K form ---------------------------
+ * scaled_fp8_matmul (examples/kernels/contraction/block_scaled.py:42-63):
+ *   out = f16((acc * lhs_scale) * rhs_scale), acc the f32 contraction (fma in
+ *   k order, Contractions.cpp:12-41) of E4M3FN values widened exactly to f32.
+ * scaled_fp8_splitk_matmul (block_scaled.py:66-98; CPU baseline
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:133-139): lhs [M, IT, SP, 256]
+ * and rhs [IT, SP, 256, N] share k = (it*SP + s)*256 + r; for s = 0 .. SP-1 in
+ * order, p = f16((acc_s * lhs_scale) * rhs_scale) and out = f16(out + p).
+ * Here a is [M, K] (K contiguous) and b is [K, N] (N contiguous), as the
+ * reference passes them; splits == 1 without accumulate is the plain form. */
+void orc_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* b, int64_t N, float ls, float rs,
+                         int64_t splits, int accumulate, uint16_t* out, int threads) {
+  const int64_t chunks = K / 256;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float o = accumulate ? orc_f16_to_f32(out[m * N + n]) : 0.0f;
+      for (int64_t s = 0; s < splits; ++s) {
+        float acc = 0.0f;
+        if (splits == 1) {
+          for (int64_t k = 0; k < K; ++k)
+            acc = fmaf(orc_e4m3fn_to_f32(a[m * K + k]), orc_e4m3fn_to_f32(b[k * N + n]), acc);
+        } else {
+          for (int64_t c = s; c < chunks; c += splits)
+            for (int64_t r = 0; r < 256; ++r) {
+              const int64_t k = c * 256 + r;
+              acc = fmaf(orc_e4m3fn_to_f32(a[m * K + k]), orc_e4m3fn_to_f32(b[k * N + n]), acc);
+            }
+        }
+        const float scaled = (acc * ls) * rs;
+        const float p = orc_f16_to_f32(orc_f32_to_f16(scaled));
+        o = accumulate ? orc_f16_to_f32(orc_f32_to_f16(o + p)) : p;
+      }
+      out[m * N + n] = orc_f32_to_f16(o);
+    }
+  }
+}
+
+/* ---- DeepGEMM-style FP8 GEMM with f32 block scales -----------------------------
+ * deepgemm_fp8_2xacc (block_scaled.py:101-122; CPU baseline cpu_runtime.py:127-131):
+ * lhs [M, KB, 128] and rhs [N, KB, 128] E4M3FN, lhs_scale f32 [M, KB], rhs_scale
+ * f32 [N/128, KB] (one scale per 128 x 128 block of rhs):
+ *   left = f32(lhs) * lhs_scale[m, kb], right = f32(rhs) * rhs_scale[n/128, kb]
+ *   out = bf16(sum_k left * right), fma in k order. */
+void orc_deepgemm_fp8(const uint8_t* a, const float* sa, int64_t M, int64_t KB, const uint8_t* b, const float* sb,
+                      int64_t N, uint16_t* out, int threads) {
+  const int64_t K = KB * 128;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) {
+        const float x = orc_e4m3fn_to_f32(a[m * K + k]) * sa[m * KB + k / 128];
+        const float y = orc_e4m3fn_to_f32(b[n * K + k]) * sb[(n / 128) * KB + k / 128];
+        acc = fmaf(x, y, acc);
+      }
+      out[m * N + n] = orc_f32_to_bf16(acc);
+    }
+  }
+}

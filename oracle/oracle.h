@@ -39,5 +39,9 @@ float orc_e4m3fn_to_f32(uint8_t v);
 float orc_e8m0_to_f32(uint8_t e);
 void orc_mxfp8_gemm(const uint8_t* a, const uint8_t* sa, int64_t M, int64_t K, const uint8_t* b, const uint8_t* sb,
                     int64_t N, float* out, int threads);
+void orc_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* b, int64_t N, float ls, float rs,
+                         int64_t splits, int accumulate, uint16_t* out, int threads);
+void orc_deepgemm_fp8(const uint8_t* a, const float* sa, int64_t M, int64_t KB, const uint8_t* b, const float* sb,
+                      int64_t N, uint16_t* out, int threads);
 
 #endif

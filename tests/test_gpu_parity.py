@@ -471,3 +471,61 @@ def test_block_scaled_matmul(gpu, threads, M, K, N, layout):
     # The scaled MFMA sums 64 products per instruction in its own order and
     # precision (measured ~1e-4 of the largest term); the gate is the float one.
     assert_close_rms(host(out), ref, what=f"mxfp8 {M}x{K}x{N}")
+
+
+# ---- per-tensor scaled FP8 GEMM, plain and split-K ----------------------------------
+
+def _fp8_bits(seed, shape):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def _f16_close(got, ref, what):
+    # f32 sums in another order may round to a neighbouring f16 (before and after
+    # the scaling): allow a few f16 ulps of the output's magnitude.
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    assert np.all(np.isfinite(got)), what
+    assert np.max(np.abs(got - ref)) <= 4e-3 * np.abs(ref).max(), what
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (130, 384, 70), (1, 256, 1), (4000, 512, 4200), (512, 4096, 1000)])
+def test_scaled_fp8_matmul(gpu, threads, M, K, N):
+    a, b = _fp8_bits(M + N, (M, K)), _fp8_bits(K + N, (K, N))
+    lhs = dev(a).view(torch.float8_e4m3fn)
+    rhs = dev(b).view(torch.float8_e4m3fn)
+    out = art(intent.scaled_fp8_matmul).run(lhs, rhs, 0.5, 1.5)
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = oracle.scaled_fp8_gemm(a[rows], b, 0.5, 1.5, threads=threads)
+    _f16_close(host(out)[rows], ref, f"scaled_fp8 {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,IT,SP,N", [(64, 1, 4, 64), (300, 2, 3, 130), (4096, 1, 2, 4352)])
+def test_scaled_fp8_splitk(gpu, threads, M, IT, SP, N):
+    K = IT * SP * 256
+    a, b = _fp8_bits(M, (M, K)), _fp8_bits(N, (K, N))
+    out0 = (torch.randn(M, N, generator=torch.Generator().manual_seed(3)) * 8).half()
+    lhs = dev(a).view(torch.float8_e4m3fn).view(M, IT, SP, 256)
+    rhs = dev(b).view(torch.float8_e4m3fn).view(IT, SP, 256, N)
+    out = out0.cuda()
+    art(intent.scaled_fp8_splitk_matmul).run(lhs, rhs, out, 0.25, 2.0)
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = oracle.scaled_fp8_gemm(a[rows], b, 0.25, 2.0, splits=SP, out=out0.numpy()[rows], threads=threads)
+    _f16_close(host(out)[rows], ref, f"splitk {M}x{K}x{N}/{SP}")
+
+
+def test_scaled_fp8_splitk_reference_size(gpu):
+    # The reference's split-K case (experiments/gpu/providers/triton/contraction.py:174-186:
+    # 4096 x 4096 x 14336, IT 4, SP 4, scales 1), checked against its CPU formula
+    # (cpu_runtime.py:133-139) evaluated with torch on the GPU in f32.
+    M, N, IT, SP = 4096, 14336, 4, 4
+    g = torch.Generator(device="cuda").manual_seed(7)
+    lhs = torch.randn((M, IT * SP * 256), device="cuda", generator=g).to(torch.float8_e4m3fn)
+    rhs = torch.randn((IT * SP * 256, N), device="cuda", generator=g).to(torch.float8_e4m3fn)
+    out = torch.zeros((M, N), device="cuda", dtype=torch.float16)
+    art(intent.scaled_fp8_splitk_matmul).run(lhs.view(M, IT, SP, 256), rhs.view(IT, SP, 256, N), out, 1.0, 1.0)
+    ref = torch.zeros_like(out)
+    l4, r4 = lhs.view(M, IT, SP, 256), rhs.view(IT, SP, 256, N)
+    for s in range(SP):
+        ref.add_((l4[:, :, s, :].float().flatten(1) @ r4[:, s, :, :].float().flatten(0, 1)).half())
+    err = (out.double() - ref.double()).abs().max().item()
+    assert torch.isfinite(out).all() and err <= 4e-3 * ref.double().abs().max().item()

@@ -492,3 +492,88 @@ def test_mxfp8_gemm_matches_reference_formula():
     fb = torch.from_numpy(b).view(torch.float8_e4m3fn).double() * torch.exp2(torch.from_numpy(sb).double() - 127).repeat_interleave(32, 1)
     ref = (fa @ fb.T).numpy()
     assert np.allclose(got, ref, rtol=1e-5, atol=1e-6 * np.abs(ref).max())
+
+
+# ---- per-tensor scaled FP8 (plain and split-K) and DeepGEMM-style FP8 -------------
+
+def _fp8_randn(gen, shape, scale=1.0):
+    return (torch.randn(shape, generator=gen) * scale).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def _f8(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits)).view(torch.float8_e4m3fn).double().numpy()
+
+
+def test_scaled_fp8_gemm_closed_form():
+    # block_scaled.py:42-63: f16((acc * lhs_scale) * rhs_scale); the f32 sum in k
+    # order differs from the exact float64 sum only by rounding.
+    g = torch.Generator().manual_seed(11)
+    a, b = _fp8_randn(g, (6, 768)), _fp8_randn(g, (768, 9))
+    got = oracle.scaled_fp8_gemm(a, b, 0.75, 1.5).astype(np.float64)
+    ref = (_f8(a) @ _f8(b)) * 0.75 * 1.5
+    assert np.max(np.abs(got - ref)) <= 2e-3 * np.abs(ref).max()
+
+
+def test_scaled_fp8_splitk_matches_reference_formula():
+    # experiments/cpu/baselines/pytorch/cpu_runtime.py:133-139 restated with torch:
+    # per split an f32 matmul, scaled, rounded to f16, added to the f16 output.
+    g = torch.Generator().manual_seed(12)
+    M, IT, SP, N = 5, 2, 3, 7
+    K = IT * SP * 256
+    a, b = _fp8_randn(g, (M, K)), _fp8_randn(g, (K, N))
+    out0 = (torch.randn(M, N, generator=g) * 4).half().numpy()
+    got = oracle.scaled_fp8_gemm(a, b, 0.5, 1.25, splits=SP, out=out0)
+    lhs = torch.from_numpy(a).view(torch.float8_e4m3fn).view(M, IT, SP, 256)
+    rhs = torch.from_numpy(b).view(torch.float8_e4m3fn).view(IT, SP, 256, N)
+    ref = torch.from_numpy(out0.copy())
+    for s in range(SP):
+        left = lhs[:, :, s, :].float().flatten(1)
+        right = rhs[:, s, :, :].float().flatten(0, 1)
+        ref.add_(((left @ right) * 0.5 * 1.25).half())
+    ref = ref.numpy().astype(np.float64)
+    # f32 sums in a different order may round to a neighbouring f16
+    assert np.max(np.abs(got.astype(np.float64) - ref)) <= 2e-3 * np.abs(ref).max()
+
+
+def test_scaled_fp8_splitk_known_answers():
+    M, N, SP, IT = 2, 3, 4, 1
+    K = SP * IT * 256
+    one = np.uint8(0x38)  # E4M3FN 1.0
+    a = np.zeros((M, K), np.uint8)
+    b = np.zeros((K, N), np.uint8)
+    # one-hot k in split 2 (k = 2*256 + 5): out = f16(b[k, n] * ls * rs)
+    a[:, 2 * 256 + 5] = one
+    b[2 * 256 + 5, :] = [0x40, 0xC8, 0x30]  # 2.0, -4.0, 0.5
+    got = oracle.scaled_fp8_gemm(a, b, 3.0, 0.5, splits=SP, out=np.zeros((M, N), np.float16))
+    assert np.array_equal(got, np.tile(np.array([3.0, -6.0, 0.75], np.float16), (M, 1)))
+    # additions happen split by split in f16: 2048 + 1 + 1 stays 2048 (ties to
+    # even), while a single sum of the partials would give 2050
+    a = np.zeros((1, K), np.uint8)
+    b = np.zeros((K, 1), np.uint8)
+    a[0, 0 * 256] = a[0, 1 * 256] = one
+    b[0 * 256, 0] = b[1 * 256, 0] = one
+    got = oracle.scaled_fp8_gemm(a, b, 1.0, 1.0, splits=SP, out=np.full((1, 1), 2048, np.float16))
+    assert got[0, 0] == np.float16(2048)
+
+
+def test_deepgemm_fp8_matches_reference_formula():
+    # cpu_runtime.py:127-131 restated in float64: operands scaled per (row, 128-k
+    # block) and per (128-row block of rhs, 128-k block), then a matmul, then bf16.
+    g = torch.Generator().manual_seed(13)
+    M, KB, N = 4, 3, 256
+    a, b = _fp8_randn(g, (M, KB * 128)), _fp8_randn(g, (N, KB * 128))
+    sa = torch.rand(M, KB, generator=g).numpy().astype(np.float32) + 0.25
+    sb = torch.rand(N // 128, KB, generator=g).numpy().astype(np.float32) + 0.25
+    got = torch.from_numpy(oracle.deepgemm_fp8(a, sa, b, sb).view(np.int16)).view(torch.bfloat16).double().numpy()
+    left = _f8(a) * np.repeat(sa.astype(np.float64), 128, axis=1)
+    right = _f8(b) * np.repeat(np.repeat(sb.astype(np.float64), 128, axis=0), 128, axis=1)
+    ref = left @ right.T
+    assert np.max(np.abs(got - ref)) <= 8e-3 * np.abs(ref).max()
+    # one-hot known answer: a single product lhs*sa * rhs*sb, exact in bf16
+    a1 = np.zeros((1, 128), np.uint8)
+    b1 = np.zeros((128, 128), np.uint8)
+    a1[0, 7] = 0x40  # 2.0
+    b1[5, 7] = 0x44  # 3.0
+    y = oracle.deepgemm_fp8(a1, np.array([[0.5]], np.float32), b1, np.array([[4.0]], np.float32))
+    vals = torch.from_numpy(y.view(np.int16)).view(torch.bfloat16).float().numpy()
+    assert vals[0, 5] == 12.0 and np.count_nonzero(vals) == 1
