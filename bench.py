@@ -191,6 +191,60 @@ def bench_w4a8(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": n}
 
 
+def bench_sfp8_splitk(steps: int, warmup: int) -> dict:
+    """The reference's split-K FP8 case (experiments/gpu/providers/triton/contraction.py:174-186):
+    M=4096, N=14336, K=4096 as [IT=4, SP=4, 256], E4M3FN, scales 1, f16 InOut output. The
+    timed operator includes the transpose of the [K, N] right operand."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    M, N, IT, SP = 4096, 14336, 4, 4
+    K = IT * SP * 256
+    g = torch.Generator(device="cuda").manual_seed(0)
+    lhs = torch.randn((M, K), device="cuda", generator=g).to(torch.float8_e4m3fn)
+    rhs = torch.randn((K, N), device="cuda", generator=g).to(torch.float8_e4m3fn)
+    work = inputs.Workload(f"scaled fp8 split-K M{M} K{K} N{N} SP{SP}", 2 * M * N * K,
+                           M * K + K * N + 2 * M * N * 2)
+    art = intent.compile(intent.scaled_fp8_splitk_matmul, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes, minimum=2)
+    sets = [(lhs.clone().view(M, IT, SP, 256), rhs.clone().view(IT, SP, 256, N),
+             torch.zeros((M, N), device="cuda", dtype=torch.float16)) for _ in range(n)]
+    calls = [art.prepare(l4, r4, o, 1.0, 1.0) for l4, r4, o in sets]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls, sets
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
+def bench_deepgemm(steps: int, warmup: int) -> dict:
+    """The reference's deepgemm_fp8_2xacc case (experiments/cpu/providers/mojo/contraction.py:227-236):
+    M = N = K = 4096, E4M3FN with f32 scales per (row, 128-k) and per 128 x 128 rhs block, bf16 out."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    M = N = K = 4096
+    KB = K // 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    lhs = torch.randn((M, K), device="cuda", generator=g).to(torch.float8_e4m3fn).view(M, KB, 128)
+    rhs = torch.randn((N, K), device="cuda", generator=g).to(torch.float8_e4m3fn).view(N, KB, 128)
+    ls = torch.rand((M, KB), device="cuda", generator=g) + 0.5
+    rs = torch.rand((N // 128, KB), device="cuda", generator=g) + 0.5
+    work = inputs.Workload(f"deepgemm fp8 M{M} K{K} N{N}", 2 * M * N * K,
+                           M * K + N * K + (M + N // 128) * KB * 4 + M * N * 2)
+    art = intent.compile(intent.deepgemm_fp8_2xacc, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes, minimum=2)
+    sets = [(lhs.clone(), rhs.clone(), ls.clone(), rs.clone()) for _ in range(n)]
+    calls = [art.prepare(*s) for s in sets]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls, sets
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
 def bench_mxfp8(steps: int, warmup: int) -> dict:
     """The reference's mxfp8_gemm case (experiments/cpu/providers/mojo/contraction.py:285-305):
     M=4096, K=4096, N=14336, E4M3FN with E8M0 scales per 32, rhs given as the [KB, 32, N]
@@ -344,6 +398,12 @@ def main() -> int:
         log("[bench] mxfp8 M=4096 K=4096 N=14336")
         r = bench_mxfp8(steps, warm)
         extra["mxfp8_m4096_n14336"] = _flop_entry(r, 5033.2, "TFLOP/s")
+        log("[bench] scaled fp8 split-K M=4096 K=4096 N=14336")
+        r = bench_sfp8_splitk(steps, warm)
+        extra["scaled_fp8_splitk_m4096_n14336"] = _flop_entry(r, 5033.2, "TFLOP/s")
+        log("[bench] deepgemm fp8 M=N=K=4096")
+        r = bench_deepgemm(steps, warm)
+        extra["deepgemm_fp8_4096"] = _flop_entry(r, 5033.2, "TFLOP/s")
         log("[bench] q4_k projection N=K=4096")
         r = bench_q4k(args.steps, args.warmup)
         extra["q4k_projection_n4096"] = _hbm_entry(r)

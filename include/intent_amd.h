@@ -349,6 +349,23 @@ int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
                            float a_scale, float b_scale, int64_t splits, int accumulate,
                            void* out, int64_t out_ld, void* stream);
 
+/* DeepGEMM-style FP8 GEMM with f32 block scales. Replaces deepgemm_fp8_2xacc
+ * (examples/kernels/contraction/block_scaled.py:101-122; CPU baseline
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:127-131).
+ * a: [M, K] E4M3FN (K = KB * 128 contiguous, a_ld bytes); a_scales: f32 [M, KB]
+ * (a_scales_ld elements); b: [N, K] E4M3FN rows (b_ld bytes); b_scales: f32
+ * [ceil(N / 128), KB], one per 128-row block of b and 128-k block;
+ * out: bf16 bits [M, N] (out_ld elements):
+ *   out[m, n] = bf16(sum_kb (sum_k a*b) * a_scales[m, kb] * b_scales[n/128, kb])
+ * The reference scales the operands before the product; the sums agree to
+ * rounding.
+ */
+int intent_deepgemm_fp8(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                        const float* a_scales, int64_t a_scales_ld,
+                        const uint8_t* b, int64_t N, int64_t b_ld,
+                        const float* b_scales, int64_t b_scales_ld,
+                        void* out, int64_t out_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -231,18 +231,23 @@ struct SplitK {
 
 template <int ROWS, int NW, bool kScales>
 struct Rows {
-  static constexpr int N_INST = ROWS / 8 / NW;                    // data instructions per wave
-  static constexpr int S_INST = kScales ? ROWS / 64 / NW : 0;     // scale instructions per wave
-  static_assert(N_INST * 8 * NW == ROWS && (!kScales || S_INST * 64 * NW == ROWS), "tile rows must split evenly");
+  static constexpr int N_INST = ROWS / 8 / NW;  // data instructions per wave
+  static_assert(N_INST * 8 * NW == ROWS && ROWS % 64 == 0, "tile rows must split evenly");
+  // Scale dwords: 64 rows per instruction; a wave with none left repeats the
+  // last one (same data, same place), so that every wave issues S_INST.
+  static constexpr int S_TOTAL = ROWS / 64;
+  static constexpr int S_INST = kScales ? (S_TOTAL + NW - 1) / NW : 0;
   static constexpr int NVM = N_INST + S_INST;
   mp::Rsrc rd, rs;
   uint32_t voff[N_INST], soff[S_INST > 0 ? S_INST : 1];
+  int srow0[S_INST > 0 ? S_INST : 1];
   int wave;
+  // Row r's scale dwords start at scales + (r / sdiv) * ld_scale bytes.
   INTENT_DEVICE void init(const uint8_t* rows, int64_t ld, int M, const uint8_t* scales, int64_t ld_scale, int m0,
-                          int w) {
+                          int w, int sdiv = 1) {
     wave = w;
     rd = make_rsrc(rows + (int64_t)m0 * ld);
-    rs = make_rsrc(kScales ? scales + (int64_t)m0 * ld_scale : rows);
+    rs = make_rsrc(kScales ? scales : rows);
     const int lane = threadIdx.x & 63;
 #pragma unroll
     for (int j = 0; j < N_INST; ++j) {
@@ -252,9 +257,11 @@ struct Rows {
     }
 #pragma unroll
     for (int j = 0; j < S_INST; ++j) {
-      const int r = (j * NW + w) * 64 + lane;
-      const int rr = m0 + r < M ? r : M - 1 - m0;
-      soff[j] = (uint32_t)(rr * ld_scale);
+      const int t = j * NW + w < S_TOTAL ? j * NW + w : S_TOTAL - 1;
+      srow0[j] = t * 64;
+      const int r = t * 64 + lane;
+      const int m = m0 + r < M ? m0 + r : M - 1;
+      soff[j] = (uint32_t)((m / sdiv) * ld_scale);
     }
   }
   // rows: this operand's row region of a stage; scl: its scale region;
@@ -266,22 +273,36 @@ struct Rows {
                                                koff, 0, 0);
 #pragma unroll
     for (int j = 0; j < S_INST; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (mp::lds_t*)(scl + (j * NW + wave) * 64 * 4), 4, soff[j],
-                                               (uint32_t)kt * 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (mp::lds_t*)(scl + srow0[j] * 4), 4, soff[j], (uint32_t)kt * 4, 0,
+                                               0);
   }
 };
 
+// How a stage's per-row scale dwords are used.
+enum class ScaleMode {
+  kNone,     // no scales: every block scale is E8M0 127 (2^0)
+  kE8M0,     // four E8M0 block scales (32 k each) feed the scaled MFMA
+  kPromote,  // one f32 scale per row and 128-k stage: each stage is summed into
+             // a fresh accumulator, then hook(acc, row scales of A, of B, kt)
+             // folds it into the caller's own accumulators
+  kHook,     // no scales; hook(acc, -, -, kt) runs after every stage (and may
+             // consume and clear acc)
+};
+
 // acc += A·B over nk stages (stage kt at byte offset koff(kt) of every row).
-// Without kScales every block scale is E8M0 127 (2^0): a plain FP8 product.
-// Starts with a barrier, so that it can run again on the same LDS, and ends
-// with no DMA in flight.
-template <bool kScales, class KOff>
-INTENT_DEVICE void dma_mainloop(char* smem, const Rows<Tile::BM, Tile::NW, kScales>& aop,
-                                const Rows<Tile::BN, Tile::NW, kScales>& bop, int nk, KOff koff,
-                                i32x16 (&acc)[Tile::TI][Tile::TJ]) {
-  using T = Tile;
-  constexpr int SB = kStage;
-  constexpr int A_SC = kRowBytes;
+// T: a 4-wave tile whose rows are multiples of 64. Starts with a barrier, so
+// that it can run again on the same LDS, and ends with no DMA in flight.
+template <class T, ScaleMode kMode, class KOff, class Hook>
+INTENT_DEVICE void dma_mainloop(char* smem,
+                                const Rows<T::BM, T::NW, kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote>& aop,
+                                const Rows<T::BN, T::NW, kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote>& bop,
+                                int nk, KOff koff,
+                                i32x16 (&acc)[T::TI][T::TJ], Hook&& hook) {
+  constexpr bool kScales = kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote;
+  constexpr bool kHooked = kMode == ScaleMode::kPromote || kMode == ScaleMode::kHook;
+  constexpr int ROWBYTES = (T::BM + T::BN) * mp::ROWB;
+  constexpr int SB = ROWBYTES + (T::BM + T::BN) * 4;
+  constexpr int A_SC = ROWBYTES;
   constexpr int B_SC = A_SC + T::BM * 4;
   constexpr int NV = Rows<T::BM, T::NW, kScales>::NVM + Rows<T::BN, T::NW, kScales>::NVM;
   static_assert(2 * NV < 64, "vmcnt range");
@@ -322,8 +343,10 @@ INTENT_DEVICE void dma_mainloop(char* smem, const Rows<Tile::BM, Tile::NW, kScal
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j) {
         f32x16 c = bit_cast<f32x16>(acc[i][j]);
-        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[s][j], af[s][i], c, 0, 0, 0, (int)((csb[j] >> sh) & 255u),
-                                                             0, (int)((csa[i] >> sh) & 255u));
+        if (kMode == ScaleMode::kPromote && s == 0) c = f32x16{};  // a fresh sum per stage
+        const int sb_ = kMode == ScaleMode::kE8M0 ? (int)((csb[j] >> sh) & 255u) : 127;
+        const int sa_ = kMode == ScaleMode::kE8M0 ? (int)((csa[i] >> sh) & 255u) : 127;
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[s][j], af[s][i], c, 0, 0, 0, sb_, 0, sa_);
         acc[i][j] = bit_cast<i32x16>(c);
       }
   };
@@ -337,6 +360,7 @@ INTENT_DEVICE void dma_mainloop(char* smem, const Rows<Tile::BM, Tile::NW, kScal
       if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
     });
   };
+  constexpr int NR = 2 * (T::TI + T::TJ);  // ds_read_b128 per step
 
   __syncthreads();  // a previous pass over this LDS is fully read
   issue(0, 0);
@@ -351,7 +375,7 @@ INTENT_DEVICE void dma_mainloop(char* smem, const Rows<Tile::BM, Tile::NW, kScal
     const char* base = smem + slot * SB;
     read(base, 1, 1);
     mfmas(0);
-    interleave(std::integral_constant<int, 2 * (T::TI + T::TJ)>{});
+    interleave(std::integral_constant<int, NR>{});
     if constexpr (decltype(more)::value) {
       mp::wait_vm_lgkm_barrier<0>();  // stage kt+1 landed everywhere; stage kt fully read
       issue(slot, kt + 2);
@@ -359,13 +383,15 @@ INTENT_DEVICE void dma_mainloop(char* smem, const Rows<Tile::BM, Tile::NW, kScal
       read_scales(nb, nsa, nsb);
       read(nb, 0, 0);
       mfmas(1);
-      interleave(std::integral_constant<int, 2 * (T::TI + T::TJ) + (kScales ? 4 : 0)>{});
+      interleave(std::integral_constant<int, NR + (kScales ? 4 : 0)>{});
+      if constexpr (kHooked) hook(acc, csa, csb, kt);
 #pragma unroll
       for (int i = 0; i < T::TI; ++i) csa[i] = nsa[i];
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j) csb[j] = nsb[j];
     } else {
       mfmas(1);
+      if constexpr (kHooked) hook(acc, csa, csb, kt);
     }
   };
   for (int kt = 0; kt < nk - 1; ++kt) stage(kt, std::true_type{});
@@ -373,11 +399,17 @@ INTENT_DEVICE void dma_mainloop(char* smem, const Rows<Tile::BM, Tile::NW, kScal
   mp::wait_vm<0>();  // no DMA may still be writing LDS when the workgroup ends
 }
 
-INTENT_DEVICE void zero(i32x16 (&acc)[Tile::TI][Tile::TJ]) {
+struct NoHook {
+  template <class... A>
+  INTENT_DEVICE void operator()(A&&...) const {}
+};
+
+template <int TI, int TJ>
+INTENT_DEVICE void zero(i32x16 (&acc)[TI][TJ]) {
 #pragma unroll
-  for (int i = 0; i < Tile::TI; ++i)
+  for (int i = 0; i < TI; ++i)
 #pragma unroll
-    for (int j = 0; j < Tile::TJ; ++j)
+    for (int j = 0; j < TJ; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;  // the bits of +0.0f
 }
@@ -399,7 +431,8 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
   bop.init(b, ldb, N, sb, ld_sb, n0, T::wave());
   i32x16 acc[T::TI][T::TJ];
   mxdma::zero(acc);
-  mxdma::dma_mainloop<true>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, acc);
+  mxdma::dma_mainloop<T, mxdma::ScaleMode::kE8M0>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, acc,
+                                                  mxdma::NoHook{});
   store_mx<T>(acc, m0, n0, M, N, out, ldo);
 }
 
@@ -407,11 +440,148 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
 // with splits > 1, the split-K form :66-98): for each split s in order,
 //   p = f16((acc_s * lhs_scale) * rhs_scale)   (acc_s: the f32 sum over split s)
 // and out = p (kAccum false, one split) or out = f16(out + p) (kAccum).
-// A lane holds four adjacent n of one m per register group.
+// bt: the right operand as [N, K] rows (K contiguous). K % (256 * splits) == 0
+// when splits > 1, K % 128 == 0 otherwise. One pipelined pass over all
+// splits' stages (split s, stage t at mxdma::SplitK order); at the end of each
+// split the hook folds the split's f32 sum into the f16 output tile, which
+// stays in registers: read once (kAccum) and written once.
+using TSk = mp::Tile<256, 128, 2, 2>;  // four waves of 128 x 64
+
 template <bool kAccum>
-INTENT_DEVICE void store_f16_scaled(const i32x16 (&acc)[mxdma::Tile::TI][mxdma::Tile::TJ], int m0, int n0, int M,
-                                    int N, float ls, float rs, f16* __restrict__ out, int64_t ldo) {
-  using T = mxdma::Tile;
+__global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                                 const uint8_t* __restrict__ bt, int64_t ldb, int N,
+                                                                 int K, int splits, float ls, float rs,
+                                                                 f16* __restrict__ out, int64_t ldo, int mblocks) {
+  using T = TSk;
+  constexpr int SB = (T::BM + T::BN) * (mp::ROWB + 4);
+  __shared__ __attribute__((aligned(1024))) char smem[2 * SB];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  mxdma::Rows<T::BM, T::NW, false> aop;
+  mxdma::Rows<T::BN, T::NW, false> bop;
+  aop.init(a, lda, M, nullptr, 0, m0, T::wave());
+  bop.init(bt, ldb, N, nullptr, 0, n0, T::wave());
+  const int nks = K / mp::ROWB / splits;
+  // The lane's outputs: m = row(i), n = col(j, g) + q, as packed f16 pairs
+  // o[i][j][2g + q/2] (64 registers).
+  f16x2 o[T::TI][T::TJ][8];
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        const f16* src = out + (int64_t)m * ldo + n;
+        f16x2 lo = splat2((f16)0.f), hi = splat2((f16)0.f);
+        if (kAccum && m < M) {
+          if (vec && n + 3 < N) {
+            const u32x2 w = *reinterpret_cast<const u32x2*>(src);
+            lo = bit_cast<f16x2>(w[0]);
+            hi = bit_cast<f16x2>(w[1]);
+          } else {
+            if (n < N) lo[0] = src[0];
+            if (n + 1 < N) lo[1] = src[1];
+            if (n + 2 < N) hi[0] = src[2];
+            if (n + 3 < N) hi[1] = src[3];
+          }
+        }
+        o[i][j][2 * g] = lo;
+        o[i][j][2 * g + 1] = hi;
+      }
+  }
+  i32x16 acc[T::TI][T::TJ];
+  mxdma::zero(acc);
+  auto fold = [&](i32x16 (&f)[T::TI][T::TJ], const uint32_t (&)[T::TI], const uint32_t (&)[T::TJ], int kt) {
+    if ((kt + 1) % nks) return;  // wave-uniform: only at the end of a split
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) {
+        const f32x16 v = bit_cast<f32x16>(f[i][j]);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const f16 p = (f16)__fmul_rn(__fmul_rn(v[e], ls), rs);
+          o[i][j][e >> 1][e & 1] = kAccum ? (f16)__fadd_rn((float)o[i][j][e >> 1][e & 1], (float)p) : p;
+        }
+        f[i][j] = i32x16{};
+      }
+  };
+  const auto koff = [nks, splits](int kt) { return mxdma::SplitK{splits, kt / nks}(kt % nks); };
+  mxdma::dma_mainloop<T, mxdma::ScaleMode::kHook>(smem, aop, bop, nks * splits, koff, acc, fold);
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        f16* dst = out + (int64_t)m * ldo + n;
+        const f16x2 lo = o[i][j][2 * g], hi = o[i][j][2 * g + 1];
+        if (vec && n + 3 < N) {
+          *reinterpret_cast<u32x2*>(dst) = u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+        } else {
+          if (n < N) dst[0] = lo[0];
+          if (n + 1 < N) dst[1] = lo[1];
+          if (n + 2 < N) dst[2] = hi[0];
+          if (n + 3 < N) dst[3] = hi[1];
+        }
+      }
+  }
+}
+
+// DeepGEMM-style FP8 GEMM with f32 block scales (deepgemm_fp8_2xacc,
+// block_scaled.py:101-122): lhs [M, KB, 128] with one f32 scale per (row, kb),
+// rhs [N, KB, 128] with one per (128-row block, kb); out = bf16(sum_kb
+// (sum_k lhs*rhs) * lhs_scale * rhs_scale). The f32 scales cannot ride the
+// MFMA's E8M0 scale operand, so each 128-k stage is summed into a fresh
+// accumulator and folded into the main one with one fma per element
+// ("2xacc"): main += fresh * (lhs_scale * rhs_scale). Tiles of 256 x 128, four
+// waves of 128 x 64; the per-row scales of a stage travel with it by DMA.
+using TDg = mp::Tile<256, 128, 2, 2>;
+
+__global__ __launch_bounds__(256, 1) void deepgemm_fp8_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                              const float* __restrict__ sa, int64_t ld_sa,
+                                                              const uint8_t* __restrict__ b, int64_t ldb, int N,
+                                                              const float* __restrict__ sb, int64_t ld_sb, int K,
+                                                              uint16_t* __restrict__ out, int64_t ldo, int mblocks) {
+  using T = TDg;
+  constexpr int SB = (T::BM + T::BN) * (mp::ROWB + 4);
+  __shared__ __attribute__((aligned(1024))) char smem[2 * SB];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  mxdma::Rows<T::BM, T::NW, true> aop;
+  mxdma::Rows<T::BN, T::NW, true> bop;
+  aop.init(a, lda, M, reinterpret_cast<const uint8_t*>(sa), ld_sa * 4, m0, T::wave(), 1);
+  bop.init(b, ldb, N, reinterpret_cast<const uint8_t*>(sb), ld_sb * 4, n0, T::wave(), 128);
+  i32x16 fresh[T::TI][T::TJ];
+  f32x16 acc[T::TI][T::TJ];
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j) acc[i][j] = f32x16{};
+  // The wave's B rows all lie in one 128-row block (BN = 128), so one rhs
+  // scale serves the stage.
+  auto promote = [&](const i32x16 (&f)[T::TI][T::TJ], const uint32_t (&xa)[T::TI], const uint32_t (&xb)[T::TJ], int) {
+    const float rs = bit_cast<float>(xb[0]);
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i) {
+      const float w = __fmul_rn(bit_cast<float>(xa[i]), rs);
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) {
+        const f32x16 v = bit_cast<f32x16>(f[i][j]);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(v[e], w, acc[i][j][e]);
+      }
+    }
+  };
+  mxdma::dma_mainloop<T, mxdma::ScaleMode::kPromote>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, fresh,
+                                                     promote);
+  // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
   const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
@@ -422,58 +592,18 @@ INTENT_DEVICE void store_f16_scaled(const i32x16 (&acc)[mxdma::Tile::TI][mxdma::
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int n = n0 + T::col(j, g);
-        const f32x16 c = bit_cast<f32x16>(acc[i][j]);
-        f16* o = out + (int64_t)m * ldo + n;
-        f16 v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = (f16)__fmul_rn(__fmul_rn(c[4 * g + q], ls), rs);
+        uint16_t* o = out + (int64_t)m * ldo + n;
         if (vec && n + 3 < N) {
-          if constexpr (kAccum) {
-            const u32x2 old = *reinterpret_cast<const u32x2*>(o);
-            const f16x2 o0 = bit_cast<f16x2>(old[0]), o1 = bit_cast<f16x2>(old[1]);
-            v[0] = (f16)__fadd_rn((float)o0[0], (float)v[0]);
-            v[1] = (f16)__fadd_rn((float)o0[1], (float)v[1]);
-            v[2] = (f16)__fadd_rn((float)o1[0], (float)v[2]);
-            v[3] = (f16)__fadd_rn((float)o1[1], (float)v[3]);
-          }
-          f16x2 lo, hi;
-          lo[0] = v[0];
-          lo[1] = v[1];
-          hi[0] = v[2];
-          hi[1] = v[3];
-          *reinterpret_cast<u32x2*>(o) = u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+          const uint32_t lo = f32_to_bf16_rne(acc[i][j][4 * g]) | ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * g + 1]) << 16);
+          const uint32_t hi =
+              f32_to_bf16_rne(acc[i][j][4 * g + 2]) | ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * g + 3]) << 16);
+          *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            if (n + q < N) o[q] = kAccum ? (f16)__fadd_rn((float)o[q], (float)v[q]) : v[q];
+            if (n + q < N) o[q] = f32_to_bf16_rne(acc[i][j][4 * g + q]);
         }
       }
-  }
-}
-
-// bt: the right operand as [N, K] rows (K contiguous). K % (256 * splits) == 0
-// when splits > 1, K % 128 == 0 otherwise. Splits run in order inside the
-// workgroup, each on the whole tile; with kAccum the f16 output tile is read
-// back by the same lanes that wrote it.
-template <bool kAccum>
-__global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
-                                                                 const uint8_t* __restrict__ bt, int64_t ldb, int N,
-                                                                 int K, int splits, float ls, float rs,
-                                                                 f16* __restrict__ out, int64_t ldo, int mblocks) {
-  using T = mxdma::Tile;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * mxdma::kStage];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
-  mxdma::Rows<T::BM, T::NW, false> aop;
-  mxdma::Rows<T::BN, T::NW, false> bop;
-  aop.init(a, lda, M, nullptr, 0, m0, T::wave());
-  bop.init(bt, ldb, N, nullptr, 0, n0, T::wave());
-  const int nks = K / mp::ROWB / splits;
-  i32x16 acc[T::TI][T::TJ];
-  for (int s = 0; s < splits; ++s) {
-    mxdma::zero(acc);
-    mxdma::dma_mainloop<false>(smem, aop, bop, nks, mxdma::SplitK{splits, s}, acc);
-    store_f16_scaled<kAccum>(acc, m0, n0, M, N, ls, rs, out, ldo);
   }
 }
 
@@ -597,8 +727,8 @@ extern "C" int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, in
                  INTENT_ERR_ALIGNMENT, "operand rows must be 16-byte aligned");
   INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, bt_ld), INTENT_ERR_UNSUPPORTED,
                  "scaled_fp8_gemm: operand too large for 31-bit buffer offsets");
-  const int mblocks = (int)((M + 255) / 256);
-  const int64_t grid = (int64_t)mblocks * ((N + 255) / 256);
+  const int mblocks = (int)((M + TSk::BM - 1) / TSk::BM);
+  const int64_t grid = (int64_t)mblocks * ((N + TSk::BN - 1) / TSk::BN);
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "scaled_fp8_gemm: grid too large");
   if (accumulate)
     hipLaunchKernelGGL(fp8_scaled_gemm_kernel<true>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a, a_ld,
@@ -608,4 +738,32 @@ extern "C" int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, in
                        a_ld, (int)M, bt, bt_ld, (int)N, (int)K, (int)splits, a_scale, b_scale, (f16*)out, out_ld,
                        mblocks);
   return intent::launch_status("scaled_fp8_gemm");
+}
+
+extern "C" int intent_deepgemm_fp8(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const float* a_scales,
+                                   int64_t a_scales_ld, const uint8_t* b, int64_t N, int64_t b_ld,
+                                   const float* b_scales, int64_t b_scales_ld, void* out, int64_t out_ld,
+                                   void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 128, got %lld", (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "empty K");
+  INTENT_REQUIRE(a && b && a_scales && b_scales && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(a_ld >= K && b_ld >= K && a_scales_ld >= K / 128 && b_scales_ld >= K / 128 && out_ld >= N,
+                 INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(b) && a_ld % 16 == 0 && b_ld % 16 == 0 &&
+                     intent::aligned4(a_scales) && intent::aligned4(b_scales),
+                 INTENT_ERR_ALIGNMENT, "operand rows 16-byte aligned, scales 4-byte aligned");
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, b_ld) &&
+                     intent::fits_offset(M, a_scales_ld * 4) && intent::fits_offset(N / 128 + 1, b_scales_ld * 4),
+                 INTENT_ERR_UNSUPPORTED, "deepgemm_fp8: operand too large for 31-bit buffer offsets");
+  const int mblocks = (int)((M + TDg::BM - 1) / TDg::BM);
+  const int64_t grid = (int64_t)mblocks * ((N + TDg::BN - 1) / TDg::BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "deepgemm_fp8: grid too large");
+  hipLaunchKernelGGL(deepgemm_fp8_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a, a_ld, (int)M,
+                     a_scales, a_scales_ld, b, b_ld, (int)N, b_scales, b_scales_ld, (int)K, (uint16_t*)out, out_ld,
+                     mblocks);
+  return intent::launch_status("deepgemm_fp8");
 }

@@ -681,9 +681,41 @@ scaled_fp8_splitk_matmul = KernelDefinition(
 )
 
 
+# ---- DeepGEMM-style FP8 with f32 block scales ------------------------------------
+
+def _deepgemm_check(env: dict) -> None:
+    if env["NB"] * 128 < env["N"]:
+        raise ValueError(f"rhs_scale has {env['NB']} row blocks; N = {env['N']} needs {(env['N'] + 127) // 128}")
+
+
+def _deepgemm_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    lhs, rhs, ls, rs, out = v["lhs"], v["rhs"], v["lhs_scale"], v["rhs_scale"], v["output"]
+    M, KB, N = env["M"], env["KB"], env["N"]
+    _native.call("intent_deepgemm_fp8", _ptr(lhs), M, KB * 128, KB * 128, _ptr(ls), KB, _ptr(rhs), N, KB * 128,
+                 _ptr(rs), KB, _ptr(out), _ld(out), stream)
+    return "intent_deepgemm_fp8"
+
+
+deepgemm_fp8_2xacc = KernelDefinition(
+    name="deepgemm_fp8_2xacc",
+    params=(
+        Param("lhs", "f8e4m3fn", ("M", "KB", 128)),
+        Param("rhs", "f8e4m3fn", ("N", "KB", 128)),
+        Param("lhs_scale", "f32", ("M", "KB")),
+        Param("rhs_scale", "f32", ("NB", "KB")),
+        Param("output", "bf16", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_deepgemm_launch,
+    check=_deepgemm_check,
+    reference="examples/kernels/contraction/block_scaled.py:101-122",
+    doc="output = bf16(sum over k-blocks of (lhs . rhs) * lhs_scale[m, kb] * rhs_scale[n // 128, kb])",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
+    deepgemm_fp8_2xacc,
 )

@@ -529,3 +529,46 @@ def test_scaled_fp8_splitk_reference_size(gpu):
         ref.add_((l4[:, :, s, :].float().flatten(1) @ r4[:, s, :, :].float().flatten(0, 1)).half())
     err = (out.double() - ref.double()).abs().max().item()
     assert torch.isfinite(out).all() and err <= 4e-3 * ref.double().abs().max().item()
+
+
+# ---- DeepGEMM-style FP8 with f32 block scales ----------------------------------------
+
+def _bf16_bits_to_f64(bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).double().numpy()
+
+
+@pytest.mark.parametrize("M,KB,N", [(64, 1, 128), (300, 3, 200), (1, 2, 1), (4000, 4, 4200)])
+def test_deepgemm_fp8(gpu, threads, M, KB, N):
+    a, b = _fp8_bits(M + 1, (M, KB * 128)), _fp8_bits(N + 2, (N, KB * 128))
+    g = torch.Generator().manual_seed(M + N)
+    NB = (N + 127) // 128
+    sa = (torch.rand(M, KB, generator=g) + 0.25).numpy()
+    sb = (torch.rand(NB, KB, generator=g) + 0.25).numpy()
+    lhs = dev(a).view(torch.float8_e4m3fn).view(M, KB, 128)
+    rhs = dev(b).view(torch.float8_e4m3fn).view(N, KB, 128)
+    out = art(intent.deepgemm_fp8_2xacc).run(lhs, rhs, dev(sa), dev(sb))
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = _bf16_bits_to_f64(oracle.deepgemm_fp8(a[rows], sa[rows], b, sb, threads))
+    got = host(out.view(torch.int16)).view(np.uint16)[rows]
+    # bf16 output: one rounding of ~2^-8 relative on either side
+    assert np.max(np.abs(_bf16_bits_to_f64(got) - ref)) <= 1e-2 * np.abs(ref).max()
+
+
+def test_deepgemm_fp8_reference_inputs(gpu):
+    # The reference's case and input construction (experiments/cpu/providers/mojo/
+    # contraction.py:227-236: per-block absmax scaling to 448, M = N = K = 4096),
+    # checked against its CPU formula (cpu_runtime.py:127-131) evaluated on the GPU.
+    g = torch.Generator(device="cuda").manual_seed(5)
+    lv = torch.randn((4096, 4096), device="cuda", generator=g).bfloat16().view(4096, 32, 128)
+    lmax = lv.abs().float().amax(dim=2).clamp_min(1e-4)
+    lhs = (lv * (448.0 / lmax[:, :, None])).to(torch.float8_e4m3fn)
+    rv = torch.randn((4096, 4096), device="cuda", generator=g).bfloat16().view(32, 128, 32, 128)
+    rmax = rv.abs().float().amax(dim=(1, 3), keepdim=True).clamp_min(1e-4)
+    rhs = (rv * (448.0 / rmax)).to(torch.float8_e4m3fn).view(4096, 32, 128)
+    ls, rs = lmax / 448.0, (rmax / 448.0).view(32, 32)
+    out = art(intent.deepgemm_fp8_2xacc).run(lhs, rhs, ls, rs.contiguous())
+    left = (lhs.float() * ls[:, :, None]).flatten(1)
+    right = (rhs.float() * rs.repeat_interleave(128, dim=0)[:, :, None]).flatten(1)
+    ref = (left @ right.T)
+    err = (out.double() - ref.double()).abs().max().item()
+    assert torch.isfinite(out.float()).all() and err <= 1e-2 * ref.abs().max().item()
