@@ -366,6 +366,17 @@ int intent_deepgemm_fp8(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
                         const float* b_scales, int64_t b_scales_ld,
                         void* out, int64_t out_ld, void* stream);
 
+/* FP8 x FP8 -> FP8 GEMM. Replaces fp8_e4m3_matmul (format 0) and
+ * fp8_e5m2_matmul (format 1) (examples/kernels/contraction/weight_only_int4.py:
+ * 178-215): out[m, n] = cast(sum_k a[m, k] * bt[n, k] in f32, format), nearest
+ * even (doc/dsl/types-numerics-and-effects.en.md:86-89: E5M2 overflows to
+ * infinity; E4M3FN results must lie within +-448, larger ones saturate here).
+ * a: [M, K], bt: [N, K] rows (K contiguous, K % 128 == 0), out: [M, N] bytes.
+ */
+int intent_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                    const uint8_t* bt, int64_t N, int64_t bt_ld, int format,
+                    uint8_t* out, int64_t out_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

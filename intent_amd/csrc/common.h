@@ -104,6 +104,35 @@ INTENT_DEVICE int xcd_swizzle(int bid, int nblocks) {
   return (bid & 7) * per_xcd + (bid >> 3);
 }
 
+// f32 -> E4M3FN bits, round half to even; |f| >= 448 saturates to 448 (inputs
+// past the format's range are outside the cast's contract), NaN -> NaN.
+INTENT_DEVICE uint32_t f32_to_e4m3fn(float f) {
+  const uint32_t u = bit_cast<uint32_t>(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  const float mag = bit_cast<float>(a);
+  if (mag >= 448.0f) return sign | 0x7eu;
+  if (mag < 0.015625f) return sign | (uint32_t)rintf(mag * 512.0f);  // subnormal step 2^-9
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  return sign | ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
+}
+
+// f32 -> E5M2 bits, round half to even; finite overflow gives infinity
+// (0x7C), NaN -> 0x7F. Subnormal step 2^-16, smallest normal 2^-14.
+INTENT_DEVICE uint32_t f32_to_e5m2(float f) {
+  const uint32_t u = bit_cast<uint32_t>(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  if (a == 0x7f800000u) return sign | 0x7cu;
+  const float mag = bit_cast<float>(a);
+  if (mag < 6.103515625e-05f) return sign | (uint32_t)rintf(mag * 65536.0f);
+  const uint32_t r = a + 0xfffffu + ((a >> 21) & 1u);
+  const uint32_t e = (r >> 23) - 112u;
+  return e >= 31u ? sign | 0x7cu : sign | (e << 2) | ((r >> 21) & 3u);
+}
+
 // ---- wave-wide reduction of V per-lane partial sums (no LDS) -----------------
 // Reduce-scatter over the 64 lanes: v_permlane32_swap pairs value i with
 // value i + V/2 across the two half-waves, v_permlane16_swap does the same

@@ -9,19 +9,6 @@
 
 namespace {
 
-// f32 -> E4M3FN bits, round half to even; |f| >= 448 saturates to 448, NaN -> NaN.
-INTENT_DEVICE uint32_t f32_to_e4m3fn(float f) {
-  const uint32_t u = bit_cast<uint32_t>(f);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t a = u & 0x7fffffffu;
-  if (a > 0x7f800000u) return sign | 0x7fu;
-  const float mag = bit_cast<float>(a);
-  if (mag >= 448.0f) return sign | 0x7eu;
-  if (mag < 0.015625f) return sign | (uint32_t)rintf(mag * 512.0f);  // subnormal step 2^-9
-  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
-  return sign | ((((r >> 23) - 120u) << 3) | ((r >> 20) & 7u));
-}
-
 // Thread t of a 32-lane half-wave holds columns 4t..4t+3 of its group.
 template <bool kBf16>
 __global__ __launch_bounds__(256) void fp8_groupwise_kernel(const void* __restrict__ xv, int64_t ldx, int M, int N,

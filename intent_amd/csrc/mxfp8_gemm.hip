@@ -292,7 +292,8 @@ enum class ScaleMode {
 // acc += A·B over nk stages (stage kt at byte offset koff(kt) of every row).
 // T: a 4-wave tile whose rows are multiples of 64. Starts with a barrier, so
 // that it can run again on the same LDS, and ends with no DMA in flight.
-template <class T, ScaleMode kMode, class KOff, class Hook>
+// kFmt: the operands' format code for the f8f6f4 MFMA (0 E4M3, 1 E5M2).
+template <class T, ScaleMode kMode, class KOff, class Hook, int kFmt = 0>
 INTENT_DEVICE void dma_mainloop(char* smem,
                                 const Rows<T::BM, T::NW, kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote>& aop,
                                 const Rows<T::BN, T::NW, kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote>& bop,
@@ -346,7 +347,7 @@ INTENT_DEVICE void dma_mainloop(char* smem,
         if (kMode == ScaleMode::kPromote && s == 0) c = f32x16{};  // a fresh sum per stage
         const int sb_ = kMode == ScaleMode::kE8M0 ? (int)((csb[j] >> sh) & 255u) : 127;
         const int sa_ = kMode == ScaleMode::kE8M0 ? (int)((csa[i] >> sh) & 255u) : 127;
-        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[s][j], af[s][i], c, 0, 0, 0, sb_, 0, sa_);
+        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[s][j], af[s][i], c, kFmt, kFmt, 0, sb_, 0, sa_);
         acc[i][j] = bit_cast<i32x16>(c);
       }
   };
@@ -607,6 +608,53 @@ __global__ __launch_bounds__(256, 1) void deepgemm_fp8_kernel(const uint8_t* __r
   }
 }
 
+// FP8 x FP8 -> FP8 GEMM (fp8_e4m3_matmul, fp8_e5m2_matmul,
+// weight_only_int4.py:178-215): out = cast(f32 sum over k, format), both
+// operands [rows, K] with K contiguous. kFmt 0: E4M3FN (nearest-even; the
+// cast's contract requires results within +-448), 1: E5M2 (nearest-even,
+// finite overflow to infinity).
+template <int kFmt>
+__global__ __launch_bounds__(256, 1) void fp8_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                          const uint8_t* __restrict__ bt, int64_t ldb, int N, int K,
+                                                          uint8_t* __restrict__ out, int64_t ldo, int mblocks) {
+  using T = mxdma::Tile;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * mxdma::kStage];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  mxdma::Rows<T::BM, T::NW, false> aop;
+  mxdma::Rows<T::BN, T::NW, false> bop;
+  aop.init(a, lda, M, nullptr, 0, m0, T::wave());
+  bop.init(bt, ldb, N, nullptr, 0, n0, T::wave());
+  i32x16 acc[T::TI][T::TJ];
+  mxdma::zero(acc);
+  mxdma::dma_mainloop<T, mxdma::ScaleMode::kNone, mxdma::SplitK, mxdma::NoHook, kFmt>(
+      smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, acc, mxdma::NoHook{});
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 3) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        const f32x16 c = bit_cast<f32x16>(acc[i][j]);
+        uint32_t q[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = kFmt == 0 ? f32_to_e4m3fn(c[4 * g + e]) : f32_to_e5m2(c[4 * g + e]);
+        uint8_t* o = out + (int64_t)m * ldo + n;
+        if (vec && n + 3 < N) {
+          *reinterpret_cast<uint32_t*>(o) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = (uint8_t)q[e];
+        }
+      }
+  }
+}
+
 // Byte-matrix transpose through a 64 x 64 LDS tile: dst[c][r] = src[r][c].
 __global__ __launch_bounds__(256) void byte_transpose_kernel(const uint8_t* __restrict__ src, int R, int C,
                                                              int64_t sld, uint8_t* __restrict__ dst, int64_t dld) {
@@ -766,4 +814,32 @@ extern "C" int intent_deepgemm_fp8(const uint8_t* a, int64_t M, int64_t K, int64
                      a_scales, a_scales_ld, b, b_ld, (int)N, b_scales, b_scales_ld, (int)K, (uint16_t*)out, out_ld,
                      mblocks);
   return intent::launch_status("deepgemm_fp8");
+}
+
+extern "C" int intent_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* bt, int64_t N,
+                               int64_t bt_ld, int format, uint8_t* out, int64_t out_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(format == 0 || format == 1, INTENT_ERR_INVALID_ARGUMENT, "format must be 0 (E4M3FN) or 1 (E5M2)");
+  INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 128, got %lld", (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "empty K");
+  INTENT_REQUIRE(a && bt && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(a_ld >= K && bt_ld >= K && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(bt) && a_ld % 16 == 0 && bt_ld % 16 == 0,
+                 INTENT_ERR_ALIGNMENT, "operand rows must be 16-byte aligned");
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, bt_ld), INTENT_ERR_UNSUPPORTED,
+                 "fp8_gemm: operand too large for 31-bit buffer offsets");
+  const int mblocks = (int)((M + 255) / 256);
+  const int64_t grid = (int64_t)mblocks * ((N + 255) / 256);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "fp8_gemm: grid too large");
+  if (format == 0)
+    hipLaunchKernelGGL(fp8_gemm_kernel<0>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a, a_ld, (int)M,
+                       bt, bt_ld, (int)N, (int)K, out, out_ld, mblocks);
+  else
+    hipLaunchKernelGGL(fp8_gemm_kernel<1>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a, a_ld, (int)M,
+                       bt, bt_ld, (int)N, (int)K, out, out_ld, mblocks);
+  return intent::launch_status("fp8_gemm");
 }

@@ -712,10 +712,40 @@ deepgemm_fp8_2xacc = KernelDefinition(
 )
 
 
+# ---- FP8 x FP8 -> FP8 ------------------------------------------------------------
+
+def _fp8_out_launch(fmt: int):
+    def launch(v: dict, env: dict, stream: int, workspace) -> str:
+        lhs, rhs, out = v["lhs"], v["rhs_transposed"], v["output"]
+        _native.call("intent_fp8_gemm", _ptr(lhs), env["M"], env["K"], _ld(lhs), _ptr(rhs), env["N"], _ld(rhs), fmt,
+                     _ptr(out), _ld(out), stream)
+        return "intent_fp8_gemm"
+    return launch
+
+
+def _fp8_out_definition(name: str, dt: str, fmt: int, lines: str) -> KernelDefinition:
+    return KernelDefinition(
+        name=name,
+        params=(
+            Param("lhs", dt, ("M", "K"), leading_stride=True),
+            Param("rhs_transposed", dt, ("N", "K"), leading_stride=True),
+            Param("output", dt, ("M", "N"), OUT, leading_stride=True),
+        ),
+        launch=_fp8_out_launch(fmt),
+        check=_sfp8_check,
+        reference=f"examples/kernels/contraction/weight_only_int4.py:{lines}",
+        doc=f"output = {dt}(lhs @ rhs_transposed^T, f32 accumulation), nearest even",
+    )
+
+
+fp8_e4m3_matmul = _fp8_out_definition("fp8_e4m3_matmul", "f8e4m3fn", 0, "178-195")
+fp8_e5m2_matmul = _fp8_out_definition("fp8_e5m2_matmul", "f8e5m2", 1, "198-215")
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
-    deepgemm_fp8_2xacc,
+    deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul,
 )

@@ -43,6 +43,7 @@ DTYPES = {
     "i64": DType("i64", 64, "signed"),
     "bool": DType("bool", 8, "bool"),
     "f8e4m3fn": DType("f8e4m3fn", 8, "float"),
+    "f8e5m2": DType("f8e5m2", 8, "float"),
 }
 
 
@@ -58,7 +59,7 @@ def torch_dtype(element: DType):
 
     return {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32, "i8": torch.int8,
             "u8": torch.uint8, "i32": torch.int32, "i64": torch.int64, "bool": torch.bool,
-            "f8e4m3fn": torch.float8_e4m3fn}[element.name]
+            "f8e4m3fn": torch.float8_e4m3fn, "f8e5m2": torch.float8_e5m2}[element.name]
 
 
 @dataclass(frozen=True, slots=True)

@@ -82,6 +82,12 @@ def lib():
         _lib.orc_scaled_fp8_gemm.restype = None
         _lib.orc_deepgemm_fp8.argtypes = [p, p, i64, i64, p, p, i64, p, ci]
         _lib.orc_deepgemm_fp8.restype = None
+        _lib.orc_e5m2_to_f32.argtypes = [ctypes.c_uint8]
+        _lib.orc_e5m2_to_f32.restype = ctypes.c_float
+        _lib.orc_f32_to_e5m2.argtypes = [ctypes.c_float]
+        _lib.orc_f32_to_e5m2.restype = ctypes.c_uint8
+        _lib.orc_fp8_gemm.argtypes = [ci, p, i64, i64, p, i64, p, ci]
+        _lib.orc_fp8_gemm.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -292,6 +298,24 @@ def deepgemm_fp8(a, sa, b, sb, threads: int = 1) -> np.ndarray:
     out = np.empty((M, N), np.uint16)
     lib().orc_deepgemm_fp8(_ptr(a), _ptr(sa), M, K // 128, _ptr(b), _ptr(sb), N, _ptr(out), threads)
     return out
+
+
+def fp8_gemm(a, bt, fmt: str, threads: int = 1) -> np.ndarray:
+    """FP8 bytes a [M, K], bt [N, K] ("e4m3fn" or "e5m2") -> FP8 bytes [M, N]."""
+    a, bt = _c(a, np.uint8), _c(bt, np.uint8)
+    M, K = a.shape
+    N = bt.shape[0]
+    out = np.empty((M, N), np.uint8)
+    lib().orc_fp8_gemm(1 if fmt == "e5m2" else 0, _ptr(a), M, K, _ptr(bt), N, _ptr(out), threads)
+    return out
+
+
+def f32_to_e5m2(values) -> np.ndarray:
+    return np.array([lib().orc_f32_to_e5m2(float(v)) for v in np.asarray(values, np.float32).reshape(-1)], np.uint8)
+
+
+def e5m2_to_f32(bits) -> np.ndarray:
+    return np.array([lib().orc_e5m2_to_f32(int(v)) for v in np.asarray(bits, np.uint8).reshape(-1)], np.float32)
 
 
 def e4m3fn_to_f32(bits) -> np.ndarray:

@@ -595,3 +595,52 @@ void orc_deepgemm_fp8(const uint8_t* a, const float* sa, int64_t M, int64_t KB, 
     }
   }
 }
+
+/* ---- FP8 x FP8 -> FP8 contractions ---------------------------------------------
+ * fp8_e4m3_matmul / fp8_e5m2_matmul (examples/kernels/contraction/weight_only_int4.py:
+ * 178-215): out = cast(f32 contraction, format), fma in k order. Casts follow
+ * doc/dsl/types-numerics-and-effects.en.md:86-89: nearest-even; E5M2 (sign1,
+ * exponent5 bias 15, fraction2, subnormals) overflows to infinity; E4M3FN
+ * results beyond 448 are outside the cast's contract (saturated here). */
+float orc_e5m2_to_f32(uint8_t v) {
+  const int sign = v >> 7, e = (v >> 2) & 31, m = v & 3;
+  float mag;
+  if (e == 31) mag = m ? NAN : INFINITY;
+  else if (e == 0) mag = ldexpf((float)m, -16);
+  else mag = ldexpf(1.0f + (float)m / 4.0f, e - 15);
+  return sign ? -mag : mag;
+}
+
+uint8_t orc_f32_to_e5m2(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint8_t)(sign | 0x7f); /* NaN */
+  if (a == 0x7f800000u) return (uint8_t)(sign | 0x7c);
+  float mag;
+  memcpy(&mag, &a, 4);
+  if (mag < ldexpf(1.0f, -14)) /* subnormal step 2^-16; 4 is the smallest normal */
+    return (uint8_t)(sign | (uint8_t)rintf(mag * 65536.0f));
+  /* normal: keep 2 mantissa bits, round half to even on the 21 dropped bits */
+  const uint32_t r = a + 0xfffffu + ((a >> 21) & 1u);
+  const uint32_t e = (r >> 23) - 127 + 15;
+  if (e >= 31) return (uint8_t)(sign | 0x7c); /* finite overflow -> infinity */
+  return (uint8_t)(sign | (e << 2) | ((r >> 21) & 3u));
+}
+
+void orc_fp8_gemm(int format, const uint8_t* a, int64_t M, int64_t K, const uint8_t* bt, int64_t N, uint8_t* out,
+                  int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) {
+        const float x = format ? orc_e5m2_to_f32(a[m * K + k]) : orc_e4m3fn_to_f32(a[m * K + k]);
+        const float y = format ? orc_e5m2_to_f32(bt[n * K + k]) : orc_e4m3fn_to_f32(bt[n * K + k]);
+        acc = fmaf(x, y, acc);
+      }
+      out[m * N + n] = format ? orc_f32_to_e5m2(acc) : orc_f32_to_e4m3fn(acc);
+    }
+  }
+}

@@ -43,5 +43,9 @@ void orc_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, const uint8_t* 
                          int64_t splits, int accumulate, uint16_t* out, int threads);
 void orc_deepgemm_fp8(const uint8_t* a, const float* sa, int64_t M, int64_t KB, const uint8_t* b, const float* sb,
                       int64_t N, uint16_t* out, int threads);
+float orc_e5m2_to_f32(uint8_t v);
+uint8_t orc_f32_to_e5m2(float f);
+void orc_fp8_gemm(int format, const uint8_t* a, int64_t M, int64_t K, const uint8_t* bt, int64_t N, uint8_t* out,
+                  int threads);
 
 #endif

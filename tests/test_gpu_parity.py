@@ -572,3 +572,26 @@ def test_deepgemm_fp8_reference_inputs(gpu):
     ref = (left @ right.T)
     err = (out.double() - ref.double()).abs().max().item()
     assert torch.isfinite(out.float()).all() and err <= 1e-2 * ref.abs().max().item()
+
+
+# ---- FP8 x FP8 -> FP8 ----------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", ["e4m3fn", "e5m2"])
+@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (4096, 1024, 4352)])
+def test_fp8_out_matmul(gpu, threads, fmt, M, K, N):
+    tdt = torch.float8_e4m3fn if fmt == "e4m3fn" else torch.float8_e5m2
+    g = torch.Generator().manual_seed(M + N)
+    a = (torch.randn(M, K, generator=g) * 0.25).to(tdt)
+    b = (torch.randn(N, K, generator=g) * 0.25).to(tdt)
+    defn = intent.fp8_e4m3_matmul if fmt == "e4m3fn" else intent.fp8_e5m2_matmul
+    out = art(defn).run(a.cuda(), b.cuda())
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = oracle.fp8_gemm(a.view(torch.uint8).numpy()[rows], b.view(torch.uint8).numpy(), fmt, threads)
+    got = host(out.view(torch.uint8))[rows]
+    # identical codes except where the two f32 sums (different order) straddle a
+    # rounding boundary: then the neighbouring code
+    assert np.mean(got == ref) >= 0.99
+    dg = torch.from_numpy(got).view(tdt).double()
+    dr = torch.from_numpy(ref).view(tdt).double()
+    step = 2.0 ** -2 if fmt == "e5m2" else 2.0 ** -3
+    assert torch.all((dg - dr).abs() <= step * dr.abs() + 2.0 ** -9)

@@ -577,3 +577,46 @@ def test_deepgemm_fp8_matches_reference_formula():
     y = oracle.deepgemm_fp8(a1, np.array([[0.5]], np.float32), b1, np.array([[4.0]], np.float32))
     vals = torch.from_numpy(y.view(np.int16)).view(torch.bfloat16).float().numpy()
     assert vals[0, 5] == 12.0 and np.count_nonzero(vals) == 1
+
+
+# ---- FP8 x FP8 -> FP8 ------------------------------------------------------------
+
+def test_e5m2_conversions_match_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e5m2).float().numpy()
+    got = oracle.e5m2_to_f32(codes)
+    finite = np.isfinite(ref)
+    assert np.array_equal(got[finite], ref[finite]) and np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isinf(got), np.isinf(ref))
+    g = torch.Generator().manual_seed(21)
+    vals = torch.cat([
+        torch.randn(20000, generator=g) * 100,
+        torch.randn(20000, generator=g) * 1e-5,                 # subnormals
+        torch.from_numpy(ref[finite]).float(),                  # every finite code
+        torch.from_numpy((ref[finite][:-1] + ref[finite][1:]) / 2).float(),  # half-way points
+        torch.tensor([57344.0, 61439.0, 61440.0, 1e6, -1e6, float("inf"), -float("inf"), 0.0, -0.0]),
+    ])
+    want = vals.to(torch.float8_e5m2).view(torch.uint8).numpy()
+    assert np.array_equal(oracle.f32_to_e5m2(vals.numpy()), want)
+
+
+@pytest.mark.parametrize("fmt,tdt", [("e4m3fn", torch.float8_e4m3fn), ("e5m2", torch.float8_e5m2)])
+def test_fp8_gemm_closed_form(fmt, tdt):
+    g = torch.Generator().manual_seed(22)
+    M, K, N = 6, 384, 9
+    a = (torch.randn(M, K, generator=g) * 0.5).to(tdt)
+    b = (torch.randn(N, K, generator=g) * 0.5).to(tdt)
+    got = oracle.fp8_gemm(a.view(torch.uint8).numpy(), b.view(torch.uint8).numpy(), fmt)
+    exact = a.double() @ b.double().T
+    want = exact.float().to(tdt).view(torch.uint8).numpy()
+    # the f32 sum in k order may round to the neighbouring code in rare cases
+    assert np.mean(got == want) >= 0.95
+    dec = torch.from_numpy(got).view(tdt).double()
+    step = 2.0 ** -2 if fmt == "e5m2" else 2.0 ** -3
+    assert torch.all((dec - exact).abs() <= step * exact.abs() + 2.0 ** -9)
+    # one-hot known answer: a single product, exact in the format
+    a1 = torch.zeros(1, 128, dtype=tdt)
+    b1 = torch.zeros(2, 128, dtype=tdt)
+    a1[0, 3], b1[1, 3] = 1.5, -2.0
+    y = oracle.fp8_gemm(a1.view(torch.uint8).numpy(), b1.view(torch.uint8).numpy(), fmt)
+    assert torch.from_numpy(y).view(tdt).float().tolist() == [[0.0, -3.0]]
