@@ -245,6 +245,29 @@ def bench_deepgemm(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": n}
 
 
+def bench_fp4(steps: int, warmup: int) -> dict:
+    """The reference's dequant_bf16_fp4 case (experiments/cpu/providers/mojo/contraction.py:220-224):
+    bf16 activations [4096, 4096] * 0.125, packed E2M1 weights [4096, 2048], bf16 out."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    M = N = K = 4096
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = (torch.randn((M, K), device="cuda", generator=g) * 0.125).bfloat16()
+    w = torch.randint(0, 256, (N, K // 2), device="cuda", generator=g, dtype=torch.uint8)
+    work = inputs.Workload(f"fp4 x bf16 M{M} K{K} N{N}", 2 * M * N * K, M * K * 2 + N * K // 2 + M * N * 2)
+    art = intent.compile(intent.dequant_bf16_fp4_matmul, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes, minimum=2)
+    sets = [(x.clone(), w.clone()) for _ in range(n)]
+    calls = [art.prepare(*s) for s in sets]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls, sets
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
 def bench_mxfp8(steps: int, warmup: int) -> dict:
     """The reference's mxfp8_gemm case (experiments/cpu/providers/mojo/contraction.py:285-305):
     M=4096, K=4096, N=14336, E4M3FN with E8M0 scales per 32, rhs given as the [KB, 32, N]
@@ -404,6 +427,9 @@ def main() -> int:
         log("[bench] deepgemm fp8 M=N=K=4096")
         r = bench_deepgemm(steps, warm)
         extra["deepgemm_fp8_4096"] = _flop_entry(r, 5033.2, "TFLOP/s")
+        log("[bench] fp4 x bf16 M=N=K=4096")
+        r = bench_fp4(steps, warm)
+        extra["fp4_bf16_4096"] = _flop_entry(r, F16_PEAK_TFLOPS, "TFLOP/s")
         log("[bench] q4_k projection N=K=4096")
         r = bench_q4k(args.steps, args.warmup)
         extra["q4k_projection_n4096"] = _hbm_entry(r)

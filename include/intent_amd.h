@@ -377,6 +377,18 @@ int intent_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
                     const uint8_t* bt, int64_t N, int64_t bt_ld, int format,
                     uint8_t* out, int64_t out_ld, void* stream);
 
+/* FP4 (E2M1) weight x bf16 activation GEMM. Replaces dequant_bf16_fp4_matmul
+ * (examples/kernels/contraction/weight_only_int4.py:127-175; CPU baseline
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:117-124).
+ * x: bf16 bits [M, K] (x_ld elements); packed: [N, K/2] bytes, each big-endian
+ * 16-bit word (p[2i] << 8 | p[2i+1]) holding k = 4i .. 4i+3 in the reference's
+ * bit layout; y: bf16 bits [M, N]: y = bf16(sum_k x * e2m1(W)), f32 accumulation.
+ * K % 64 == 0.
+ */
+int intent_fp4_bf16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld,
+                           const uint8_t* packed, int64_t N, int64_t packed_ld,
+                           void* y, int64_t y_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,135 @@ struct WeightOp<T, W8Args> {
   INTENT_DEVICE static void init(Op& op, const W8Args& w, int n0, int N) { op.init(w.q, w.ldq, ClampRows{n0, N}); }
 };
 
+// ---- FP4 (E2M1) weights, bf16 activations: dequant_bf16_fp4_matmul --------------
+// weight_only_int4.py:127-175 (CPU baseline cpu_runtime.py:117-124). Row n of
+// the packed weights holds K/4 big-endian 16-bit words, word w = (p[2w] << 8) |
+// p[2w+1] carrying k = 4w .. 4w+3 at the bit masks below; each 4-bit code
+// becomes the bf16 pattern (bits & 0x81C0), and bf16(f32(pattern) * 2^126) is
+// the E2M1 value (0, ±0.5, ±1, ±1.5, ±2, ±3, ±4, ±6), exactly: a normal
+// pattern gains 126 in its exponent field, the one subnormal pattern is 0.5.
+INTENT_DEVICE uint32_t fp4_bf16(uint32_t v) {
+  const uint32_t mag = v & 0x7fffu;
+  return mag >= 0x80u ? v + 0x3f00u : mag ? (v & 0x8000u) | 0x3f00u : v;
+}
+// Eight bf16 (k = 8c .. 8c+7) from packed dword d (memory bytes b0 b1 b2 b3).
+INTENT_DEVICE u32x4 fp4x8_to_bf16(uint32_t d) {
+  u32x4 out;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t w = (((d >> (16 * h)) & 0xffu) << 8) | ((d >> (16 * h + 8)) & 0xffu);
+    const uint32_t v0 = w & 0x81c0u;
+    const uint32_t v1 = (w << 3) & 0x81c0u;
+    const uint32_t v2 = (w << 6) & 0x81c0u;
+    const uint32_t v3 = ((w << 1) & 0x8000u) | ((w >> 3) & 0x0180u) | ((w >> 7) & 0x0040u);
+    out[2 * h] = fp4_bf16(v0) | (fp4_bf16(v1) << 16);
+    out[2 * h + 1] = fp4_bf16(v2) | (fp4_bf16(v3) << 16);
+  }
+  return out;
+}
+
+// Packed FP4 weight rows decoded to bf16 on the way to LDS (same staging
+// contract as mp::W8Operand: a stage is 64 k = 32 packed bytes per row).
+template <int ROWS, int NT>
+struct Fp4Operand {
+  static constexpr int PIECE = (ROWS * 2) % NT == 0 ? 16 : (ROWS * 4) % NT == 0 ? 8 : 4;  // bytes per load
+  static constexpr int P = 32 / PIECE;
+  static constexpr int NS = ROWS * P / NT;
+  static_assert(NS * NT == ROWS * P, "FP4 staging must divide evenly");
+  static constexpr int NVM = NS;
+  mp::Rsrc rq;
+  uint32_t qoff[NS];
+  int lrow[NS], part[NS];
+  struct Regs {
+    u32x4 w[NS];
+  };
+  template <class RowMap>
+  INTENT_DEVICE void init(const uint8_t* q, int64_t ldq, const RowMap& wrow) {
+    rq = make_rsrc(q);
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int c = (int)(threadIdx.x % NT) + i * NT;
+      lrow[i] = c / P;
+      part[i] = c % P;
+      qoff[i] = (uint32_t)((int64_t)wrow(lrow[i]) * ldq + part[i] * PIECE);
+    }
+  }
+  INTENT_DEVICE void load(int kt, Regs& r) const {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      if constexpr (PIECE == 16) {
+        r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, qoff[i], (uint32_t)kt * 32, 0);
+      } else if constexpr (PIECE == 8) {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff[i], (uint32_t)kt * 32, 0);
+        r.w[i] = u32x4{v[0], v[1], 0u, 0u};
+      } else {
+        r.w[i] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(rq, qoff[i], (uint32_t)kt * 32, 0), 0u, 0u, 0u};
+      }
+    }
+  }
+  template <bool kAsm = false>
+  INTENT_DEVICE void store(const Regs& r, char* lds_b) const {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      char* row = lds_b + lrow[i] * mp::ROWB;
+      const int sw = mp::swz(lrow[i]);
+#pragma unroll
+      for (int d = 0; d < PIECE / 4; ++d) {
+        const int chunk = part[i] * (PIECE / 4) + d;  // each dword = 8 k = one 16-byte bf16 chunk
+        const u32x4 v = fp4x8_to_bf16(r.w[i][d]);
+        if constexpr (kAsm)
+          mp::lds_store16(row + ((chunk ^ sw) << 4), v);
+        else
+          *reinterpret_cast<u32x4*>(row + ((chunk ^ sw) << 4)) = v;
+      }
+    }
+  }
+};
+
+// y[m, n] = bf16(sum_k x[m, k] * fp4(W)[n, k]), bf16 activations, f32 accumulation.
+template <class T>
+__global__ __launch_bounds__(T::NT_WS, 1) void fp4_bf16_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                    int M, const uint8_t* __restrict__ wq,
+                                                                    int64_t ldw, int N, int K,
+                                                                    uint16_t* __restrict__ y, int64_t ldy,
+                                                                    int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  char* const bufs[2] = {buf0, buf1};
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  Fp4Operand<T::BN, T::NT> bop;
+  bop.init(wq, ldw, ClampRows{n0, N});
+  f32x16 acc[T::TI][T::TJ];
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave() % T::NW);
+  if (!mp::mainloop_ws<T, mp::BF16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
+  const bool vec = (ldy & 3) == 0 && (((uintptr_t)y) & 7) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        uint16_t* o = y + (int64_t)m * ldy + n;
+        if (vec && n + 3 < N) {
+          const uint32_t lo = f32_to_bf16_rne(acc[i][j][4 * g]) | ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * g + 1]) << 16);
+          const uint32_t hi =
+              f32_to_bf16_rne(acc[i][j][4 * g + 2]) | ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * g + 3]) << 16);
+          *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (n + c < N) o[c] = f32_to_bf16_rne(acc[i][j][4 * g + c]);
+        }
+      }
+  }
+}
+
 // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
 template <class T, bool kColScale>
 INTENT_DEVICE void store_dense(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N, f16* __restrict__ y,
@@ -212,4 +341,33 @@ extern "C" int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t 
   W8Args ws{w, w_ld};
   return launch_dense<W8Args, true>((const f16*)x, x_ld, (int)M, (int)N, (int)K, ws, (f16*)y, y_ld,
                                       (const f16*)scales, (hipStream_t)stream, "w8a16_matmul");
+}
+
+extern "C" int intent_fp4_bf16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t* packed,
+                                      int64_t N, int64_t packed_ld, void* y, int64_t y_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "empty K");
+  INTENT_REQUIRE(x && packed && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(x_ld >= K && packed_ld >= K / 2 && y_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(x) && x_ld % 8 == 0 && intent::aligned16(packed) && packed_ld % 16 == 0,
+                 INTENT_ERR_ALIGNMENT, "x and packed must be 16-byte aligned with 16-byte row strides");
+  INTENT_REQUIRE(intent::fits_offset(N, packed_ld) && intent::fits_offset(M, x_ld * 2), INTENT_ERR_UNSUPPORTED,
+                 "fp4_bf16_matmul: operand too large for 31-bit buffer offsets");
+  auto launch = [&](auto tile) -> int {
+    using T = decltype(tile);
+    const int mblocks = (int)((M + T::BM - 1) / T::BM);
+    const int64_t grid = (int64_t)mblocks * ((N + T::BN - 1) / T::BN);
+    INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "fp4_bf16_matmul: grid too large");
+    hipLaunchKernelGGL((fp4_bf16_gemm_kernel<T>), dim3((unsigned)grid), dim3(T::NT_WS), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, x_ld, (int)M, packed, packed_ld, (int)N, (int)K, (uint16_t*)y, y_ld,
+                       mblocks);
+    return intent::launch_status("fp4_bf16_matmul");
+  };
+  if (M > 128) return launch(mp::Tile<256, 192, 2, 2>{});
+  return launch(mp::Tile<128, 128, 2, 2>{});
 }

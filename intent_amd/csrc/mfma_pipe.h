@@ -101,6 +101,14 @@ struct F16Math {
   using Frag = f16x8;
   INTENT_DEVICE static Acc mfma(Frag b, Frag a, Acc c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, c, 0, 0, 0); }
 };
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+struct BF16Math {
+  using Acc = f32x16;
+  using Frag = bf16x8;
+  INTENT_DEVICE static Acc mfma(Frag b, Frag a, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(b, a, c, 0, 0, 0);
+  }
+};
 struct I8Math {
   using Acc = i32x16;
   using Frag = i32x4;

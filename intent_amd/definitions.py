@@ -742,10 +742,40 @@ fp8_e4m3_matmul = _fp8_out_definition("fp8_e4m3_matmul", "f8e4m3fn", 0, "178-195
 fp8_e5m2_matmul = _fp8_out_definition("fp8_e5m2_matmul", "f8e5m2", 1, "198-215")
 
 
+# ---- FP4 (E2M1) weights x bf16 activations ---------------------------------------
+
+def _fp4_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    x, w, y = v["activation"], v["packed_weight"], v["output"]
+    _native.call("intent_fp4_bf16_matmul", _ptr(x), env["M"], env["K"], _ld(x), _ptr(w), env["N"], _ld(w), _ptr(y),
+                 _ld(y), stream)
+    return "intent_fp4_bf16_matmul"
+
+
+def _fp4_check(env: dict) -> None:
+    if env["P"] * 2 != env["K"]:
+        raise ValueError(f"packed_weight.shape[1] ({env['P']}) must be K / 2 ({env['K'] // 2})")
+    if env["K"] % 64:
+        raise NotImplementedError(f"K ({env['K']}) must be a multiple of 64")
+
+
+dequant_bf16_fp4_matmul = KernelDefinition(
+    name="dequant_bf16_fp4_matmul",
+    params=(
+        Param("activation", "bf16", ("M", "K"), leading_stride=True),
+        Param("packed_weight", "u8", ("N", "P"), leading_stride=True),
+        Param("output", "bf16", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_fp4_launch,
+    check=_fp4_check,
+    reference="examples/kernels/contraction/weight_only_int4.py:127-175",
+    doc="output = bf16(activation @ e2m1(packed_weight)^T), f32 accumulation",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
-    deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul,
+    deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul, dequant_bf16_fp4_matmul,
 )

@@ -88,6 +88,10 @@ def lib():
         _lib.orc_f32_to_e5m2.restype = ctypes.c_uint8
         _lib.orc_fp8_gemm.argtypes = [ci, p, i64, i64, p, i64, p, ci]
         _lib.orc_fp8_gemm.restype = None
+        _lib.orc_fp4_decode.argtypes = [p, i64]
+        _lib.orc_fp4_decode.restype = ctypes.c_float
+        _lib.orc_fp4_bf16_matmul.argtypes = [p, i64, i64, p, i64, p, ci]
+        _lib.orc_fp4_bf16_matmul.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -316,6 +320,22 @@ def f32_to_e5m2(values) -> np.ndarray:
 
 def e5m2_to_f32(bits) -> np.ndarray:
     return np.array([lib().orc_e5m2_to_f32(int(v)) for v in np.asarray(bits, np.uint8).reshape(-1)], np.float32)
+
+
+def fp4_decode_row(row) -> np.ndarray:
+    """Decoded E2M1 values of one packed FP4 row (K = 2 * len(row))."""
+    row = _c(row, np.uint8)
+    return np.array([lib().orc_fp4_decode(_ptr(row), k) for k in range(2 * row.shape[0])], np.float32)
+
+
+def fp4_bf16_matmul(x_bits, packed, threads: int = 1) -> np.ndarray:
+    """bf16 bits x [M, K] and packed FP4 [N, K/2] -> bf16 bits [M, N]."""
+    x, packed = _c(x_bits, np.uint16), _c(packed, np.uint8)
+    M, K = x.shape
+    N = packed.shape[0]
+    out = np.empty((M, N), np.uint16)
+    lib().orc_fp4_bf16_matmul(_ptr(x), M, K, _ptr(packed), N, _ptr(out), threads)
+    return out
 
 
 def e4m3fn_to_f32(bits) -> np.ndarray:

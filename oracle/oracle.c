@@ -644,3 +644,42 @@ void orc_fp8_gemm(int format, const uint8_t* a, int64_t M, int64_t K, const uint
     }
   }
 }
+
+/* ---- FP4 (E2M1) weights x bf16 activations ----------------------------------------
+ * dequant_bf16_fp4_matmul (examples/kernels/contraction/weight_only_int4.py:127-175;
+ * CPU baseline experiments/cpu/baselines/pytorch/cpu_runtime.py:117-124): row n holds
+ * big-endian 16-bit words w = (p[2i] << 8) | p[2i+1], each carrying k = 4i .. 4i+3 at
+ * the bf16 bit patterns below; decoded = bf16(f32(bf16 pattern) * 2^126);
+ * out = bf16(sum_k f32(x) * decoded), fma in k order. */
+static float bf16_bits_to_f32(uint16_t b) {
+  const uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+float orc_fp4_decode(const uint8_t* row, int64_t k) {
+  const int64_t pair = (k / 4) * 2;
+  const uint32_t w = ((uint32_t)row[pair] << 8) | row[pair + 1];
+  uint32_t bits;
+  switch (k % 4) {
+    case 0: bits = w & 0x81C0u; break;
+    case 1: bits = (w << 3) & 0x81C0u; break;
+    case 2: bits = (w << 6) & 0x81C0u; break;
+    default: bits = ((w << 1) & 0x8000u) | ((w >> 3) & 0x0180u) | ((w >> 7) & 0x0040u); break;
+  }
+  const float v = bf16_bits_to_f32((uint16_t)bits) * ldexpf(1.0f, 126);
+  return bf16_bits_to_f32(orc_f32_to_bf16(v));
+}
+
+void orc_fp4_bf16_matmul(const uint16_t* x, int64_t M, int64_t K, const uint8_t* packed, int64_t N, uint16_t* out,
+                         int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) acc = fmaf(bf16_bits_to_f32(x[m * K + k]), orc_fp4_decode(packed + n * (K / 2), k), acc);
+      out[m * N + n] = orc_f32_to_bf16(acc);
+    }
+  }
+}

@@ -47,5 +47,8 @@ float orc_e5m2_to_f32(uint8_t v);
 uint8_t orc_f32_to_e5m2(float f);
 void orc_fp8_gemm(int format, const uint8_t* a, int64_t M, int64_t K, const uint8_t* bt, int64_t N, uint8_t* out,
                   int threads);
+float orc_fp4_decode(const uint8_t* row, int64_t k);
+void orc_fp4_bf16_matmul(const uint16_t* x, int64_t M, int64_t K, const uint8_t* packed, int64_t N, uint16_t* out,
+                         int threads);
 
 #endif

@@ -595,3 +595,19 @@ def test_fp8_out_matmul(gpu, threads, fmt, M, K, N):
     dr = torch.from_numpy(ref).view(tdt).double()
     step = 2.0 ** -2 if fmt == "e5m2" else 2.0 ** -3
     assert torch.all((dg - dr).abs() <= step * dr.abs() + 2.0 ** -9)
+
+
+# ---- FP4 (E2M1) weights x bf16 activations --------------------------------------------
+
+@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (17, 256, 40), (4096, 4096, 4096)])
+def test_dequant_bf16_fp4_matmul(gpu, threads, M, K, N):
+    g = torch.Generator().manual_seed(M + K)
+    x = (torch.randn(M, K, generator=g) * 0.125).bfloat16()   # the reference's input scale
+    packed = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
+    out = art(intent.dequant_bf16_fp4_matmul).run(x.cuda(), packed.cuda())
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = oracle.fp4_bf16_matmul(x.view(torch.int16).numpy().view(np.uint16)[rows], packed.numpy(), threads)
+    got = host(out.view(torch.int16)).view(np.uint16)[rows]
+    r64 = torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).double().numpy()
+    g64 = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).double().numpy()
+    assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()

@@ -620,3 +620,36 @@ def test_fp8_gemm_closed_form(fmt, tdt):
     a1[0, 3], b1[1, 3] = 1.5, -2.0
     y = oracle.fp8_gemm(a1.view(torch.uint8).numpy(), b1.view(torch.uint8).numpy(), fmt)
     assert torch.from_numpy(y).view(tdt).float().tolist() == [[0.0, -3.0]]
+
+
+# ---- FP4 (E2M1) x bf16 ---------------------------------------------------------------
+
+def _fp4_reference_decode(packed):
+    # cpu_runtime.py:117-124 restated with torch (the reference's own recipe)
+    p = torch.from_numpy(np.ascontiguousarray(packed))
+    word = (p[:, 0::2].int() << 8) | p[:, 1::2].int()
+    bits = torch.stack((word & 0x81C0, (word << 3) & 0x81C0, (word << 6) & 0x81C0,
+                        ((word << 1) & 0x8000) | ((word >> 3) & 0x0180) | ((word >> 7) & 0x0040)),
+                       dim=-1).flatten(1).to(torch.int16)
+    return (bits.view(torch.bfloat16).float() * (2.0 ** 126)).bfloat16().float().numpy()
+
+
+def test_fp4_decode_matches_reference_recipe():
+    words = np.arange(65536, dtype=np.uint32)  # every 16-bit word once
+    packed = np.stack(((words >> 8) & 255, words & 255), axis=1).astype(np.uint8).reshape(1, -1)
+    ref = _fp4_reference_decode(packed)[0]
+    got = oracle.fp4_decode_row(packed[0])
+    assert np.array_equal(got, ref)
+    # the values are exactly the E2M1 set
+    assert set(np.unique(np.abs(got)).tolist()) == {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0}
+
+
+def test_fp4_bf16_matmul_closed_form():
+    g = torch.Generator().manual_seed(32)
+    M, K, N = 5, 256, 7
+    x = torch.randn(M, K, generator=g).bfloat16()
+    packed = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8).numpy()
+    got = oracle.fp4_bf16_matmul(x.view(torch.int16).numpy().view(np.uint16), packed)
+    ref = x.double().numpy() @ _fp4_reference_decode(packed).astype(np.float64).T
+    dec = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).double().numpy()
+    assert np.max(np.abs(dec - ref)) <= 8e-3 * np.abs(ref).max()
