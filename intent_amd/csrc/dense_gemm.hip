@@ -368,6 +368,8 @@ extern "C" int intent_fp4_bf16_matmul(const void* x, int64_t M, int64_t K, int64
                        mblocks);
     return intent::launch_status("fp4_bf16_matmul");
   };
-  if (M > 128) return launch(mp::Tile<256, 192, 2, 2>{});
+  // 256 x 128 tiles (consumers of 128 x 64) once M fills them: at 4096 x 4096
+  // that is 512 workgroups, two full rounds of 256 CUs (256 x 192 gives 1.38).
+  if (M > 128) return launch(mp::Tile<256, 128, 2, 2>{});
   return launch(mp::Tile<128, 128, 2, 2>{});
 }
