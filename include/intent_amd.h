@@ -389,6 +389,19 @@ int intent_fp4_bf16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld,
                            const uint8_t* packed, int64_t N, int64_t packed_ld,
                            void* y, int64_t y_ld, void* stream);
 
+/* Repacks the reference's own W4 layout for the W4A16 entries. Used by
+ * weight_only_int4_matmul (examples/kernels/contraction/weight_only_int4.py:18-51):
+ * packed int32 [P = K/8, N] (eight signed nibbles of consecutive k per word,
+ * nibble k % 8 at bits 4(k % 8); packed_ld elements) and f16 scales [G, N]
+ * (scales_ld elements) become q_out [N, K/2] bytes (low nibble = even k, each
+ * nibble with its top bit flipped), s_out f16 [N, G] and z_out [N, G] = 8, so
+ * that (q - z) * s equals the reference's signed nibble times its scale.
+ */
+int intent_w4_sym_repack(const int32_t* packed, int64_t P, int64_t N, int64_t packed_ld,
+                         const void* scales, int64_t G, int64_t scales_ld,
+                         uint8_t* q_out, int64_t q_ld, void* s_out, uint8_t* z_out, int64_t sz_ld,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

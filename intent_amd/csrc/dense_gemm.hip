@@ -174,6 +174,33 @@ __global__ __launch_bounds__(T::NT_WS, 1) void fp4_bf16_gemm_kernel(const uint16
   }
 }
 
+// ---- the reference's own W4 layout -> the asymmetric nibble layout --------------
+// weight_only_int4_matmul (weight_only_int4.py:18-51) packs eight signed nibbles
+// of consecutive k into an int32 of [K/8, N] (nibble k % 8 at bits 4(k % 8)),
+// with f16 scales [K/64, N]. Flipping each nibble's top bit gives u = n ^ 8 with
+// u - 8 = the two's-complement value, so (u - z) * s with z = 8 is the same f16
+// product; the int32's bytes already hold nibble pairs low = even k. Repacking
+// is a transpose of the int32 words (xor 0x88888888) and of the scales.
+template <class E, uint32_t kXor>
+__global__ __launch_bounds__(256) void transpose32_kernel(const E* __restrict__ src, int R, int C, int64_t sld,
+                                                          E* __restrict__ dst, int64_t dld) {
+  __shared__ E t[32][33];
+  const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+  for (int i = ty; i < 32; i += 8)
+    if (r0 + i < R && c0 + tx < C) t[i][tx] = src[(int64_t)(r0 + i) * sld + c0 + tx];
+  __syncthreads();
+#pragma unroll
+  for (int i = ty; i < 32; i += 8)
+    if (c0 + i < C && r0 + tx < R) dst[(int64_t)(c0 + i) * dld + r0 + tx] = (E)(t[tx][i] ^ (E)kXor);
+}
+
+__global__ void fill_u8_kernel(uint8_t* __restrict__ z, int rows, int cols, int64_t ld, uint8_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < (int64_t)rows * cols) z[(i / cols) * ld + i % cols] = v;
+}
+
 // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
 template <class T, bool kColScale>
 INTENT_DEVICE void store_dense(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N, f16* __restrict__ y,
@@ -372,4 +399,34 @@ extern "C" int intent_fp4_bf16_matmul(const void* x, int64_t M, int64_t K, int64
   // that is 512 workgroups, two full rounds of 256 CUs (256 x 192 gives 1.38).
   if (M > 128) return launch(mp::Tile<256, 128, 2, 2>{});
   return launch(mp::Tile<128, 128, 2, 2>{});
+}
+
+extern "C" int intent_w4_sym_repack(const int32_t* packed, int64_t P, int64_t N, int64_t packed_ld,
+                                    const void* scales, int64_t G, int64_t scales_ld, uint8_t* q_out, int64_t q_ld,
+                                    void* s_out, uint8_t* z_out, int64_t sz_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(P >= 0 && N >= 0 && G >= 0 && P <= INT32_MAX && N <= INT32_MAX && G <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  if (N == 0) return INTENT_OK;
+  INTENT_REQUIRE(packed_ld >= N && scales_ld >= N && q_ld >= 4 * P && sz_ld >= G, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE((P == 0 || (packed && q_out)) && (G == 0 || (scales && s_out && z_out)), INTENT_ERR_INVALID_ARGUMENT,
+                 "null pointer argument");
+  INTENT_REQUIRE(q_ld % 4 == 0 && intent::aligned4(q_out), INTENT_ERR_ALIGNMENT, "q_out rows must be 4-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (P > 0) {
+    hipLaunchKernelGGL((transpose32_kernel<uint32_t, 0x88888888u>), dim3((unsigned)((N + 31) / 32), (unsigned)((P + 31) / 32)),
+                       dim3(256), 0, st, (const uint32_t*)packed, (int)P, (int)N, packed_ld, (uint32_t*)q_out, q_ld / 4);
+    int rc = intent::launch_status("w4_sym_repack");
+    if (rc != INTENT_OK) return rc;
+  }
+  if (G > 0) {
+    hipLaunchKernelGGL((transpose32_kernel<uint16_t, 0u>), dim3((unsigned)((N + 31) / 32), (unsigned)((G + 31) / 32)),
+                       dim3(256), 0, st, (const uint16_t*)scales, (int)G, (int)N, scales_ld, (uint16_t*)s_out, sz_ld);
+    int rc = intent::launch_status("w4_sym_repack");
+    if (rc != INTENT_OK) return rc;
+    hipLaunchKernelGGL(fill_u8_kernel, dim3((unsigned)((N * G + 255) / 256)), dim3(256), 0, st, z_out, (int)N, (int)G,
+                       sz_ld, (uint8_t)8);
+  }
+  return intent::launch_status("w4_sym_repack");
 }

@@ -772,8 +772,63 @@ dequant_bf16_fp4_matmul = KernelDefinition(
 )
 
 
+# ---- the reference's own weight_only_int4_matmul layout ---------------------------
+
+W4_SYM_GROUP = 64  # weight_only_int4.py:9 (GROUP_SIZE)
+
+
+def _w4sym_layout(env: dict) -> tuple:
+    N, K, G = env["N"], env["K"], env["G"]
+    q = 0
+    s = -(-(N * K // 2) // 256) * 256
+    z = s + -(-(N * G * 2) // 256) * 256
+    return q, s, z, z + N * G
+
+
+def _w4sym_workspace(env: dict) -> int:
+    return _w4sym_layout(env)[3]
+
+
+def _w4sym_check(env: dict) -> None:
+    if env["P"] * 8 != env["K"]:
+        raise ValueError(f"packed_weight.shape[0] ({env['P']}) must be K / 8 ({env['K'] // 8})")
+    if env["G"] * W4_SYM_GROUP != env["K"]:
+        raise ValueError(f"scales.shape[0] ({env['G']}) must be K / {W4_SYM_GROUP} ({env['K'] // W4_SYM_GROUP})")
+    if env["K"] % 64:
+        raise NotImplementedError(f"K ({env['K']}) must be a multiple of 64")
+
+
+def _w4sym_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    x, packed, scales, y = v["activation"], v["packed_weight"], v["scales"], v["output"]
+    M, K, N, G = env["M"], env["K"], env["N"], env["G"]
+    oq, os_, oz, _ = _w4sym_layout(env)
+    base = workspace.data_ptr()
+    _native.call("intent_w4_sym_repack", _ptr(packed), env["P"], N, packed.stride(0), _ptr(scales), G,
+                 scales.stride(0), base + oq, K // 2, base + os_, base + oz, G, stream)
+    entry = "intent_w4a16_gemv" if M <= 16 else "intent_w4a16_gemm"
+    _native.call(entry, _ptr(x), M, K, _ld(x), base + oq, N, K // 2, base + os_, base + oz, G, W4_SYM_GROUP, _ptr(y),
+                 _ld(y), stream)
+    return entry
+
+
+weight_only_int4_matmul = KernelDefinition(
+    name="weight_only_int4_matmul",
+    params=(
+        Param("activation", "f16", ("M", "K"), leading_stride=True),
+        Param("packed_weight", "i32", ("P", "N"), leading_stride=True),
+        Param("scales", "f16", ("G", "N"), leading_stride=True),
+        Param("output", "f16", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_w4sym_launch,
+    check=_w4sym_check,
+    workspace=_w4sym_workspace,
+    reference="examples/kernels/contraction/weight_only_int4.py:18-51",
+    doc="the reference's symmetric signed-nibble W4 (int32 [K/8, N], f16 scales [K/64, N]) on the W4A16 kernels",
+)
+
+
 ALL_DEFINITIONS = (
-    weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
+    weight_only_int4_matmul, weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,

@@ -92,6 +92,8 @@ def lib():
         _lib.orc_fp4_decode.restype = ctypes.c_float
         _lib.orc_fp4_bf16_matmul.argtypes = [p, i64, i64, p, i64, p, ci]
         _lib.orc_fp4_bf16_matmul.restype = None
+        _lib.orc_w4_sym.argtypes = [p, i64, i64, p, p, i64, p, ci]
+        _lib.orc_w4_sym.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -336,6 +338,17 @@ def fp4_bf16_matmul(x_bits, packed, threads: int = 1) -> np.ndarray:
     out = np.empty((M, N), np.uint16)
     lib().orc_fp4_bf16_matmul(_ptr(x), M, K, _ptr(packed), N, _ptr(out), threads)
     return out
+
+
+def w4_sym(x, packed, scales, threads: int = 1) -> np.ndarray:
+    """The reference's weight_only_int4_matmul: f16 x [M, K], int32 packed [K/8, N],
+    f16 scales [K/64, N] -> f16 [M, N]."""
+    x, packed, scales = _c(x, np.float16), _c(packed, np.int32), _c(scales, np.float16)
+    M, K = x.shape
+    N = packed.shape[1]
+    y = np.empty((M, N), np.float16)
+    lib().orc_w4_sym(_ptr(x), M, K, _ptr(packed), _ptr(scales), N, _ptr(y), threads)
+    return y
 
 
 def e4m3fn_to_f32(bits) -> np.ndarray:

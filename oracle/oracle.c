@@ -683,3 +683,27 @@ void orc_fp4_bf16_matmul(const uint16_t* x, int64_t M, int64_t K, const uint8_t*
     }
   }
 }
+
+/* ---- the reference's own W4 layout -------------------------------------------------
+ * weight_only_int4_matmul (examples/kernels/contraction/weight_only_int4.py:18-51;
+ * CPU baseline experiments/cpu/baselines/pytorch/cpu_runtime.py:97-102): packed int32
+ * [K/8, N], nibble k % 8 of word [k/8, n] at bits 4(k % 8), two's complement; scales
+ * f16 [K/64, N]; dequantized = f32(signed) * f32(scale) (exact); y = f16(sum_k
+ * f32(x) * dequantized), fma in k order. */
+void orc_w4_sym(const uint16_t* x, int64_t M, int64_t K, const int32_t* packed, const uint16_t* scales, int64_t N,
+                uint16_t* y, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) {
+        const uint32_t word = (uint32_t)packed[(k / 8) * N + n];
+        const int nib = (int)((word >> (4 * (k % 8))) & 15u);
+        const int sgn = nib - ((nib & 8) << 1);
+        const float w = (float)sgn * orc_f16_to_f32(scales[(k / 64) * N + n]);
+        acc = fmaf(orc_f16_to_f32(x[m * K + k]), w, acc);
+      }
+      y[m * N + n] = orc_f32_to_f16(acc);
+    }
+  }
+}

@@ -50,5 +50,7 @@ void orc_fp8_gemm(int format, const uint8_t* a, int64_t M, int64_t K, const uint
 float orc_fp4_decode(const uint8_t* row, int64_t k);
 void orc_fp4_bf16_matmul(const uint16_t* x, int64_t M, int64_t K, const uint8_t* packed, int64_t N, uint16_t* out,
                          int threads);
+void orc_w4_sym(const uint16_t* x, int64_t M, int64_t K, const int32_t* packed, const uint16_t* scales, int64_t N,
+                uint16_t* y, int threads);
 
 #endif

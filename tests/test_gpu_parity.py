@@ -611,3 +611,18 @@ def test_dequant_bf16_fp4_matmul(gpu, threads, M, K, N):
     r64 = torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).double().numpy()
     g64 = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).double().numpy()
     assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()
+
+
+# ---- the reference's own weight_only_int4_matmul layout --------------------------------
+
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 4096), (1, 2048, 4096), (3, 256, 100), (40, 128, 33)])
+def test_weight_only_int4_matmul_reference_layout(gpu, threads, M, K, N):
+    # (512, 2048, 4096) is the reference's own example size (weight_only_int4.py:6-8)
+    rng = np.random.default_rng(M + N)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    packed = rng.integers(-2**31, 2**31, (K // 8, N), dtype=np.int64).astype(np.int32)
+    scales = rng.uniform(0.005, 0.02, (K // 64, N)).astype(np.float16)
+    y = art(intent.weight_only_int4_matmul).run(dev(x), dev(packed), dev(scales))
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = oracle.w4_sym(x[rows], packed, scales, threads)
+    assert_close_rms(host(y)[rows], ref.astype(np.float32), what=f"w4 sym {M}x{K}x{N}")

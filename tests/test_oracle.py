@@ -653,3 +653,40 @@ def test_fp4_bf16_matmul_closed_form():
     ref = x.double().numpy() @ _fp4_reference_decode(packed).astype(np.float64).T
     dec = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).double().numpy()
     assert np.max(np.abs(dec - ref)) <= 8e-3 * np.abs(ref).max()
+
+
+# ---- the reference's own weight_only_int4_matmul layout --------------------------------
+
+def _w4_sym_case(seed, M, K, N):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    packed = rng.integers(-2**31, 2**31, (K // 8, N), dtype=np.int64).astype(np.int32)
+    scales = rng.uniform(0.005, 0.02, (K // 64, N)).astype(np.float16)
+    return x, packed, scales
+
+
+def test_w4_sym_matches_reference_formula():
+    # cpu_runtime.py:97-102 restated with torch
+    x, packed, scales = _w4_sym_case(41, 4, 256, 9)
+    got = oracle.w4_sym(x, packed, scales).astype(np.float64)
+    p = torch.from_numpy(packed)
+    positions = torch.arange(x.shape[1])
+    nibble = (p[positions // 8] >> ((positions % 8) * 4)[:, None]) & 15
+    signed = nibble - ((nibble & 8) << 1)
+    deq = signed.float() * torch.from_numpy(scales).float().repeat_interleave(64, dim=0)
+    ref = (torch.from_numpy(x).float() @ deq).half().double().numpy()
+    assert np.max(np.abs(got - ref)) <= 2e-3 * np.abs(ref).max()
+
+
+def test_w4_sym_known_answers():
+    # one nibble per position: word 0x8000000F at [0, n] puts 15 -> -1 at k = 0 and
+    # 8 -> -8 at k = 7; x one-hot at k = 7 picks -8 * scale
+    K, N = 64, 2
+    packed = np.zeros((K // 8, N), np.int32)
+    packed[0, 1] = np.int32(-0x7FFFFFF1)  # bits 0x8000000F
+    scales = np.full((1, N), 0.5, np.float16)
+    x = np.zeros((2, K), np.float16)
+    x[0, 7] = 1.0
+    x[1, 0] = 2.0
+    y = oracle.w4_sym(x, packed, scales)
+    assert y.tolist() == [[0.0, -4.0], [0.0, -1.0]]
