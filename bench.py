@@ -268,6 +268,34 @@ def bench_fp4(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": n}
 
 
+def bench_quantized_gemm(steps: int, warmup: int) -> dict:
+    """The reference's quantized_gemm case (experiments/cpu/providers/mojo/contraction.py:177-186):
+    f16 [4096, 4096] x [4096, 14336] with bias, ReLU, residual, per-column scale, int8 out;
+    the timed operator includes the transpose of the [K, N] right operand."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    M, K, N = 4096, 4096, 14336
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a = torch.randn((M, K), device="cuda", generator=g).half() / 64.0
+    b = torch.randn((K, N), device="cuda", generator=g).half()
+    bias = torch.randn((N,), device="cuda", generator=g) * 0.25
+    residual = (torch.randn((M, N), device="cuda", generator=g) * 0.25).half()
+    scale = torch.linspace(1.0 / 48.0, 1.0 / 24.0, N, device="cuda")
+    work = inputs.Workload(f"quantized_gemm M{M} K{K} N{N}", 2 * M * N * K,
+                           M * K * 2 + K * N * 2 + N * 8 + M * N * 2 + M * N)
+    art = intent.compile(intent.quantized_gemm, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes, minimum=2)
+    sets = [(a.clone(), b.clone(), bias, residual.clone(), scale) for _ in range(n)]
+    calls = [art.prepare(*s) for s in sets]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls, sets
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
 def bench_mxfp8(steps: int, warmup: int) -> dict:
     """The reference's mxfp8_gemm case (experiments/cpu/providers/mojo/contraction.py:285-305):
     M=4096, K=4096, N=14336, E4M3FN with E8M0 scales per 32, rhs given as the [KB, 32, N]
@@ -430,6 +458,9 @@ def main() -> int:
         log("[bench] fp4 x bf16 M=N=K=4096")
         r = bench_fp4(steps, warm)
         extra["fp4_bf16_4096"] = _flop_entry(r, F16_PEAK_TFLOPS, "TFLOP/s")
+        log("[bench] quantized_gemm M=4096 K=4096 N=14336")
+        r = bench_quantized_gemm(steps, warm)
+        extra["quantized_gemm_m4096_n14336"] = _flop_entry(r, F16_PEAK_TFLOPS, "TFLOP/s")
         log("[bench] q4_k projection N=K=4096")
         r = bench_q4k(args.steps, args.warmup)
         extra["q4k_projection_n4096"] = _hbm_entry(r)

@@ -402,6 +402,27 @@ int intent_w4_sym_repack(const int32_t* packed, int64_t P, int64_t N, int64_t pa
                          uint8_t* q_out, int64_t q_ld, void* s_out, uint8_t* z_out, int64_t sz_ld,
                          void* stream);
 
+/* f16 matrix transpose: dst[c * dst_ld + r] = src[r * src_ld + c] (elements).
+ * Plumbing for quantized_gemm, whose right operand the reference passes as
+ * [K, N]. Replaces no reference function.
+ */
+int intent_f16_transpose(const void* src, int64_t rows, int64_t cols, int64_t src_ld,
+                         void* dst, int64_t dst_ld, void* stream);
+
+/* f16 GEMM with the fused int8 epilogue of quantized_gemm
+ * (examples/kernels/contraction/gemm.py:83-106; CPU baseline
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:91-94):
+ *   out = i8(trunc(clamp((relu(acc + bias[n]) + residual[m, n]) / output_scale[n],
+ *                        -128, 127)))
+ * a: f16 [M, K]; bt: the right operand as f16 [N, K] rows (use
+ * intent_f16_transpose for a [K, N] operand); bias, output_scale: f32 [N];
+ * residual: f16 [M, N]; out: int8 [M, N]. K % 64 == 0.
+ */
+int intent_quantized_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld,
+                          const void* bt, int64_t N, int64_t bt_ld,
+                          const float* bias, const void* residual, int64_t residual_ld,
+                          const float* output_scale, int8_t* out, int64_t out_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

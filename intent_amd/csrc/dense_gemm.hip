@@ -201,6 +201,61 @@ __global__ void fill_u8_kernel(uint8_t* __restrict__ z, int rows, int cols, int6
   if (i < (int64_t)rows * cols) z[(i / cols) * ld + i % cols] = v;
 }
 
+// ---- quantized_gemm (gemm.py:83-106): f16 GEMM with a fused int8 epilogue ---------
+//   out = i8(trunc(clamp((relu(acc + bias[n]) + f32(residual)) / output_scale[n],
+//                        -128, 127)))
+// (CPU baseline cpu_runtime.py:91-94; relu keeps NaN, the division is IEEE and
+// the float -> integer cast truncates toward zero). Both operands are f16 rows
+// with K contiguous (the right operand transposed beforehand), staged through
+// VGPRs into the swizzled LDS stages of mfma_pipe.h.
+template <class T>
+__global__ __launch_bounds__(T::NT, 1) void quantized_gemm_kernel(
+    const f16* __restrict__ a, int64_t lda, int M, const f16* __restrict__ bt, int64_t ldb, int N, int K,
+    const float* __restrict__ bias, const f16* __restrict__ residual, int64_t ldr, const float* __restrict__ oscale,
+    int8_t* __restrict__ out, int64_t ldo, int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  const int wave = T::wave();
+  mp::RegRowsOperand<T::BN, mp::DenseRows, false, T::NW> bop;
+  bop.init(mp::DenseRows{bt, ldb * 2, N}, n0, wave);
+  mp::RegRowsOperand<T::BM, mp::DenseRows, false, T::NW> aop;
+  aop.init(mp::DenseRows{a, lda * 2, M}, m0, wave);
+  f32x16 acc[T::TI][T::TJ];
+  mp::mainloop<T, mp::F16Math>(aop, bop, K / 64, buf0, buf1, acc);
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        int8_t* o = out + (int64_t)m * ldo + n;
+        uint32_t packed = 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (n + c >= N) continue;
+          float v = __fadd_rn(acc[i][j][4 * g + c], bias[n + c]);
+          v = v < 0.f ? 0.f : v;
+          v = __fadd_rn(v, (float)residual[(int64_t)m * ldr + n + c]);
+          v = __fdiv_rn(v, oscale[n + c]);
+          v = fminf(fmaxf(v, -128.f), 127.f);
+          packed |= ((uint32_t)(int32_t)v & 255u) << (8 * c);
+        }
+        if (n + 3 < N && ((((uintptr_t)o) & 3) == 0)) {
+          *reinterpret_cast<uint32_t*>(o) = packed;
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (n + c < N) o[c] = (int8_t)((packed >> (8 * c)) & 255u);
+        }
+      }
+  }
+}
+
 // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
 template <class T, bool kColScale>
 INTENT_DEVICE void store_dense(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N, f16* __restrict__ y,
@@ -429,4 +484,45 @@ extern "C" int intent_w4_sym_repack(const int32_t* packed, int64_t P, int64_t N,
                        sz_ld, (uint8_t)8);
   }
   return intent::launch_status("w4_sym_repack");
+}
+
+extern "C" int intent_f16_transpose(const void* src, int64_t rows, int64_t cols, int64_t src_ld, void* dst,
+                                    int64_t dst_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(rows >= 0 && cols >= 0 && rows <= INT32_MAX && cols <= INT32_MAX, INTENT_ERR_INVALID_ARGUMENT,
+                 "bad extents");
+  if (rows == 0 || cols == 0) return INTENT_OK;
+  INTENT_REQUIRE(src && dst, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(src_ld >= cols && dst_ld >= rows, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE((rows + 31) / 32 < 65536, INTENT_ERR_UNSUPPORTED, "f16_transpose: grid too large");
+  hipLaunchKernelGGL((transpose32_kernel<uint16_t, 0u>), dim3((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32)),
+                     dim3(256), 0, (hipStream_t)stream, (const uint16_t*)src, (int)rows, (int)cols, src_ld,
+                     (uint16_t*)dst, dst_ld);
+  return intent::launch_status("f16_transpose");
+}
+
+extern "C" int intent_quantized_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* bt, int64_t N,
+                                     int64_t bt_ld, const float* bias, const void* residual, int64_t residual_ld,
+                                     const float* output_scale, int8_t* out, int64_t out_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(a && bt && bias && residual && output_scale && out, INTENT_ERR_INVALID_ARGUMENT,
+                 "null pointer argument");
+  INTENT_REQUIRE(a_ld >= K && bt_ld >= K && residual_ld >= N && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(bt) && a_ld % 8 == 0 && bt_ld % 8 == 0,
+                 INTENT_ERR_ALIGNMENT, "operands must be 16-byte aligned with 16-byte row strides");
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld * 2) && intent::fits_offset(N, bt_ld * 2), INTENT_ERR_UNSUPPORTED,
+                 "quantized_gemm: operand too large for 31-bit buffer offsets");
+  using T = mp::Tile<256, 256, 2, 2>;  // four waves of 128 x 128, accumulators in AGPRs
+  const int mblocks = (int)((M + T::BM - 1) / T::BM);
+  const int64_t grid = (int64_t)mblocks * ((N + T::BN - 1) / T::BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "quantized_gemm: grid too large");
+  hipLaunchKernelGGL((quantized_gemm_kernel<T>), dim3((unsigned)grid), dim3(T::NT), 0, (hipStream_t)stream,
+                     (const f16*)a, a_ld, (int)M, (const f16*)bt, bt_ld, (int)N, (int)K, bias, (const f16*)residual,
+                     residual_ld, output_scale, out, out_ld, mblocks);
+  return intent::launch_status("quantized_gemm");
 }

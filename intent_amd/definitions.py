@@ -827,10 +827,49 @@ weight_only_int4_matmul = KernelDefinition(
 )
 
 
+# ---- quantized_gemm: f16 GEMM with the fused int8 epilogue -------------------------
+
+def _qgemm_workspace(env: dict) -> int:
+    return env["K"] * env["N"] * 2
+
+
+def _qgemm_check(env: dict) -> None:
+    if env["K"] % 64:
+        raise NotImplementedError(f"K ({env['K']}) must be a multiple of 64")
+
+
+def _qgemm_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    a, b, out = v["a"], v["b"], v["output"]
+    M, K, N = env["M"], env["K"], env["N"]
+    bt = workspace.data_ptr()
+    _native.call("intent_f16_transpose", _ptr(b), K, N, b.stride(0), bt, K, stream)
+    _native.call("intent_quantized_gemm", _ptr(a), M, K, _ld(a), bt, N, K, _ptr(v["bias"]), _ptr(v["residual"]),
+                 _ld(v["residual"]), _ptr(v["output_scale"]), _ptr(out), _ld(out), stream)
+    return "intent_quantized_gemm"
+
+
+quantized_gemm = KernelDefinition(
+    name="quantized_gemm",
+    params=(
+        Param("a", "f16", ("M", "K"), leading_stride=True),
+        Param("b", "f16", ("K", "N"), leading_stride=True),
+        Param("bias", "f32", ("N",)),
+        Param("residual", "f16", ("M", "N"), leading_stride=True),
+        Param("output_scale", "f32", ("N",)),
+        Param("output", "i8", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_qgemm_launch,
+    check=_qgemm_check,
+    workspace=_qgemm_workspace,
+    reference="examples/kernels/contraction/gemm.py:83-106",
+    doc="output = i8(clamp((relu(a @ b + bias) + residual) / output_scale, -128, 127))",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_matmul, weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
-    deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul, dequant_bf16_fp4_matmul,
+    deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul, dequant_bf16_fp4_matmul, quantized_gemm,
 )

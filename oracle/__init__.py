@@ -94,6 +94,8 @@ def lib():
         _lib.orc_fp4_bf16_matmul.restype = None
         _lib.orc_w4_sym.argtypes = [p, i64, i64, p, p, i64, p, ci]
         _lib.orc_w4_sym.restype = None
+        _lib.orc_quantized_gemm.argtypes = [p, i64, i64, p, i64, p, p, p, p, ci]
+        _lib.orc_quantized_gemm.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -349,6 +351,17 @@ def w4_sym(x, packed, scales, threads: int = 1) -> np.ndarray:
     y = np.empty((M, N), np.float16)
     lib().orc_w4_sym(_ptr(x), M, K, _ptr(packed), _ptr(scales), N, _ptr(y), threads)
     return y
+
+
+def quantized_gemm(a, b, bias, residual, output_scale, threads: int = 1) -> np.ndarray:
+    """f16 a [M, K], b [K, N], f32 bias [N], f16 residual [M, N], f32 scale [N] -> int8 [M, N]."""
+    a, b, r = _c(a, np.float16), _c(b, np.float16), _c(residual, np.float16)
+    bias, sc = _c(bias, np.float32), _c(output_scale, np.float32)
+    M, K = a.shape
+    N = b.shape[1]
+    out = np.empty((M, N), np.int8)
+    lib().orc_quantized_gemm(_ptr(a), M, K, _ptr(b), N, _ptr(bias), _ptr(r), _ptr(sc), _ptr(out), threads)
+    return out
 
 
 def e4m3fn_to_f32(bits) -> np.ndarray:

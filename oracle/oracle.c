@@ -707,3 +707,25 @@ void orc_w4_sym(const uint16_t* x, int64_t M, int64_t K, const int32_t* packed, 
     }
   }
 }
+
+/* ---- quantized_gemm -------------------------------------------------------------
+ * examples/kernels/contraction/gemm.py:83-106; CPU baseline
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:91-94: acc = f32 contraction of
+ * f16 a [M, K] and b [K, N] (fma in k order); v = relu(acc + bias[n]) + f32(residual);
+ * out = i8(trunc(clamp(v / output_scale[n], -128, 127))). */
+void orc_quantized_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t* b, int64_t N, const float* bias,
+                        const uint16_t* residual, const float* oscale, int8_t* out, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) acc = fmaf(orc_f16_to_f32(a[m * K + k]), orc_f16_to_f32(b[k * N + n]), acc);
+      float v = acc + bias[n];
+      v = v < 0.0f ? 0.0f : v;
+      v = v + orc_f16_to_f32(residual[m * N + n]);
+      v = v / oscale[n];
+      v = fminf(fmaxf(v, -128.0f), 127.0f);
+      out[m * N + n] = (int8_t)(int32_t)v;
+    }
+  }
+}

@@ -52,5 +52,7 @@ void orc_fp4_bf16_matmul(const uint16_t* x, int64_t M, int64_t K, const uint8_t*
                          int threads);
 void orc_w4_sym(const uint16_t* x, int64_t M, int64_t K, const int32_t* packed, const uint16_t* scales, int64_t N,
                 uint16_t* y, int threads);
+void orc_quantized_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t* b, int64_t N, const float* bias,
+                        const uint16_t* residual, const float* oscale, int8_t* out, int threads);
 
 #endif

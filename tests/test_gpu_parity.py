@@ -626,3 +626,24 @@ def test_weight_only_int4_matmul_reference_layout(gpu, threads, M, K, N):
     rows = np.r_[0:min(M, 8), max(0, M - 8):M]
     ref = oracle.w4_sym(x[rows], packed, scales, threads)
     assert_close_rms(host(y)[rows], ref.astype(np.float32), what=f"w4 sym {M}x{K}x{N}")
+
+
+# ---- quantized_gemm -------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (1, 64, 1), (4096, 4096, 14336)])
+def test_quantized_gemm(gpu, threads, M, K, N):
+    # the reference's input construction (experiments/cpu/providers/mojo/contraction.py:177-186)
+    g = torch.Generator().manual_seed(M + N)
+    a = torch.randn((M, K), generator=g).half() / (K ** 0.5)
+    b = torch.randn((K, N), generator=g).half()
+    bias = torch.randn((N,), generator=g) * 0.25
+    residual = (torch.randn((M, N), generator=g) * 0.25).half()
+    scale = torch.linspace(1.0 / 48.0, 1.0 / 24.0, N)
+    out = art(intent.quantized_gemm).run(a.cuda(), b.cuda(), bias.cuda(), residual.cuda(), scale.cuda())
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = oracle.quantized_gemm(a.numpy()[rows], b.numpy(), bias.numpy(), residual.numpy()[rows], scale.numpy(),
+                                threads)
+    got = host(out)[rows]
+    # the reference's own gate is IntegerTolerance(max_abs=2) (contraction.py:183-186)
+    assert np.max(np.abs(got.astype(np.int32) - ref.astype(np.int32))) <= 2
+    assert np.mean(got == ref) >= 0.99

@@ -690,3 +690,38 @@ def test_w4_sym_known_answers():
     x[1, 0] = 2.0
     y = oracle.w4_sym(x, packed, scales)
     assert y.tolist() == [[0.0, -4.0], [0.0, -1.0]]
+
+
+# ---- quantized_gemm ---------------------------------------------------------------------
+
+def test_quantized_gemm_matches_reference_formula():
+    # cpu_runtime.py:91-94 restated with torch, on the reference's input construction
+    # (experiments/cpu/providers/mojo/contraction.py:177-186) at a small size
+    g = torch.Generator().manual_seed(51)
+    M, K, N = 6, 128, 40
+    a = torch.randn((M, K), generator=g).half() / (K ** 0.5)
+    b = torch.randn((K, N), generator=g).half()
+    bias = torch.randn((N,), generator=g) * 0.25
+    residual = (torch.randn((M, N), generator=g) * 0.25).half()
+    scale = torch.linspace(1.0 / 48.0, 1.0 / 24.0, N)
+    got = oracle.quantized_gemm(a.numpy(), b.numpy(), bias.numpy(), residual.numpy(), scale.numpy())
+    acc = a.float() @ b.float()
+    ref = ((torch.relu(acc + bias) + residual.float()) / scale).clamp(-128.0, 127.0).to(torch.int8).numpy()
+    # the f32 sum in another order can move a value across an integer boundary
+    assert np.max(np.abs(got.astype(np.int32) - ref.astype(np.int32))) <= 1
+    assert np.mean(got == ref) >= 0.95
+
+
+def test_quantized_gemm_known_answers():
+    # relu, residual, division, clamp and truncation toward zero
+    K, N = 64, 5
+    a = np.zeros((1, K), np.float16)
+    a[0, 0] = 1.0
+    b = np.zeros((K, N), np.float16)
+    b[0, :] = [2.0, -3.0, 1000.0, -1000.0, 1.5]
+    bias = np.array([0.5, 0.0, 0.0, 0.0, 0.0], np.float32)
+    residual = np.array([[0.25, 0.5, 0.0, -2.0, -3.0]], np.float16)
+    scale = np.array([1.0, 0.25, 1.0, 1.0, 1.0], np.float32)
+    got = oracle.quantized_gemm(a, b, bias, residual, scale)
+    # 2.75 -> 2; relu(-3)+0.5 = 0.5, /0.25 = 2; 1000 -> 127; relu(-1000)-2 = -2; 1.5-3 = -1.5 -> -1
+    assert got.tolist() == [[2, 2, 127, -2, -1]]
