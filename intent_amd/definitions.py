@@ -213,6 +213,31 @@ gemm_i8_nt = KernelDefinition(
 )
 
 
+def _gemm_i8_kn_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    a, b, bias, c = v["a"], v["b"], v["bias"], v["c"]
+    M, K, N = env["M"], env["K"], env["N"]
+    bt = workspace.data_ptr()  # b [K, N] -> [N, K] rows
+    _native.call("intent_fp8_transpose", _ptr(b), K, N, b.stride(0), bt, -(-K // 16) * 16, stream)
+    _native.call("intent_i8_gemm_i32", _ptr(a), M, K, _ld(a), bt, N, -(-K // 16) * 16, _ptr(bias), _ptr(c), _ld(c),
+                 stream)
+    return "intent_i8_gemm_i32"
+
+
+gemm_i8 = KernelDefinition(
+    name="gemm_i8",
+    params=(
+        Param("a", "i8", ("M", "K"), leading_stride=True),
+        Param("b", "i8", ("K", "N"), leading_stride=True),
+        Param("bias", "i32", ("N",)),
+        Param("c", "i32", ("M", "N"), OUT, leading_stride=True),
+    ),
+    launch=_gemm_i8_kn_launch,
+    workspace=lambda env: env["N"] * (-(-env["K"] // 16) * 16),
+    reference="examples/kernels/contraction/gemm.py:29-39",
+    doc="c = a @ b + bias in int32 (modulo 2^32); b [K, N] is transposed into the workspace first",
+)
+
+
 # ---- MoE --------------------------------------------------------------------------
 
 def _route_launch(v: dict, env: dict, stream: int, workspace) -> str:
@@ -868,6 +893,7 @@ quantized_gemm = KernelDefinition(
 
 ALL_DEFINITIONS = (
     weight_only_int4_matmul, weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
+    gemm_i8,
     moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,

@@ -647,3 +647,15 @@ def test_quantized_gemm(gpu, threads, M, K, N):
     # the reference's own gate is IntegerTolerance(max_abs=2) (contraction.py:183-186)
     assert np.max(np.abs(got.astype(np.int32) - ref.astype(np.int32))) <= 2
     assert np.mean(got == ref) >= 0.99
+
+
+@pytest.mark.parametrize("M,K,N", [(100, 192, 77), (129, 640, 257), (4000, 192, 4100)])
+def test_gemm_i8_reference_layout(gpu, threads, M, K, N):
+    # gemm.py:29-39 with b as [K, N], exact int32 against the oracle
+    rng = np.random.default_rng(M + K)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    b = rng.integers(-128, 128, (K, N), dtype=np.int8)
+    bias = rng.integers(-2**31, 2**31 - 1, N, dtype=np.int64).astype(np.int32)
+    c = art(intent.gemm_i8).run(dev(a), dev(b), dev(bias))
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    assert np.array_equal(host(c)[rows], oracle.i8_gemm_i32(a[rows], np.ascontiguousarray(b.T), bias, threads))
