@@ -423,6 +423,31 @@ int intent_quantized_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld,
                           const float* bias, const void* residual, int64_t residual_ld,
                           const float* output_scale, int8_t* out, int64_t out_ld, void* stream);
 
+/* Batched f16/bf16 transpose: matrix b (b < batch) of src (rows x cols,
+ * src_ld elements, src_batch elements apart) to dst (cols x rows). Plumbing
+ * for ragged_grouped_gemm, whose weights the reference passes as [G, K, N].
+ * Replaces no reference function.
+ */
+int intent_f16_transpose_batched(const void* src, int64_t batch, int64_t rows, int64_t cols,
+                                 int64_t src_ld, int64_t src_batch, void* dst, int64_t dst_ld,
+                                 int64_t dst_batch, void* stream);
+
+/* f16 / bf16 grouped GEMM over row groups. Replaces ragged_grouped_gemm and
+ * ragged_grouped_gemm_bf16 (examples/kernels/ragged/grouped_gemm.py:11-70;
+ * routes == NULL: group g owns rows offsets[g] .. offsets[g+1] of x and out)
+ * and routed_expert_projection_bf16 (grouped_gemm.py:101-138; routes != NULL:
+ * group g owns routes[offsets[g] .. offsets[g+1]], route r reads x row r / top_k
+ * and writes out row r of [T * top_k, N]).
+ * x: [rows, K] (x_ld elements); w: group g's weights as [N, K] rows at
+ * w + g * w_group_stride (w_ld elements; use intent_f16_transpose_batched for
+ * [G, K, N]); bf16 selects bf16 (else f16) elements; f32 accumulation.
+ * `rows` bounds the rows (routes) a group can hold. K % 64 == 0.
+ */
+int intent_grouped_gemm(const void* x, int64_t rows, int64_t K, int64_t x_ld, const int32_t* offsets,
+                        int64_t G, const int32_t* routes, int64_t top_k, const void* w, int64_t N,
+                        int64_t w_ld, int64_t w_group_stride, int bf16, void* out, int64_t out_ld,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,6 +4,8 @@
 #include "internal.h"
 #include "mfma_pipe.h"
 
+#include <type_traits>
+
 namespace {
 
 // Weight row of B-tile row c; tail rows read the last valid row and their
@@ -183,8 +185,11 @@ __global__ __launch_bounds__(T::NT_WS, 1) void fp4_bf16_gemm_kernel(const uint16
 // is a transpose of the int32 words (xor 0x88888888) and of the scales.
 template <class E, uint32_t kXor>
 __global__ __launch_bounds__(256) void transpose32_kernel(const E* __restrict__ src, int R, int C, int64_t sld,
-                                                          E* __restrict__ dst, int64_t dld) {
+                                                          E* __restrict__ dst, int64_t dld, int64_t sbatch = 0,
+                                                          int64_t dbatch = 0) {
   __shared__ E t[32][33];
+  src += blockIdx.z * sbatch;  // one matrix per blockIdx.z
+  dst += blockIdx.z * dbatch;
   const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
 #pragma unroll
@@ -251,6 +256,83 @@ __global__ __launch_bounds__(T::NT, 1) void quantized_gemm_kernel(
 #pragma unroll
           for (int c = 0; c < 4; ++c)
             if (n + c < N) o[c] = (int8_t)((packed >> (8 * c)) & 255u);
+        }
+      }
+  }
+}
+
+// ---- f16 / bf16 grouped GEMMs over row groups -----------------------------------
+// ragged_grouped_gemm(_bf16) (grouped_gemm.py:11-70): group g owns rows
+// offsets[g] .. offsets[g+1] of x and y; y[rows] = x[rows] @ W[g].
+// routed_expert_projection_bf16 (grouped_gemm.py:101-138): expert e owns
+// entries offsets[e] .. offsets[e+1] of member_routes; route r reads token
+// r / TOP_K and writes row r of the [T * TOP_K, N] output.
+// Weights arrive as [G][N][K] rows (K contiguous). A workgroup owns one
+// 256 x 256 tile of one group; the grid covers every group's worst case
+// (all rows) and workgroups past their group's rows exit at once.
+struct RoutedRows {  // tile row p = route routes[m0 + p]; rows past the group repeat the last
+  const void* base;
+  int64_t ld_bytes;
+  const int32_t* routes;
+  int end;
+  int top_k;
+  INTENT_DEVICE const void* tile_base(int) const { return base; }
+  INTENT_DEVICE uint32_t off(int m0, int p) const {
+    const int i = m0 + p < end ? m0 + p : end - 1;
+    return (uint32_t)((routes[i] / top_k) * ld_bytes);
+  }
+};
+
+template <class T, class Math, bool kRouted>
+__global__ __launch_bounds__(T::NT, 1) void grouped_gemm_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ routes, int top_k, const uint16_t* __restrict__ w, int64_t ldw, int64_t gstride,
+    int N, int K, int mbmax, int nblocks, uint16_t* __restrict__ out, int64_t ldo) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  const int nb = blockIdx.x % nblocks;
+  const int rest = blockIdx.x / nblocks;
+  const int mb = rest % mbmax;
+  const int g = rest / mbmax;
+  const int start = offsets[g] + mb * T::BM;
+  const int end = offsets[g + 1];
+  if (start >= end) return;  // workgroup-uniform
+  const int n0 = nb * T::BN;
+  const int wave = T::wave();
+  mp::RegRowsOperand<T::BN, mp::DenseRows, false, T::NW> bop;
+  bop.init(mp::DenseRows{w + g * gstride, ldw * 2, N}, n0, wave);
+  f32x16 acc[T::TI][T::TJ];
+  if constexpr (kRouted) {
+    mp::RegRowsOperand<T::BM, RoutedRows, false, T::NW> aop;
+    aop.init(RoutedRows{x, ldx * 2, routes, end, top_k}, start, wave);
+    mp::mainloop<T, Math>(aop, bop, K / 64, buf0, buf1, acc);
+  } else {
+    mp::RegRowsOperand<T::BM, mp::DenseRows, false, T::NW> aop;
+    aop.init(mp::DenseRows{x, ldx * 2, end}, start, wave);
+    mp::mainloop<T, Math>(aop, bop, K / 64, buf0, buf1, acc);
+  }
+  constexpr bool kBf16 = std::is_same<Math, mp::BF16Math>::value;
+  auto cvt = [](float v) -> uint32_t { return kBf16 ? f32_to_bf16_rne(v) : bit_cast<uint16_t>((f16)v); };
+  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int idx = start + T::row(i);
+    if (idx >= end) continue;
+    const int64_t orow = kRouted ? routes[idx] : idx;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int n = n0 + T::col(j, gq);
+        uint16_t* o = out + orow * ldo + n;
+        if (vec && n + 3 < N) {
+          const uint32_t lo = cvt(acc[i][j][4 * gq]) | (cvt(acc[i][j][4 * gq + 1]) << 16);
+          const uint32_t hi = cvt(acc[i][j][4 * gq + 2]) | (cvt(acc[i][j][4 * gq + 3]) << 16);
+          *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (n + c < N) o[c] = (uint16_t)cvt(acc[i][j][4 * gq + c]);
         }
       }
   }
@@ -525,4 +607,66 @@ extern "C" int intent_quantized_gemm(const void* a, int64_t M, int64_t K, int64_
                      (const f16*)a, a_ld, (int)M, (const f16*)bt, bt_ld, (int)N, (int)K, bias, (const f16*)residual,
                      residual_ld, output_scale, out, out_ld, mblocks);
   return intent::launch_status("quantized_gemm");
+}
+
+extern "C" int intent_f16_transpose_batched(const void* src, int64_t batch, int64_t rows, int64_t cols,
+                                            int64_t src_ld, int64_t src_batch, void* dst, int64_t dst_ld,
+                                            int64_t dst_batch, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(batch >= 0 && rows >= 0 && cols >= 0 && rows <= INT32_MAX && cols <= INT32_MAX && batch < 65536,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  if (batch == 0 || rows == 0 || cols == 0) return INTENT_OK;
+  INTENT_REQUIRE(src && dst, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(src_ld >= cols && dst_ld >= rows, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE((rows + 31) / 32 < 65536, INTENT_ERR_UNSUPPORTED, "f16_transpose: grid too large");
+  hipLaunchKernelGGL((transpose32_kernel<uint16_t, 0u>),
+                     dim3((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32), (unsigned)batch), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)src, (int)rows, (int)cols, src_ld, (uint16_t*)dst, dst_ld,
+                     src_batch, dst_batch);
+  return intent::launch_status("f16_transpose_batched");
+}
+
+extern "C" int intent_grouped_gemm(const void* x, int64_t rows, int64_t K, int64_t x_ld, const int32_t* offsets,
+                                   int64_t G, const int32_t* routes, int64_t top_k, const void* w, int64_t N,
+                                   int64_t w_ld, int64_t w_group_stride, int bf16, void* out, int64_t out_ld,
+                                   void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(rows >= 0 && K >= 0 && N >= 0 && G >= 0 && rows <= INT32_MAX && K <= INT32_MAX && N <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
+  if (rows == 0 || N == 0 || G == 0) return INTENT_OK;
+  INTENT_REQUIRE(K > 0 && (!routes || top_k >= 1), INTENT_ERR_INVALID_ARGUMENT, "bad K or top_k");
+  INTENT_REQUIRE(x && offsets && w && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(x_ld >= K && w_ld >= K && out_ld >= N && w_group_stride >= N * w_ld, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(x) && intent::aligned16(w) && x_ld % 8 == 0 && w_ld % 8 == 0 &&
+                     w_group_stride % 8 == 0,
+                 INTENT_ERR_ALIGNMENT, "operands must be 16-byte aligned with 16-byte row strides");
+  INTENT_REQUIRE(intent::fits_offset(N, w_ld * 2) && intent::fits_offset(rows, x_ld * 2), INTENT_ERR_UNSUPPORTED,
+                 "grouped_gemm: operand too large for 31-bit buffer offsets");
+  using T = mp::Tile<256, 256, 2, 2>;
+  // Worst case per group: every row (or route) in one group.
+  const int mbmax = (int)((rows + T::BM - 1) / T::BM);
+  const int nblocks = (int)((N + T::BN - 1) / T::BN);
+  const int64_t grid = G * mbmax * (int64_t)nblocks;
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grouped_gemm: grid too large");
+  const uint16_t* xx = (const uint16_t*)x;
+  const uint16_t* ww = (const uint16_t*)w;
+  uint16_t* oo = (uint16_t*)out;
+  hipStream_t st = (hipStream_t)stream;
+  if (routes && bf16)
+    hipLaunchKernelGGL((grouped_gemm_kernel<T, mp::BF16Math, true>), dim3((unsigned)grid), dim3(T::NT), 0, st, xx,
+                       x_ld, offsets, routes, (int)top_k, ww, w_ld, w_group_stride, (int)N, (int)K, mbmax, nblocks, oo,
+                       out_ld);
+  else if (routes)
+    hipLaunchKernelGGL((grouped_gemm_kernel<T, mp::F16Math, true>), dim3((unsigned)grid), dim3(T::NT), 0, st, xx,
+                       x_ld, offsets, routes, (int)top_k, ww, w_ld, w_group_stride, (int)N, (int)K, mbmax, nblocks, oo,
+                       out_ld);
+  else if (bf16)
+    hipLaunchKernelGGL((grouped_gemm_kernel<T, mp::BF16Math, false>), dim3((unsigned)grid), dim3(T::NT), 0, st, xx,
+                       x_ld, offsets, routes, 1, ww, w_ld, w_group_stride, (int)N, (int)K, mbmax, nblocks, oo, out_ld);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<T, mp::F16Math, false>), dim3((unsigned)grid), dim3(T::NT), 0, st, xx,
+                       x_ld, offsets, routes, 1, ww, w_ld, w_group_stride, (int)N, (int)K, mbmax, nblocks, oo, out_ld);
+  return intent::launch_status("grouped_gemm");
 }

@@ -891,6 +891,84 @@ quantized_gemm = KernelDefinition(
 )
 
 
+# ---- f16 / bf16 grouped GEMMs (the reference's ragged kernels) ------------------
+
+def _ragged_workspace(env: dict) -> int:
+    return env["G"] * env["N"] * env["K"] * 2
+
+
+def _ragged_check(env: dict) -> None:
+    if env["G_PLUS_1"] != env["G"] + 1:
+        raise ValueError(f"group_offsets has {env['G_PLUS_1']} entries; {env['G'] + 1} groups need G + 1")
+    if env["K"] % 64:
+        raise NotImplementedError(f"K ({env['K']}) must be a multiple of 64")
+
+
+def _ragged_launch(bf16: bool):
+    def launch(v: dict, env: dict, stream: int, workspace) -> str:
+        x, offs, w, y = v["x"], v["group_offsets"], v["weight"], v["y"]
+        G, K, N = env["G"], env["K"], env["N"]
+        wt = workspace.data_ptr()  # [G, K, N] -> [G, N, K]
+        _native.call("intent_f16_transpose_batched", _ptr(w), G, K, N, w.stride(1), w.stride(0), wt, K, N * K, stream)
+        _native.call("intent_grouped_gemm", _ptr(x), env["R"], K, _ld(x), _ptr(offs), G, None, 1, wt, N, K, N * K,
+                     int(bf16), _ptr(y), _ld(y), stream)
+        return "intent_grouped_gemm"
+    return launch
+
+
+def _ragged_definition(name: str, dt: str, lines: str) -> KernelDefinition:
+    return KernelDefinition(
+        name=name,
+        params=(
+            Param("x", dt, ("R", "K"), leading_stride=True),
+            Param("group_offsets", "i32", ("G_PLUS_1",)),
+            Param("weight", dt, ("G", "K", "N")),
+            Param("y", dt, ("R", "N"), OUT, leading_stride=True),
+        ),
+        launch=_ragged_launch(dt == "bf16"),
+        check=_ragged_check,
+        workspace=_ragged_workspace,
+        reference=f"examples/kernels/ragged/grouped_gemm.py:{lines}",
+        doc="y[rows of g] = x[rows of g] @ weight[g], rows of g = group_offsets[g] .. group_offsets[g+1]",
+    )
+
+
+ragged_grouped_gemm = _ragged_definition("ragged_grouped_gemm", "f16", "11-38")
+ragged_grouped_gemm_bf16 = _ragged_definition("ragged_grouped_gemm_bf16", "bf16", "41-70")
+
+
+def _routed_check(env: dict) -> None:
+    if env["E_PLUS_1"] != env["E"] + 1:
+        raise ValueError(f"expert_offsets has {env['E_PLUS_1']} entries; {env['E'] + 1} experts need E + 1")
+    if env["K"] % 64:
+        raise NotImplementedError(f"K ({env['K']}) must be a multiple of 64")
+
+
+def _routed_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    x, offs, routes, w, out = v["x"], v["expert_offsets"], v["member_routes"], v["weight"], v["output"]
+    E, K, N = env["E"], env["K"], env["N"]
+    _native.call("intent_grouped_gemm", _ptr(x), env["R"], K, _ld(x), _ptr(offs), E, _ptr(routes), env["TOP_K"],
+                 _ptr(w), N, K, N * K, 1, _ptr(out), N, stream)
+    return "intent_grouped_gemm"
+
+
+routed_expert_projection_bf16 = KernelDefinition(
+    name="routed_expert_projection_bf16",
+    params=(
+        Param("x", "bf16", ("T", "K"), leading_stride=True),
+        Param("expert_offsets", "i32", ("E_PLUS_1",)),
+        Param("member_routes", "i32", ("R",)),
+        Param("weight", "bf16", ("E", "N", "K")),
+        Param("output", "bf16", ("T", "TOP_K", "N"), OUT),
+    ),
+    launch=_routed_launch,
+    constexprs={"TOP_K": 2},
+    check=_routed_check,
+    reference="examples/kernels/ragged/grouped_gemm.py:101-138",
+    doc="output[r // TOP_K, r % TOP_K] = x[r // TOP_K] @ weight[e].T for the routes r of expert e",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_matmul, weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     gemm_i8,
@@ -898,4 +976,5 @@ ALL_DEFINITIONS = (
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
     deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul, dequant_bf16_fp4_matmul, quantized_gemm,
+    ragged_grouped_gemm, ragged_grouped_gemm_bf16, routed_expert_projection_bf16,
 )

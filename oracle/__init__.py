@@ -96,6 +96,8 @@ def lib():
         _lib.orc_w4_sym.restype = None
         _lib.orc_quantized_gemm.argtypes = [p, i64, i64, p, i64, p, p, p, p, ci]
         _lib.orc_quantized_gemm.restype = None
+        _lib.orc_grouped_gemm.argtypes = [p, ci, i64, p, i64, p, i64, p, i64, p, ci]
+        _lib.orc_grouped_gemm.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -361,6 +363,22 @@ def quantized_gemm(a, b, bias, residual, output_scale, threads: int = 1) -> np.n
     N = b.shape[1]
     out = np.empty((M, N), np.int8)
     lib().orc_quantized_gemm(_ptr(a), M, K, _ptr(b), N, _ptr(bias), _ptr(r), _ptr(sc), _ptr(out), threads)
+    return out
+
+
+def grouped_gemm(x_bits, bf16: bool, offsets, w_bits, out_rows: int, routes=None, top_k: int = 1,
+                 threads: int = 1) -> np.ndarray:
+    """16-bit element bits: x [rows, K]; w [G, K, N] (ragged) or [G, N, K] (routed).
+    Returns the [out_rows, N] bits; rows no group writes stay 0."""
+    x, w = _c(x_bits, np.uint16), _c(w_bits, np.uint16)
+    offs = _c(offsets, np.int32)
+    K = x.shape[1]
+    G = offs.shape[0] - 1
+    N = w.shape[2] if routes is None else w.shape[1]
+    out = np.zeros((out_rows, N), np.uint16)
+    r = None if routes is None else _c(routes, np.int32)
+    lib().orc_grouped_gemm(_ptr(x), int(bf16), K, _ptr(offs), G, None if r is None else _ptr(r), top_k, _ptr(w), N,
+                           _ptr(out), threads)
     return out
 
 

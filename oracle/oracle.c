@@ -729,3 +729,32 @@ void orc_quantized_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t*
     }
   }
 }
+
+/* ---- f16 / bf16 grouped GEMMs ------------------------------------------------------
+ * ragged_grouped_gemm(_bf16) (examples/kernels/ragged/grouped_gemm.py:11-70; CPU
+ * baseline cpu_runtime.py:859-864): y[rows of g] = x[rows of g] @ W[g], W [G, K, N].
+ * routed_expert_projection_bf16 (grouped_gemm.py:101-138; cpu_runtime.py:874-881):
+ * route r = routes[i] for i in the expert's range reads token r / top_k, writes
+ * output row r of [T * top_k, N]; W [E, N, K]. f32 accumulation (fma in k order),
+ * one rounding to the element type. */
+static float u16_to_f32(uint16_t v, int bf16) { return bf16 ? bf16_bits_to_f32(v) : orc_f16_to_f32(v); }
+
+void orc_grouped_gemm(const uint16_t* x, int bf16, int64_t K, const int32_t* offsets, int64_t G, const int32_t* routes,
+                      int64_t top_k, const uint16_t* w, int64_t N, uint16_t* out, int threads) {
+  for (int64_t g = 0; g < G; ++g) {
+    const int64_t b = offsets[g], e = offsets[g + 1];
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+    for (int64_t i = b; i < e; ++i) {
+      const int64_t orow = routes ? routes[i] : i;
+      const int64_t xrow = routes ? routes[i] / top_k : i;
+      for (int64_t n = 0; n < N; ++n) {
+        float acc = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+          const uint16_t wv = routes ? w[(g * N + n) * K + k] : w[(g * K + k) * N + n];
+          acc = fmaf(u16_to_f32(x[xrow * K + k], bf16), u16_to_f32(wv, bf16), acc);
+        }
+        out[orow * N + n] = bf16 ? orc_f32_to_bf16(acc) : orc_f32_to_f16(acc);
+      }
+    }
+  }
+}

@@ -54,5 +54,7 @@ void orc_w4_sym(const uint16_t* x, int64_t M, int64_t K, const int32_t* packed, 
                 uint16_t* y, int threads);
 void orc_quantized_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t* b, int64_t N, const float* bias,
                         const uint16_t* residual, const float* oscale, int8_t* out, int threads);
+void orc_grouped_gemm(const uint16_t* x, int bf16, int64_t K, const int32_t* offsets, int64_t G, const int32_t* routes,
+                      int64_t top_k, const uint16_t* w, int64_t N, uint16_t* out, int threads);
 
 #endif

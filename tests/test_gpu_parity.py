@@ -659,3 +659,60 @@ def test_gemm_i8_reference_layout(gpu, threads, M, K, N):
     c = art(intent.gemm_i8).run(dev(a), dev(b), dev(bias))
     rows = np.r_[0:min(M, 8), max(0, M - 8):M]
     assert np.array_equal(host(c)[rows], oracle.i8_gemm_i32(a[rows], np.ascontiguousarray(b.T), bias, threads))
+
+
+# ---- f16 / bf16 grouped GEMMs (ragged, routed) -------------------------------------------
+
+def _bits16(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_ragged_grouped_gemm(gpu, threads, dt):
+    tdt = torch.float16 if dt == "f16" else torch.bfloat16
+    g = torch.Generator().manual_seed(61)
+    R, K, N = 1000, 256, 300
+    offsets = torch.tensor([0, 100, 100, 650, 1000], dtype=torch.int32)  # group 1 is empty
+    x = torch.randn(R, K, generator=g).to(tdt)
+    w = (torch.randn(4, K, N, generator=g) / 16).to(tdt)
+    defn = intent.ragged_grouped_gemm if dt == "f16" else intent.ragged_grouped_gemm_bf16
+    y = art(defn).run(x.cuda(), offsets.cuda(), w.cuda())
+    ref = oracle.grouped_gemm(_bits16(x), dt == "bf16", offsets.numpy(), _bits16(w), R, threads=threads)
+    got = _bits16(y.cpu())
+    r64 = torch.from_numpy(ref.view(np.int16)).view(tdt).double().numpy()
+    g64 = torch.from_numpy(got.view(np.int16)).view(tdt).double().numpy()
+    assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()
+
+
+def test_ragged_grouped_gemm_reference_size(gpu):
+    # grouped_gemm.py:6-9: 8192 rows, K = N = 4096, 8 groups (ragged offsets here)
+    g = torch.Generator(device="cuda").manual_seed(62)
+    R, K, N, G = 8192, 4096, 4096, 8
+    cuts = torch.sort(torch.randint(0, R, (G - 1,), device="cuda", generator=g)).values
+    offsets = torch.cat([torch.zeros(1, device="cuda"), cuts, torch.full((1,), R, device="cuda")]).int()
+    x = torch.randn(R, K, device="cuda", generator=g).half()
+    w = (torch.randn(G, K, N, device="cuda", generator=g) / 64).half()
+    y = art(intent.ragged_grouped_gemm).run(x, offsets, w)
+    ref = torch.empty(R, N, device="cuda")
+    o = offsets.tolist()
+    for e in range(G):
+        ref[o[e]:o[e + 1]] = x[o[e]:o[e + 1]].float() @ w[e].float()
+    assert (y.double() - ref.double()).abs().max().item() <= 1e-2 * ref.abs().max().item()
+
+
+def test_routed_expert_projection_bf16(gpu, threads):
+    g = torch.Generator().manual_seed(63)
+    T, TOP_K, E, K, N = 300, 2, 4, 256, 200
+    experts = torch.randint(0, E, (T * TOP_K,), generator=g)
+    member_routes = torch.sort(experts, stable=True).indices.int()   # routes grouped by expert
+    offsets = torch.zeros(E + 1, dtype=torch.int32)
+    offsets[1:] = torch.cumsum(torch.bincount(experts, minlength=E), 0).int()
+    x = torch.randn(T, K, generator=g).bfloat16()
+    w = (torch.randn(E, N, K, generator=g) / 16).bfloat16()
+    out = art(intent.routed_expert_projection_bf16).run(x.cuda(), offsets.cuda(), member_routes.cuda(), w.cuda())
+    ref = oracle.grouped_gemm(_bits16(x), True, offsets.numpy(), _bits16(w), T * TOP_K, routes=member_routes.numpy(),
+                              top_k=TOP_K, threads=threads)
+    got = _bits16(out.cpu().view(T * TOP_K, N))
+    r64 = torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).double().numpy()
+    g64 = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).double().numpy()
+    assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()

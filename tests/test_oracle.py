@@ -725,3 +725,33 @@ def test_quantized_gemm_known_answers():
     got = oracle.quantized_gemm(a, b, bias, residual, scale)
     # 2.75 -> 2; relu(-3)+0.5 = 0.5, /0.25 = 2; 1000 -> 127; relu(-1000)-2 = -2; 1.5-3 = -1.5 -> -1
     assert got.tolist() == [[2, 2, 127, -2, -1]]
+
+
+# ---- f16 / bf16 grouped GEMMs ------------------------------------------------------------
+
+def _u16(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_grouped_gemm_ragged_and_routed_closed_form():
+    g = torch.Generator().manual_seed(71)
+    K, N = 128, 12
+    x = torch.randn(10, K, generator=g).half()
+    w = (torch.randn(3, K, N, generator=g) / 8).half()
+    offsets = np.array([0, 4, 4, 10], np.int32)          # group 1 empty
+    y = oracle.grouped_gemm(_u16(x), False, offsets, _u16(w), 10)
+    yy = torch.from_numpy(y.view(np.int16)).view(torch.float16).double()
+    for gi, (b, e) in enumerate(zip(offsets[:-1], offsets[1:])):
+        ref = x[b:e].double() @ w[gi].double()
+        assert torch.allclose(yy[b:e], ref, rtol=2e-3, atol=2e-3 * max(1.0, ref.abs().max().item()))
+    # routed: route r of expert e reads token r // top_k and writes row r
+    xb = torch.randn(3, K, generator=g).bfloat16()
+    wb = (torch.randn(2, N, K, generator=g) / 8).bfloat16()
+    routes = np.array([5, 0, 3, 1, 2, 4], np.int32)      # expert 0: routes 5, 0; expert 1: 3, 1, 2, 4
+    offs = np.array([0, 2, 6], np.int32)
+    out = oracle.grouped_gemm(_u16(xb), True, offs, _u16(wb), 6, routes=routes, top_k=2)
+    ob = torch.from_numpy(out.view(np.int16)).view(torch.bfloat16).double()
+    for i, r in enumerate(routes):
+        e = 0 if i < 2 else 1
+        ref = xb[r // 2].double() @ wb[e].double().T
+        assert torch.allclose(ob[r], ref, rtol=1e-2, atol=1e-2 * max(1.0, ref.abs().max().item()))
