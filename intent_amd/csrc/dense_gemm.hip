@@ -201,6 +201,52 @@ __global__ __launch_bounds__(256) void transpose32_kernel(const E* __restrict__ 
     if (c0 + i < C && r0 + tx < R) dst[(int64_t)(c0 + i) * dld + r0 + tx] = (E)(t[tx][i] ^ (E)kXor);
 }
 
+// f16 / bf16 transpose through a 64 x 64 LDS tile with 16-byte accesses:
+// thread t moves 8 elements of row t / 8 (twice: rows and rows + 32), then
+// writes 8 elements of one output row. dst[c][r] = src[r][c]; blockIdx.z
+// selects a matrix of a batch.
+__global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __restrict__ src, int R, int C, int64_t sld,
+                                                          uint16_t* __restrict__ dst, int64_t dld, int64_t sbatch,
+                                                          int64_t dbatch) {
+  __shared__ uint16_t t[64][72];
+  src += blockIdx.z * sbatch;
+  dst += blockIdx.z * dbatch;
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int row = threadIdx.x >> 3, seg = (threadIdx.x & 7) * 8;
+  const bool full = r0 + 64 <= R && c0 + 64 <= C;
+  const bool svec = full && ((sld | (int64_t)(uintptr_t)src) & 7) == 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = row + 32 * h;
+    if (svec) {
+      *reinterpret_cast<u32x4*>(&t[r][seg]) = *reinterpret_cast<const u32x4*>(src + (int64_t)(r0 + r) * sld + c0 + seg);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        t[r][seg + i] = (r0 + r < R && c0 + seg + i < C) ? src[(int64_t)(r0 + r) * sld + c0 + seg + i] : 0;
+    }
+  }
+  __syncthreads();
+  const bool dvec = full && ((dld | (int64_t)(uintptr_t)dst) & 7) == 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = row + 32 * h;  // output row c0 + c, elements r0 + seg .. +7
+    uint16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = t[seg + i][c];
+    if (dvec) {
+      u32x4 w;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) w[d] = (uint32_t)v[2 * d] | ((uint32_t)v[2 * d + 1] << 16);
+      *reinterpret_cast<u32x4*>(dst + (int64_t)(c0 + c) * dld + r0 + seg) = w;
+    } else if (c0 + c < C) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (r0 + seg + i < R) dst[(int64_t)(c0 + c) * dld + r0 + seg + i] = v[i];
+    }
+  }
+}
+
 __global__ void fill_u8_kernel(uint8_t* __restrict__ z, int rows, int cols, int64_t ld, uint8_t v) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < (int64_t)rows * cols) z[(i / cols) * ld + i % cols] = v;
@@ -576,10 +622,10 @@ extern "C" int intent_f16_transpose(const void* src, int64_t rows, int64_t cols,
   if (rows == 0 || cols == 0) return INTENT_OK;
   INTENT_REQUIRE(src && dst, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(src_ld >= cols && dst_ld >= rows, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
-  INTENT_REQUIRE((rows + 31) / 32 < 65536, INTENT_ERR_UNSUPPORTED, "f16_transpose: grid too large");
-  hipLaunchKernelGGL((transpose32_kernel<uint16_t, 0u>), dim3((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32)),
-                     dim3(256), 0, (hipStream_t)stream, (const uint16_t*)src, (int)rows, (int)cols, src_ld,
-                     (uint16_t*)dst, dst_ld);
+  INTENT_REQUIRE((rows + 63) / 64 < 65536, INTENT_ERR_UNSUPPORTED, "f16_transpose: grid too large");
+  hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)src, (int)rows, (int)cols, src_ld, (uint16_t*)dst, dst_ld,
+                     (int64_t)0, (int64_t)0);
   return intent::launch_status("f16_transpose");
 }
 
@@ -618,11 +664,10 @@ extern "C" int intent_f16_transpose_batched(const void* src, int64_t batch, int6
   if (batch == 0 || rows == 0 || cols == 0) return INTENT_OK;
   INTENT_REQUIRE(src && dst, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(src_ld >= cols && dst_ld >= rows, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
-  INTENT_REQUIRE((rows + 31) / 32 < 65536, INTENT_ERR_UNSUPPORTED, "f16_transpose: grid too large");
-  hipLaunchKernelGGL((transpose32_kernel<uint16_t, 0u>),
-                     dim3((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32), (unsigned)batch), dim3(256), 0,
-                     (hipStream_t)stream, (const uint16_t*)src, (int)rows, (int)cols, src_ld, (uint16_t*)dst, dst_ld,
-                     src_batch, dst_batch);
+  INTENT_REQUIRE((rows + 63) / 64 < 65536, INTENT_ERR_UNSUPPORTED, "f16_transpose: grid too large");
+  hipLaunchKernelGGL(transpose16_kernel, dim3((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64), (unsigned)batch),
+                     dim3(256), 0, (hipStream_t)stream, (const uint16_t*)src, (int)rows, (int)cols, src_ld,
+                     (uint16_t*)dst, dst_ld, src_batch, dst_batch);
   return intent::launch_status("f16_transpose_batched");
 }
 
