@@ -257,24 +257,27 @@ __global__ void fill_u8_kernel(uint8_t* __restrict__ z, int rows, int cols, int6
 //                        -128, 127)))
 // (CPU baseline cpu_runtime.py:91-94; relu keeps NaN, the division is IEEE and
 // the float -> integer cast truncates toward zero). Both operands are f16 rows
-// with K contiguous (the right operand transposed beforehand), staged through
-// VGPRs into the swizzled LDS stages of mfma_pipe.h.
+// with K contiguous (the right operand transposed beforehand), on producer/
+// consumer workgroups (mainloop_ws): activations by LDS DMA, weight rows
+// staged by the producer waves.
 template <class T>
-__global__ __launch_bounds__(T::NT, 1) void quantized_gemm_kernel(
+__global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
     const f16* __restrict__ a, int64_t lda, int M, const f16* __restrict__ bt, int64_t ldb, int N, int K,
     const float* __restrict__ bias, const f16* __restrict__ residual, int64_t ldr, const float* __restrict__ oscale,
     int8_t* __restrict__ out, int64_t ldo, int mblocks) {
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
-  const int wave = T::wave();
+  char* const bufs[2] = {buf0, buf1};
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  const int pw = T::wave() % T::NW;
   mp::RegRowsOperand<T::BN, mp::DenseRows, false, T::NW> bop;
-  bop.init(mp::DenseRows{bt, ldb * 2, N}, n0, wave);
-  mp::RegRowsOperand<T::BM, mp::DenseRows, false, T::NW> aop;
-  aop.init(mp::DenseRows{a, lda * 2, M}, m0, wave);
+  bop.init(mp::DenseRows{bt, ldb * 2, N}, n0, pw);
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{a, lda * 2, M}, m0, pw);
   f32x16 acc[T::TI][T::TJ];
-  mp::mainloop<T, mp::F16Math>(aop, bop, K / 64, buf0, buf1, acc);
+  if (!mp::mainloop_ws<T, mp::F16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
     const int m = m0 + T::row(i);
@@ -645,11 +648,11 @@ extern "C" int intent_quantized_gemm(const void* a, int64_t M, int64_t K, int64_
                  INTENT_ERR_ALIGNMENT, "operands must be 16-byte aligned with 16-byte row strides");
   INTENT_REQUIRE(intent::fits_offset(M, a_ld * 2) && intent::fits_offset(N, bt_ld * 2), INTENT_ERR_UNSUPPORTED,
                  "quantized_gemm: operand too large for 31-bit buffer offsets");
-  using T = mp::Tile<256, 256, 2, 2>;  // four waves of 128 x 128, accumulators in AGPRs
+  using T = mp::Tile<256, 192, 2, 2>;  // producer/consumer: 4 consumers of 128 x 96 + 4 producers
   const int mblocks = (int)((M + T::BM - 1) / T::BM);
   const int64_t grid = (int64_t)mblocks * ((N + T::BN - 1) / T::BN);
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "quantized_gemm: grid too large");
-  hipLaunchKernelGGL((quantized_gemm_kernel<T>), dim3((unsigned)grid), dim3(T::NT), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL((quantized_gemm_kernel<T>), dim3((unsigned)grid), dim3(T::NT_WS), 0, (hipStream_t)stream,
                      (const f16*)a, a_ld, (int)M, (const f16*)bt, bt_ld, (int)N, (int)K, bias, (const f16*)residual,
                      residual_ld, output_scale, out, out_ld, mblocks);
   return intent::launch_status("quantized_gemm");

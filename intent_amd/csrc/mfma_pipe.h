@@ -182,9 +182,15 @@ struct RegRowsOperand {
 #pragma unroll
     for (int j = 0; j < N_INST; ++j) r.v[j] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[j] - adj, (uint32_t)kt * ROWB, 0);
   }
+  template <bool kAsm = false>  // kAsm: see lds_store16
   INTENT_DEVICE void store(const Regs& r, char* lds_region) const {
 #pragma unroll
-    for (int j = 0; j < N_INST; ++j) *reinterpret_cast<u32x4*>(lds_region + lds_off[j]) = r.v[j];
+    for (int j = 0; j < N_INST; ++j) {
+      if constexpr (kAsm)
+        lds_store16(lds_region + lds_off[j], r.v[j]);
+      else
+        *reinterpret_cast<u32x4*>(lds_region + lds_off[j]) = r.v[j];
+    }
   }
 };
 
