@@ -448,6 +448,16 @@ int intent_grouped_gemm(const void* x, int64_t rows, int64_t K, int64_t x_ld, co
                         int64_t w_ld, int64_t w_group_stride, int bf16, void* out, int64_t out_ld,
                         void* stream);
 
+/* Float GEMM on the same tiles as intent_quantized_gemm. Replaces gemm
+ * (examples/kernels/contraction/gemm.py:42-61; epilogue 0: c = f16(acc),
+ * 1: ACTIVATION RELU, c = f16(max(acc, 0))) and bf16_gemm (gemm.py:64-80;
+ * epilogue 2: bf16 operands, c = bf16(acc)). a: [M, K]; bt: the right operand
+ * as [N, K] rows (use intent_f16_transpose for [K, N]); f32 accumulation;
+ * c: [M, N] of the operands' type. K % 64 == 0.
+ */
+int intent_f16_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* bt, int64_t N,
+                    int64_t bt_ld, int epilogue, void* c, int64_t c_ld, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -260,11 +260,16 @@ __global__ void fill_u8_kernel(uint8_t* __restrict__ z, int rows, int cols, int6
 // with K contiguous (the right operand transposed beforehand), on producer/
 // consumer workgroups (mainloop_ws): activations by LDS DMA, weight rows
 // staged by the producer waves.
-template <class T>
+// The plain float GEMMs share this kernel (gemm.py:42-80): f16 outputs
+// c = f16(acc) or f16(max(acc, 0)) (NaN kept) through the run-time f16_epi of
+// the kQuantI8 instances, and kGemmBf16: c = bf16(acc) with bf16 operands.
+enum class DenseEpi { kQuantI8, kGemmBf16 };
+
+template <class T, DenseEpi E = DenseEpi::kQuantI8, class Math = mp::F16Math>
 __global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
     const f16* __restrict__ a, int64_t lda, int M, const f16* __restrict__ bt, int64_t ldb, int N, int K,
     const float* __restrict__ bias, const f16* __restrict__ residual, int64_t ldr, const float* __restrict__ oscale,
-    int8_t* __restrict__ out, int64_t ldo, int mblocks) {
+    int8_t* __restrict__ out, int64_t ldo, int mblocks, int f16_epi = 0) {
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   char* const bufs[2] = {buf0, buf1};
@@ -277,7 +282,44 @@ __global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
   mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
   aop.init(mp::DenseRows{a, lda * 2, M}, m0, pw);
   f32x16 acc[T::TI][T::TJ];
-  if (!mp::mainloop_ws<T, mp::F16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
+  if (!mp::mainloop_ws<T, Math, 2>(aop, bop, K / 64, bufs, acc)) return;
+  // kQuantI8 instances also serve the f16 GEMM epilogues, chosen at run time
+  // (f16_epi 1: f16(acc), 2: f16(max(acc, 0))).
+  if (E != DenseEpi::kQuantI8 || f16_epi != 0) {
+    uint16_t* y = reinterpret_cast<uint16_t*>(out);
+    const bool relu = f16_epi == 2;
+    auto cvt = [relu](float v) -> uint32_t {
+      if constexpr (E == DenseEpi::kGemmBf16) {
+        return f32_to_bf16_rne(v);
+      } else {
+        if (relu) v = v < 0.f ? 0.f : v;
+        return bit_cast<uint16_t>((f16)v);
+      }
+    };
+    const bool vec = (ldo & 3) == 0 && (((uintptr_t)y) & 7) == 0;
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i) {
+      const int m = m0 + T::row(i);
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int n = n0 + T::col(j, g);
+          uint16_t* o = y + (int64_t)m * ldo + n;
+          if (vec && n + 3 < N) {
+            const uint32_t lo = cvt(acc[i][j][4 * g]) | (cvt(acc[i][j][4 * g + 1]) << 16);
+            const uint32_t hi = cvt(acc[i][j][4 * g + 2]) | (cvt(acc[i][j][4 * g + 3]) << 16);
+            *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
+          } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              if (n + c < N) o[c] = (uint16_t)cvt(acc[i][j][4 * g + c]);
+          }
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
     const int m = m0 + T::row(i);
@@ -717,4 +759,35 @@ extern "C" int intent_grouped_gemm(const void* x, int64_t rows, int64_t K, int64
     hipLaunchKernelGGL((grouped_gemm_kernel<T, mp::F16Math, false>), dim3((unsigned)grid), dim3(T::NT), 0, st, xx,
                        x_ld, offsets, routes, 1, ww, w_ld, w_group_stride, (int)N, (int)K, mbmax, nblocks, oo, out_ld);
   return intent::launch_status("grouped_gemm");
+}
+
+extern "C" int intent_f16_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* bt, int64_t N,
+                               int64_t bt_ld, int epilogue, void* c, int64_t c_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(epilogue >= 0 && epilogue <= 2, INTENT_ERR_INVALID_ARGUMENT,
+                 "epilogue must be 0 (f16), 1 (f16 relu) or 2 (bf16)");
+  INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(a && bt && c, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(a_ld >= K && bt_ld >= K && c_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(bt) && a_ld % 8 == 0 && bt_ld % 8 == 0,
+                 INTENT_ERR_ALIGNMENT, "operands must be 16-byte aligned with 16-byte row strides");
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld * 2) && intent::fits_offset(N, bt_ld * 2), INTENT_ERR_UNSUPPORTED,
+                 "f16_gemm: operand too large for 31-bit buffer offsets");
+  using T = mp::Tile<256, 192, 2, 2>;
+  const int mblocks = (int)((M + T::BM - 1) / T::BM);
+  const int64_t grid = (int64_t)mblocks * ((N + T::BN - 1) / T::BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "f16_gemm: grid too large");
+  if (epilogue == 2)
+    hipLaunchKernelGGL((quantized_gemm_kernel<T, DenseEpi::kGemmBf16, mp::BF16Math>), dim3((unsigned)grid),
+                       dim3(T::NT_WS), 0, (hipStream_t)stream, (const f16*)a, a_ld, (int)M, (const f16*)bt, bt_ld,
+                       (int)N, (int)K, nullptr, nullptr, 0, nullptr, (int8_t*)c, c_ld, mblocks, 0);
+  else
+    hipLaunchKernelGGL((quantized_gemm_kernel<T>), dim3((unsigned)grid), dim3(T::NT_WS), 0, (hipStream_t)stream,
+                       (const f16*)a, a_ld, (int)M, (const f16*)bt, bt_ld, (int)N, (int)K, nullptr, nullptr, 0,
+                       nullptr, (int8_t*)c, c_ld, mblocks, epilogue + 1);
+  return intent::launch_status("f16_gemm");
 }

@@ -969,6 +969,41 @@ routed_expert_projection_bf16 = KernelDefinition(
 )
 
 
+# ---- plain float GEMMs (gemm.py) -------------------------------------------------
+
+def _fgemm_launch(kind: str):
+    def launch(v: dict, env: dict, stream: int, workspace) -> str:
+        a, b, c = v["a"], v["b"], v["c"]
+        M, K, N = env["M"], env["K"], env["N"]
+        bt = workspace.data_ptr()
+        _native.call("intent_f16_transpose", _ptr(b), K, N, b.stride(0), bt, K, stream)
+        epi = 2 if kind == "bf16" else (1 if int(env.get("ACTIVATION", 0)) == 1 else 0)
+        _native.call("intent_f16_gemm", _ptr(a), M, K, _ld(a), bt, N, K, epi, _ptr(c), _ld(c), stream)
+        return "intent_f16_gemm"
+    return launch
+
+
+def _fgemm_definition(name: str, dt: str, lines: str, constexprs: dict) -> KernelDefinition:
+    return KernelDefinition(
+        name=name,
+        params=(
+            Param("a", dt, ("M", "K"), leading_stride=True),
+            Param("b", dt, ("K", "N"), leading_stride=True),
+            Param("c", dt, ("M", "N"), OUT, leading_stride=True),
+        ),
+        launch=_fgemm_launch(dt),
+        constexprs=constexprs,
+        check=_qgemm_check,
+        workspace=_qgemm_workspace,
+        reference=f"examples/kernels/contraction/gemm.py:{lines}",
+        doc=f"c = {dt}(a @ b) with f32 accumulation" + (" (ACTIVATION 1 = RELU: max(acc, 0))" if constexprs else ""),
+    )
+
+
+gemm = _fgemm_definition("gemm", "f16", "42-61", {"ACTIVATION": 0})
+bf16_gemm = _fgemm_definition("bf16_gemm", "bf16", "64-80", {})
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_matmul, weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     gemm_i8,
@@ -976,5 +1011,5 @@ ALL_DEFINITIONS = (
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
     deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul, dequant_bf16_fp4_matmul, quantized_gemm,
-    ragged_grouped_gemm, ragged_grouped_gemm_bf16, routed_expert_projection_bf16,
+    ragged_grouped_gemm, ragged_grouped_gemm_bf16, routed_expert_projection_bf16, gemm, bf16_gemm,
 )

@@ -98,6 +98,8 @@ def lib():
         _lib.orc_quantized_gemm.restype = None
         _lib.orc_grouped_gemm.argtypes = [p, ci, i64, p, i64, p, i64, p, i64, p, ci]
         _lib.orc_grouped_gemm.restype = None
+        _lib.orc_float_gemm.argtypes = [p, i64, i64, p, i64, ci, ci, p, ci]
+        _lib.orc_float_gemm.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -380,6 +382,16 @@ def grouped_gemm(x_bits, bf16: bool, offsets, w_bits, out_rows: int, routes=None
     lib().orc_grouped_gemm(_ptr(x), int(bf16), K, _ptr(offs), G, None if r is None else _ptr(r), top_k, _ptr(w), N,
                            _ptr(out), threads)
     return out
+
+
+def float_gemm(a_bits, b_bits, bf16: bool, relu: bool = False, threads: int = 1) -> np.ndarray:
+    """16-bit element bits a [M, K], b [K, N] -> c bits [M, N] (f16 or bf16)."""
+    a, b = _c(a_bits, np.uint16), _c(b_bits, np.uint16)
+    M, K = a.shape
+    N = b.shape[1]
+    c = np.empty((M, N), np.uint16)
+    lib().orc_float_gemm(_ptr(a), M, K, _ptr(b), N, int(bf16), int(relu), _ptr(c), threads)
+    return c
 
 
 def e4m3fn_to_f32(bits) -> np.ndarray:

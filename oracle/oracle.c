@@ -758,3 +758,19 @@ void orc_grouped_gemm(const uint16_t* x, int bf16, int64_t K, const int32_t* off
     }
   }
 }
+
+/* ---- float GEMMs ----------------------------------------------------------------------
+ * gemm (examples/kernels/contraction/gemm.py:42-61, ACTIVATION RELU: max(acc, 0)) and
+ * bf16_gemm (gemm.py:64-80): c = cast(f32 contraction (fma in k order)); b is [K, N]. */
+void orc_float_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t* b, int64_t N, int bf16, int relu,
+                    uint16_t* c, int threads) {
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < K; ++k) acc = fmaf(u16_to_f32(a[m * K + k], bf16), u16_to_f32(b[k * N + n], bf16), acc);
+      if (relu) acc = acc < 0.0f ? 0.0f : acc;
+      c[m * N + n] = bf16 ? orc_f32_to_bf16(acc) : orc_f32_to_f16(acc);
+    }
+  }
+}

@@ -716,3 +716,23 @@ def test_routed_expert_projection_bf16(gpu, threads):
     r64 = torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).double().numpy()
     g64 = torch.from_numpy(got.view(np.int16)).view(torch.bfloat16).double().numpy()
     assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()
+
+
+# ---- plain float GEMMs (gemm.py) ----------------------------------------------------------
+
+@pytest.mark.parametrize("kind", ["f16", "f16_relu", "bf16"])
+@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (4096, 4096, 4096)])
+def test_float_gemm(gpu, threads, kind, M, K, N):
+    tdt = torch.bfloat16 if kind == "bf16" else torch.float16
+    g = torch.Generator().manual_seed(M + K + N)
+    a = torch.randn(M, K, generator=g).to(tdt) / (K ** 0.5)
+    b = torch.randn(K, N, generator=g).to(tdt)
+    if kind == "bf16":
+        c = art(intent.bf16_gemm).run(a.cuda(), b.cuda())
+    else:
+        c = art(intent.gemm, ACTIVATION=1 if kind == "f16_relu" else 0).run(a.cuda(), b.cuda())
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = oracle.float_gemm(_bits16(a)[rows], _bits16(b), kind == "bf16", kind == "f16_relu", threads)
+    r64 = torch.from_numpy(ref.view(np.int16)).view(tdt).double().numpy()
+    g64 = torch.from_numpy(_bits16(c.cpu())[rows].view(np.int16)).view(tdt).double().numpy()
+    assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()

@@ -757,3 +757,20 @@ def test_grouped_gemm_ragged_and_routed_closed_form():
         e = 0 if i < 2 else 1
         ref = xb[r // 2].double() @ wb[e].double().T
         assert torch.allclose(ob[r], ref, rtol=1e-2, atol=1e-2 * max(1.0, ref.abs().max().item()))
+
+
+def test_float_gemm_closed_form_and_relu():
+    g = torch.Generator().manual_seed(81)
+    for bf16 in (False, True):
+        tdt = torch.bfloat16 if bf16 else torch.float16
+        a = torch.randn(5, 128, generator=g).to(tdt)
+        b = (torch.randn(128, 7, generator=g) / 8).to(tdt)
+        for relu in (False, True):
+            c = oracle.float_gemm(_u16(a), _u16(b), bf16, relu)
+            got = torch.from_numpy(c.view(np.int16)).view(tdt).double()
+            ref = a.double() @ b.double()
+            if relu:
+                ref = ref.clamp_min(0.0)
+            assert torch.allclose(got, ref, rtol=1e-2, atol=1e-2)
+            if relu:
+                assert (got >= 0).all()
