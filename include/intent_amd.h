@@ -458,6 +458,19 @@ int intent_grouped_gemm(const void* x, int64_t rows, int64_t K, int64_t x_ld, co
 int intent_f16_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* bt, int64_t N,
                     int64_t bt_ld, int epilogue, void* c, int64_t c_ld, void* stream);
 
+/* NVFP4 activation quantizer. Replaces nvfp4_quantize
+ * (examples/kernels/quantization/nvfp4.py; CPU baseline
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:1325-1340): x bf16 [M, N]
+ * (x_ld elements, N % 16 == 0), global_scale f32 [1] (device); per row and group
+ * of 16: scale = e4m3fn(max((amax / 6) * gs, 1.5258789e-5)), values
+ * x * (gs / scale) encoded as E2M1 (thresholds of the reference), two per byte
+ * into packed [M, N/2]; scale bytes into the reference's swizzled blocks
+ * scales[M/128][G/4][32][4][4] (row r, group g at [r/128][g/4][r%32][(r%128)/32][g%4]).
+ * Only valid groups are written.
+ */
+int intent_nvfp4_quantize(const void* x, int64_t M, int64_t N, int64_t x_ld, const float* global_scale,
+                          uint8_t* packed, int64_t packed_ld, uint8_t* scales, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

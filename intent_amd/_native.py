@@ -54,6 +54,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_f16_transpose_batched": ([P, I64, I64, I64, I64, I64, P, I64, I64, P], INT),
     "intent_grouped_gemm": ([P, I64, I64, I64, P, I64, P, I64, P, I64, I64, I64, INT, P, I64, P], INT),
     "intent_f16_gemm": ([P, I64, I64, I64, P, I64, I64, INT, P, I64, P], INT),
+    "intent_nvfp4_quantize": ([P, I64, I64, I64, P, P, I64, P, P], INT),
     "intent_fp4_bf16_matmul": ([P, I64, I64, I64, P, I64, I64, P, I64, P], INT),
     "intent_fp8_gemm": ([P, I64, I64, I64, P, I64, I64, INT, P, I64, P], INT),
     "intent_deepgemm_fp8": ([P, I64, I64, I64, P, I64, P, I64, I64, P, I64, P, I64, P], INT),

@@ -1004,6 +1004,37 @@ gemm = _fgemm_definition("gemm", "f16", "42-61", {"ACTIVATION": 0})
 bf16_gemm = _fgemm_definition("bf16_gemm", "bf16", "64-80", {})
 
 
+# ---- NVFP4 activation quantizer ---------------------------------------------------
+
+def _nvfp4_check(env: dict) -> None:
+    if env["N"] % 16 or env["P"] * 2 != env["N"]:
+        raise ValueError(f"N ({env['N']}) must be a multiple of 16 and packed.shape[1] ({env['P']}) N / 2")
+    if env["MT"] * 128 < env["M"] or env["NT"] * 64 < env["N"]:
+        raise ValueError(f"scales blocks ({env['MT']}, {env['NT']}) do not cover M = {env['M']}, N = {env['N']}")
+
+
+def _nvfp4_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    x, gs, packed, scales = v["x"], v["global_scale"], v["packed"], v["scales"]
+    _native.call("intent_nvfp4_quantize", _ptr(x), env["M"], env["N"], _ld(x), _ptr(gs), _ptr(packed), _ld(packed),
+                 _ptr(scales), stream)
+    return "intent_nvfp4_quantize"
+
+
+nvfp4_quantize = KernelDefinition(
+    name="nvfp4_quantize",
+    params=(
+        Param("x", "bf16", ("M", "N"), leading_stride=True),
+        Param("global_scale", "f32", (1,)),
+        Param("packed", "u8", ("M", "P"), INOUT, leading_stride=True),
+        Param("scales", "u8", ("MT", "NT", 32, 4, 4), INOUT),
+    ),
+    launch=_nvfp4_launch,
+    check=_nvfp4_check,
+    reference="examples/kernels/quantization/nvfp4.py",
+    doc="E2M1 values two per byte and E4M3 scales per 16 in the reference's swizzled 128 x 4 blocks",
+)
+
+
 ALL_DEFINITIONS = (
     weight_only_int4_matmul, weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     gemm_i8,
@@ -1012,4 +1043,5 @@ ALL_DEFINITIONS = (
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
     deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul, dequant_bf16_fp4_matmul, quantized_gemm,
     ragged_grouped_gemm, ragged_grouped_gemm_bf16, routed_expert_projection_bf16, gemm, bf16_gemm,
+    nvfp4_quantize,
 )

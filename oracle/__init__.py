@@ -100,6 +100,8 @@ def lib():
         _lib.orc_grouped_gemm.restype = None
         _lib.orc_float_gemm.argtypes = [p, i64, i64, p, i64, ci, ci, p, ci]
         _lib.orc_float_gemm.restype = None
+        _lib.orc_nvfp4_quantize.argtypes = [p, i64, i64, ctypes.c_float, p, p]
+        _lib.orc_nvfp4_quantize.restype = None
         _lib.orc_bitnet_int2.restype = None
         for name in ("orc_w8a16", "orc_w4a16", "orc_i8_gemm_i32", "orc_w8a8", "orc_moe_route", "orc_moe_align",
                      "orc_moe_ffn_w4", "orc_q8k_quantize", "orc_q4k_gemv"):
@@ -392,6 +394,18 @@ def float_gemm(a_bits, b_bits, bf16: bool, relu: bool = False, threads: int = 1)
     c = np.empty((M, N), np.uint16)
     lib().orc_float_gemm(_ptr(a), M, K, _ptr(b), N, int(bf16), int(relu), _ptr(c), threads)
     return c
+
+
+def nvfp4_quantize(x_bits, global_scale: float, packed=None, scales=None):
+    """bf16 bits x [M, N] -> (packed [M, N/2], scales [ceil(M/128), ceil(N/64), 32, 4, 4]);
+    entries no group writes keep the given (or zero) contents."""
+    x = _c(x_bits, np.uint16)
+    M, N = x.shape
+    p = np.zeros((M, N // 2), np.uint8) if packed is None else _c(packed, np.uint8).copy()
+    s = np.zeros(((M + 127) // 128, (N // 16 + 3) // 4, 32, 4, 4), np.uint8) if scales is None else \
+        _c(scales, np.uint8).copy()
+    lib().orc_nvfp4_quantize(_ptr(x), M, N, float(global_scale), _ptr(p), _ptr(s))
+    return p, s
 
 
 def e4m3fn_to_f32(bits) -> np.ndarray:

@@ -774,3 +774,43 @@ void orc_float_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t* b, 
     }
   }
 }
+
+/* ---- NVFP4 quantization -----------------------------------------------------------------
+ * nvfp4_quantize (examples/kernels/quantization/nvfp4.py; CPU baseline
+ * experiments/cpu/baselines/pytorch/cpu_runtime.py:1325-1340), per row and group of 16:
+ * scale = e4m3fn(max((amax / 6) * gs, 1.5258789e-5)); multiplier = gs / f32(scale);
+ * v = x * multiplier; E2M1 code by thresholds on |v| (> 0.25, >= 0.75, > 1.25, >= 1.75,
+ * > 2.5, >= 3.5, > 5.0) with the sign bit of v; packed byte = code(2i) | code(2i+1) << 4;
+ * the scale byte at scales[row/128][group/4][row%32][(row%128)/32][group%4] (NT = the
+ * number of 4-group blocks). */
+void orc_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t N, float gs, uint8_t* packed, uint8_t* scales) {
+  const int64_t G = N / 16, NT = (G + 3) / 4;
+  static const float thr[7] = {0.25f, 0.75f, 1.25f, 1.75f, 2.5f, 3.5f, 5.0f};
+  for (int64_t r = 0; r < M; ++r) {
+    for (int64_t g = 0; g < G; ++g) {
+      float v[16], amax = 0.0f;
+      for (int i = 0; i < 16; ++i) {
+        v[i] = bf16_bits_to_f32(x[r * N + g * 16 + i]);
+        amax = fmaxf(amax, fabsf(v[i]));
+      }
+      float s = (amax / 6.0f) * gs;
+      if (s < 1.5258789e-5f) s = 1.5258789e-5f;
+      const uint8_t sb = orc_f32_to_e4m3fn(s);
+      const float mult = gs / orc_e4m3fn_to_f32(sb);
+      uint8_t code[16];
+      for (int i = 0; i < 16; ++i) {
+        const float t = v[i] * mult, a = fabsf(t);
+        uint8_t c = 0;
+        for (int q = 0; q < 7; ++q) {
+          const int sel = (q % 2 == 0) ? a > thr[q] : a >= thr[q]; /* codes 1,3,5,7 strict; 2,4,6 inclusive */
+          if (sel) c = (uint8_t)(q + 1);
+        }
+        uint32_t bits;
+        memcpy(&bits, &t, 4);
+        code[i] = (uint8_t)(c | ((bits >> 31) << 3));
+      }
+      for (int i = 0; i < 8; ++i) packed[r * (N / 2) + g * 8 + i] = (uint8_t)(code[2 * i] | (code[2 * i + 1] << 4));
+      scales[((((r / 128) * NT + g / 4) * 32 + r % 32) * 4 + (r % 128) / 32) * 4 + g % 4] = sb;
+    }
+  }
+}

@@ -58,5 +58,6 @@ void orc_grouped_gemm(const uint16_t* x, int bf16, int64_t K, const int32_t* off
                       int64_t top_k, const uint16_t* w, int64_t N, uint16_t* out, int threads);
 void orc_float_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t* b, int64_t N, int bf16, int relu,
                     uint16_t* c, int threads);
+void orc_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t N, float gs, uint8_t* packed, uint8_t* scales);
 
 #endif

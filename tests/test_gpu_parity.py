@@ -736,3 +736,21 @@ def test_float_gemm(gpu, threads, kind, M, K, N):
     r64 = torch.from_numpy(ref.view(np.int16)).view(tdt).double().numpy()
     g64 = torch.from_numpy(_bits16(c.cpu())[rows].view(np.int16)).view(tdt).double().numpy()
     assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()
+
+
+# ---- NVFP4 quantizer --------------------------------------------------------------------
+
+@pytest.mark.parametrize("M,N", [(256, 128), (300, 80), (1, 16), (8192, 4096)])
+def test_nvfp4_quantize_bit_exact(gpu, M, N):
+    # (8192, 4096) is the reference's registry case (experiments/cpu/registry.py:11)
+    g = torch.Generator().manual_seed(M + N)
+    x = (torch.randn(M, N, generator=g) * 3).bfloat16()
+    gs = torch.tensor([1.25])
+    MT, NT = (M + 127) // 128, (N // 16 + 3) // 4
+    packed0 = np.full((M, N // 2), 0xAA, np.uint8)
+    scales0 = np.full((MT, NT, 32, 4, 4), 0x55, np.uint8)   # entries no group writes must keep this
+    packed, scales = dev(packed0), dev(scales0)
+    art(intent.nvfp4_quantize).run(x.cuda(), gs.cuda(), packed, scales)
+    rp, rs = oracle.nvfp4_quantize(_bits16(x), 1.25, packed0, scales0)
+    assert np.array_equal(host(packed), rp)
+    assert np.array_equal(host(scales), rs)

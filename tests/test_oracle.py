@@ -774,3 +774,30 @@ def test_float_gemm_closed_form_and_relu():
             assert torch.allclose(got, ref, rtol=1e-2, atol=1e-2)
             if relu:
                 assert (got >= 0).all()
+
+
+# ---- NVFP4 quantizer ----------------------------------------------------------------------
+
+def test_nvfp4_quantize_matches_reference_formula():
+    # cpu_runtime.py:1325-1340 restated with torch (elementwise f32: bit-exact)
+    g = torch.Generator().manual_seed(91)
+    M, N = 256, 128
+    x = (torch.randn(M, N, generator=g) * torch.rand(M, 1, generator=g) * 4).bfloat16()
+    x[3, :16] = 0.0                                  # a zero group: scale clamps to its minimum
+    x[5, 16:32] = -0.0
+    gs = torch.tensor([0.75])
+    packed, scales = oracle.nvfp4_quantize(_u16(x), 0.75)
+    groups = x.float().reshape(M, N // 16, 16)
+    scale = ((groups.abs().amax(-1) / 6.0) * gs[0]).clamp_min(1.5258789e-5).to(torch.float8_e4m3fn)
+    values = groups * (gs[0] / scale.float())[..., None]
+    mag = values.abs()
+    enc = (mag > 0.25).to(torch.uint8)
+    for code, t in enumerate((0.75, 1.25, 1.75, 2.5, 3.5, 5.0), start=2):
+        sel = mag >= t if code % 2 == 0 else mag > t
+        enc = torch.where(sel, code, enc)
+    enc |= torch.signbit(values).to(torch.uint8) << 3
+    pairs = enc.reshape(M, N // 2, 2)
+    ref_packed = (pairs[..., 0] | (pairs[..., 1] << 4)).numpy()
+    ref_scales = scale.view(torch.uint8).reshape(M // 128, 4, 32, N // 64, 4).permute(0, 3, 2, 1, 4).numpy()
+    assert np.array_equal(packed, ref_packed)
+    assert np.array_equal(scales, ref_scales)
