@@ -385,7 +385,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
-                                   "(multi-GPU sharding is described in DESIGN.md, not launched)"}))
+                                   "(multi-GPU sharding is not launched in this build)"}))
         return 2
     import torch
 
