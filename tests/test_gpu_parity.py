@@ -630,7 +630,7 @@ def test_weight_only_int4_matmul_reference_layout(gpu, threads, M, K, N):
 
 # ---- quantized_gemm -------------------------------------------------------------------
 
-@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (1, 64, 1), (4096, 4096, 14336)])
+@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (1, 64, 1), (200, 256, 260), (4096, 4096, 14336)])
 def test_quantized_gemm(gpu, threads, M, K, N):
     # the reference's input construction (experiments/cpu/providers/mojo/contraction.py:177-186)
     g = torch.Generator().manual_seed(M + N)
