@@ -21,20 +21,46 @@ from .errors import CompilationStageError
 from .runtime import HIPRuntime
 
 
-@dataclass(frozen=True, slots=True)
+NUMERICS_POLICIES = ("source", "relaxed_normalization")
+
+
 class CompileOptions:
-    """Numerical policy (python/intent/compiler/options.py:7-57). The HIP kernels
-    implement the "source" contract; the other fields are accepted and recorded."""
+    """Numerical policy accepted by ``compile`` (fields of python/intent/compiler/options.py:8-35).
 
-    numerics: Literal["source", "relaxed_normalization"] = "source"
-    online_reduction: bool = True
-    optimization_remarks: bool = False
+    The HIP kernels implement the ``"source"`` contract (f32 accumulation, no
+    TF32, no flush-to-zero); the other settings are validated and recorded so
+    that calls written for the reference keep working. Instances are immutable
+    and compare by value.
+    """
 
-    def __post_init__(self) -> None:
-        if self.numerics not in ("source", "relaxed_normalization"):
-            raise ValueError("numerics must be 'source' or 'relaxed_normalization'")
-        if type(self.online_reduction) is not bool or type(self.optimization_remarks) is not bool:
-            raise TypeError("online_reduction and optimization_remarks must be booleans")
+    __slots__ = ("numerics", "online_reduction", "optimization_remarks")
+
+    def __init__(self, numerics: Literal["source", "relaxed_normalization"] = "source",
+                 online_reduction: bool = True, optimization_remarks: bool = False) -> None:
+        if numerics not in NUMERICS_POLICIES:
+            raise ValueError(f"numerics={numerics!r} is not one of {NUMERICS_POLICIES}")
+        for label, flag in (("online_reduction", online_reduction), ("optimization_remarks", optimization_remarks)):
+            if not isinstance(flag, bool):
+                raise TypeError(f"{label} takes a bool, got {type(flag).__name__}")
+        object.__setattr__(self, "numerics", numerics)
+        object.__setattr__(self, "online_reduction", online_reduction)
+        object.__setattr__(self, "optimization_remarks", optimization_remarks)
+
+    def __setattr__(self, name, value):
+        raise AttributeError("CompileOptions is immutable")
+
+    def _key(self) -> tuple:
+        return (self.numerics, self.online_reduction, self.optimization_remarks)
+
+    def __eq__(self, other) -> bool:
+        return isinstance(other, CompileOptions) and self._key() == other._key()
+
+    def __hash__(self) -> int:
+        return hash(self._key())
+
+    def __repr__(self) -> str:
+        return ("CompileOptions(numerics={!r}, online_reduction={!r}, optimization_remarks={!r})"
+                .format(*self._key()))
 
 
 @dataclass(frozen=True)

@@ -1,67 +1,108 @@
-"""PyTorch custom-op registration for compiled artifacts.
+"""Expose a compiled artifact as a PyTorch custom operator.
 
-Behaviour of the reference's registration (python/intent/runtime/torch.py:
-27-93): the schema lists every input in author order, InOut views become
-``Tensor(aN!)`` and are declared in ``mutates_args``; Out views are returned;
-the fake implementation infers outputs from shapes without running device
-code; a mutable input sharing storage with another input is rejected.
+Contract kept from the reference (python/intent/runtime/torch.py:27-93):
+* every input appears in the schema in author order; an InOut view is written
+  ``Tensor(aN!)`` (N = its input position) and declared mutated; Out views are
+  the returned tensors (``()`` when there are none);
+* integer scalars are ``SymInt``, floating ones ``float``, booleans ``bool``;
+* the fake kernel derives outputs from shapes through the runtime's binder and
+  never launches device code;
+* a writable view that shares storage with another input raises
+  ``NotImplementedError`` (functionalization may clone it on its own);
+* a name that is not ``namespace::operator`` raises ``ValueError``.
+
+Here the schema arguments carry the interface's own parameter names, so a
+traced graph reads like the operator's signature.
 """
 from __future__ import annotations
 
-from inspect import Parameter, Signature
+from dataclasses import dataclass
 
-from .interface import ScalarParameter, ViewParameter
+from .interface import PublicInterface, ScalarParameter, ViewParameter
+
+# Schema spelling of a scalar parameter, keyed by the dtype category.
+SCALAR_TYPES = {"bool": "bool", "signed": "SymInt", "unsigned": "SymInt", "float": "float", "bfloat": "float"}
+
+
+@dataclass(frozen=True)
+class OperatorSchema:
+    """Schema text plus what the kernel wrapper needs to enforce it."""
+
+    text: str
+    names: tuple[str, ...]
+    mutated: tuple[str, ...]
+    writable_positions: tuple[int, ...]
+    tensor_positions: tuple[int, ...]
+
+    @classmethod
+    def from_interface(cls, interface: PublicInterface) -> "OperatorSchema":
+        fields, names, mutated, writable, tensors = [], [], [], [], []
+        for position, p in enumerate(interface.inputs):
+            if isinstance(p, ViewParameter):
+                tensors.append(position)
+                if p.writable:
+                    writable.append(position)
+                    mutated.append(p.name)
+                    token = f"Tensor(a{position}!)"
+                else:
+                    token = "Tensor"
+            elif isinstance(p, ScalarParameter) and p.dtype.category in SCALAR_TYPES:
+                token = SCALAR_TYPES[p.dtype.category]
+            else:
+                raise NotImplementedError(f"no PyTorch schema type for parameter {p.name} ({p.dtype})")
+            fields.append(f"{token} {p.name}")
+            names.append(p.name)
+        if not tensors:
+            raise NotImplementedError("a PyTorch operator needs at least one tensor input to pick its device")
+        results = ["Tensor"] * len(interface.outputs)
+        returns = results[0] if len(results) == 1 else f"({', '.join(results)})"
+        return cls(f"({', '.join(fields)}) -> {returns}", tuple(names), tuple(mutated), tuple(writable),
+                   tuple(tensors))
+
+    def positional(self, args: tuple, kwargs: dict) -> tuple:
+        """Arguments in schema order, whether the dispatcher passed them by position or by name."""
+        if not kwargs:
+            return args
+        values = list(args) + [None] * (len(self.names) - len(args))
+        for name, value in kwargs.items():
+            values[self.names.index(name)] = value
+        return tuple(values)
+
+    def reject_shared_storage(self, args: tuple) -> None:
+        import torch
+
+        for w in self.writable_positions:
+            for other in self.tensor_positions:
+                if other != w and torch._C._is_alias_of(args[w], args[other]):
+                    raise NotImplementedError(
+                        f"{self.names[w]} is written in place but shares storage with {self.names[other]}; "
+                        "a PyTorch operator needs separate storage here (call the artifact directly instead)")
+
+
+def _checked_namespace(name: str) -> str:
+    parts = name.split("::")
+    if len(parts) == 2 and all(part.isidentifier() for part in parts):
+        return name
+    raise ValueError(f"operator name {name!r} must have the form 'namespace::operator'")
 
 
 def register_operator(artifact, name: str):
     import torch
 
-    interface = artifact.interface
-    inputs = interface.inputs
-    views = tuple((index, p) for index, p in enumerate(inputs) if isinstance(p, ViewParameter))
-    if not views:
-        raise NotImplementedError("PyTorch registration requires an input tensor to determine device dispatch")
-    pieces = name.split("::")
-    if len(pieces) != 2 or not all(piece.isidentifier() for piece in pieces):
-        raise ValueError("operator name must be 'your_namespace::your_operator'")
-    mutable_names = tuple(f"arg{index}" for index, p in views if p.writable)
-    writable_pairs = tuple((i, j, a.name, b.name) for n, (i, a) in enumerate(views) for j, b in views[n + 1:]
-                           if a.writable or b.writable)
-    parameters = []
-    for index, p in enumerate(inputs):
-        if isinstance(p, ViewParameter):
-            kind = f"Tensor(a{index}!)" if p.writable else "Tensor"
-        elif isinstance(p, ScalarParameter):
-            if p.dtype.category == "bool":
-                kind = "bool"
-            elif p.dtype.category in ("signed", "unsigned"):
-                kind = "SymInt"
-            else:
-                kind = "float"
-        parameters.append(f"{kind} arg{len(parameters)}")
-    outs = interface.outputs
-    if not outs:
-        returns = "()"
-    elif len(outs) == 1:
-        returns = "Tensor"
-    else:
-        returns = "(" + ", ".join("Tensor" for _ in outs) + ")"
-    schema = f"({', '.join(parameters)}) -> {returns}"
-    signature = Signature(Parameter(f"arg{i}", Parameter.POSITIONAL_OR_KEYWORD) for i in range(len(parameters)))
+    qualified = _checked_namespace(name)
+    schema = OperatorSchema.from_interface(artifact.interface)
 
-    def wrap(invoke):
-        def operator(*arguments, **keywords):
-            arguments = signature.bind(*arguments, **keywords).args
-            for left, right, left_name, right_name in writable_pairs:
-                if torch._C._is_alias_of(arguments[left], arguments[right]):
-                    raise NotImplementedError(
-                        f"PyTorch mutable calls require independent input storage: {left_name} and "
-                        f"{right_name} share storage; use ordinary artifact calls for this binding")
-            return invoke(*arguments)
+    def real(*args, **kwargs):
+        bound = schema.positional(args, kwargs)
+        schema.reject_shared_storage(bound)
+        return artifact.run(*bound)
 
-        return operator
+    def fake(*args, **kwargs):
+        bound = schema.positional(args, kwargs)
+        schema.reject_shared_storage(bound)
+        return artifact.runtime.infer_outputs(bound)
 
-    operator = torch.library.custom_op(name, wrap(artifact.run), mutates_args=mutable_names,
-                                       device_types=artifact.device_type, schema=schema)
-    operator.register_fake(wrap(lambda *arguments: artifact.runtime.infer_outputs(arguments)))
-    return operator
+    op = torch.library.custom_op(qualified, real, mutates_args=schema.mutated,
+                                 device_types=artifact.device_type, schema=schema.text)
+    op.register_fake(fake)
+    return op

@@ -119,12 +119,35 @@ def test_torch_op_schema():
     art = CompiledArtifact("", "", 0, rt)
     op = art.as_torch_op("intent_amd_cpu_test::combine")
     schema = str(op._opoverload._schema)
-    assert "Tensor(a2!) arg2" in schema and schema.endswith("-> ()")
+    assert "(Tensor route_out, Tensor topk_weights, Tensor(a2!) y) -> ()" in schema
     rt4 = runtime_for(intent.weight_only_int4_asym_matmul)
     op4 = CompiledArtifact("", "", 0, rt4).as_torch_op("intent_amd_cpu_test::w4")
     assert str(op4._opoverload._schema).endswith("-> Tensor")
     with pytest.raises(ValueError):
         CompiledArtifact("", "", 0, rt4).as_torch_op("bad name")
+    # the fake kernel infers outputs from shapes alone
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        y = op4(torch.empty(3, 256, dtype=torch.float16), torch.empty(8, 128, dtype=torch.uint8),
+                torch.empty(8, 2, dtype=torch.float16), torch.empty(8, 2, dtype=torch.uint8))
+    assert tuple(y.shape) == (3, 8) and y.dtype == torch.float16
+    # an in-place view may not share storage with another input
+    with FakeTensorMode(), pytest.raises(NotImplementedError, match="shares storage"):
+        ro = torch.zeros(8, 16)
+        op(ro, torch.zeros(4, 2), ro[:4])
+
+
+def test_compile_options():
+    o = intent.CompileOptions()
+    assert (o.numerics, o.online_reduction, o.optimization_remarks) == ("source", True, False)
+    assert o == intent.CompileOptions("source", True, False) and hash(o) == hash(intent.CompileOptions())
+    with pytest.raises(ValueError):
+        intent.CompileOptions(numerics="fast")
+    with pytest.raises(TypeError):
+        intent.CompileOptions(online_reduction=1)
+    with pytest.raises(AttributeError):
+        o.numerics = "relaxed_normalization"
 
 
 def test_inputs_generators():
