@@ -8,8 +8,9 @@ M=2048 TFLOP/s, W8A8, quantized MoE, W8A16), each measured the same way.
 
 A step is one pass of the hot path over one batch already resident in HBM.
 Steps are captured into a HIP graph and replayed; HIP events on the launch
-stream bracket the replay, so the per-step time is the average kernel
-duration plus inter-kernel gaps. Inputs rotate over enough copies to exceed
+stream time it (graph_time explains how the graph-start latency is taken
+out), so the per-step time is the average kernel duration plus the gaps
+between back-to-back kernels. Inputs rotate over enough copies to exceed
 the 256 MB Infinity Cache, so decode weights stream from HBM, not MALL.
 ``cpu_baseline`` times the C oracle (a port of the reference's CPU numerics)
 on this host's cores over a bounded sample of the headline workload.
@@ -48,35 +49,73 @@ def parse():
                     help="'decode' times only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--probe", choices=["traffic"], default=None,
+    ap.add_argument("--probe", choices=["traffic", "read", "mfma"], default=None,
                     help="'traffic': only run 40 decode launches over distinct weight copies, then four 64 MiB "
                          "device copies (run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE; the copies calibrate "
-                         "the counters)")
+                         "the counters). 'read': time the plain HBM read of the decode's byte count (the floor "
+                         "of any kernel streaming those bytes) beside the decode GEMV itself. 'mfma': three "
+                         "launches each of the compute-bound lines (prefill, W8A8, MoE), for rocprofv3 --pmc "
+                         "MFMA-busy counters")
     return ap.parse_args()
 
 
+WARM_SECONDS = 0.2
+PAIRS = 9
+
+
 def graph_time(launches, steps: int, warmup: int) -> float:
-    """Average ms per step of `launches[i % len](...)` replayed from a HIP graph."""
+    """Average ms per step of `steps` launches replayed from a HIP graph.
+
+    Launch i uses input set i % len(launches). Two graphs are captured: the
+    rotation R (every input set once, in cyclic order) and R followed by the
+    `steps` timed launches. The timed launches start at set 0, whose last use
+    lies a full rotation (more than the 256 MB Infinity Cache, see copies_for)
+    behind them, so every one reads its operands from HBM whatever `steps` is.
+    Each graph replay carries a fixed start latency (about 10 us on this
+    stack, far above a decode kernel); timing both graphs with HIP events on
+    their stream and subtracting cancels it, leaving exactly the `steps`
+    launches and the gaps between them. The median of PAIRS back-to-back
+    pairs is returned, after at least WARM_SECONDS of rotation replays.
+    """
     import torch
 
+    n = len(launches)
     for i in range(warmup):
-        launches[i % len(launches)]()
+        launches[i % n]()
     torch.cuda.synchronize()
     stream = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
+    rotation = torch.cuda.CUDAGraph()
+    timed = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(rotation, stream=stream):
+        for i in range(n):
+            launches[i]()
+    with torch.cuda.graph(timed, stream=stream):
+        for i in range(n):
+            launches[i]()
         for i in range(steps):
-            launches[i % len(launches)]()
-    graph.replay()  # warm replay
+            launches[i % n]()
+    timed.replay()  # first replay of a fresh graph carries one-time set-up
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    while True:
+        rotation.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= WARM_SECONDS:
+            break
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(4 * PAIRS)]
     with torch.cuda.stream(stream):
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-    end.synchronize()
-    return start.elapsed_time(end) / steps
+        for p in range(PAIRS):
+            a, b, c, d = marks[4 * p: 4 * p + 4]
+            a.record(stream)
+            rotation.replay()
+            b.record(stream)
+            c.record(stream)
+            timed.replay()
+            d.record(stream)
+    torch.cuda.synchronize()
+    diffs = sorted(marks[4 * p + 2].elapsed_time(marks[4 * p + 3]) - marks[4 * p].elapsed_time(marks[4 * p + 1])
+                   for p in range(PAIRS))
+    return diffs[PAIRS // 2] / steps
 
 
 def copies_for(bytes_per_set: int, minimum: int = 1) -> int:
@@ -97,10 +136,11 @@ def bench_w4a16(M: int, K: int, N: int, steps: int, warmup: int, kernel: str = "
     sets = [(d["x"].clone(), d["packed"].clone(), d["scales"].clone(), d["zeros"].clone()) for _ in range(n)]
     calls = [art.prepare(*s) for s in sets]
     ms = graph_time([c.launch for c in calls], steps, warmup)
-    entry = art.observation.entry
+    entry, kernel = art.observation.entry, art.observation.kernel
     del calls, sets
     torch.cuda.empty_cache()
-    return {"ms": ms, "work": work, "entry": entry, "copies": n}
+    return {"ms": ms, "work": work, "entry": entry, "kernel": kernel, "copies": n,
+            "rotation_bytes": n * work.bytes}
 
 
 def bench_w8a16(steps: int, warmup: int) -> dict:
@@ -328,12 +368,37 @@ def bench_mxfp8(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": n}
 
 
-def measured_traffic() -> int | None:
-    """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE profile."""
+def bench_i8_quant(steps: int, warmup: int) -> dict:
+    """Per-token int8 quantizer feeding config 3: f16 [4096, 8192] -> int8 + f32 scales."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    M, K = 4096, 8192
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn((M, K), device="cuda", generator=g).half()
+    work = inputs.Workload(f"per-token int8 quantize M{M} K{K} f16", 0, M * K * 2 + M * K + M * 4)
+    art = intent.compile(intent.per_token_int8_quantize, target=intent.MI355XTarget(0))
+    n = copies_for(work.bytes, minimum=2)
+    calls = [art.prepare(x.clone()) for _ in range(n)]
+    ms = graph_time([c.launch for c in calls], steps, warmup)
+    del calls
+    torch.cuda.empty_cache()
+    return {"ms": ms, "work": work, "copies": n}
+
+
+def measured_traffic(kernel: str) -> int | None:
+    """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE profile, if that
+    profile covers `kernel` (the variant this run dispatched to); otherwise None."""
     path = ROOT / "profiles" / "w4a16_gemv_dot_m1_traffic.md"
     if not path.exists():
         return None
-    for line in path.read_text().splitlines():
+    text = path.read_text().splitlines()
+    covered = next((ln.split(":", 1)[1].strip() for ln in text if ln.startswith("kernel:")), None)
+    if covered is None or covered.replace(" ", "") != kernel.replace(" ", ""):
+        return None
+    for line in text:
         if line.startswith("traffic_bytes_per_launch:"):
             return int(line.split(":")[1])
     return None
@@ -357,6 +422,114 @@ def traffic_probe() -> None:
         b = torch.empty(n, dtype=torch.uint8, device="cuda")
         b.copy_(a)
     torch.cuda.synchronize()
+
+
+def read_probe(steps: int) -> None:
+    """Plain HBM read of the decode's bytes vs the decode GEMV, both rotated over the same copy count."""
+    import ctypes
+
+    import torch
+
+    from intent_amd import _native, inputs
+
+    work = inputs.w4a16_work(1, 4096, 4096)
+    nbytes = (work.bytes + 15) // 16 * 16
+    n = copies_for(nbytes)
+    bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(n)]
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    lib = _native.library()
+    results = {}
+    for unroll in (1, 2, 4, 8, 16):
+        def make(buf, u=unroll):
+            def go():
+                stream = torch.cuda.current_stream().cuda_stream
+                st = lib.intent_hbm_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes, u,
+                                               ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream))
+                if st != 0:
+                    raise RuntimeError(_native.last_error())
+            return go
+        ms = graph_time([make(b) for b in bufs], steps, 10)
+        results[f"hbm_read_probe_kernel<{unroll}>"] = ms
+        log(f"[probe] read unroll={unroll}: {ms * 1e3:.3f} us, {nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
+    del bufs
+    torch.cuda.empty_cache()
+    dec = bench_w4a16(1, 4096, 4096, steps, 10)
+    results[dec["kernel"]] = dec["ms"]
+    log(f"[probe] decode {dec['kernel']}: {dec['ms'] * 1e3:.3f} us")
+    print(json.dumps({"probe": "read", "bytes": nbytes, "copies": n, "steps": steps,
+                      "us": {k: round(v * 1e3, 4) for k, v in results.items()},
+                      "GB/s": {k: round(nbytes / (v * 1e-3) / 1e9, 1) for k, v in results.items()}}), flush=True)
+
+
+def mfma_ceiling() -> dict:
+    """Sustained register-only MFMA rate (f16 and i8) over the whole chip, timed with HIP events."""
+    import ctypes
+
+    import torch
+
+    from intent_amd import _native
+
+    lib = _native.library()
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    out = {}
+    wgs, iters = 2048, 64  # 8 waves per SIMD; about 35 ms per launch
+    for kind, label, per in ((0, "f16", 32768), (1, "i8", 65536)):
+        def go():
+            st = lib.intent_mfma_peak_probe(kind, iters, wgs, ctypes.c_void_p(sink.data_ptr()),
+                                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if st != 0:
+                raise RuntimeError(_native.last_error())
+        go()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(5):
+            go()
+        b.record()
+        b.synchronize()
+        ms = a.elapsed_time(b) / 5
+        flops = wgs * 4 * iters * 4 * per
+        out[label] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1)}
+        log(f"[probe] mfma ceiling {label}: {out[label]}")
+    return out
+
+
+def mfma_probe() -> None:
+    """The MFMA ceiling probe, then three plain launches of each compute-bound line, for
+    per-dispatch rocprofv3 counters."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    print(json.dumps({"probe": "mfma_ceiling", **mfma_ceiling()}), flush=True)
+    target = intent.MI355XTarget(0)
+    d = inputs.to_device(inputs.config1_w4a16_decode(0, M=2048, K=4096, N=11008))
+    art = intent.compile(intent.weight_only_int4_asym_matmul, target=target)
+    call = art.prepare(d["x"], d["packed"], d["scales"], d["zeros"])
+    for _ in range(3):
+        call.launch()
+    torch.cuda.synchronize()
+    log(f"[probe] prefill: {art.observation.kernel}")
+    del call, d
+    d = inputs.to_device(inputs.config3_w8a8(0))
+    art = intent.compile(intent.w8a8_scaled_matmul, target=target)
+    call = art.prepare(d["a"], d["a_scales"], d["w"], d["w_scales"])
+    for _ in range(3):
+        call.launch()
+    torch.cuda.synchronize()
+    log(f"[probe] w8a8: {art.observation.kernel}")
+    del call, d
+    h = inputs.config4_moe(0)
+    d = inputs.to_device(h)
+    T, H = h["x"].shape
+    art = intent.compile(intent.moe_expert_ffn_w4, target=target, constexprs={"TOP_K": 2})
+    y = torch.zeros(T, H, dtype=torch.float32, device="cuda")
+    call = art.prepare(d["logits"], d["x"], d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"], y)
+    for _ in range(3):
+        call.launch()
+    torch.cuda.synchronize()
+    log("[probe] moe done")
 
 
 def cpu_baseline(budget_s: float) -> dict:
@@ -397,6 +570,12 @@ def main() -> int:
     if args.probe == "traffic":
         traffic_probe()
         return 0
+    if args.probe == "read":
+        read_probe(args.steps)
+        return 0
+    if args.probe == "mfma":
+        mfma_probe()
+        return 0
     arch = _native.device_arch(0)
     log(f"[bench] device 0: {arch}; decode M=1 steps={args.steps} warmup={args.warmup}")
     dec = bench_w4a16(1, 4096, 4096, args.steps, args.warmup)
@@ -416,21 +595,25 @@ def main() -> int:
         "dtype": "f16",
         "data": "synthetic: seeded numpy draws of BASELINE configs (weights copied to exceed MALL)",
         "config": {"workload": "w4a16 decode GEMV M=1 K=4096 N=4096 g128 asymmetric uint4 (BASELINE configs[1])",
-                   "kernel": dec["entry"], "weight_copies": dec["copies"], "arch": arch},
+                   "entry": dec["entry"], "weight_copies": dec["copies"],
+                   "rotation_bytes": dec["rotation_bytes"], "arch": arch},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "bytes_per_launch": dec["work"].bytes, "kernel": "w4a16_gemv_dot_kernel<1,2,4,4>"},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dec["kernel"]),
+                     "bytes_per_launch": dec["work"].bytes, "kernel": dec["kernel"]},
     }
     extra = {}
     if args.only == "all":
         steps = max(10, min(args.steps, 50))
-        warm = max(2, min(args.warmup, 5))
+        warm = max(2, min(args.warmup, 5))  # plus WARM_SECONDS of rotation replays inside graph_time
         log("[bench] decode M=16")
         r = bench_w4a16(16, 4096, 4096, args.steps, args.warmup)
-        extra["w4a16_decode_m16"] = _hbm_entry(r)
+        extra["w4a16_decode_m16"] = dict(_hbm_entry(r), kernel=r["kernel"], rotation_bytes=r["rotation_bytes"])
         log("[bench] prefill M=2048 N=11008")
         r = bench_w4a16(2048, 4096, 11008, steps, warm)
         extra["w4a16_prefill_m2048"] = _flop_entry(r, F16_PEAK_TFLOPS, "TFLOP/s")
+        log("[bench] per-token int8 quantize M=4096 K=8192")
+        r = bench_i8_quant(args.steps, args.warmup)
+        extra["i8_per_token_quantize_m4096_k8192"] = _hbm_entry(r)
         log("[bench] w8a8 M=4096 K=N=8192")
         r = bench_w8a8(steps, warm)
         extra["w8a8_m4096"] = _flop_entry(r, I8_PEAK_TOPS, "TOP/s")

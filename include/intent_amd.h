@@ -48,6 +48,10 @@ extern "C" {
 /* Library facts. */
 int intent_amd_abi_version(void);
 const char* intent_amd_last_error(void);
+/* Name of the last kernel the calling thread launched through this library
+ * (the kernel variant an entry dispatched to, e.g. for profiling reports);
+ * "" before the first launch. */
+const char* intent_amd_last_kernel(void);
 /* Writes the gcnArchName of `device` into buf; returns INTENT_OK or an error. */
 int intent_amd_device_arch(int device, char* buf, int64_t buf_len);
 
@@ -470,6 +474,36 @@ int intent_f16_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld, const voi
  */
 int intent_nvfp4_quantize(const void* x, int64_t M, int64_t N, int64_t x_ld, const float* global_scale,
                           uint8_t* packed, int64_t packed_ld, uint8_t* scales, void* stream);
+
+/* Per-token symmetric int8 activation quantizer, the producer of
+ * intent_w8a8_gemm's int8 activations and f32 per-token scales. Applies the
+ * reference's integer quantization rule (clamp to [-128, 127], then round half
+ * to even: lib/Conversion/KIRToGPU/Quantization.cpp:191-203) per row:
+ * scale[m] = absmax / 127, q = rne(clamp(x * (127 / absmax))), both divisions
+ * IEEE f32; a zero row gives scale 0 and q 0. x f16 (x_is_bf16 = 0) or bf16
+ * [M, K] (x_ld elements, 16-byte aligned rows, K % 8 == 0); q int8 [M, K]
+ * (q_ld, 8-byte aligned rows); scales f32 [M]. Inputs are finite.
+ */
+int intent_i8_per_token_quantize(const void* x, int x_is_bf16, int64_t M, int64_t K, int64_t x_ld,
+                                 int8_t* q, int64_t q_ld, float* scales, void* stream);
+
+/* Measurement support, no counterpart in the reference: reads `bytes` (a
+ * multiple of 16) of `buf` once with the plainest coalesced 16-byte loads,
+ * each workgroup of 256 lanes covering 256 * unroll * 16 contiguous bytes
+ * (unroll in {1, 2, 4, 8, 16}). Its duration is the HBM read floor that a
+ * streaming kernel over the same bytes is compared with. `sink` (256 uint32,
+ * device) is written only on a hash coincidence.
+ */
+int intent_hbm_read_probe(const void* buf, int64_t bytes, int unroll, uint32_t* sink, void* stream);
+
+/* Measurement support, no counterpart in the reference: `workgroups` groups of
+ * four waves each issue `iters` rounds of four independent register-only
+ * 32x32 MFMAs (kind 0: f16, 32768 flops each; kind 1: i8, 65536 ops each). The
+ * rate it reaches is the matrix cores' sustained ceiling at the clock the chip
+ * holds under that load, the practical bound for the compute-bound kernels.
+ * `sink` (256 uint32, device) is written only on a value coincidence.
+ */
+int intent_mfma_peak_probe(int kind, int64_t iters, int64_t workgroups, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,6 +27,7 @@ F32 = ctypes.c_float
 SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_amd_abi_version": ([], INT),
     "intent_amd_last_error": ([], ctypes.c_char_p),
+    "intent_amd_last_kernel": ([], ctypes.c_char_p),
     "intent_amd_device_arch": ([INT, ctypes.c_char_p, I64], INT),
     "intent_w8a16_matmul": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P], INT),
     "intent_w4a16_matmul": ([P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, I64, P], INT),
@@ -61,6 +62,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_moe_workspace_size": ([I64, I64, I64, I64, I64, I64], SIZE),
     "intent_moe_expert_ffn_w4": ([P, P, I64, I64, I64, I64, INT, P, P, P, P, P, P, I64, I64, P, P, SIZE, P, P, P],
                                  INT),
+    "intent_i8_per_token_quantize": ([P, INT, I64, I64, I64, P, I64, P, P], INT),
+    "intent_hbm_read_probe": ([P, I64, INT, P, P], INT),
+    "intent_mfma_peak_probe": ([INT, I64, I64, P, P], INT),
 }
 
 _lock = threading.Lock()
@@ -96,6 +100,12 @@ def library() -> ctypes.CDLL:
 
 def last_error() -> str:
     raw = library().intent_amd_last_error()
+    return raw.decode("utf-8", "replace") if raw else ""
+
+
+def last_kernel() -> str:
+    """The kernel variant the calling thread's latest launch dispatched to."""
+    raw = library().intent_amd_last_kernel()
     return raw.decode("utf-8", "replace") if raw else ""
 
 

@@ -24,8 +24,11 @@ inline bool fits_offset(int64_t rows, int64_t stride_bytes) {
          rows * stride_bytes < ((int64_t)1 << 31);
 }
 
-// Checks hipGetLastError() after a launch.
+// Checks hipGetLastError() after a launch and records `kernel` as the
+// thread's last launched kernel (intent_amd_last_kernel()).
 int launch_status(const char* kernel);
+// Same, with a printf-formatted kernel name (template parameters).
+int launch_status_fmt(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 
 }  // namespace intent
 

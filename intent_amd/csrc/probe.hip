@@ -1,0 +1,103 @@
+// HBM read-floor probe: the fastest plain read of a buffer, used to measure
+// what any kernel that streams the same bytes once can reach (the decode
+// GEMV's own floor at its size). Not part of any operator.
+//
+// A workgroup of 256 lanes reads 256 * U * 16 contiguous bytes: lane t loads
+// 16 bytes at t, t + 256, ... (U loads, all issued before any is used). The
+// values are folded with XOR and stored only if they hit a magic word, which
+// keeps the loads live without writing anything in practice.
+#include "common.h"
+#include "internal.h"
+
+namespace {
+
+template <int U>
+__global__ __launch_bounds__(256) void hbm_read_probe_kernel(const u32x4* __restrict__ src, int64_t n16,
+                                                             uint32_t* __restrict__ sink) {
+  const int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x;
+  u32x4 v[U];
+#pragma unroll
+  for (int i = 0; i < U; ++i) {
+    const int64_t idx = base + (int64_t)i * 256;
+    v[i] = idx < n16 ? src[idx] : u32x4{0u, 0u, 0u, 0u};
+  }
+  uint32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < U; ++i) s ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+  if (s == 0x9e3779b9u) sink[blockIdx.x & 255] = s;
+}
+
+template <int U>
+void launch_probe(const void* buf, int64_t n16, uint32_t* sink, hipStream_t st) {
+  const int64_t per = 256 * U;
+  const unsigned blocks = (unsigned)((n16 + per - 1) / per);
+  hipLaunchKernelGGL(hbm_read_probe_kernel<U>, dim3(blocks), dim3(256), 0, st, (const u32x4*)buf, n16, sink);
+}
+
+// MFMA issue-rate probe: every wave runs `iters` rounds of four independent
+// 32x32 MFMAs on register operands (no memory traffic), so the measured rate
+// is the matrix cores' sustained throughput at the clock the chip holds under
+// that load. kind 0: v_mfma_f32_32x32x16_f16 (32768 flops each); kind 1:
+// v_mfma_i32_32x32x32_i8 (65536 ops each).
+template <int kKind>
+__global__ __launch_bounds__(256) void mfma_peak_probe_kernel(int64_t iters, uint32_t* __restrict__ sink) {
+  const uint32_t seed = threadIdx.x * 2654435761u + blockIdx.x;
+  if constexpr (kKind == 0) {
+    const f16x8 a = bit_cast<f16x8>(u32x4{seed, seed ^ 1u, seed ^ 2u, seed ^ 3u} & 0x3bff3bffu);
+    const f16x8 b = bit_cast<f16x8>(u32x4{seed ^ 5u, seed ^ 6u, seed ^ 7u, seed ^ 8u} & 0x3bff3bffu);
+    f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int64_t i = 0; i < iters; ++i) {
+      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, a, c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, b, c3, 0, 0, 0);
+    }
+    const float t = c0[0] + c1[1] + c2[2] + c3[3];
+    if (t == 1234.5f) sink[blockIdx.x & 255] = 1u;
+  } else {
+    const i32x4 a4 = {(int)seed, (int)(seed ^ 1u), (int)(seed ^ 2u), (int)(seed ^ 3u)};
+    const i32x4 b4 = {(int)(seed ^ 5u), (int)(seed ^ 6u), (int)(seed ^ 7u), (int)(seed ^ 8u)};
+    i32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+    for (int64_t i = 0; i < iters; ++i) {
+      c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, b4, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b4, a4, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a4, a4, c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b4, b4, c3, 0, 0, 0);
+    }
+    const int t = c0[0] + c1[1] + c2[2] + c3[3];
+    if (t == 1234567) sink[blockIdx.x & 255] = 1u;
+  }
+}
+
+}  // namespace
+
+extern "C" int intent_mfma_peak_probe(int kind, int64_t iters, int64_t workgroups, uint32_t* sink, void* stream) {
+  INTENT_REQUIRE(sink, INTENT_ERR_INVALID_ARGUMENT, "null sink");
+  INTENT_REQUIRE(iters > 0 && workgroups > 0 && workgroups <= (1 << 20), INTENT_ERR_INVALID_ARGUMENT,
+                 "bad iters / workgroups");
+  hipStream_t st = (hipStream_t)stream;
+  if (kind == 0)
+    hipLaunchKernelGGL(mfma_peak_probe_kernel<0>, dim3((unsigned)workgroups), dim3(256), 0, st, iters, sink);
+  else if (kind == 1)
+    hipLaunchKernelGGL(mfma_peak_probe_kernel<1>, dim3((unsigned)workgroups), dim3(256), 0, st, iters, sink);
+  else
+    return intent::fail(INTENT_ERR_UNSUPPORTED, "kind must be 0 (f16) or 1 (i8), got %d", kind);
+  return intent::launch_status_fmt("mfma_peak_probe_kernel<%d>", kind);
+}
+
+extern "C" int intent_hbm_read_probe(const void* buf, int64_t bytes, int unroll, uint32_t* sink, void* stream) {
+  INTENT_REQUIRE(buf && sink, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(bytes > 0 && bytes % 16 == 0, INTENT_ERR_INVALID_ARGUMENT, "bytes must be a positive multiple of 16");
+  INTENT_REQUIRE(intent::aligned16(buf), INTENT_ERR_ALIGNMENT, "buffer must be 16-byte aligned");
+  const int64_t n16 = bytes / 16;
+  hipStream_t st = (hipStream_t)stream;
+  switch (unroll) {
+    case 1: launch_probe<1>(buf, n16, sink, st); break;
+    case 2: launch_probe<2>(buf, n16, sink, st); break;
+    case 4: launch_probe<4>(buf, n16, sink, st); break;
+    case 8: launch_probe<8>(buf, n16, sink, st); break;
+    case 16: launch_probe<16>(buf, n16, sink, st); break;
+    default: return intent::fail(INTENT_ERR_UNSUPPORTED, "unroll must be 1, 2, 4, 8 or 16, got %d", unroll);
+  }
+  return intent::launch_status_fmt("hbm_read_probe_kernel<%d>", unroll);
+}

@@ -297,6 +297,8 @@ void launch_dot(const f16* x, int64_t ldx, int K, const uint8_t* wq, int64_t ldw
                      ldq, gs, y, ldy, N);
 }
 
+
+
 // Picks the chunk count CH (K <= 2048*CH) for the dot kernel; returns false if
 // M*CH exceeds the register budget.
 template <int M>
@@ -419,7 +421,11 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
     case 3: done = dispatch_dot<3>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
     default: break;
   }
-  if (done) return launch_status("w4a16_gemv_dot");
+  if (done) {
+    const int ch = (int)((K + 2047) / 2048);
+    const int chv = ch <= 1 ? 1 : ch <= 2 ? 2 : ch <= 4 ? 4 : 8;
+    return launch_status_fmt("w4a16_gemv_dot_kernel<%d, %d, %d, 4>", (int)M, chv, chv >= 8 ? 1 : 8 / chv);
+  }
   const int steps = (int)(K / 128);
   if (steps >= 16)
     launch_gemv<1, 16>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
@@ -427,7 +433,7 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
     launch_gemv<1, 8>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
   else
     launch_gemv<1, 4>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
-  return launch_status("w4a16_gemv");
+  return launch_status_fmt("w4a16_gemv_kernel<1, %d>", steps >= 16 ? 16 : steps >= 8 ? 8 : 4);
 }
 
 int w8a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const int8_t* w, int64_t N, int64_t w_ld,

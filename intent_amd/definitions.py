@@ -540,6 +540,35 @@ bf16_groupwise_fp8_quantize = _fp8q_definition("bf16_groupwise_fp8_quantize", "b
 f32_groupwise_fp8_quantize = _fp8q_definition("f32_groupwise_fp8_quantize", "f32", "42-69")
 
 
+# ---- per-token int8 activation quantizer (feeds w8a8_scaled_matmul) -------------------
+
+def _i8q_launch(bf16: bool):
+    def launch(v: dict, env: dict, stream: int, workspace) -> str:
+        x, q, sc = v["x"], v["quantized"], v["scales"]
+        _native.call("intent_i8_per_token_quantize", _ptr(x), int(bf16), env["M"], env["K"], _ld(x), _ptr(q),
+                     _ld(q), _ptr(sc), stream)
+        return "intent_i8_per_token_quantize"
+    return launch
+
+
+def _i8q_definition(name: str, src: str) -> KernelDefinition:
+    return KernelDefinition(
+        name=name,
+        params=(
+            Param("x", src, ("M", "K"), leading_stride=True),
+            Param("quantized", "i8", ("M", "K"), OUT, leading_stride=True),
+            Param("scales", "f32", ("M",), OUT),
+        ),
+        launch=_i8q_launch(src == "bf16"),
+        reference="lib/Conversion/KIRToGPU/Quantization.cpp:191-203 (clamp, then round half to even)",
+        doc="scale = absmax(row) / 127; quantized = rne(clamp(x * (127 / absmax), -128, 127)); zero row -> 0",
+    )
+
+
+per_token_int8_quantize = _i8q_definition("per_token_int8_quantize", "f16")
+bf16_per_token_int8_quantize = _i8q_definition("bf16_per_token_int8_quantize", "bf16")
+
+
 # ---- low-bit weight x int8 activation (exact int32) ---------------------------------
 
 def _lowbit_check(per_byte: int):
@@ -1043,5 +1072,5 @@ ALL_DEFINITIONS = (
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
     deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul, dequant_bf16_fp4_matmul, quantized_gemm,
     ragged_grouped_gemm, ragged_grouped_gemm_bf16, routed_expert_projection_bf16, gemm, bf16_gemm,
-    nvfp4_quantize,
+    nvfp4_quantize, per_token_int8_quantize, bf16_per_token_int8_quantize,
 )

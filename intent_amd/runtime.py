@@ -26,6 +26,7 @@ class NativeObservation:
     arch: str
     library: str
     constexprs: dict = field(default_factory=dict)
+    kernel: str = ""  # the kernel variant the entry dispatched to
 
 
 @dataclass(frozen=True)
@@ -186,7 +187,7 @@ class HIPRuntime:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         entry = self.definition.launch(binding.views, binding.env, stream, binding.workspace)
         self.observation = NativeObservation(entry, self.definition.name, self.arch, str(_native.LIBRARY_PATH),
-                                             dict(self.constexprs))
+                                             dict(self.constexprs), _native.last_kernel())
 
     # ---- provider surface -------------------------------------------------------
     def run(self, *arguments):

@@ -69,6 +69,8 @@ def lib():
         _lib.orc_f32_to_e4m3fn.restype = ctypes.c_uint8
         _lib.orc_fp8_groupwise_quantize.argtypes = [p, i64, i64, i64, i64, ctypes.c_float, p, i64, p, i64]
         _lib.orc_fp8_groupwise_quantize.restype = None
+        _lib.orc_i8_per_token_quantize.argtypes = [p, i64, i64, i64, p, i64, p]
+        _lib.orc_i8_per_token_quantize.restype = None
         _lib.orc_w4a8.argtypes = [p, i64, i64, p, i64, p, ci]
         _lib.orc_bitnet_int2.argtypes = [p, i64, i64, p, i64, p, ci]
         _lib.orc_w4a8.restype = None
@@ -251,6 +253,29 @@ def fp8_groupwise_quantize(x, groups: int | None = None, source: str = "f32"):
     sc = np.empty((M, G), np.float32)
     lib().orc_fp8_groupwise_quantize(_ptr(x), M, N, N, G, FP8_EPS[source], _ptr(q), N, _ptr(sc), G)
     return q, sc
+
+
+def i8_per_token_quantize(x):
+    """[M, K] values (f16 / bf16 widened exactly to f32, or f32) -> (int8 [M, K], scales f32 [M])."""
+    x = _c(x, np.float32)
+    M, K = x.shape
+    q = np.empty((M, K), np.int8)
+    sc = np.empty((M,), np.float32)
+    lib().orc_i8_per_token_quantize(_ptr(x), M, K, K, _ptr(q), K, _ptr(sc))
+    return q, sc
+
+
+def i8_per_token_quantize_np(x):
+    """numpy restatement, written apart from the C one: np.rint is round-half-even."""
+    x = np.asarray(x, np.float32)
+    amax = np.max(np.abs(x), axis=1) if x.shape[1] else np.zeros(x.shape[0], np.float32)
+    amax = amax.astype(np.float32)
+    zero = amax == 0
+    safe = np.where(zero, np.float32(1), amax)
+    scale = np.where(zero, np.float32(0), safe / np.float32(127)).astype(np.float32)
+    inv = np.where(zero, np.float32(0), np.float32(127) / safe).astype(np.float32)
+    t = np.clip(x * inv[:, None], np.float32(-128), np.float32(127))
+    return np.rint(t).astype(np.int8), scale
 
 
 def f32_to_e4m3fn(values) -> np.ndarray:

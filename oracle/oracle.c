@@ -814,3 +814,32 @@ void orc_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t N, float gs, uint8
     }
   }
 }
+
+/* ---- per-token symmetric int8 activation quantizer -------------------------
+ * absmax = max |x[m,:]|, scale = absmax / 127, inv = 127 / absmax (f32
+ * divisions), q = rne(clamp(x * inv, -128, 127)); a zero row gives scale 0 and
+ * q 0. The clamp-then-round-half-even rule is the reference's integer
+ * quantization (lib/Conversion/KIRToGPU/Quantization.cpp:191-203), written
+ * here with floor and the parity of the floor as it does. */
+void orc_i8_per_token_quantize(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq,
+                               float* scales) {
+  for (int64_t m = 0; m < M; ++m) {
+    float amax = 0.0f;
+    for (int64_t k = 0; k < K; ++k) {
+      const float a = fabsf(x[m * ldx + k]);
+      if (a > amax) amax = a;
+    }
+    const float scale = amax == 0.0f ? 0.0f : amax / 127.0f;
+    const float inv = amax == 0.0f ? 0.0f : 127.0f / amax;
+    scales[m] = scale;
+    for (int64_t k = 0; k < K; ++k) {
+      float t = x[m * ldx + k] * inv;
+      t = t < -128.0f ? -128.0f : (t > 127.0f ? 127.0f : t);
+      const float fl = floorf(t);
+      const float frac = t - fl;
+      const int32_t base = (int32_t)fl;
+      const int up = frac > 0.5f || (frac == 0.5f && (base & 1) != 0);
+      q[m * ldq + k] = (int8_t)(base + up);
+    }
+  }
+}

@@ -32,6 +32,8 @@ void orc_q4k_gemv(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld, const ui
 uint8_t orc_f32_to_e4m3fn(float f);
 void orc_fp8_groupwise_quantize(const float* x, int64_t M, int64_t N, int64_t ldx, int64_t G, float eps,
                                 uint8_t* q, int64_t ldq, float* scales, int64_t lds_);
+void orc_i8_per_token_quantize(const float* x, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq,
+                               float* scales);
 void orc_w4a8(const int8_t* a, int64_t M, int64_t K, const uint8_t* packed, int64_t N, int32_t* out, int threads);
 void orc_bitnet_int2(const int8_t* a, int64_t M, int64_t K, const uint8_t* packed, int64_t N, int32_t* out,
                      int threads);

@@ -408,6 +408,56 @@ def test_fp8_groupwise_quantize_bit_exact(gpu, src, M, N, G):
     assert np.array_equal(host(scales).view(np.uint32), ref_s.view(np.uint32))
 
 
+# ---- per-token int8 quantizer: bit-exact ------------------------------------------------
+
+@pytest.mark.parametrize("src", ["f16", "bf16"])
+@pytest.mark.parametrize("M,K", [(1, 8), (3, 24), (5, 2056), (64, 4096), (17, 16392), (4096, 8192), (2, 0)])
+def test_i8_per_token_quantize_bit_exact(gpu, src, M, K):
+    rng = np.random.default_rng(M * 13 + K)
+    x = (rng.standard_normal((M, K)) * rng.uniform(1e-3, 1e3, (M, 1))).astype(np.float32)
+    if K >= 16:
+        x[0, :10] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5, 126.5, -127.0]  # ties at scale 1
+        x[0, 10:] = 0.0
+    if M > 2 and K:
+        x[1] = 0.0  # zero row
+        x[2, K // 2] = -1e-6  # lone tiny value
+    tdt = torch.float16 if src == "f16" else torch.bfloat16
+    xt = torch.from_numpy(x).to(tdt)
+    ref_q, ref_s = oracle.i8_per_token_quantize(xt.float().numpy())  # exact widening of the same values
+    defn = intent.per_token_int8_quantize if src == "f16" else intent.bf16_per_token_int8_quantize
+    q, sc = art(defn).run(xt.cuda())
+    assert np.array_equal(host(q), ref_q)
+    assert np.array_equal(host(sc).view(np.uint32), ref_s.view(np.uint32))
+
+
+def test_i8_per_token_strided_rows(gpu):
+    rng = np.random.default_rng(11)
+    big = torch.from_numpy(rng.standard_normal((9, 1040)).astype(np.float16))
+    x = big[:, 8:1032]  # rows 2080 bytes apart, 16-byte aligned start
+    qbuf = torch.full((9, 1040), 77, dtype=torch.int8, device="cuda")
+    q = qbuf[:, :1024]
+    sc = torch.empty(9, dtype=torch.float32, device="cuda")
+    art(intent.per_token_int8_quantize).launch(big.cuda()[:, 8:1032], q, sc)
+    ref_q, ref_s = oracle.i8_per_token_quantize(x.float().numpy())
+    got = host(qbuf)
+    assert np.array_equal(got[:, :1024], ref_q) and np.all(got[:, 1024:] == 77)
+    assert np.array_equal(host(sc), ref_s)
+
+
+def test_quantize_then_w8a8_chain(gpu, threads):
+    """Per-token int8 quantizer feeding the W8A8 GEMM, against the oracle's chain (bit-exact bf16)."""
+    rng = np.random.default_rng(21)
+    M, K, N = 256, 1024, 384
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16))
+    w = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    sw = rng.uniform(0.001, 0.01, N).astype(np.float32)
+    q, sa = art(intent.per_token_int8_quantize).run(x.cuda())
+    out = art(intent.w8a8_scaled_matmul).run(q, sa, dev(w), dev(sw))
+    rq, rs = oracle.i8_per_token_quantize(x.float().numpy())
+    ref = oracle.w8a8(rq, rs, w, sw, threads)
+    assert np.array_equal(host(out.view(torch.int16)).view(np.uint16), ref)
+
+
 # ---- W4A8 and BitNet int2: exact int32 ----------------------------------------------
 
 @pytest.mark.parametrize("M,K,N", [(1, 128, 1), (37, 256, 100), (300, 384, 130), (512, 2048, 1024), (4000, 256, 4100),

@@ -801,3 +801,51 @@ def test_nvfp4_quantize_matches_reference_formula():
     ref_scales = scale.view(torch.uint8).reshape(M // 128, 4, 32, N // 64, 4).permute(0, 3, 2, 1, 4).numpy()
     assert np.array_equal(packed, ref_packed)
     assert np.array_equal(scales, ref_scales)
+
+
+# ---- per-token int8 quantizer ---------------------------------------------------------
+
+def test_i8_per_token_known_answers():
+    # amax 127 makes 127/amax exactly 1, so q is x rounded half to even
+    x = np.zeros((3, 16), np.float32)
+    x[0, :10] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5, 126.5, -127.0]
+    x[2, 3] = -0.25  # lone value: amax 0.25, q -127, scale 0.25/127
+    q, s = oracle.i8_per_token_quantize(x)
+    assert list(q[0, :10]) == [127, 2, 4, -2, -4, 0, 0, 2, 126, -127]
+    assert s[0] == np.float32(1.0)
+    assert s[1] == 0 and not q[1].any()  # zero row: scale 0, codes 0
+    assert q[2, 3] == -127 and s[2] == np.float32(0.25) / np.float32(127)
+    assert not np.delete(q[2], 3).any()
+
+
+@pytest.mark.parametrize("M,K", [(7, 64), (33, 1000), (4, 8200)])
+def test_i8_per_token_matches_numpy_and_bounds(M, K):
+    rng = np.random.default_rng(M + K)
+    x = (rng.standard_normal((M, K)) * rng.uniform(1e-4, 1e3, (M, 1))).astype(np.float16).astype(np.float32)
+    x[0] = 0.0
+    q, s = oracle.i8_per_token_quantize(x)
+    qn, sn = oracle.i8_per_token_quantize_np(x)
+    assert np.array_equal(q, qn) and np.array_equal(s.view(np.uint32), sn.view(np.uint32))
+    # every code is the nearest level: |x - q*scale| <= scale/2 (float64, a little slack for the f32 inverse)
+    err = np.abs(x.astype(np.float64) - q.astype(np.float64) * s[:, None].astype(np.float64))
+    assert np.all(err <= s[:, None] * (0.5 + 1e-5) + 1e-30)
+    # the largest magnitude of every non-zero row lands on +-127 and nothing leaves [-127, 127]
+    nz = s > 0
+    assert np.all(np.abs(q[nz]).max(axis=1) == 127) and np.abs(q.astype(np.int32)).max() <= 127
+
+
+def test_i8_per_token_brute_force_tiny():
+    # python float64 restatement of every step on a handful of values, including ties
+    rng = np.random.default_rng(3)
+    x = (rng.integers(-300, 301, (5, 8)) / 4.0).astype(np.float32)
+    q, s = oracle.i8_per_token_quantize(x)
+    for m in range(5):
+        amax = float(np.float32(max(abs(float(v)) for v in x[m])))
+        inv = float(np.float32(127.0) / np.float32(amax)) if amax else 0.0
+        for k in range(8):
+            t = float(np.float32(np.float32(x[m, k]) * np.float32(inv)))
+            t = min(max(t, -128.0), 127.0)
+            lo = np.floor(t)
+            frac = t - lo
+            r = lo + (1 if frac > 0.5 or (frac == 0.5 and int(lo) % 2 != 0) else 0)
+            assert q[m, k] == int(r), (m, k, x[m, k], t)
