@@ -272,6 +272,21 @@ int intent_q4k_projection(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld,
                           float* y, void* stream);
 
 /*
+ * intent_q4k_projection without the caller's record buffer: no counterpart in
+ * the reference; for callers that cannot allocate (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc). Same arguments and
+ * result as intent_q4k_projection minus xq_records; the Q8_K records live in a
+ * fixed device array of the library (one per GPU, 299,008 bytes, kept until
+ * the process ends), so G <= 1024 (K <= 262144), else INTENT_ERR_UNSUPPORTED.
+ * Allocates nothing (the array's device address is looked up on the first
+ * call on each device, with that device current: make that first call
+ * outside graph capture). Calls that overlap on one GPU share the array and
+ * race; serialise them (one stream, or events).
+ */
+int intent_q4k_projection_noalloc(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld,
+                                  const float* x, int64_t x_ld, float* y, void* stream);
+
+/*
  * Groupwise FP8 activation quantizer, bit-exact: for each row and group of
  * 128 columns, scale = max(absmax, eps) / 448 (eps = 1e-12 for bf16 input,
  * 1e-4 for f32), q = E4M3FN(min(max(x / scale, -448), 448)) rounded to

@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_q8k_quantize": ([P, I64, I64, P, I64, P], INT),
     "intent_q4k_q8k_gemv": ([P, I64, I64, I64, P, P, P], INT),
     "intent_q4k_projection": ([P, I64, I64, I64, P, I64, P, P, P], INT),
+    "intent_q4k_projection_noalloc": ([P, I64, I64, I64, P, I64, P, P], INT),
     "intent_fp8_groupwise_quantize": ([P, INT, I64, I64, I64, P, I64, P, I64, I64, P], INT),
     "intent_w4a8_gemm": ([P, I64, I64, I64, P, I64, I64, P, I64, P], INT),
     "intent_bitnet_int2_gemm": ([P, I64, I64, I64, P, I64, I64, P, I64, P], INT),

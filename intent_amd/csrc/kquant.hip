@@ -13,6 +13,8 @@
 // from +0. The kernels reproduce that order exactly, so results are bit-equal
 // to a sequential CPU evaluation.
 #include "common.h"
+#include <mutex>
+
 #include "internal.h"
 
 namespace {
@@ -334,4 +336,54 @@ extern "C" int intent_q4k_projection(const uint8_t* w, int64_t N, int64_t G, int
     if (st != INTENT_OK) return st;
   }
   return intent_q4k_q8k_gemv(w, N, G, w_ld, xq_records, y, stream);
+}
+
+// ---- allocation-free Q4_K projection ----------------------------------------------
+// intent_q4k_projection_noalloc keeps the Q8_K records of the activation in
+// `scratch`, a fixed device array (one copy per GPU, held until the process
+// ends), instead of a caller workspace: for callers that cannot allocate
+// (code under HIP graph capture, tight serving loops). The records are fully
+// written by each call before they are read, so nothing needs clearing; calls
+// that overlap on one GPU share the array and race.
+constexpr int64_t kScratchMaxG = 1024;  // K <= 262144; 299,008 bytes
+static __device__ __align__(256) uint8_t scratch[kScratchMaxG * kQ8Bytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's `scratch` (looked up once per device,
+// with that device current; the array's name is not a device address in host code).
+int current_scratch(uint8_t** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return intent::fail(INTENT_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return intent::fail(INTENT_ERR_UNSUPPORTED, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return intent::fail(INTENT_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                          hipGetErrorString(e));
+    g_scratch_ptr[dev] = (uint8_t*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return INTENT_OK;
+}
+
+}  // namespace
+
+extern "C" int intent_q4k_projection_noalloc(const uint8_t* w, int64_t N, int64_t G, int64_t w_ld, const float* x,
+                                             int64_t x_ld, float* y, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(G >= 0 && G <= kScratchMaxG, INTENT_ERR_UNSUPPORTED,
+                 "G=%lld records exceed the allocation-free limit of %lld (K <= %lld)", (long long)G,
+                 (long long)kScratchMaxG, (long long)(kScratchMaxG * 256));
+  uint8_t* records = nullptr;
+  const int st = current_scratch(&records);
+  if (st != INTENT_OK) return st;
+  return intent_q4k_projection(w, N, G, w_ld, x, x_ld, records, y, stream);
 }
