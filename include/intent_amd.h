@@ -484,8 +484,11 @@ int intent_f16_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld, const voi
  * of 16: scale = e4m3fn(max((amax / 6) * gs, 1.5258789e-5)), values
  * x * (gs / scale) encoded as E2M1 (thresholds of the reference), two per byte
  * into packed [M, N/2]; scale bytes into the reference's swizzled blocks
- * scales[M/128][G/4][32][4][4] (row r, group g at [r/128][g/4][r%32][(r%128)/32][g%4]).
- * Only valid groups are written.
+ * scales[ceil(M/128)][ceil(G/4)][32][4][4] exactly (row r, group g at
+ * [r/128][g/4][r%32][(r%128)/32][g%4]; the block stride follows from N).
+ * Only valid groups are written. As torch's E4M3FN cast in the CPU formula,
+ * a scale in (448, 464] rounds to 448 and one above 464 is NaN (0x7f), whose
+ * group then encodes every value as code 0.
  */
 int intent_nvfp4_quantize(const void* x, int64_t M, int64_t N, int64_t x_ld, const float* global_scale,
                           uint8_t* packed, int64_t packed_ld, uint8_t* scales, void* stream);

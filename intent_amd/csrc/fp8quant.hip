@@ -138,7 +138,11 @@ __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __r
 #pragma unroll
   for (int i = 1; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
   const float s = fmaxf(__fmul_rn(__fdiv_rn(amax, 6.0f), gs), 1.5258789e-05f);
-  const uint32_t sbyte = f32_to_e4m3fn(s);
+  // The E4M3FN cast of the CPU formula (torch's) rounds (448, 464] to 448 and
+  // turns anything above into NaN (0x7f); a NaN scale leaves every value of the
+  // group NaN, which encodes as code 0.
+  const bool nan_scale = !(s <= 464.0f);
+  const uint32_t sbyte = nan_scale ? 0x7fu : f32_to_e4m3fn(s);
   const float mult = __fdiv_rn(gs, e4m3fn_to_f32(sbyte));
   uint32_t lo = 0, hi = 0;
 #pragma unroll
@@ -147,6 +151,7 @@ __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __r
     if (i < 4) lo |= b << (8 * i);
     else hi |= b << (8 * (i - 4));
   }
+  if (nan_scale) lo = hi = 0u;
   uint8_t* dst = packed + (int64_t)row * ldp + g * 8;
   if ((((uintptr_t)dst) & 7) == 0) {
     *reinterpret_cast<u32x2*>(dst) = u32x2{lo, hi};

@@ -1038,8 +1038,11 @@ bf16_gemm = _fgemm_definition("bf16_gemm", "bf16", "64-80", {})
 def _nvfp4_check(env: dict) -> None:
     if env["N"] % 16 or env["P"] * 2 != env["N"]:
         raise ValueError(f"N ({env['N']}) must be a multiple of 16 and packed.shape[1] ({env['P']}) N / 2")
-    if env["MT"] * 128 < env["M"] or env["NT"] * 64 < env["N"]:
-        raise ValueError(f"scales blocks ({env['MT']}, {env['NT']}) do not cover M = {env['M']}, N = {env['N']}")
+    # The CPU formula copies into scales of exactly this block shape (cpu_runtime.py:1338-1339);
+    # the kernel's block stride follows from N, so a wider tensor is refused rather than misindexed.
+    want = ((env["M"] + 127) // 128, (env["N"] + 63) // 64)
+    if (env["MT"], env["NT"]) != want:
+        raise ValueError(f"scales blocks ({env['MT']}, {env['NT']}) must be {want} for M = {env['M']}, N = {env['N']}")
 
 
 def _nvfp4_launch(v: dict, env: dict, stream: int, workspace) -> str:

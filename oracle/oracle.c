@@ -795,12 +795,19 @@ void orc_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t N, float gs, uint8
       }
       float s = (amax / 6.0f) * gs;
       if (s < 1.5258789e-5f) s = 1.5258789e-5f;
-      const uint8_t sb = orc_f32_to_e4m3fn(s);
-      const float mult = gs / orc_e4m3fn_to_f32(sb);
+      /* torch's E4M3FN cast (the CPU formula's) rounds (448, 464] to 448 and gives NaN
+       * above; a NaN scale makes every value NaN and every code of the group 0 */
+      const int nan_scale = !(s <= 464.0f);
+      const uint8_t sb = nan_scale ? (uint8_t)0x7f : orc_f32_to_e4m3fn(s);
+      const float mult = nan_scale ? 0.0f : gs / orc_e4m3fn_to_f32(sb);
       uint8_t code[16];
       for (int i = 0; i < 16; ++i) {
         const float t = v[i] * mult, a = fabsf(t);
         uint8_t c = 0;
+        if (nan_scale) {
+          code[i] = 0;
+          continue;
+        }
         for (int q = 0; q < 7; ++q) {
           const int sel = (q % 2 == 0) ? a > thr[q] : a >= thr[q]; /* codes 1,3,5,7 strict; 2,4,6 inclusive */
           if (sel) c = (uint8_t)(q + 1);

@@ -70,11 +70,31 @@ def test_w4a16_decode_config1(gpu, threads, M):
 @pytest.mark.parametrize("M,K,N,group", [(3, 256, 100, 64), (1, 384, 48, 32), (16, 128, 17, 128),
                                          (5, 2048, 1000, 256), (1, 8192, 64, 128),
                                          (2, 8192, 33, 128), (1, 16384, 24, 128), (2, 384, 40, 128),
-                                         (1, 1024, 20, 64), (3, 3072, 77, 128), (3, 8192, 40, 128)])
+                                         (1, 1024, 20, 64), (3, 3072, 77, 128), (3, 8192, 40, 128),
+                                         (1, 8192, 100, 32), (1, 4224, 50, 96), (1, 2944, 30, 128),
+                                         (2, 16384, 20, 32), (1, 4096, 4100, 128)])
 def test_w4a16_gemv_shapes(gpu, threads, M, K, N, group):
+    # G = K/group even and small: the workgroup-shared kernel (1..4 scale pairs per thread);
+    # odd G (2944/128) or 512 groups (16384/32): the per-wave kernel
     x, q, s, z = w4_case(1, M, K, N, group)
     y = art(intent.weight_only_int4_asym_matmul, KERNEL="gemv").run(dev(x), dev(q), dev(s), dev(z))
     assert_close_rms(host(y), oracle.w4a16(x, q, s, z, threads), what="gemv shapes")
+
+
+@pytest.mark.parametrize("M,K,N,group", [(1, 4096, 300, 128), (3, 2048, 70, 64)])
+def test_w4a16_gemv_strided_operands(gpu, threads, M, K, N, group):
+    # x rows and scale/zero rows with leading strides wider than the row
+    x, q, s, z = w4_case(2, M, K, N, group)
+    G = K // group
+    xw = torch.zeros(M, K + 64, dtype=torch.float16)
+    xw[:, :K] = torch.from_numpy(x)
+    sw = torch.zeros(N, G + 6, dtype=torch.float16)
+    sw[:, :G] = torch.from_numpy(s)
+    zw = torch.zeros(N, G + 6, dtype=torch.uint8)
+    zw[:, :G] = torch.from_numpy(z)
+    xd, sd, zd = xw.cuda(), sw.cuda(), zw.cuda()
+    y = art(intent.weight_only_int4_asym_matmul, KERNEL="gemv").run(xd[:, :K], dev(q), sd[:, :G], zd[:, :G])
+    assert_close_rms(host(y), oracle.w4a16(x, q, s, z, threads), what="gemv strided")
 
 
 @pytest.mark.parametrize("M,K,N,group", [(16, 4096, 4096, 128), (17, 512, 200, 128), (130, 256, 64, 64),
@@ -790,17 +810,30 @@ def test_float_gemm(gpu, threads, kind, M, K, N):
 
 # ---- NVFP4 quantizer --------------------------------------------------------------------
 
-@pytest.mark.parametrize("M,N", [(256, 128), (300, 80), (1, 16), (8192, 4096)])
-def test_nvfp4_quantize_bit_exact(gpu, M, N):
-    # (8192, 4096) is the reference's registry case (experiments/cpu/registry.py:11)
+@pytest.mark.parametrize("M,N,gsv", [(256, 128, 1.25), (300, 80, 1.25), (1, 16, 1.25), (8192, 4096, 1.25),
+                                     (256, 128, 300.0)])
+def test_nvfp4_quantize_bit_exact(gpu, M, N, gsv):
+    # (8192, 4096) is the reference's registry case (experiments/cpu/registry.py:11); gs = 300
+    # drives many group scales past E4M3FN's range (NaN scale bytes, zero codes)
     g = torch.Generator().manual_seed(M + N)
     x = (torch.randn(M, N, generator=g) * 3).bfloat16()
-    gs = torch.tensor([1.25])
+    gs = torch.tensor([gsv])
     MT, NT = (M + 127) // 128, (N // 16 + 3) // 4
     packed0 = np.full((M, N // 2), 0xAA, np.uint8)
     scales0 = np.full((MT, NT, 32, 4, 4), 0x55, np.uint8)   # entries no group writes must keep this
     packed, scales = dev(packed0), dev(scales0)
     art(intent.nvfp4_quantize).run(x.cuda(), gs.cuda(), packed, scales)
-    rp, rs = oracle.nvfp4_quantize(_bits16(x), 1.25, packed0, scales0)
+    rp, rs = oracle.nvfp4_quantize(_bits16(x), gsv, packed0, scales0)
     assert np.array_equal(host(packed), rp)
     assert np.array_equal(host(scales), rs)
+    if gsv > 100:
+        assert (rs == 0x7f).any()
+
+
+def test_nvfp4_rejects_wider_scale_blocks(gpu):
+    M, N = 256, 128
+    x = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+    packed = torch.zeros(M, N // 2, dtype=torch.uint8, device="cuda")
+    scales = torch.zeros(2, 3, 32, 4, 4, dtype=torch.uint8, device="cuda")   # NT 3 where N needs 2
+    with pytest.raises(ValueError):
+        art(intent.nvfp4_quantize).run(x, torch.tensor([1.0], device="cuda"), packed, scales)

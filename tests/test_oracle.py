@@ -778,15 +778,19 @@ def test_float_gemm_closed_form_and_relu():
 
 # ---- NVFP4 quantizer ----------------------------------------------------------------------
 
-def test_nvfp4_quantize_matches_reference_formula():
-    # cpu_runtime.py:1325-1340 restated with torch (elementwise f32: bit-exact)
+@pytest.mark.parametrize("gsv", [0.75, 300.0])
+def test_nvfp4_quantize_matches_reference_formula(gsv):
+    # cpu_runtime.py:1325-1340 restated with torch (elementwise f32: bit-exact). At gs = 300
+    # many group scales pass 464, where torch's E4M3FN cast gives NaN (0x7f) and every code
+    # of the group becomes 0; scales in [448, 464] round to 448.
     g = torch.Generator().manual_seed(91)
     M, N = 256, 128
     x = (torch.randn(M, N, generator=g) * torch.rand(M, 1, generator=g) * 4).bfloat16()
     x[3, :16] = 0.0                                  # a zero group: scale clamps to its minimum
     x[5, 16:32] = -0.0
-    gs = torch.tensor([0.75])
-    packed, scales = oracle.nvfp4_quantize(_u16(x), 0.75)
+    x[7, 32:48] = 9.25                               # (9.25 / 6) * 300 = 462.5: rounds to 448
+    gs = torch.tensor([gsv])
+    packed, scales = oracle.nvfp4_quantize(_u16(x), gsv)
     groups = x.float().reshape(M, N // 16, 16)
     scale = ((groups.abs().amax(-1) / 6.0) * gs[0]).clamp_min(1.5258789e-5).to(torch.float8_e4m3fn)
     values = groups * (gs[0] / scale.float())[..., None]
@@ -799,6 +803,8 @@ def test_nvfp4_quantize_matches_reference_formula():
     pairs = enc.reshape(M, N // 2, 2)
     ref_packed = (pairs[..., 0] | (pairs[..., 1] << 4)).numpy()
     ref_scales = scale.view(torch.uint8).reshape(M // 128, 4, 32, N // 64, 4).permute(0, 3, 2, 1, 4).numpy()
+    if gsv > 100:
+        assert (ref_scales == 0x7f).any() and (ref_scales == 0x7e).any()
     assert np.array_equal(packed, ref_packed)
     assert np.array_equal(scales, ref_scales)
 
