@@ -308,10 +308,34 @@ def bench_fp4(steps: int, warmup: int) -> dict:
     return {"ms": ms, "work": work, "copies": n}
 
 
+def bench_moe_f16(steps: int, warmup: int) -> dict:
+    """The reference's f16 moe_expert_ffn at its own size (moe.py:6-10: T = D = 4096, F = 14336,
+    E = 8, top-2, routes by support.py:113-130): two grouped [K, N] projections + combine."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    T, D, F, E, K = 4096, 4096, 14336, 8, 2
+    d = {k: torch.from_numpy(v).cuda() for k, v in inputs.moe_routes(T, K, E, "reference").items()}
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(T, D, device="cuda", generator=g).half()
+    w1 = (torch.randn(E, D, F, device="cuda", generator=g) / 64).half()
+    w2 = (torch.randn(E, F, D, device="cuda", generator=g) / 128).half()
+    y = torch.zeros(T, D, device="cuda")
+    R = T * K
+    work = inputs.Workload(f"moe_expert_ffn f16 T{T} D{D} F{F} E{E} top{K}", 2 * 2 * R * D * F,
+                           2 * E * D * F * 2 + T * D * 2 + T * D * 8)
+    art = intent.compile(intent.moe_expert_ffn, target=intent.MI355XTarget(0))
+    call = art.prepare(x, d["route_offsets"], d["member_routes"], d["route_token"], d["route_weights"], w1, w2, y)
+    ms = graph_time([call.launch], steps, warmup)
+    return {"ms": ms, "work": work}
+
+
 def bench_quantized_gemm(steps: int, warmup: int) -> dict:
     """The reference's quantized_gemm case (experiments/cpu/providers/mojo/contraction.py:177-186):
     f16 [4096, 4096] x [4096, 14336] with bias, ReLU, residual, per-column scale, int8 out;
-    the timed operator includes the transpose of the [K, N] right operand."""
+    b reaches the kernel as [K, N] (no transposed copy)."""
     import torch
 
     import intent_amd as intent
@@ -644,6 +668,9 @@ def main() -> int:
         log("[bench] quantized_gemm M=4096 K=4096 N=14336")
         r = bench_quantized_gemm(steps, warm)
         extra["quantized_gemm_m4096_n14336"] = _flop_entry(r, F16_PEAK_TFLOPS, "TFLOP/s")
+        log("[bench] f16 moe_expert_ffn T=D=4096 F=14336")
+        r = bench_moe_f16(max(2, steps // 10), 1)
+        extra["moe_expert_ffn_f16_t4096"] = _flop_entry(r, F16_PEAK_TFLOPS, "TFLOP/s")
         log("[bench] q4_k projection N=K=4096")
         r = bench_q4k(args.steps, args.warmup)
         extra["q4k_projection_n4096"] = _hbm_entry(r)

@@ -477,6 +477,50 @@ int intent_grouped_gemm(const void* x, int64_t rows, int64_t K, int64_t x_ld, co
 int intent_f16_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* bt, int64_t N,
                     int64_t bt_ld, int epilogue, void* c, int64_t c_ld, void* stream);
 
+/* The float GEMMs with the right operand as the reference passes it: b
+ * [K, N] with N contiguous (b_ld elements per k-row), read in place (no
+ * transposed copy): gemm / bf16_gemm (examples/kernels/contraction/gemm.py:42-80,
+ * epilogue as intent_f16_gemm) and quantized_gemm (gemm.py:83-106, epilogue as
+ * intent_quantized_gemm). N % 8 == 0, b_ld % 8 == 0, 16-byte aligned operands,
+ * K % 64 == 0; otherwise INTENT_ERR_UNSUPPORTED / INTENT_ERR_ALIGNMENT.
+ */
+int intent_f16_gemm_kn(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* b, int64_t N,
+                       int64_t b_ld, int epilogue, void* c, int64_t c_ld, void* stream);
+int intent_quantized_gemm_kn(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* b, int64_t N,
+                             int64_t b_ld, const float* bias, const void* residual, int64_t residual_ld,
+                             const float* output_scale, int8_t* out, int64_t out_ld, void* stream);
+
+/* ragged_grouped_gemm / ragged_grouped_gemm_bf16 (examples/kernels/ragged/
+ * grouped_gemm.py:11-70) with the weights as the reference lays them out,
+ * [G][K][N] (w_ld elements per k-row, w_group_stride per group), read in
+ * place. Rows offsets[g] .. offsets[g+1] of x [rows, K] and out [rows, N]
+ * belong to group g (offsets clamped to [0, rows]). N and w_ld multiples of 8,
+ * K % 64 == 0, 16-byte aligned operands.
+ */
+int intent_grouped_gemm_kn(const void* x, int64_t rows, int64_t K, int64_t x_ld, const int32_t* offsets,
+                           int64_t G, const void* w, int64_t N, int64_t w_ld, int64_t w_group_stride, int bf16,
+                           void* out, int64_t out_ld, void* stream);
+
+/* The reference's f16 MoE expert FFN, moe_expert_ffn
+ * (examples/kernels/ragged/moe.py:12-53; host reference
+ * experiments/_common/support.py:133-151): x f16 [T, D] (x_ld), route_offsets
+ * i32 [E + 1], member_routes i32 [R], route_token i32 [NR], route_weights f32
+ * [NR], w1 f16 [E, D, F], w2 f16 [E, F, D] (both contiguous), y f32 [T, D]
+ * (y_ld) updated in place:
+ *   for each expert e, member i in route_offsets[e] .. route_offsets[e+1]:
+ *     r = member_routes[i], t = route_token[r]
+ *     y[t] += route_weights[r] * (f16(max(x[t] @ w1[e], 0)) @ w2[e])
+ * with f32 accumulation; a token's contributions are added in member order
+ * (deterministic). Out-of-range routing entries are clamped, never
+ * dereferenced. D and F multiples of 64. workspace: at least
+ * intent_moe_expert_ffn_workspace_size(T, R, D, F) bytes, 16-byte aligned.
+ */
+size_t intent_moe_expert_ffn_workspace_size(int64_t T, int64_t R, int64_t D, int64_t F);
+int intent_moe_expert_ffn(const void* x, int64_t T, int64_t D, int64_t x_ld, const int32_t* route_offsets,
+                          int64_t E, const int32_t* member_routes, int64_t R, const int32_t* route_token,
+                          const float* route_weights, int64_t NR, const void* w1, const void* w2, int64_t F,
+                          float* y, int64_t y_ld, void* workspace, size_t workspace_bytes, void* stream);
+
 /* NVFP4 activation quantizer. Replaces nvfp4_quantize
  * (examples/kernels/quantization/nvfp4.py; CPU baseline
  * experiments/cpu/baselines/pytorch/cpu_runtime.py:1325-1340): x bf16 [M, N]

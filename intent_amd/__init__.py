@@ -42,6 +42,7 @@ from .definitions import (
     moe_align_block_size,
     moe_combine,
     moe_down_w4,
+    moe_expert_ffn,
     moe_expert_ffn_w4,
     moe_gate_up_w4,
     moe_route_topk,
@@ -68,7 +69,7 @@ __all__ = [
     "ALL_DEFINITIONS", "CompilationStageError", "bitnet_int2_matmul", "block_scaled_matmul", "scaled_fp8_matmul", "scaled_fp8_splitk_matmul", "deepgemm_fp8_2xacc", "fp8_e4m3_matmul", "fp8_e5m2_matmul", "dequant_bf16_fp4_matmul", "weight_only_int4_matmul", "quantized_gemm", "gemm", "bf16_gemm", "nvfp4_quantize", "ragged_grouped_gemm", "ragged_grouped_gemm_bf16", "routed_expert_projection_bf16", "gemm_i8", "w4a8_packed_matmul", "bf16_groupwise_fp8_quantize", "f32_groupwise_fp8_quantize", "per_token_int8_quantize", "bf16_per_token_int8_quantize", "CompileOptions", "CompiledArtifact", "DType", "KernelDefinition",
     "LanguageUseError", "MI355XTarget", "NativeLibraryError", "PublicInterface", "ScalarParameter", "ViewKind",
     "ViewParameter", "compile", "gemm_i8_nt", "kernel", "moe_align_block_size", "moe_combine", "moe_down_w4",
-    "moe_expert_ffn_w4", "moe_gate_up_w4", "moe_route_topk", "q4_k_q8_k_dot", "q8_k_quantize",
+    "moe_expert_ffn", "moe_expert_ffn_w4", "moe_gate_up_w4", "moe_route_topk", "q4_k_q8_k_dot", "q8_k_quantize",
     "quantized_projection", "w8a8_scaled_matmul", "weight_only_int4_asym_matmul",
     "weight_only_int8_matmul",
 ]

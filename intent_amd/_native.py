@@ -55,7 +55,12 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_quantized_gemm": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P, P, I64, P], INT),
     "intent_f16_transpose_batched": ([P, I64, I64, I64, I64, I64, P, I64, I64, P], INT),
     "intent_grouped_gemm": ([P, I64, I64, I64, P, I64, P, I64, P, I64, I64, I64, INT, P, I64, P], INT),
+    "intent_grouped_gemm_kn": ([P, I64, I64, I64, P, I64, P, I64, I64, I64, INT, P, I64, P], INT),
+    "intent_moe_expert_ffn_workspace_size": ([I64, I64, I64, I64], SIZE),
+    "intent_moe_expert_ffn": ([P, I64, I64, I64, P, I64, P, I64, P, P, I64, P, P, I64, P, I64, P, SIZE, P], INT),
     "intent_f16_gemm": ([P, I64, I64, I64, P, I64, I64, INT, P, I64, P], INT),
+    "intent_f16_gemm_kn": ([P, I64, I64, I64, P, I64, I64, INT, P, I64, P], INT),
+    "intent_quantized_gemm_kn": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P, P, I64, P], INT),
     "intent_nvfp4_quantize": ([P, I64, I64, I64, P, P, I64, P, P], INT),
     "intent_fp4_bf16_matmul": ([P, I64, I64, I64, P, I64, I64, P, I64, P], INT),
     "intent_fp8_gemm": ([P, I64, I64, I64, P, I64, I64, INT, P, I64, P], INT),

@@ -1,5 +1,6 @@
 // Dense weight-only contractions on the shared f16 MFMA tile GEMM:
 //   W4A16 (asymmetric group-quant nibbles) and W8A16 (per-channel int8).
+
 #include "common.h"
 #include "internal.h"
 #include "mfma_pipe.h"
@@ -265,24 +266,12 @@ __global__ void fill_u8_kernel(uint8_t* __restrict__ z, int rows, int cols, int6
 // the kQuantI8 instances, and kGemmBf16: c = bf16(acc) with bf16 operands.
 enum class DenseEpi { kQuantI8, kGemmBf16 };
 
-template <class T, DenseEpi E = DenseEpi::kQuantI8, class Math = mp::F16Math>
-__global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
-    const f16* __restrict__ a, int64_t lda, int M, const f16* __restrict__ bt, int64_t ldb, int N, int K,
-    const float* __restrict__ bias, const f16* __restrict__ residual, int64_t ldr, const float* __restrict__ oscale,
-    int8_t* __restrict__ out, int64_t ldo, int mblocks, int f16_epi = 0) {
-  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  char* const bufs[2] = {buf0, buf1};
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
-  const int pw = T::wave() % T::NW;
-  mp::RegRowsOperand<T::BN, mp::DenseRows, false, T::NW> bop;
-  bop.init(mp::DenseRows{bt, ldb * 2, N}, n0, pw);
-  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
-  aop.init(mp::DenseRows{a, lda * 2, M}, m0, pw);
-  f32x16 acc[T::TI][T::TJ];
-  if (!mp::mainloop_ws<T, Math, 2>(aop, bop, K / 64, bufs, acc)) return;
+// Epilogues of the dense f16 / bf16 GEMMs (lane holds m = row(i), n = col(j, g) + 0..3).
+template <class T, DenseEpi E>
+INTENT_DEVICE void dense_epilogue(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N,
+                                  const float* __restrict__ bias, const f16* __restrict__ residual, int64_t ldr,
+                                  const float* __restrict__ oscale, int8_t* __restrict__ out, int64_t ldo,
+                                  int f16_epi) {
   // kQuantI8 instances also serve the f16 GEMM epilogues, chosen at run time
   // (f16_epi 1: f16(acc), 2: f16(max(acc, 0))).
   if (E != DenseEpi::kQuantI8 || f16_epi != 0) {
@@ -290,6 +279,7 @@ __global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
     const bool relu = f16_epi == 2;
     auto cvt = [relu](float v) -> uint32_t {
       if constexpr (E == DenseEpi::kGemmBf16) {
+        (void)relu;
         return f32_to_bf16_rne(v);
       } else {
         if (relu) v = v < 0.f ? 0.f : v;
@@ -382,6 +372,53 @@ __global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
       }
     }
   }
+}
+
+template <class T, DenseEpi E = DenseEpi::kQuantI8, class Math = mp::F16Math>
+__global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
+    const f16* __restrict__ a, int64_t lda, int M, const f16* __restrict__ bt, int64_t ldb, int N, int K,
+    const float* __restrict__ bias, const f16* __restrict__ residual, int64_t ldr, const float* __restrict__ oscale,
+    int8_t* __restrict__ out, int64_t ldo, int mblocks, int f16_epi = 0) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  char* const bufs[2] = {buf0, buf1};
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  const int pw = T::wave() % T::NW;
+  mp::RegRowsOperand<T::BN, mp::DenseRows, false, T::NW> bop;
+  bop.init(mp::DenseRows{bt, ldb * 2, N}, n0, pw);
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{a, lda * 2, M}, m0, pw);
+  f32x16 acc[T::TI][T::TJ];
+  if (!mp::mainloop_ws<T, Math, 2>(aop, bop, K / 64, bufs, acc)) return;
+  dense_epilogue<T, E>(acc, m0, n0, M, N, bias, residual, ldr, oscale, out, ldo, f16_epi);
+}
+
+// The same GEMMs with the right operand as the reference passes it, b [K, N]
+// (N contiguous): both operands reach LDS by DMA and the B fragments come
+// out of LDS through transpose reads (mfma_pipe.h, DmaKNOperand), so no
+// transposed copy of b is made. 256 x 256 tiles (KNTile), a ring of two
+// 64-KB stages.
+template <class T, DenseEpi E = DenseEpi::kQuantI8, class Math = mp::F16Math, bool kSched = false>
+__global__ __launch_bounds__(T::NT, 1) void gemm_kn_kernel(
+    const f16* __restrict__ a, int64_t lda, int M, const f16* __restrict__ b, int64_t ldb, int N, int K,
+    const float* __restrict__ bias, const f16* __restrict__ residual, int64_t ldr, const float* __restrict__ oscale,
+    int8_t* __restrict__ out, int64_t ldo, int mblocks, int f16_epi = 0) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  const int wave = T::wave();
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{a, lda * 2, M}, m0, wave);
+  mp::DmaKNOperand<T::BN, T::NW> bop;
+  bop.init(b + n0, ldb, N - n0, wave);
+  f32x16 acc[T::TI][T::TJ];
+  mp::mainloop_kn<T, Math, mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW>, mp::DmaKNOperand<T::BN, T::NW>, kSched>(
+      aop, bop, K / 64, buf0, buf1, acc);
+  dense_epilogue<T, E>(acc, m0, n0, M, N, bias, residual, ldr, oscale, out, ldo, f16_epi);
 }
 
 // ---- f16 / bf16 grouped GEMMs over row groups -----------------------------------
@@ -822,4 +859,72 @@ extern "C" int intent_f16_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld
                        (const f16*)a, a_ld, (int)M, (const f16*)bt, bt_ld, (int)N, (int)K, nullptr, nullptr, 0,
                        nullptr, (int8_t*)c, c_ld, mblocks, epilogue + 1);
   return intent::launch_status("f16_gemm");
+}
+
+namespace {
+
+int gemm_kn_check(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* b, int64_t N, int64_t b_ld,
+                  int64_t c_ld, const char* what) {
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "%s: bad extents", what);
+  INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "%s: K must be a multiple of 64, got %lld", what, (long long)K);
+  INTENT_REQUIRE(N % 8 == 0, INTENT_ERR_UNSUPPORTED, "%s: N must be a multiple of 8 for the [K, N] operand, got %lld",
+                 what, (long long)N);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(a && b, INTENT_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
+  INTENT_REQUIRE(a_ld >= K && b_ld >= N && c_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+                 "%s: leading stride smaller than the row", what);
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(b) && a_ld % 8 == 0 && b_ld % 8 == 0,
+                 INTENT_ERR_ALIGNMENT, "%s: operands must be 16-byte aligned with 16-byte row strides", what);
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld * 2) && intent::fits_offset(K, b_ld * 2), INTENT_ERR_UNSUPPORTED,
+                 "%s: operand too large for 31-bit buffer offsets", what);
+  return INTENT_OK;
+}
+
+// Eight waves (two per SIMD) of 128 x 64: measured at 4096 x 4096 x 14336
+// (quantized_gemm) 525 us against 710 us for four waves of 128 x 128 (which
+// spill) and 576 us without the MFMA / LDS-read interleaving schedule.
+using KNTile = mp::Tile<256, 256, 2, 4>;
+
+}  // namespace
+
+extern "C" int intent_quantized_gemm_kn(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* b, int64_t N,
+                                        int64_t b_ld, const float* bias, const void* residual, int64_t residual_ld,
+                                        const float* output_scale, int8_t* out, int64_t out_ld, void* stream) {
+  intent::clear_error();
+  int st = gemm_kn_check(a, M, K, a_ld, b, N, b_ld, out_ld, "quantized_gemm_kn");
+  if (st != INTENT_OK || M == 0 || N == 0) return st;
+  INTENT_REQUIRE(bias && residual && output_scale && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(residual_ld >= N, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  using T = KNTile;
+  const int mblocks = (int)((M + T::BM - 1) / T::BM);
+  const int64_t grid = (int64_t)mblocks * ((N + T::BN - 1) / T::BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "quantized_gemm_kn: grid too large");
+  hipLaunchKernelGGL((gemm_kn_kernel<T, DenseEpi::kQuantI8, mp::F16Math, true>), dim3((unsigned)grid), dim3(T::NT), 0,
+                     (hipStream_t)stream, (const f16*)a, a_ld, (int)M, (const f16*)b, b_ld, (int)N, (int)K, bias,
+                     (const f16*)residual, residual_ld, output_scale, out, out_ld, mblocks, 0);
+  return intent::launch_status("gemm_kn_kernel<quantized_gemm>");
+}
+
+extern "C" int intent_f16_gemm_kn(const void* a, int64_t M, int64_t K, int64_t a_ld, const void* b, int64_t N,
+                                  int64_t b_ld, int epilogue, void* c, int64_t c_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(epilogue >= 0 && epilogue <= 2, INTENT_ERR_INVALID_ARGUMENT,
+                 "epilogue must be 0 (f16), 1 (f16 relu) or 2 (bf16)");
+  int st = gemm_kn_check(a, M, K, a_ld, b, N, b_ld, c_ld, "f16_gemm_kn");
+  if (st != INTENT_OK || M == 0 || N == 0) return st;
+  INTENT_REQUIRE(c, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  using T = KNTile;
+  const int mblocks = (int)((M + T::BM - 1) / T::BM);
+  const int64_t grid = (int64_t)mblocks * ((N + T::BN - 1) / T::BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "f16_gemm_kn: grid too large");
+  if (epilogue == 2)
+    hipLaunchKernelGGL((gemm_kn_kernel<T, DenseEpi::kGemmBf16, mp::BF16Math, true>), dim3((unsigned)grid), dim3(T::NT), 0,
+                       (hipStream_t)stream, (const f16*)a, a_ld, (int)M, (const f16*)b, b_ld, (int)N, (int)K, nullptr,
+                       nullptr, 0, nullptr, (int8_t*)c, c_ld, mblocks, 0);
+  else
+    hipLaunchKernelGGL((gemm_kn_kernel<T, DenseEpi::kQuantI8, mp::F16Math, true>), dim3((unsigned)grid), dim3(T::NT),
+                       0, (hipStream_t)stream, (const f16*)a, a_ld, (int)M, (const f16*)b, b_ld, (int)N, (int)K,
+                       nullptr, nullptr, 0, nullptr, (int8_t*)c, c_ld, mblocks, epilogue + 1);
+  return intent::launch_status(epilogue == 2 ? "gemm_kn_kernel<bf16>" : "gemm_kn_kernel<f16>");
 }

@@ -42,6 +42,15 @@ typedef __attribute__((address_space(3))) void lds_t;
 
 INTENT_DEVICE constexpr int swz(int row) { return (row >> 1) & 7; }
 
+// f(std::integral_constant<int, S>) for S = B .. E-1.
+template <int B, int E, class F>
+INTENT_DEVICE void static_for_mp(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for_mp<B + 1, E>(f);
+  }
+}
+
 using Rsrc = __amdgpu_buffer_rsrc_t;
 
 // s_waitcnt with only vmcnt constrained (expcnt 7, lgkmcnt 15 = no wait).
@@ -611,6 +620,204 @@ INTENT_DEVICE void mainloop(const AOp& aop, const BOp& bop, int nk, char* buf0, 
     compute_stage<T, Math, 2>(last, aaddr, baddr, acc);
   else
     compute_stage<T, Math, 4>(last, aaddr, baddr, acc);
+}
+
+// ---- right operand as [K][N] rows (N contiguous), no transpose pass ---------------
+//
+// A stage holds 64 k-rows of BN columns (BN * 2 bytes each) copied global ->
+// LDS by DMA: the stage is one linear block and DMA instruction j fills its
+// kilobyte j, lane i moving 16-byte slot q = 64j + i (k-row q / CH, slot
+// q % CH). Slot s of k-row r holds column chunk s ^ kn_swz(r). MFMA B
+// fragments (8 consecutive k of one column per lane) are read with
+// ds_read_b64_tr_b16: inside a group of 16 lanes, output lane t element e is
+// element t % 4 of the 8 bytes addressed by lane 4e + t / 4. Lane j of a
+// group therefore addresses k-row k0 + j / 4, columns n0 + 4 (j % 4) .. + 3,
+// and lane t receives column n0 + t at k-rows k0 .. k0 + 3; two such reads
+// (k0 and k0 + 4) make a fragment. The four k-rows of one read then fall
+// into four distinct 32-byte bank windows thanks to kn_swz.
+INTENT_DEVICE constexpr int kn_swz(int krow) { return 2 * (krow & 3); }
+
+template <int BN, int NW>
+struct DmaKNOperand {
+  static constexpr int CH = BN / 8;      // 16-byte column chunks per k-row
+  static constexpr int RB = BN * 2;      // bytes per k-row in LDS
+  static constexpr int TOTAL = BN / 8;   // kilobyte DMA instructions per stage (64 * RB / 1024)
+  static constexpr int N_INST = (TOTAL + NW - 1) / NW;
+  static constexpr int NVM = N_INST;
+  static_assert(BN % 64 == 0, "KN tiles need a multiple of 64 columns");
+  Rsrc rs;
+  uint32_t voff[N_INST];
+  int lds_kb[N_INST];  // destination kilobyte of instruction j
+  uint32_t kstep;      // bytes per stage (64 k-rows)
+  // b: element (0, n0) of the [K][N] matrix; ldb elements per k-row; ncols:
+  // valid columns from n0 (chunks past them re-read a valid chunk; their
+  // products land in output columns that are never stored).
+  INTENT_DEVICE void init(const void* b, int64_t ldb, int ncols, int wave) {
+    rs = make_rsrc(b);
+    kstep = (uint32_t)(64 * ldb * 2);
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) {
+      const int t = j * NW + wave < TOTAL ? j * NW + wave : TOTAL - 1;
+      const int q = t * 64 + lane;
+      const int r = q / CH;
+      const int c = (q % CH) ^ kn_swz(r);
+      int col = c * 8;
+      col = col + 8 <= ncols ? col : ((ncols - 8) > 0 ? ((ncols - 8) & ~7) : 0);
+      voff[j] = (uint32_t)(r * ldb * 2 + col * 2);
+      lds_kb[j] = t;
+    }
+  }
+  INTENT_DEVICE void issue(char* lds_b, int kt) const {
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_t*)(lds_b + lds_kb[j] * 1024), 16, voff[j],
+                                               (uint32_t)kt * kstep, 0, 0);
+  }
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
+
+// B fragment of 32x32x16 step kk for column block n (wave-tile relative n0 +
+// 32 * j): lane l takes column n + l % 32, k-rows 16kk + 8(l / 32) .. + 7.
+template <class Frag>
+INTENT_DEVICE Frag kn_frag(const char* b, uint32_t addr0, uint32_t addr1) {
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(__attribute__((address_space(3))) char*)(b + addr0));
+  const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(__attribute__((address_space(3))) char*)(b + addr1));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return bit_cast<Frag>(v);
+}
+
+// LDS byte offset (within the B region) of a lane's transpose read for step
+// kk, column block j and half hh (k-rows +0 / +4). The lane addresses k-row
+// krow = 16kk + 8(g / 2) + 4hh + t / 4 and column col = wave_n * WTN + 32j +
+// 16(g % 2) + 4(t % 4) (g = lane / 16, t = lane % 16), i.e. 32-byte window
+// w = col / 16 = wave_n * WTN / 16 + 2j + g % 2 stored at w ^ (krow & 3),
+// where krow & 3 = t / 4 for every kk, hh. Only bit 0 of j meets the swizzle,
+// so two per-lane bases (even / odd j) plus constant offsets cover all reads.
+template <class T>
+struct KNAddr {
+  static constexpr int RB = T::BN * 2;
+  static_assert(T::WTN % 32 == 0, "column blocks of 32");
+  uint32_t base[2];
+  INTENT_DEVICE void init() {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, t = lane & 15;
+    const int r = t >> 2;  // krow & 3
+    const int w0 = (g & 1) ^ (r & 1);  // bit 0 of the stored window
+    const uint32_t row = (uint32_t)((8 * (g >> 1) + r) * RB);
+    const uint32_t in = (uint32_t)(T::wave_n() * T::WTN * 2 + w0 * 32 + (t & 3) * 8);
+    // stored window bit 1 = (j & 1) ^ (r >> 1): +64 for even j when r >> 1,
+    // -64 for odd j
+    base[0] = row + in + ((r >> 1) ? 64u : 0u);
+    base[1] = row + in - ((r >> 1) ? 64u : 0u);
+  }
+  INTENT_DEVICE uint32_t at(int kk, int j, int hh) const {
+    return base[j & 1] + (uint32_t)(j * 64 + kk * 16 * RB + hh * 4 * RB);
+  }
+};
+
+// One stage: A fragments as compute_stage, B fragments by transpose reads.
+template <class T, class Math, bool kSched = false>
+INTENT_DEVICE void compute_stage_kn(const char* buf, const uint32_t (&aaddr)[4], const KNAddr<T>& ka,
+                                    typename Math::Acc (&acc)[T::TI][T::TJ]) {
+  using Frag = typename Math::Frag;
+  const char* a = buf;
+  const char* b = buf + T::A_BYTES;
+  Frag af[2][T::TI], bf[2][T::TJ];
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) af[0][i] = *reinterpret_cast<const Frag*>(a + aaddr[0] + i * 32 * ROWB);
+#pragma unroll
+  for (int j = 0; j < T::TJ; ++j) bf[0][j] = kn_frag<Frag>(b, ka.at(0, j, 0), ka.at(0, j, 1));
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    const int cb = kk & 1;
+    if (kk + 1 < 4) {
+#pragma unroll
+      for (int i = 0; i < T::TI; ++i)
+        af[cb ^ 1][i] = *reinterpret_cast<const Frag*>(a + aaddr[kk + 1] + i * 32 * ROWB);
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) bf[cb ^ 1][j] = kn_frag<Frag>(b, ka.at(kk + 1, j, 0), ka.at(kk + 1, j, 1));
+    }
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) acc[i][j] = Math::mfma(bf[cb][j], af[cb][i], acc[i][j]);
+  }
+  if constexpr (kSched) {
+    // the first step's reads, then the next step's reads paired with MFMAs
+    // (a B fragment is two transpose reads)
+    constexpr int NR = T::TI + 2 * T::TJ;
+    constexpr int NM = T::TI * T::TJ;
+    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk + 1 < 4) {
+        constexpr int PAIRS = NR < NM ? NR : NM;
+#pragma unroll
+        for (int x = 0; x < PAIRS; ++x) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        if (NR > NM) __builtin_amdgcn_sched_group_barrier(0x100, NR - NM, 0);
+        if (NM > NR) __builtin_amdgcn_sched_group_barrier(0x008, NM - NR, 0);
+      } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+      }
+    }
+  }
+}
+
+// All-consumer main loop over two stage buffers, both operands by DMA (A rows
+// as DmaRowsOperand, B as DmaKNOperand): stage kt + 1 is issued into the
+// other buffer while stage kt computes; one barrier per stage. Stage indices
+// past the end clamp to the last stage (a copy into a buffer nobody reads
+// again), so every step issues the same DMA count and vmcnt(0) before the
+// barrier is exact.
+template <class T, class Math, class ADma, class BDma, bool kSched>
+INTENT_DEVICE void mainloop_kn(const ADma& aop, const BDma& bop, int nk, char* buf0, char* buf1,
+                               typename Math::Acc (&acc)[T::TI][T::TJ]) {
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;
+  if (nk <= 0) return;
+  const int lane = threadIdx.x & 63;
+  uint32_t aaddr[4];
+  {
+    const int r = lane & 31;
+    const int x = (lane >> 5) ^ swz(r);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) aaddr[kk] = (uint32_t)((T::wave_m() * T::WTM + r) * ROWB) + (((2 * kk) ^ x) << 4);
+  }
+  KNAddr<T> ka;
+  ka.init();
+  aop.issue(buf0, 0);
+  bop.issue(buf0 + T::A_BYTES, 0);
+  wait_vm_lgkm_barrier<0>();
+  for (int kt = 0; kt < nk; kt += 2) {
+    {
+      const int nx = kt + 1 < nk ? kt + 1 : nk - 1;
+      aop.issue(buf1, nx);
+      bop.issue(buf1 + T::A_BYTES, nx);
+      compute_stage_kn<T, Math, kSched>(buf0, aaddr, ka, acc);
+      if (kt + 1 >= nk) break;
+      wait_vm_lgkm_barrier<0>();
+    }
+    {
+      const int nx = kt + 2 < nk ? kt + 2 : nk - 1;
+      aop.issue(buf0, nx);
+      bop.issue(buf0 + T::A_BYTES, nx);
+      compute_stage_kn<T, Math, kSched>(buf1, aaddr, ka, acc);
+      if (kt + 2 >= nk) break;
+      wait_vm_lgkm_barrier<0>();
+    }
+  }
+  wait_vm<0>();  // no DMA may land in LDS that an epilogue reuses
 }
 
 // Producer/consumer variant. Waves 0..NW-1 (consumers) only read fragments

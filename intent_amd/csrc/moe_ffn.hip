@@ -1,0 +1,185 @@
+// The reference's f16 MoE expert FFN (examples/kernels/ragged/moe.py:12-53)
+// on the grouped [K, N] kernel (grouped_kn.h): two grouped projections over
+// the ragged routing, then a deterministic per-token combine.
+#include "grouped_kn.h"
+
+using namespace gkn;
+
+namespace {
+
+// ---- the expert FFN's combine: y[token] += contributions of its members, in
+// member order (the reference adds expert by expert: experts.py index_add_
+// loop), through a per-token member list built on the device.
+//
+// One workgroup builds the list: counts per token (order-free atomics), an
+// exclusive scan, a placement with per-token cursors (order-free), then each
+// token's entries sorted ascending (a token has at most a few members), so
+// the list is the same on every run.
+constexpr int kListThreads = 1024;
+
+__global__ __launch_bounds__(kListThreads) void token_member_list_kernel(
+    const int32_t* __restrict__ route_offsets, int E, const int32_t* __restrict__ members,
+    const int32_t* __restrict__ route_token, int T, int R, int NR, int32_t* __restrict__ count,
+    int32_t* __restrict__ start, int32_t* __restrict__ list) {
+  __shared__ int32_t part[kListThreads];
+  const int tid = threadIdx.x;
+  const int m0 = clampi(route_offsets[0], 0, R);
+  int m1 = m0;  // end of the last non-empty group, as find_tile clamps it
+  for (int g = 0; g < E; ++g) m1 = clampi(route_offsets[g + 1], m1, R);
+  auto token_of = [&](int i) { return clampi(route_token[clampi(members[i], 0, NR - 1)], 0, T - 1); };
+  for (int t = tid; t < T; t += kListThreads) count[t] = 0;
+  __syncthreads();
+  for (int i = m0 + tid; i < m1; i += kListThreads) atomicAdd(&count[token_of(i)], 1);
+  __syncthreads();
+  // exclusive scan of count over T: each thread scans a contiguous slice
+  const int per = (T + kListThreads - 1) / kListThreads;
+  const int t0 = tid * per;
+  int sum = 0;
+  for (int t = t0; t < t0 + per && t < T; ++t) sum += count[t];
+  part[tid] = sum;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int k = 0; k < kListThreads; ++k) {
+      const int v = part[k];
+      part[k] = run;
+      run += v;
+    }
+    start[T] = run;
+  }
+  __syncthreads();
+  int run = part[tid];
+  for (int t = t0; t < t0 + per && t < T; ++t) {
+    start[t] = run;
+    run += count[t];
+    count[t] = 0;  // reused as the placement cursor
+  }
+  __syncthreads();
+  for (int i = m0 + tid; i < m1; i += kListThreads) {
+    const int t = token_of(i);
+    const int pos = atomicAdd(&count[t], 1);
+    list[start[t] + pos] = i;
+  }
+  __syncthreads();
+  for (int t = tid; t < T; t += kListThreads) {
+    const int b = start[t], e = start[t + 1];
+    for (int a = b + 1; a < e; ++a) {  // insertion sort: ascending member index
+      const int v = list[a];
+      int c = a - 1;
+      while (c >= b && list[c] > v) {
+        list[c + 1] = list[c];
+        --c;
+      }
+      list[c + 1] = v;
+    }
+  }
+}
+
+// y[t, d] += contrib[i, d] for the members i of token t in ascending order
+// (one add per member, no fma): f32 throughout.
+__global__ __launch_bounds__(256) void token_combine_kernel(const float* __restrict__ contrib, int64_t ldc,
+                                                            const int32_t* __restrict__ start,
+                                                            const int32_t* __restrict__ list, int T, int D,
+                                                            float* __restrict__ y, int64_t ldy) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int d4 = (D + 3) / 4;
+  if (id >= (int64_t)T * d4) return;
+  const int t = (int)(id / d4);
+  const int d = (int)(id % d4) * 4;
+  const int b = start[t], e = start[t + 1];
+  float* yo = y + (int64_t)t * ldy + d;
+  if (d + 3 < D && (ldy & 3) == 0 && (ldc & 3) == 0) {
+    f32x4 acc = *reinterpret_cast<const f32x4*>(yo);
+    for (int k = b; k < e; ++k) {
+      const f32x4 c = *reinterpret_cast<const f32x4*>(contrib + (int64_t)list[k] * ldc + d);
+      acc = f32x4{__fadd_rn(acc[0], c[0]), __fadd_rn(acc[1], c[1]), __fadd_rn(acc[2], c[2]), __fadd_rn(acc[3], c[3])};
+    }
+    *reinterpret_cast<f32x4*>(yo) = acc;
+  } else {
+    for (int c = 0; c < 4 && d + c < D; ++c) {
+      float acc = yo[c];
+      for (int k = b; k < e; ++k) acc = __fadd_rn(acc, contrib[(int64_t)list[k] * ldc + d + c]);
+      yo[c] = acc;
+    }
+  }
+}
+
+size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct FfnLayout {
+  size_t hidden, contrib, count, start, list, bytes;
+};
+
+FfnLayout ffn_layout(int64_t T, int64_t R, int64_t D, int64_t F) {
+  FfnLayout L{};
+  size_t o = 0;
+  L.hidden = o;  o = round256(o + sizeof(uint16_t) * (size_t)R * F);
+  L.contrib = o; o = round256(o + sizeof(float) * (size_t)R * D);
+  L.count = o;   o = round256(o + sizeof(int32_t) * (size_t)T);
+  L.start = o;   o = round256(o + sizeof(int32_t) * (size_t)(T + 1));
+  L.list = o;    o = round256(o + sizeof(int32_t) * (size_t)R);
+  L.bytes = o;
+  return L;
+}
+
+}  // namespace
+
+extern "C" size_t intent_moe_expert_ffn_workspace_size(int64_t T, int64_t R, int64_t D, int64_t F) {
+  if (T < 0 || R < 0 || D < 0 || F < 0) return 0;
+  return ffn_layout(T, R, D, F).bytes;
+}
+
+extern "C" int intent_moe_expert_ffn(const void* x, int64_t T, int64_t D, int64_t x_ld, const int32_t* route_offsets,
+                                     int64_t E, const int32_t* member_routes, int64_t R, const int32_t* route_token,
+                                     const float* route_weights, int64_t NR, const void* w1, const void* w2,
+                                     int64_t F, float* y, int64_t y_ld, void* workspace, size_t workspace_bytes,
+                                     void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(T >= 0 && D >= 0 && E >= 1 && R >= 0 && NR >= 0 && F >= 0 && T <= INT32_MAX && R <= INT32_MAX &&
+                     D <= INT32_MAX && F <= INT32_MAX && E <= (1 << 20),
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  if (T == 0 || D == 0 || R == 0) return INTENT_OK;
+  int st = kn_shape_check(D, F, F, w1, "moe_expert_ffn (w1)");
+  if (st != INTENT_OK) return st;
+  st = kn_shape_check(F, D, D, w2, "moe_expert_ffn (w2)");
+  if (st != INTENT_OK) return st;
+  INTENT_REQUIRE(x && route_offsets && member_routes && route_token && route_weights && y,
+                 INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(x_ld >= D && y_ld >= D, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(x) && x_ld % 8 == 0, INTENT_ERR_ALIGNMENT,
+                 "x must be 16-byte aligned with 16-byte row strides");
+  INTENT_REQUIRE(intent::fits_offset(T, x_ld * 2) && intent::fits_offset(R, F * 2) && intent::fits_offset(R, D * 4),
+                 INTENT_ERR_UNSUPPORTED, "moe_expert_ffn: operands exceed 31-bit buffer offsets");
+  const FfnLayout L = ffn_layout(T, R, D, F);
+  INTENT_REQUIRE(workspace && workspace_bytes >= L.bytes, INTENT_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
+                 L.bytes, workspace_bytes);
+  INTENT_REQUIRE(intent::aligned16(workspace), INTENT_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+  char* ws = (char*)workspace;
+  uint16_t* hidden = (uint16_t*)(ws + L.hidden);
+  float* contrib = (float*)(ws + L.contrib);
+  int32_t* count = (int32_t*)(ws + L.count);
+  int32_t* start = (int32_t*)(ws + L.start);
+  int32_t* list = (int32_t*)(ws + L.list);
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t ntiles = (R + GTile::BM - 1) / GTile::BM + E;
+  INTENT_REQUIRE(ntiles * ((F + GTile::BN - 1) / GTile::BN) < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+  // hidden[i] = f16(relu(x[token(i)] @ w1[e])) for the members i of expert e
+  launch_grouped<mp::F16Math, true, GEpi::kReluF16>(x, x_ld, route_offsets, E, R, member_routes, route_token, NR, T,
+                                                    nullptr, w1, F, D * F, F, D, (int)ntiles, hidden, F, s);
+  st = intent::launch_status("grouped_kn_kernel<moe w1 relu>");
+  if (st != INTENT_OK) return st;
+  // contrib[i] = route_weight * (hidden[i] @ w2[e])
+  launch_grouped<mp::F16Math, false, GEpi::kRouteWeight>(hidden, F, route_offsets, E, R, member_routes, nullptr, NR,
+                                                         T, route_weights, w2, D, F * D, D, F, (int)ntiles, contrib,
+                                                         D, s);
+  st = intent::launch_status("grouped_kn_kernel<moe w2 weighted>");
+  if (st != INTENT_OK) return st;
+  hipLaunchKernelGGL(token_member_list_kernel, dim3(1), dim3(kListThreads), 0, s, route_offsets, (int)E,
+                     member_routes, route_token, (int)T, (int)R, (int)NR, count, start, list);
+  st = intent::launch_status("token_member_list");
+  if (st != INTENT_OK) return st;
+  const int64_t items = T * ((D + 3) / 4);
+  hipLaunchKernelGGL(token_combine_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s, contrib, D, start,
+                     list, (int)T, (int)D, y, y_ld);
+  return intent::launch_status("token_combine");
+}

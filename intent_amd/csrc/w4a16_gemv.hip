@@ -13,7 +13,6 @@
 // operands, so four MFMAs cover the 128 k of the step. Activation rows m >= M
 // are zero and never loaded. Partial sums of the KW waves are reduced through
 // LDS in a fixed order and rounded to f16 once.
-#include <stdlib.h>
 
 #include "common.h"
 #include "internal.h"

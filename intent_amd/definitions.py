@@ -343,6 +343,48 @@ moe_expert_ffn_w4 = KernelDefinition(
 )
 
 
+# ---- the reference's f16 MoE expert FFN (moe.py:12-53) -----------------------------
+
+def _f16ffn_check(env: dict) -> None:
+    if env["E_PLUS_1"] != env["E"] + 1:
+        raise ValueError(f"route_offsets has {env['E_PLUS_1']} entries; {env['E'] + 1} experts need E + 1")
+    if env["D"] % 64 or env["F"] % 64:
+        raise NotImplementedError(f"D ({env['D']}) and F ({env['F']}) must be multiples of 64")
+
+
+def _f16ffn_workspace(env: dict) -> int:
+    lib = _native.library()
+    return int(lib.intent_moe_expert_ffn_workspace_size(env["T"], env["R"], env["D"], env["F"]))
+
+
+def _f16ffn_launch(v: dict, env: dict, stream: int, workspace) -> str:
+    _native.call("intent_moe_expert_ffn", _ptr(v["x"]), env["T"], env["D"], _ld(v["x"]), _ptr(v["route_offsets"]),
+                 env["E"], _ptr(v["member_routes"]), env["R"], _ptr(v["route_token"]), _ptr(v["route_weights"]),
+                 env["NR"], _ptr(v["w1"]), _ptr(v["w2"]), env["F"], _ptr(v["y"]), _ld(v["y"]), workspace.data_ptr(),
+                 workspace.numel(), stream)
+    return "intent_moe_expert_ffn"
+
+
+moe_expert_ffn = KernelDefinition(
+    name="moe_expert_ffn",
+    params=(
+        Param("x", "f16", ("T", "D"), leading_stride=True),
+        Param("route_offsets", "i32", ("E_PLUS_1",)),
+        Param("member_routes", "i32", ("R",)),
+        Param("route_token", "i32", ("NR",)),
+        Param("route_weights", "f32", ("NR",)),
+        Param("w1", "f16", ("E", "D", "F")),
+        Param("w2", "f16", ("E", "F", "D")),
+        Param("y", "f32", ("T", "D"), INOUT, leading_stride=True),
+    ),
+    launch=_f16ffn_launch,
+    check=_f16ffn_check,
+    workspace=_f16ffn_workspace,
+    reference="examples/kernels/ragged/moe.py:12-53",
+    doc="y[token] += route_weight * (f16(relu(x[token] @ w1[e])) @ w2[e]) over the ragged routes of each expert e",
+)
+
+
 def _gate_up_check(env: dict) -> None:
     if env["HP"] * 2 != env["H"] or env["F2"] % 2 or env["H"] % env["G1"]:
         raise ValueError("inconsistent gate/up weight shapes")
@@ -884,7 +926,8 @@ weight_only_int4_matmul = KernelDefinition(
 # ---- quantized_gemm: f16 GEMM with the fused int8 epilogue -------------------------
 
 def _qgemm_workspace(env: dict) -> int:
-    return env["K"] * env["N"] * 2
+    # the transposed copy of b is needed only when N is not a multiple of 8
+    return 0 if env["N"] % 8 == 0 else env["K"] * env["N"] * 2
 
 
 def _qgemm_check(env: dict) -> None:
@@ -892,11 +935,33 @@ def _qgemm_check(env: dict) -> None:
         raise NotImplementedError(f"K ({env['K']}) must be a multiple of 64")
 
 
+def _kn_direct(env: dict, *mats) -> bool:
+    """b [K, N] feeds the kernels directly (no transposed copy) when N and every
+    row stride are multiples of 8 elements and the operands 16-byte aligned."""
+    return env["N"] % 8 == 0 and all(t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0 for t in mats)
+
+
+def _transposed(b, K: int, N: int, workspace, stream: int) -> int:
+    """[K, N] -> [N, K] copy of b in the workspace (the fallback of the [K, N] entries:
+    N a multiple of 8 with an unaligned operand gets a scratch copy whose memory the
+    caching allocator holds back until the launch stream has passed it)."""
+    if workspace is None or workspace.numel() < K * N * 2:
+        import torch
+
+        workspace = torch.empty(K * N * 2, dtype=torch.uint8, device=b.device)
+        workspace.record_stream(torch.cuda.ExternalStream(stream, device=b.device))
+    _native.call("intent_f16_transpose", _ptr(b), K, N, b.stride(0), workspace.data_ptr(), K, stream)
+    return workspace.data_ptr()
+
+
 def _qgemm_launch(v: dict, env: dict, stream: int, workspace) -> str:
     a, b, out = v["a"], v["b"], v["output"]
     M, K, N = env["M"], env["K"], env["N"]
-    bt = workspace.data_ptr()
-    _native.call("intent_f16_transpose", _ptr(b), K, N, b.stride(0), bt, K, stream)
+    if _kn_direct(env, a, b):
+        _native.call("intent_quantized_gemm_kn", _ptr(a), M, K, _ld(a), _ptr(b), N, b.stride(0), _ptr(v["bias"]),
+                     _ptr(v["residual"]), _ld(v["residual"]), _ptr(v["output_scale"]), _ptr(out), _ld(out), stream)
+        return "intent_quantized_gemm_kn"
+    bt = _transposed(b, K, N, workspace, stream)
     _native.call("intent_quantized_gemm", _ptr(a), M, K, _ld(a), bt, N, K, _ptr(v["bias"]), _ptr(v["residual"]),
                  _ld(v["residual"]), _ptr(v["output_scale"]), _ptr(out), _ld(out), stream)
     return "intent_quantized_gemm"
@@ -923,7 +988,8 @@ quantized_gemm = KernelDefinition(
 # ---- f16 / bf16 grouped GEMMs (the reference's ragged kernels) ------------------
 
 def _ragged_workspace(env: dict) -> int:
-    return env["G"] * env["N"] * env["K"] * 2
+    # the transposed copy of the weights is needed only when N is not a multiple of 8
+    return 0 if env["N"] % 8 == 0 else env["G"] * env["N"] * env["K"] * 2
 
 
 def _ragged_check(env: dict) -> None:
@@ -937,6 +1003,16 @@ def _ragged_launch(bf16: bool):
     def launch(v: dict, env: dict, stream: int, workspace) -> str:
         x, offs, w, y = v["x"], v["group_offsets"], v["weight"], v["y"]
         G, K, N = env["G"], env["K"], env["N"]
+        if _kn_direct(env, x) and w.data_ptr() % 16 == 0:
+            # [G, K, N] weights in place (grouped_kn.hip)
+            _native.call("intent_grouped_gemm_kn", _ptr(x), env["R"], K, _ld(x), _ptr(offs), G, _ptr(w), N,
+                         w.stride(1), w.stride(0), int(bf16), _ptr(y), _ld(y), stream)
+            return "intent_grouped_gemm_kn"
+        if workspace is None or workspace.numel() < G * N * K * 2:
+            import torch
+
+            workspace = torch.empty(G * N * K * 2, dtype=torch.uint8, device=w.device)
+            workspace.record_stream(torch.cuda.ExternalStream(stream, device=w.device))
         wt = workspace.data_ptr()  # [G, K, N] -> [G, N, K]
         _native.call("intent_f16_transpose_batched", _ptr(w), G, K, N, w.stride(1), w.stride(0), wt, K, N * K, stream)
         _native.call("intent_grouped_gemm", _ptr(x), env["R"], K, _ld(x), _ptr(offs), G, None, 1, wt, N, K, N * K,
@@ -1004,9 +1080,12 @@ def _fgemm_launch(kind: str):
     def launch(v: dict, env: dict, stream: int, workspace) -> str:
         a, b, c = v["a"], v["b"], v["c"]
         M, K, N = env["M"], env["K"], env["N"]
-        bt = workspace.data_ptr()
-        _native.call("intent_f16_transpose", _ptr(b), K, N, b.stride(0), bt, K, stream)
         epi = 2 if kind == "bf16" else (1 if int(env.get("ACTIVATION", 0)) == 1 else 0)
+        if _kn_direct(env, a, b):
+            _native.call("intent_f16_gemm_kn", _ptr(a), M, K, _ld(a), _ptr(b), N, b.stride(0), epi, _ptr(c), _ld(c),
+                         stream)
+            return "intent_f16_gemm_kn"
+        bt = _transposed(b, K, N, workspace, stream)
         _native.call("intent_f16_gemm", _ptr(a), M, K, _ld(a), bt, N, K, epi, _ptr(c), _ld(c), stream)
         return "intent_f16_gemm"
     return launch
@@ -1070,7 +1149,7 @@ nvfp4_quantize = KernelDefinition(
 ALL_DEFINITIONS = (
     weight_only_int4_matmul, weight_only_int4_asym_matmul, weight_only_int8_matmul, w8a8_scaled_matmul, gemm_i8_nt,
     gemm_i8,
-    moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine,
+    moe_route_topk, moe_align_block_size, moe_expert_ffn_w4, moe_gate_up_w4, moe_down_w4, moe_combine, moe_expert_ffn,
     q8_k_quantize, q4_k_q8_k_dot, quantized_projection, bf16_groupwise_fp8_quantize, f32_groupwise_fp8_quantize,
     w4a8_packed_matmul, bitnet_int2_matmul, block_scaled_matmul, scaled_fp8_matmul, scaled_fp8_splitk_matmul,
     deepgemm_fp8_2xacc, fp8_e4m3_matmul, fp8_e5m2_matmul, dequant_bf16_fp4_matmul, quantized_gemm,

@@ -82,6 +82,47 @@ def config4_moe(seed: int = 0, T: int = 512, H: int = 4096, E: int = 8, top_k: i
             "wd": wd, "sd": sd, "zd": zd}
 
 
+def moe_routes(T: int, top_k: int, E: int, kind: str = "reference", seed: int = 0) -> dict:
+    """Ragged routing of the reference's f16 MoE FFN (moe.py:12-53).
+
+    kind "reference": the construction of experiments/_common/support.py:113-130 (route r =
+    token r // top_k, weight 1/top_k, expert r % E, members = stable argsort by expert);
+    kind "random": top-k experts of seeded N(0,1) logits per token with their renormalised
+    softmax weights, members stable-sorted by expert (the moe_align order)."""
+    R = T * top_k
+    route_token = np.repeat(np.arange(T, dtype=np.int32), top_k)
+    if kind == "reference":
+        experts = (np.arange(R) % E).astype(np.int64)
+        weights = np.full(R, 1.0 / top_k, np.float32)
+    else:
+        rng = np.random.default_rng(seed)
+        logits = rng.standard_normal((T, E)).astype(np.float32)
+        ids = np.argsort(-logits, axis=1, kind="stable")[:, :top_k]
+        p = np.exp(logits - logits.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        pw = np.take_along_axis(p, ids, axis=1)
+        weights = (pw / pw.sum(axis=1, keepdims=True)).astype(np.float32).reshape(-1)
+        experts = ids.reshape(-1).astype(np.int64)
+    members = np.argsort(experts, kind="stable").astype(np.int32)
+    counts = np.bincount(experts, minlength=E)
+    offsets = np.concatenate(([0], np.cumsum(counts))).astype(np.int32)
+    return {"route_offsets": offsets, "member_routes": members, "route_token": route_token,
+            "route_weights": weights}
+
+
+def moe_ffn_f16(seed: int = 0, T: int = 512, D: int = 4096, E: int = 8, top_k: int = 2, F: int = 14336,
+                kind: str = "reference") -> dict:
+    """Inputs of the reference's f16 moe_expert_ffn: x [T, D], w1 [E, D, F], w2 [E, F, D] ~ N(0,1)
+    scaled by 1/sqrt(fan-in) (keeps f16 hidden values in range), f32 y [T, D] zeros."""
+    rng = np.random.default_rng(seed)
+    d = moe_routes(T, top_k, E, kind, seed)
+    d["x"] = normal_f16(rng, (T, D))
+    d["w1"] = (rng.standard_normal((E, D, F), dtype=np.float32) / np.sqrt(D)).astype(np.float16)
+    d["w2"] = (rng.standard_normal((E, F, D), dtype=np.float32) / np.sqrt(F)).astype(np.float16)
+    d["y"] = np.zeros((T, D), np.float32)
+    return d
+
+
 def q4k_records(rng: np.random.Generator, shape, d_range=(0.0005, 0.005)) -> np.ndarray:
     """Random Q4_K records uint8 [*shape, 144]: f16 d and dmin drawn from d_range;
     every other byte (6-bit sc/m fields, nibbles) uniform, which is always a

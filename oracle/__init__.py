@@ -102,6 +102,8 @@ def lib():
         _lib.orc_grouped_gemm.restype = None
         _lib.orc_float_gemm.argtypes = [p, i64, i64, p, i64, ci, ci, p, ci]
         _lib.orc_float_gemm.restype = None
+        _lib.orc_moe_expert_ffn.argtypes = [p, i64, i64, p, i64, p, p, p, p, p, i64, p, p, ctypes.c_int]
+        _lib.orc_moe_expert_ffn.restype = None
         _lib.orc_nvfp4_quantize.argtypes = [p, i64, i64, ctypes.c_float, p, p]
         _lib.orc_nvfp4_quantize.restype = None
         _lib.orc_bitnet_int2.restype = None
@@ -408,6 +410,26 @@ def grouped_gemm(x_bits, bf16: bool, offsets, w_bits, out_rows: int, routes=None
     r = None if routes is None else _c(routes, np.int32)
     lib().orc_grouped_gemm(_ptr(x), int(bf16), K, _ptr(offs), G, None if r is None else _ptr(r), top_k, _ptr(w), N,
                            _ptr(out), threads)
+    return out
+
+
+def moe_expert_ffn(x, route_offsets, member_routes, route_token, route_weights, w1, w2, y=None, tokens=None,
+                   threads: int = 1) -> np.ndarray:
+    """f16 x [T, D], i32 route_offsets [E+1], member_routes [R], route_token [NR], f32 route_weights [NR],
+    f16 w1 [E, D, F], w2 [E, F, D] -> f32 y [T, D] (y += ..., from zeros if y is None). tokens: optional
+    indices whose rows are computed (others keep y's values)."""
+    x, w1, w2 = _c(x, np.float16), _c(w1, np.float16), _c(w2, np.float16)
+    offs, mem, tok = _c(route_offsets, np.int32), _c(member_routes, np.int32), _c(route_token, np.int32)
+    rw = _c(route_weights, np.float32)
+    T, D = x.shape
+    E, _, F = w1.shape
+    out = np.zeros((T, D), np.float32) if y is None else _c(y, np.float32).copy()
+    sel = None
+    if tokens is not None:
+        sel = np.zeros(T, np.uint8)
+        sel[np.asarray(tokens)] = 1
+    lib().orc_moe_expert_ffn(_ptr(x), T, D, _ptr(offs), E, _ptr(mem), _ptr(tok), _ptr(rw), _ptr(w1), _ptr(w2), F,
+                             _ptr(out), None if sel is None else _ptr(sel), threads)
     return out
 
 

@@ -759,6 +759,49 @@ void orc_grouped_gemm(const uint16_t* x, int bf16, int64_t K, const int32_t* off
   }
 }
 
+/* ---- f16 MoE expert FFN ---------------------------------------------------------------
+ * moe_expert_ffn (examples/kernels/ragged/moe.py:12-53; host reference
+ * experiments/_common/support.py:133-151): for expert e in order and each member i of
+ * [route_offsets[e], route_offsets[e+1]): route r = member_routes[i], token t =
+ * route_token[r]; hidden = f16(max(x[t] @ w1[e], 0)) (f32 fma in k order, ReLU in f32,
+ * one rounding); out = hidden @ w2[e] (f32 fma in f order); y[t] += route_weights[r] * out
+ * (f32 product, then f32 add: scatter_reduce add). w1 [E, D, F], w2 [E, F, D] f16.
+ * token_sel (T entries, or NULL = all): members of unselected tokens are skipped. */
+void orc_moe_expert_ffn(const uint16_t* x, int64_t T, int64_t D, const int32_t* route_offsets, int64_t E,
+                        const int32_t* member_routes, const int32_t* route_token, const float* route_weights,
+                        const uint16_t* w1, const uint16_t* w2, int64_t F, float* y, const uint8_t* token_sel,
+                        int threads) {
+  float* hid = (float*)malloc(sizeof(float) * (size_t)(F > 0 ? F : 1));
+  float* out = (float*)malloc(sizeof(float) * (size_t)(D > 0 ? D : 1));
+  for (int64_t e = 0; e < E; ++e) {
+    for (int64_t i = route_offsets[e]; i < route_offsets[e + 1]; ++i) {
+      const int64_t r = member_routes[i];
+      const int64_t t = route_token[r];
+      if (token_sel && !token_sel[t]) continue;
+      const uint16_t* xr = x + t * D;
+      const uint16_t* a = w1 + e * D * F;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+      for (int64_t f = 0; f < F; ++f) {
+        float acc = 0.0f;
+        for (int64_t k = 0; k < D; ++k) acc = fmaf(orc_f16_to_f32(xr[k]), orc_f16_to_f32(a[k * F + f]), acc);
+        acc = acc < 0.0f ? 0.0f : acc;
+        hid[f] = orc_f16_to_f32(orc_f32_to_f16(acc));
+      }
+      const uint16_t* b = w2 + e * F * D;
+#pragma omp parallel for num_threads(threads > 0 ? threads : 1) schedule(static)
+      for (int64_t d = 0; d < D; ++d) {
+        float acc = 0.0f;
+        for (int64_t f = 0; f < F; ++f) acc = fmaf(hid[f], orc_f16_to_f32(b[f * D + d]), acc);
+        out[d] = acc;
+      }
+      const float wt = route_weights[r];
+      for (int64_t d = 0; d < D; ++d) y[t * D + d] = y[t * D + d] + wt * out[d];
+    }
+  }
+  free(hid);
+  free(out);
+}
+
 /* ---- float GEMMs ----------------------------------------------------------------------
  * gemm (examples/kernels/contraction/gemm.py:42-61, ACTIVATION RELU: max(acc, 0)) and
  * bf16_gemm (gemm.py:64-80): c = cast(f32 contraction (fma in k order)); b is [K, N]. */

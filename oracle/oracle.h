@@ -58,6 +58,10 @@ void orc_quantized_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t*
                         const uint16_t* residual, const float* oscale, int8_t* out, int threads);
 void orc_grouped_gemm(const uint16_t* x, int bf16, int64_t K, const int32_t* offsets, int64_t G, const int32_t* routes,
                       int64_t top_k, const uint16_t* w, int64_t N, uint16_t* out, int threads);
+void orc_moe_expert_ffn(const uint16_t* x, int64_t T, int64_t D, const int32_t* route_offsets, int64_t E,
+                        const int32_t* member_routes, const int32_t* route_token, const float* route_weights,
+                        const uint16_t* w1, const uint16_t* w2, int64_t F, float* y, const uint8_t* token_sel,
+                        int threads);
 void orc_float_gemm(const uint16_t* a, int64_t M, int64_t K, const uint16_t* b, int64_t N, int bf16, int relu,
                     uint16_t* c, int threads);
 void orc_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t N, float gs, uint8_t* packed, uint8_t* scales);

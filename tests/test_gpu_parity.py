@@ -700,7 +700,8 @@ def test_weight_only_int4_matmul_reference_layout(gpu, threads, M, K, N):
 
 # ---- quantized_gemm -------------------------------------------------------------------
 
-@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (1, 64, 1), (200, 256, 260), (4096, 4096, 14336)])
+@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (1, 64, 1), (200, 256, 260), (4096, 4096, 14336),
+                                   (300, 384, 136), (513, 640, 264)])
 def test_quantized_gemm(gpu, threads, M, K, N):
     # the reference's input construction (experiments/cpu/providers/mojo/contraction.py:177-186)
     g = torch.Generator().manual_seed(M + N)
@@ -738,15 +739,18 @@ def _bits16(t):
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-def test_ragged_grouped_gemm(gpu, threads, dt):
+@pytest.mark.parametrize("N", [300, 296])
+def test_ragged_grouped_gemm(gpu, threads, dt, N):
+    # N = 296: weights read in place as [G, K, N]; N = 300: the transposed-copy fallback
     tdt = torch.float16 if dt == "f16" else torch.bfloat16
     g = torch.Generator().manual_seed(61)
-    R, K, N = 1000, 256, 300
+    R, K = 1000, 256
     offsets = torch.tensor([0, 100, 100, 650, 1000], dtype=torch.int32)  # group 1 is empty
     x = torch.randn(R, K, generator=g).to(tdt)
     w = (torch.randn(4, K, N, generator=g) / 16).to(tdt)
     defn = intent.ragged_grouped_gemm if dt == "f16" else intent.ragged_grouped_gemm_bf16
     y = art(defn).run(x.cuda(), offsets.cuda(), w.cuda())
+    assert art(defn).observation.entry == ("intent_grouped_gemm_kn" if N % 8 == 0 else "intent_grouped_gemm")
     ref = oracle.grouped_gemm(_bits16(x), dt == "bf16", offsets.numpy(), _bits16(w), R, threads=threads)
     got = _bits16(y.cpu())
     r64 = torch.from_numpy(ref.view(np.int16)).view(tdt).double().numpy()
@@ -770,6 +774,50 @@ def test_ragged_grouped_gemm_reference_size(gpu):
     assert (y.double() - ref.double()).abs().max().item() <= 1e-2 * ref.abs().max().item()
 
 
+# ---- the reference's f16 MoE expert FFN (moe.py:12-53) ------------------------------------
+
+def _ffn_run(d, y0):
+    dv = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda() for k, v in d.items() if k != "y"}
+    y = torch.from_numpy(y0.copy()).cuda()
+    art(intent.moe_expert_ffn).run(dv["x"], dv["route_offsets"], dv["member_routes"], dv["route_token"],
+                                   dv["route_weights"], dv["w1"], dv["w2"], y)
+    return host(y)
+
+
+@pytest.mark.parametrize("T,D,E,k,F,kind", [(64, 256, 4, 2, 384, "random"), (37, 128, 3, 1, 192, "random"),
+                                            (16, 128, 8, 2, 128, "reference"), (300, 512, 8, 2, 1024, "random")])
+def test_moe_expert_ffn(gpu, threads, T, D, E, k, F, kind):
+    d = inputs.moe_ffn_f16(T + D, T=T, D=D, E=E, top_k=k, F=F, kind=kind)
+    y0 = np.random.default_rng(T).standard_normal((T, D)).astype(np.float32)
+    got = _ffn_run(d, y0)
+    ref = oracle.moe_expert_ffn(d["x"], d["route_offsets"], d["member_routes"], d["route_token"], d["route_weights"],
+                                d["w1"], d["w2"], y=y0, threads=threads)
+    assert_close_rms(got - y0, ref - y0, what=f"moe_expert_ffn {T}x{D}x{F}")
+    again = _ffn_run(d, y0)
+    assert np.array_equal(got, again), "the combine must be deterministic"
+
+
+@pytest.mark.parametrize("T", [512, 4096])
+def test_moe_expert_ffn_reference_size(gpu, threads, T):
+    # moe.py:6-10 (T = 4096, D = 4096, F = 14336, E = 8, top-2) and the config-4 token count,
+    # routes by support.py:113-130; 8 tokens checked against the oracle
+    D, F, E, K = 4096, 14336, 8, 2
+    d = inputs.moe_routes(T, K, E, "reference")
+    g = torch.Generator(device="cuda").manual_seed(T)
+    x = torch.randn(T, D, device="cuda", generator=g).half()
+    w1 = (torch.randn(E, D, F, device="cuda", generator=g) / D ** 0.5).half()
+    w2 = (torch.randn(E, F, D, device="cuda", generator=g) / F ** 0.5).half()
+    y = torch.zeros(T, D, device="cuda")
+    dv = {k: torch.from_numpy(v).cuda() for k, v in d.items()}
+    art(intent.moe_expert_ffn).run(x, dv["route_offsets"], dv["member_routes"], dv["route_token"],
+                                   dv["route_weights"], w1, w2, y)
+    toks = np.r_[0:4, T - 4:T]
+    ref = oracle.moe_expert_ffn(x.cpu().numpy(), d["route_offsets"], d["member_routes"], d["route_token"],
+                                d["route_weights"], w1.cpu().numpy(), w2.cpu().numpy(), tokens=toks,
+                                threads=threads)
+    assert_close_rms(host(y)[toks], ref[toks], what=f"moe_expert_ffn T={T}")
+
+
 def test_routed_expert_projection_bf16(gpu, threads):
     g = torch.Generator().manual_seed(63)
     T, TOP_K, E, K, N = 300, 2, 4, 256, 200
@@ -791,21 +839,35 @@ def test_routed_expert_projection_bf16(gpu, threads):
 # ---- plain float GEMMs (gemm.py) ----------------------------------------------------------
 
 @pytest.mark.parametrize("kind", ["f16", "f16_relu", "bf16"])
-@pytest.mark.parametrize("M,K,N", [(64, 128, 64), (300, 384, 130), (4096, 4096, 4096)])
-def test_float_gemm(gpu, threads, kind, M, K, N):
+@pytest.mark.parametrize("M,K,N,bpad", [(64, 128, 64, 0), (300, 384, 130, 0), (4096, 4096, 4096, 0),
+                                        (300, 384, 136, 0), (77, 192, 520, 8), (257, 128, 264, 3)])
+def test_float_gemm(gpu, threads, kind, M, K, N, bpad):
+    # N % 8 == 0 with aligned rows: b [K, N] feeds the kernel directly (transpose reads in LDS);
+    # N = 130 or a row stride of N + 3: the transposed-copy fallback. Rows 0..7 and the last 8
+    # against the C oracle, the whole matrix against a float64 product on the GPU.
     tdt = torch.bfloat16 if kind == "bf16" else torch.float16
     g = torch.Generator().manual_seed(M + K + N)
     a = torch.randn(M, K, generator=g).to(tdt) / (K ** 0.5)
     b = torch.randn(K, N, generator=g).to(tdt)
+    bdev = torch.zeros(K, N + bpad, dtype=tdt, device="cuda")
+    bdev[:, :N] = b.cuda()
+    bdev = bdev[:, :N]
     if kind == "bf16":
-        c = art(intent.bf16_gemm).run(a.cuda(), b.cuda())
+        art_ = art(intent.bf16_gemm)
     else:
-        c = art(intent.gemm, ACTIVATION=1 if kind == "f16_relu" else 0).run(a.cuda(), b.cuda())
+        art_ = art(intent.gemm, ACTIVATION=1 if kind == "f16_relu" else 0)
+    c = art_.run(a.cuda(), bdev)
+    direct = N % 8 == 0 and bpad % 8 == 0
+    assert art_.observation.entry == ("intent_f16_gemm_kn" if direct else "intent_f16_gemm")
     rows = np.r_[0:min(M, 8), max(0, M - 8):M]
     ref = oracle.float_gemm(_bits16(a)[rows], _bits16(b), kind == "bf16", kind == "f16_relu", threads)
     r64 = torch.from_numpy(ref.view(np.int16)).view(tdt).double().numpy()
     g64 = torch.from_numpy(_bits16(c.cpu())[rows].view(np.int16)).view(tdt).double().numpy()
     assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()
+    full = a.cuda().double() @ b.cuda().double()
+    if kind == "f16_relu":
+        full = full.clamp_min(0.0)
+    assert (c.double() - full).abs().max().item() <= 1e-2 * full.abs().max().item()
 
 
 # ---- NVFP4 quantizer --------------------------------------------------------------------

@@ -855,3 +855,44 @@ def test_i8_per_token_brute_force_tiny():
             frac = t - lo
             r = lo + (1 if frac > 0.5 or (frac == 0.5 and int(lo) % 2 != 0) else 0)
             assert q[m, k] == int(r), (m, k, x[m, k], t)
+
+
+# ---- f16 MoE expert FFN (moe.py:12-53) --------------------------------------------------
+
+@pytest.mark.parametrize("kind", ["reference", "random"])
+def test_moe_expert_ffn_oracle_matches_restatements(kind):
+    # float64 restatement of the kernel's formula (hidden rounded to f16 after the f32 ReLU) and the
+    # reference's host formula experiments/_common/support.py:133-151 (hidden kept in f32)
+    d = inputs.moe_ffn_f16(3, T=12, D=64, E=4, top_k=2, F=96, kind=kind)
+    y0 = np.random.default_rng(1).standard_normal((12, 64)).astype(np.float32)
+    got = oracle.moe_expert_ffn(d["x"], d["route_offsets"], d["member_routes"], d["route_token"], d["route_weights"],
+                                d["w1"], d["w2"], y=y0, threads=2)
+    x = d["x"].astype(np.float64)
+    want = y0.astype(np.float64).copy()
+    host = y0.astype(np.float64).copy()
+    offs = d["route_offsets"]
+    for e in range(4):
+        routes = d["member_routes"][offs[e]:offs[e + 1]]
+        tok = d["route_token"][routes]
+        h32 = np.maximum(x[tok] @ d["w1"][e].astype(np.float64), 0.0)
+        h16 = h32.astype(np.float16).astype(np.float64)
+        wts = d["route_weights"][routes].astype(np.float64)[:, None]
+        np.add.at(want, tok, wts * (h16 @ d["w2"][e].astype(np.float64)))
+        np.add.at(host, tok, wts * (h32 @ d["w2"][e].astype(np.float64)))
+    assert np.max(np.abs(got - want)) <= 1e-4 * np.abs(want).max()
+    assert np.max(np.abs(got - host)) <= 1e-2 * np.sqrt(np.mean(host ** 2))
+    # every route lands once: with zero w2 the output is y0 exactly
+    z = oracle.moe_expert_ffn(d["x"], d["route_offsets"], d["member_routes"], d["route_token"], d["route_weights"],
+                              d["w1"], np.zeros_like(d["w2"]), y=y0)
+    assert np.array_equal(z, y0)
+
+
+def test_moe_routes_reference_construction():
+    # support.py:113-130 at its own T/E/top_k ratio: expert r % E, members grouped by expert
+    d = inputs.moe_routes(16, 2, 8)
+    assert d["route_offsets"].tolist() == list(range(0, 33, 4))
+    exp = np.arange(32) % 8
+    for e in range(8):
+        mem = d["member_routes"][d["route_offsets"][e]:d["route_offsets"][e + 1]]
+        assert (exp[mem] == e).all() and (np.diff(mem) > 0).all()
+    assert np.allclose(d["route_weights"], 0.5) and (d["route_token"] == np.arange(32) // 2).all()
