@@ -145,6 +145,23 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t*
 // and selects the weight base pointers. Token rows reach LDS by DMA through
 // the route ids; weights go through VGPRs with the W4 decode.
 
+// XCD-aware tile order. Workgroup b runs on XCD b % 8, and each XCD takes
+// the column tiles [x * ct / 8, (x + 1) * ct / 8) of every row block, row
+// block outer: the workgroups an XCD runs back to back share their token
+// rows in its L2 instead of re-reading them from MALL for every column tile,
+// and no weight tile is read by two XCDs. Plain order when ct % 8 != 0.
+INTENT_DEVICE void moe_tile_order(int bid, int mblocks, int ctiles, int& mb, int& ct) {
+  if ((ctiles & 7) != 0) {
+    mb = bid % mblocks;
+    ct = bid / mblocks;
+    return;
+  }
+  const int per = ctiles >> 3;
+  const int local = bid >> 3;
+  mb = local / per;
+  ct = (bid & 7) * per + local % per;
+}
+
 // Tiles per alignment block size B: gate/up covers 256 weight rows (128
 // features, gate and up), down 128 output columns. Producer/consumer
 // workgroups (mainloop_ws): 4 consumer waves + 4 producer waves.
@@ -241,8 +258,9 @@ __global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_ker
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf2[T::STAGE_BYTES];
   char* const bufs[3] = {buf0, buf1, buf2};
-  const int mb = blockIdx.x % mblocks;
-  const int f0 = (blockIdx.x / mblocks) * (T::BN / 2);
+  int mb, ct;
+  moe_tile_order(blockIdx.x, mblocks, gridDim.x / mblocks, mb, ct);
+  const int f0 = ct * (T::BN / 2);
   const int e = blocks[mb];
   if (e < 0) return;
   const int64_t ldq = H / 2;
@@ -280,8 +298,9 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
   char* bufs[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) bufs[b] = smem[b];
-  const int mb = blockIdx.x % mblocks;
-  const int f0 = (blockIdx.x / mblocks) * (T::BN / 2);
+  int mb, ct;
+  moe_tile_order(blockIdx.x, mblocks, gridDim.x / mblocks, mb, ct);
+  const int f0 = ct * (T::BN / 2);
   const int e = blocks[mb];
   if (e < 0) return;
   const int64_t ldq = H / 2;
@@ -296,7 +315,23 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
   mp::GroupParamsDma<T::BN, T::NW> pop;
   pop.init(ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs, rows, wave);
   f32x16 acc[T::TI][T::TJ];
-  mp::mainloop_pk<T, NB>(aop, bop, pop, H / 64, bufs, acc);
+  // An expert's padding rows (sentinel route R) sit at the end of its last
+  // block: only the 32-row blocks holding a route are computed.
+  int ta = 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) ta += sorted[m0 + 32 * i] < R ? 1 : 0;
+  ta = __builtin_amdgcn_readfirstlane(ta);
+  using ADma = decltype(aop);
+  using BDma = decltype(bop);
+  using PDma = decltype(pop);
+  if (ta <= 1)
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 1>(aop, bop, pop, H / 64, bufs, acc);
+  else if (ta == 2)
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 2>(aop, bop, pop, H / 64, bufs, acc);
+  else if (ta == 3)
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 3>(aop, bop, pop, H / 64, bufs, acc);
+  else
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, H / 64, bufs, acc);
   store_gate_up<T>(acc, m0, f0, F, sorted, R, act, ld_act);
 }
 
@@ -340,8 +375,9 @@ __global__ __launch_bounds__(MoeTiles<B>::Down::NT_WS, 1) void moe_down_kernel(
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf2[T::STAGE_BYTES];
   char* const bufs[3] = {buf0, buf1, buf2};
-  const int mb = blockIdx.x % mblocks;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  int mb, ct;
+  moe_tile_order(blockIdx.x, mblocks, ntiles, mb, ct);
+  const int n0 = ct * T::BN;
   const int e = blocks[mb];
   if (e < 0) return;
   const int64_t ldq = F / 2;
@@ -357,10 +393,71 @@ __global__ __launch_bounds__(MoeTiles<B>::Down::NT_WS, 1) void moe_down_kernel(
   store_down<T>(acc, m0, n0, H, sorted, R, out, ldo);
 }
 
+// Down projection on the packed-weight core (the gate/up tile: 128-row blocks
+// x 256 output columns, four waves decoding their own weight fragments, two
+// workgroups per CU). K (= F) is split into `splits` equal parts, each a
+// multiple of four quantisation groups (so a part starts on a group dword),
+// and part p writes its f32 partial sums to out + p * part_stride; the
+// combine adds the parts in order. Measured on config 4: 328 us for the
+// producer/consumer kernel below, which runs 384 workgroups of 128 x 128 with
+// the decode in separate waves.
+__global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
+    const f16* __restrict__ act, int64_t ld_act, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ blocks, int mblocks, int ntiles, int R, const uint8_t* __restrict__ wq,
+    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int H, int F, int gs, int splits,
+    float* __restrict__ out, int64_t ldo, int64_t part_stride) {
+  using T = GateUpPk;
+  constexpr int NB = kGateUpPkStages;
+  __shared__ __attribute__((aligned(16))) char smem[NB][mp::stage_bytes_pk<T>()];
+  char* bufs[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) bufs[b] = smem[b];
+  const int per_part = mblocks * ntiles;
+  const int part = blockIdx.x / per_part;
+  int mb, ct;
+  moe_tile_order(blockIdx.x - part * per_part, mblocks, ntiles, mb, ct);
+  const int n0 = ct * T::BN;
+  const int e = blocks[mb];
+  if (e < 0) return;
+  const int kpart = F / splits;
+  const int k0 = part * kpart;
+  const int64_t ldq = F / 2;
+  const int64_t ldp = F / gs;
+  const int m0 = mb * T::BM;
+  const int wave = T::wave();
+  const ClampRows rows{n0, H};
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{act + k0, ld_act * 2, m0 + T::BM}, m0, wave);
+  mp::PackedRowsDma<T::BN, T::NW> bop;
+  bop.init(wq + (int64_t)e * H * ldq + k0 / 2, ldq, rows, wave);
+  mp::GroupParamsDma<T::BN, T::NW> pop;
+  pop.init(ws + (int64_t)e * H * ldp + k0 / gs, wz + (int64_t)e * H * ldp + k0 / gs, ldp, gs, rows, wave);
+  f32x16 acc[T::TI][T::TJ];
+  int ta = 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) ta += sorted[m0 + 32 * i] < R ? 1 : 0;
+  ta = __builtin_amdgcn_readfirstlane(ta);
+  using ADma = decltype(aop);
+  using BDma = decltype(bop);
+  using PDma = decltype(pop);
+  const int nk = kpart / 64;
+  if (ta <= 1)
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 1>(aop, bop, pop, nk, bufs, acc);
+  else if (ta == 2)
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 2>(aop, bop, pop, nk, bufs, acc);
+  else if (ta == 3)
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 3>(aop, bop, pop, nk, bufs, acc);
+  else
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, nk, bufs, acc);
+  store_down<T>(acc, m0, n0, H, sorted, R, out + part * part_stride, ldo);
+}
+
 // y[t, d] += w[t, s] * out[t*k + s, d], slot by slot (mul then add, no fma).
+// With splits > 1 the route's output is the in-order sum of its K parts
+// (part p at route_out + p * part_stride).
 __global__ void moe_combine_kernel(const float* __restrict__ route_out, int64_t ldo,
                                    const float* __restrict__ weights, int T, int top_k, float* __restrict__ y, int H,
-                                   int64_t ldy) {
+                                   int64_t ldy, int splits = 1, int64_t part_stride = 0) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)T * H;
   if (i >= total) return;
@@ -368,7 +465,10 @@ __global__ void moe_combine_kernel(const float* __restrict__ route_out, int64_t 
   const int d = (int)(i % H);
   float acc = y[(int64_t)t * ldy + d];
   for (int s = 0; s < top_k; ++s) {
-    const float prod = __fmul_rn(weights[(int64_t)t * top_k + s], route_out[((int64_t)t * top_k + s) * ldo + d]);
+    const int64_t o = ((int64_t)t * top_k + s) * ldo + d;
+    float v = route_out[o];
+    for (int p = 1; p < splits; ++p) v = __fadd_rn(v, route_out[o + p * part_stride]);
+    const float prod = __fmul_rn(weights[(int64_t)t * top_k + s], v);
     acc = __fadd_rn(acc, prod);
   }
   y[(int64_t)t * ldy + d] = acc;
@@ -562,6 +662,9 @@ extern "C" int intent_moe_combine(const float* route_out, int64_t out_ld, const 
 
 namespace {
 
+// K parts of the composite's down projection (moe_down_pk_kernel).
+constexpr int kDownSplits = 2;
+
 struct MoEWorkspace {
   size_t ids, weights, sorted, blocks, offsets, total, act, out, bytes;
   int64_t capacity, nblocks;
@@ -582,7 +685,7 @@ MoEWorkspace moe_layout(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t 
   w.offsets = o; o = round256(o + sizeof(int32_t) * (E + 1));
   w.total = o;   o = round256(o + sizeof(int32_t));
   w.act = o;     o = round256(o + sizeof(uint16_t) * (size_t)(w.nblocks * B) * F);
-  w.out = o;     o = round256(o + sizeof(float) * (size_t)R * H);
+  w.out = o;     o = round256(o + sizeof(float) * (size_t)R * H * kDownSplits);
   w.bytes = o;
   return w;
 }
@@ -632,8 +735,30 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
   st = intent_moe_gate_up_w4(x, T, H, H, sorted, blocks, L.nblocks, B, top_k, wgu_packed, wgu_scales, wgu_zeros, E, F,
                              group_size, act, F, stream);
   if (st != INTENT_OK) return st;
-  st = intent_moe_down_w4(act, F, sorted, blocks, L.nblocks, B, T * top_k, wd_packed, wd_scales, wd_zeros, E, H, F,
-                          group_size, out, H, stream);
+  const int64_t R = T * top_k;
+  const int64_t ldp = F / group_size;
+  const bool pk = ldp % 4 == 0 && F % (kDownSplits * 4 * group_size) == 0 && (F / kDownSplits) % 64 == 0 &&
+                  intent::aligned4(wd_scales) && intent::aligned4(wd_zeros);
+  int splits = 1;
+  if (pk) {
+    st = down_check(act, F, sorted, blocks, L.nblocks, B, R, wd_packed, wd_scales, wd_zeros, E, H, F, group_size, out,
+                    H);
+    if (st != INTENT_OK) return st;
+    splits = kDownSplits;
+    const int64_t ntiles = (H + GateUpPk::BN - 1) / GateUpPk::BN;
+    const int64_t grid = splits * L.nblocks * ntiles;
+    INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+    hipLaunchKernelGGL(moe_down_pk_kernel, dim3((unsigned)grid), dim3(GateUpPk::NT), 0, (hipStream_t)stream,
+                       (const f16*)act, F, sorted, blocks, (int)L.nblocks, (int)ntiles, (int)R, wd_packed,
+                       (const f16*)wd_scales, wd_zeros, (int)H, (int)F, (int)group_size, splits, out, H, R * H);
+    st = intent::launch_status("moe_down_pk");
+  } else {
+    st = intent_moe_down_w4(act, F, sorted, blocks, L.nblocks, B, R, wd_packed, wd_scales, wd_zeros, E, H, F,
+                            group_size, out, H, stream);
+  }
   if (st != INTENT_OK) return st;
-  return intent_moe_combine(out, H, wts, T, top_k, y, H, H, stream);
+  const int threads = 256;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((T * H + threads - 1) / threads)), dim3(threads), 0,
+                     (hipStream_t)stream, out, H, wts, (int)T, (int)top_k, y, (int)H, H, splits, R * H);
+  return intent::launch_status("moe_combine");
 }

@@ -134,7 +134,7 @@ struct StagePk {
 
 // Reads of a stage that the first MFMA needs. sshift / zshift select the
 // lane's scale half and zero byte inside the staged dwords.
-template <class T>
+template <class T, int TA>
 INTENT_DEVICE void stage_prologue(const char* buf, const uint32_t (&aaddr)[4], uint32_t baddr, uint32_t paddr,
                                   int sshift, int zshift, StagePk<T>& st) {
   const char* a = buf;
@@ -149,20 +149,20 @@ INTENT_DEVICE void stage_prologue(const char* buf, const uint32_t (&aaddr)[4], u
     st.sc[j] = splat2(bit_cast<f16>((uint16_t)(sw >> sshift)));
   }
 #pragma unroll
-  for (int i = 0; i < T::TI; ++i) st.af[i] = *reinterpret_cast<const f16x8*>(a + aaddr[0] + i * 32 * ROWB);
+  for (int i = 0; i < TA; ++i) st.af[i] = *reinterpret_cast<const f16x8*>(a + aaddr[0] + i * 32 * ROWB);
 #pragma unroll
   for (int j = 0; j < T::TJ; ++j) st.bf[j] = dequant8(st.bq[j][0], st.zo[j], st.sc[j]);
 }
 
 // The four MFMA steps of a stage; the A reads and weight decodes of step
 // kk + 1 are interleaved with the MFMAs of step kk.
-template <class T>
+template <class T, int TA>
 INTENT_DEVICE void stage_body(const char* buf, const uint32_t (&aaddr)[4], const StagePk<T>& st,
                               f32x16 (&acc)[T::TI][T::TJ]) {
   const char* a = buf;
   f16x8 af[2][T::TI], bf[2][T::TJ];
 #pragma unroll
-  for (int i = 0; i < T::TI; ++i) af[0][i] = st.af[i];
+  for (int i = 0; i < TA; ++i) af[0][i] = st.af[i];
 #pragma unroll
   for (int j = 0; j < T::TJ; ++j) bf[0][j] = st.bf[j];
 #pragma unroll
@@ -170,20 +170,20 @@ INTENT_DEVICE void stage_body(const char* buf, const uint32_t (&aaddr)[4], const
     const int cb = kk & 1;
     if (kk + 1 < 4) {
 #pragma unroll
-      for (int i = 0; i < T::TI; ++i)
+      for (int i = 0; i < TA; ++i)
         af[cb ^ 1][i] = *reinterpret_cast<const f16x8*>(a + aaddr[kk + 1] + i * 32 * ROWB);
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j) bf[cb ^ 1][j] = dequant8(st.bq[j][kk + 1], st.zo[j], st.sc[j]);
     }
 #pragma unroll
-    for (int i = 0; i < T::TI; ++i)
+    for (int i = 0; i < TA; ++i)
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cb][j], af[cb][i], acc[i][j], 0, 0, 0);
   }
   // Schedule (masks: 0x008 MFMA, 0x002 VALU, 0x100 DS read): per step one
   // MFMA followed by its share of the next step's reads and decode VALU.
-  constexpr int NM = T::TI * T::TJ;
+  constexpr int NM = TA * T::TJ;
   constexpr int VALU_STEP = T::TJ * 17;  // decode of one step (dequant8)
   static_for<0, 4>([&](auto KK) {
     constexpr int kk = decltype(KK)::value;
@@ -191,7 +191,7 @@ INTENT_DEVICE void stage_body(const char* buf, const uint32_t (&aaddr)[4], const
       constexpr int x = decltype(X)::value;
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if constexpr (kk < 3) {
-        if constexpr (x < T::TI) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if constexpr (x < TA) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         constexpr int v = (x + 1) * VALU_STEP / NM - x * VALU_STEP / NM;
         if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
       }
@@ -214,7 +214,9 @@ constexpr int stage_bytes_pk() {
   return T::A_BYTES + T::BN * 32 + GroupParamsDma<T::BN, T::NW>::BYTES;
 }
 
-template <class T, int NB, class ADma, class BDma, class PDma>
+// TA <= T::TI: only the first TA 32-row blocks of the tile are computed (the
+// others are padding); their accumulators stay zero.
+template <class T, int NB, class ADma, class BDma, class PDma, int TA = T::TI>
 INTENT_DEVICE void mainloop_pk(const ADma& aop, const BDma& bop, const PDma& pop, int nk, char* const (&bufs)[NB],
                                f32x16 (&acc)[T::TI][T::TJ]) {
   static_assert(NB >= 2 && NB <= 8, "stage ring");
@@ -252,7 +254,7 @@ INTENT_DEVICE void mainloop_pk(const ADma& aop, const BDma& bop, const PDma& pop
   auto prologue = [&](auto J, int kt, StagePk<T>& st) {
     const int g0 = pop.group(kt);
     const int g = pop.gs == 32 ? g0 + h : g0;
-    stage_prologue<T>(bufs[decltype(J)::value], aaddr, baddr, paddr, (g & 1) * 16, (g & 3) * 8, st);
+    stage_prologue<T, TA>(bufs[decltype(J)::value], aaddr, baddr, paddr, (g & 1) * 16, (g & 3) * 8, st);
   };
   static_for<0, NB>([&](auto S) { issue(S, decltype(S)::value); });
   StagePk<T> st;
@@ -261,7 +263,7 @@ INTENT_DEVICE void mainloop_pk(const ADma& aop, const BDma& bop, const PDma& pop
 
   auto step = [&](auto J, int kt) {
     constexpr int j = decltype(J)::value;
-    stage_body<T>(bufs[j], aaddr, st, acc);
+    stage_body<T, TA>(bufs[j], aaddr, st, acc);
     if (kt + 1 < nk) {
       wait_vm_lgkm_barrier<(NB - 2) * NV>();
       issue(J, kt + NB);
