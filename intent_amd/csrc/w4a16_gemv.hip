@@ -120,9 +120,145 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
 }
 
 
-// ---- M <= 3: K-resident dot-product GEMV --------------------------------------
-// (Measured at K = N = 4096: M = 3 takes 6.7 us here against 7.4 us on the MFMA
-// kernel; from M = 4 on the per-row dot work makes it the slower one.)
+// 4 x 4 transpose of 16-byte pieces across the 16-lane rows of a wave: on
+// return, piece t of row g holds what piece g of row t held. v_permlane32_swap
+// exchanges the upper 32 lanes of its first operand with the lower 32 of its
+// second; v_permlane16_swap exchanges the odd 16-lane rows of the first with
+// the even rows of the second.
+INTENT_DEVICE void rows16_transpose4(u32x4 (&v)[4]) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const auto a = __builtin_amdgcn_permlane32_swap(v[0][d], v[2][d], false, false);
+    v[0][d] = a[0];
+    v[2][d] = a[1];
+    const auto b = __builtin_amdgcn_permlane32_swap(v[1][d], v[3][d], false, false);
+    v[1][d] = b[0];
+    v[3][d] = b[1];
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const auto a = __builtin_amdgcn_permlane16_swap(v[0][d], v[1][d], false, false);
+    v[0][d] = a[0];
+    v[1][d] = a[1];
+    const auto b = __builtin_amdgcn_permlane16_swap(v[2][d], v[3][d], false, false);
+    v[2][d] = b[0];
+    v[3][d] = b[1];
+  }
+}
+
+// ---- 4 <= M <= 16: MFMA GEMV with every load issued up front ------------------
+// Same split and MFMA operand roles as w4a16_gemv_kernel: 16 weight rows per
+// workgroup, KW waves taking 128-wide K steps in turn, lane (r, quad) holding
+// k = step*128 + quad*32 + t*8 + [0, 8) of weight row n0 + r (bytes quad*16 ..
+// of the step, one 16-byte load) and of activation row r. A wave owns at most
+// SPW steps and issues all of its loads before the first MFMA.
+//
+// Loads are laid out for the L1, whose request slots bound this kernel:
+//  * scales and zeros of the workgroup's 16 rows are fetched once, first, as
+//    contiguous row segments (wave w: row w), packed into LDS records and read
+//    back after one barrier (per-lane scattered u16/u8 loads cost 1.6 us at
+//    M = 16, K = N = 4096);
+//  * activations are loaded as 64 contiguous bytes per row and instruction
+//    (instruction j, quad q: bytes j*64 + q*16 of the step) and moved into
+//    operand order by a 4 x 4 transpose across the 16-lane rows
+//    (rows16_transpose4), so an instruction touches 16 row segments, not 64.
+// Activation rows r >= M lie past the end of the x buffer resource (its size
+// is exactly the bytes of rows 0..M-1), so their loads return zeros without a
+// memory access. The product of a step is exact in fp32; the KW partial tiles
+// are summed through LDS in wave order and rounded to f16 once.
+constexpr int kFrontMaxGroups = 256;
+
+template <int KW, int SPW>
+__global__ __launch_bounds__(64 * KW) void w4a16_gemv_front_kernel(
+    const f16* __restrict__ x, int ldx, int x_bytes, const uint8_t* __restrict__ wq, int ldw,
+    const f16* __restrict__ sc, const uint8_t* __restrict__ zp, int ldq, int nsteps, int G, float inv_cpg, int N,
+    f16* __restrict__ y, int ldy, int M) {
+  static_assert(KW == 16, "the record fetch gives wave w row w");
+  __shared__ f32x4 red[KW][64];
+  __shared__ uint32_t rec[16][kFrontMaxGroups];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15;
+  const int quad = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int nr = n0 + r < N ? r : N - 1 - n0;  // tail rows compute on a valid row; their outputs are dropped
+
+  // Records of row n0 + wave (clamped): groups lane, lane + 64, ...
+  constexpr int RPL = kFrontMaxGroups / 64;
+  uint32_t sq[RPL], zq[RPL];
+  {
+    const int rn = n0 + wave < N ? wave : N - 1 - n0;
+    const auto srs = make_rsrc(sc + (int64_t)(n0 + rn) * ldq);
+    const auto zrs = make_rsrc(zp + (int64_t)(n0 + rn) * ldq);
+#pragma unroll
+    for (int u = 0; u < RPL; ++u) {
+      if (u * 64 < G) {  // uniform
+        const int g = min(lane + u * 64, G - 1);
+        sq[u] = __builtin_amdgcn_raw_buffer_load_b16(srs, g * 2, 0, 0);
+        zq[u] = __builtin_amdgcn_raw_buffer_load_b8(zrs, g, 0, 0);
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const auto wrs = make_rsrc(wq + (int64_t)n0 * ldw);
+  const auto xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(x), (short)0, x_bytes, 0x00020000);
+  const int wvo = nr * ldw + quad * 16;
+  const int xvo = r * ldx * 2 + quad * 16;
+  u32x4 wv[SPW], xv[SPW][4];
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const int s = min(wave + KW * i, nsteps - 1);
+    wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo, s * 64, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xv[i][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo, s * 256 + j * 64, 0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (int u = 0; u < RPL; ++u)
+    if (u * 64 < G && lane + u * 64 < G) rec[wave][lane + u * 64] = (sq[u] & 0xffffu) | ((zq[u] & 0xffu) << 16);
+  __syncthreads();
+
+  // No branch on a step's validity (a branch lets the compiler sink that
+  // step's loads behind the first wait): a step past K, a repeat of the last
+  // one, gets scale 0, so its weights dequantize to exact zeros.
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+    const int sraw = wave + KW * i;
+    const int s = min(sraw, nsteps - 1);
+    const int g = (int)(((float)(s * 4 + quad) + 0.5f) * inv_cpg);  // chunk -> group (exact for these magnitudes)
+    const uint32_t rq = rec[r][g];
+    rows16_transpose4(xv[i]);
+    const f16x2 zoff = splat2((f16)(float)(1024 + (rq >> 16)));
+    const f16x2 scale = splat2(sraw < nsteps ? bit_cast<f16>((uint16_t)rq) : (f16)0.0f);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(bit_cast<f16x8>(xv[i][t]), dequant8(wv[i][t], zoff, scale), acc, 0,
+                                                   0, 0);
+  }
+  red[wave][lane] = acc;
+  __syncthreads();
+  // 16x16 MFMA result layout: lane l holds column l%16, rows (l/16)*4 + i.
+  if (threadIdx.x < 256) {
+    const int o = threadIdx.x;
+    const int m = o >> 4;
+    const int nc = o & 15;
+    const int src = (m >> 2) * 16 + nc;
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < KW; ++w) sum += red[w][src][m & 3];
+    const int n = n0 + nc;
+    if (m < M && n < N) y[(int64_t)m * ldy + n] = (f16)sum;
+  }
+}
+
+
+// ---- M <= 5: K-resident dot-product GEMV --------------------------------------
+// (Measured at K = N = 4096, launch included: M = 1..5 take 3.53, 3.94, 4.58,
+// 5.14, 6.09 us here against 5.78, 5.89, 5.99, 6.10, 6.13 us on the MFMA
+// front kernel; from M = 6 on the per-row dot work makes it the slower one.)
 //
 // A lane owns CH fixed 32-element K chunks (chunk c = lane + 64*i: bytes
 // [16c, 16c+16) of every weight row, so a wave reads 1 KB contiguous per row
@@ -637,6 +773,14 @@ __global__ __launch_bounds__(64 * KW) void w8a16_gemv_kernel(const f16* __restri
   }
 }
 
+template <int SPW>
+void launch_front(const f16* x, int64_t ldx, int M, int K, const uint8_t* wq, int64_t ldw, const f16* sc,
+                  const uint8_t* zp, int64_t ldq, int gs, f16* y, int64_t ldy, int N, hipStream_t st) {
+  const int x_bytes = (int)(((int64_t)(M - 1) * ldx + K) * 2);
+  hipLaunchKernelGGL((w4a16_gemv_front_kernel<16, SPW>), dim3((N + 15) / 16), dim3(1024), 0, st, x, (int)ldx, x_bytes,
+                     wq, (int)ldw, sc, zp, (int)ldq, K / 128, K / gs, 32.0f / (float)gs, N, y, (int)ldy, M);
+}
+
 template <int NT, int KW>
 void launch_gemv(const f16* x, int64_t ldx, int M, int K, const uint8_t* wq, int64_t ldw, const f16* sc,
                  const uint8_t* zp, int64_t ldq, int gs, f16* y, int64_t ldy, int N, hipStream_t st) {
@@ -683,6 +827,8 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
     case 1: done = dispatch_dot_shared<1>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
     case 2: done = dispatch_dot_shared<2>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
     case 3: done = dispatch_dot_shared<3>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
+    case 4: done = dispatch_dot_shared<4>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
+    case 5: done = dispatch_dot_shared<5>(xx, x_ld, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st); break;
     default: break;
   }
   if (done) {
@@ -704,6 +850,16 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
     return launch_status_fmt("w4a16_gemv_dot_kernel<%d, %d, %d, 4>", (int)M, chv, chv >= 8 ? 1 : 8 / chv);
   }
   const int steps = (int)(K / 128);
+  if (fits_offset(M, x_ld * 2) && fits_offset(N, packed_ld) && fits_offset(N, qparam_ld * 2) && steps <= 64 &&
+      K / gs <= kFrontMaxGroups) {
+    if (steps <= 16)
+      launch_front<1>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
+    else if (steps <= 32)
+      launch_front<2>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
+    else
+      launch_front<4>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
+    return launch_status_fmt("w4a16_gemv_front_kernel<16, %d>", steps <= 16 ? 1 : steps <= 32 ? 2 : 4);
+  }
   if (steps >= 16)
     launch_gemv<1, 16>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
   else if (steps >= 8)

@@ -67,6 +67,22 @@ def test_w4a16_decode_config1(gpu, threads, M):
     assert art(intent.weight_only_int4_asym_matmul).observation.entry == "intent_w4a16_gemv"
 
 
+@pytest.mark.parametrize("M,K,N,group", [(16, 4096, 4100, 128), (6, 2048, 64, 256), (7, 8192, 100, 32),
+                                         (16, 8192, 333, 512), (9, 384, 31, 128), (12, 1152, 50, 64),
+                                         (16, 16384, 40, 128), (4, 4096, 77, 128), (5, 2048, 129, 64)])
+def test_w4a16_gemv_kernel_choices(gpu, threads, M, K, N, group):
+    # M >= 6 with K <= 8192 and at most 256 groups per row: the MFMA GEMV with its loads issued up
+    # front (1, 2 or 4 steps per wave, steps past K zero-scaled); K = 16384 takes the looping MFMA
+    # kernel; M = 4, 5 the dot-product kernel. N not a multiple of 16 exercises the clamped tail rows.
+    x, q, s, z = w4_case(3, M, K, N, group)
+    a = art(intent.weight_only_int4_asym_matmul, KERNEL="gemv")
+    y = a.run(dev(x), dev(q), dev(s), dev(z))
+    want = ("w4a16_gemv_dot_shared_kernel" if M <= 5 else
+            "w4a16_gemv_kernel" if K > 8192 else "w4a16_gemv_front_kernel")
+    assert a.observation.kernel.startswith(want), a.observation.kernel
+    assert_close_rms(host(y), oracle.w4a16(x, q, s, z, threads), what=f"gemv {M}x{K}x{N} g{group}")
+
+
 @pytest.mark.parametrize("M,K,N,group", [(3, 256, 100, 64), (1, 384, 48, 32), (16, 128, 17, 128),
                                          (5, 2048, 1000, 256), (1, 8192, 64, 128),
                                          (2, 8192, 33, 128), (1, 16384, 24, 128), (2, 384, 40, 128),
@@ -81,7 +97,7 @@ def test_w4a16_gemv_shapes(gpu, threads, M, K, N, group):
     assert_close_rms(host(y), oracle.w4a16(x, q, s, z, threads), what="gemv shapes")
 
 
-@pytest.mark.parametrize("M,K,N,group", [(1, 4096, 300, 128), (3, 2048, 70, 64)])
+@pytest.mark.parametrize("M,K,N,group", [(1, 4096, 300, 128), (3, 2048, 70, 64), (8, 2048, 200, 128)])
 def test_w4a16_gemv_strided_operands(gpu, threads, M, K, N, group):
     # x rows and scale/zero rows with leading strides wider than the row
     x, q, s, z = w4_case(2, M, K, N, group)
