@@ -16,37 +16,96 @@ constexpr int kAlignWaves = kAlignThreads / 64;
 constexpr int kMaxAlignExperts = 512;
 
 // ---- router ---------------------------------------------------------------
-// One thread per token. Selection compares raw logits (softmax is monotonic),
-// strictly greater wins, so ties keep the lower expert index.
-__global__ void moe_route_kernel(const float* __restrict__ logits, int T, int E, int top_k, int renorm,
-                                 int32_t* __restrict__ ids, float* __restrict__ weights) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
+// One wave per token; lane L holds the logits of experts 4L .. 4L+3. Every
+// selection reproduces the sequential scan "best = first untaken expert, then
+// any later one strictly greater replaces it": a NaN wins only as the first
+// untaken expert, otherwise the largest non-NaN logit wins and ties keep the
+// lower index (softmax is monotonic, so raw logits are compared). A run of
+// consecutive experts is summarised by its first untaken candidate and its
+// best non-NaN one, and two adjacent runs merge exactly, so a butterfly over
+// the lanes gives the scan's answer. The max for the softmax is the same
+// selection over all experts; the softmax denominator is a lane-tree sum.
+struct RouteSel {
+  float fv;  // first untaken candidate of the run (fi < 0: none)
+  int fi;
+  float mv;  // best non-NaN candidate of the run (mi < 0: none)
+  int mi;
+};
+
+INTENT_DEVICE RouteSel route_merge(const RouteSel& a, const RouteSel& b) {  // run a precedes run b
+  RouteSel r;
+  r.fv = a.fi >= 0 ? a.fv : b.fv;
+  r.fi = a.fi >= 0 ? a.fi : b.fi;
+  const bool take_b = a.mi < 0 || (b.mi >= 0 && b.mv > a.mv);
+  r.mv = take_b ? b.mv : a.mv;
+  r.mi = take_b ? b.mi : a.mi;
+  return r;
+}
+
+// Selection over the untaken experts of the wave (bit i of `taken`: expert 4L + i).
+INTENT_DEVICE int route_select(const float (&v)[4], int e0, int E, uint32_t taken, float& value) {
+  RouteSel s{0.f, -1, 0.f, -1};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int e = e0 + i;
+    if (e < E && !(taken & (1u << i))) {
+      const RouteSel one{v[i], e, v[i], v[i] == v[i] ? e : -1};
+      s = route_merge(s, one);
+    }
+  }
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    RouteSel o;
+    o.fv = __shfl_xor(s.fv, d);
+    o.fi = __shfl_xor(s.fi, d);
+    o.mv = __shfl_xor(s.mv, d);
+    o.mi = __shfl_xor(s.mi, d);
+    s = (lane & d) ? route_merge(o, s) : route_merge(s, o);
+  }
+  const bool first_nan = s.fi >= 0 && !(s.fv == s.fv);
+  value = first_nan ? s.fv : s.mv;
+  return first_nan ? s.fi : s.mi;
+}
+
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int T, int E, int top_k,
+                                                        int renorm, int32_t* __restrict__ ids,
+                                                        float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // whole waves
   const float* l = logits + (int64_t)t * E;
-  float mx = l[0];
-  for (int e = 1; e < E; ++e) mx = l[e] > mx ? l[e] : mx;
-  float sum = 0.f;
-  for (int e = 0; e < E; ++e) sum += expf(l[e] - mx);
-  uint32_t taken[kMaxRouteExperts / 32];
-  for (int i = 0; i < kMaxRouteExperts / 32; ++i) taken[i] = 0;
+  const int e0 = 4 * lane;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = e0 + i < E ? l[e0 + i] : 0.f;
+  float mx;
+  route_select(v, e0, E, 0u, mx);
+  float part = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (e0 + i < E) part += expf(v[i] - mx);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) part += __shfl_xor(part, d);
+  const float sum = part;
+  uint32_t taken = 0;
   float p[kMaxTopK];
   float psum = 0.f;
-  for (int j = 0; j < top_k; ++j) {
-    int best = -1;
-    float bv = 0.f;
-    for (int e = 0; e < E; ++e) {
-      if (taken[e >> 5] & (1u << (e & 31))) continue;
-      if (best < 0 || l[e] > bv) {
-        best = e;
-        bv = l[e];
-      }
-    }
-    taken[best >> 5] |= 1u << (best & 31);
-    ids[(int64_t)t * top_k + j] = best;
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) {  // unrolled: p stays in registers
+    if (j >= top_k) break;
+    float bv;
+    const int best = route_select(v, e0, E, taken, bv);
+    if ((best >> 2) == lane) taken |= 1u << (best & 3);
     p[j] = expf(bv - mx) / sum;
     psum += p[j];
+    if (lane == 0) ids[(int64_t)t * top_k + j] = best;
   }
-  for (int j = 0; j < top_k; ++j) weights[(int64_t)t * top_k + j] = renorm ? p[j] / psum : p[j];
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j)
+      if (j < top_k) weights[(int64_t)t * top_k + j] = renorm ? p[j] / psum : p[j];
+  }
 }
 
 // ---- alignment --------------------------------------------------------------
@@ -474,6 +533,46 @@ __global__ void moe_combine_kernel(const float* __restrict__ route_out, int64_t 
   y[(int64_t)t * ldy + d] = acc;
 }
 
+// The same sums four columns per thread with 16-byte loads (H, the strides
+// and the part stride multiples of 4, 16-byte aligned bases).
+__global__ void moe_combine4_kernel(const float* __restrict__ route_out, int64_t ldo,
+                                    const float* __restrict__ weights, int T, int top_k, float* __restrict__ y, int H,
+                                    int64_t ldy, int splits, int64_t part_stride) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int H4 = H >> 2;
+  if (i >= (int64_t)T * H4) return;
+  const int t = (int)(i / H4);
+  const int d = (int)(i % H4) * 4;
+  f32x4 acc = *reinterpret_cast<const f32x4*>(y + (int64_t)t * ldy + d);
+  for (int s = 0; s < top_k; ++s) {
+    const float* o = route_out + ((int64_t)t * top_k + s) * ldo + d;
+    f32x4 v = *reinterpret_cast<const f32x4*>(o);
+    for (int p = 1; p < splits; ++p) {
+      const f32x4 q = *reinterpret_cast<const f32x4*>(o + p * part_stride);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[c] = __fadd_rn(v[c], q[c]);
+    }
+    const float w = weights[(int64_t)t * top_k + s];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = __fadd_rn(acc[c], __fmul_rn(w, v[c]));
+  }
+  *reinterpret_cast<f32x4*>(y + (int64_t)t * ldy + d) = acc;
+}
+
+void launch_combine(const float* route_out, int64_t ldo, const float* weights, int64_t T, int64_t top_k, float* y,
+                    int64_t H, int64_t ldy, int splits, int64_t part_stride, hipStream_t st) {
+  const int threads = 256;
+  if (H % 4 == 0 && ldo % 4 == 0 && ldy % 4 == 0 && part_stride % 4 == 0 && intent::aligned16(route_out) &&
+      intent::aligned16(y)) {
+    const int64_t n = T * (H / 4);
+    hipLaunchKernelGGL(moe_combine4_kernel, dim3((unsigned)((n + threads - 1) / threads)), dim3(threads), 0, st,
+                       route_out, ldo, weights, (int)T, (int)top_k, y, (int)H, ldy, splits, part_stride);
+  } else {
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((T * H + threads - 1) / threads)), dim3(threads), 0, st,
+                       route_out, ldo, weights, (int)T, (int)top_k, y, (int)H, ldy, splits, part_stride);
+  }
+}
+
 int64_t align_capacity(int64_t R, int64_t E, int64_t B) { return R + E * (B - 1); }
 
 }  // namespace
@@ -488,8 +587,7 @@ extern "C" int intent_moe_route(const float* logits, int64_t T, int64_t E, int64
                  "top_k must be in [1, min(E, %d)], got %lld", kMaxTopK, (long long)top_k);
   if (T == 0) return INTENT_OK;
   INTENT_REQUIRE(logits && topk_ids && topk_weights, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
-  const int threads = 256;
-  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + threads - 1) / threads)), dim3(threads), 0,
+  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0,
                      (hipStream_t)stream, logits, (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights);
   return intent::launch_status("moe_route");
 }
@@ -562,11 +660,8 @@ int down_launch(const void* act, int64_t act_ld, const int32_t* sorted, const in
 
 int combine_launch(const float* route_out, int64_t out_ld, const float* topk_weights, int64_t T, int64_t top_k,
                    float* y, int64_t H, int64_t y_ld, void* stream) {
-  const int threads = 256;
-  const int64_t blocks = (T * H + threads - 1) / threads;
-  INTENT_REQUIRE(blocks < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(threads), 0, (hipStream_t)stream, route_out,
-                     out_ld, topk_weights, (int)T, (int)top_k, y, (int)H, y_ld);
+  INTENT_REQUIRE((T * H + 255) / 256 < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+  launch_combine(route_out, out_ld, topk_weights, T, top_k, y, H, y_ld, 1, 0, (hipStream_t)stream);
   return intent::launch_status("moe_combine");
 }
 
@@ -663,7 +758,16 @@ extern "C" int intent_moe_combine(const float* route_out, int64_t out_ld, const 
 namespace {
 
 // K parts of the composite's down projection (moe_down_pk_kernel).
-constexpr int kDownSplits = 2;
+// At most this many; the composite takes the largest of 4, 2, 1 that splits F
+// into whole dwords of groups (measured on config 4: 2 parts 653 us, 4 parts
+// 603 us, 7 parts 631 us for the whole layer).
+constexpr int kDownSplits = 4;
+
+int down_splits(int64_t F, int64_t gs) {
+  for (int s = kDownSplits; s > 1; s /= 2)
+    if (F % (s * 4 * gs) == 0 && (F / s) % 64 == 0) return s;
+  return 1;
+}
 
 struct MoEWorkspace {
   size_t ids, weights, sorted, blocks, offsets, total, act, out, bytes;
@@ -737,14 +841,15 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
   if (st != INTENT_OK) return st;
   const int64_t R = T * top_k;
   const int64_t ldp = F / group_size;
-  const bool pk = ldp % 4 == 0 && F % (kDownSplits * 4 * group_size) == 0 && (F / kDownSplits) % 64 == 0 &&
+  const int want = down_splits(F, group_size);
+  const bool pk = ldp % 4 == 0 && F % (want * 4 * group_size) == 0 && (F / want) % 64 == 0 &&
                   intent::aligned4(wd_scales) && intent::aligned4(wd_zeros);
   int splits = 1;
   if (pk) {
     st = down_check(act, F, sorted, blocks, L.nblocks, B, R, wd_packed, wd_scales, wd_zeros, E, H, F, group_size, out,
                     H);
     if (st != INTENT_OK) return st;
-    splits = kDownSplits;
+    splits = want;
     const int64_t ntiles = (H + GateUpPk::BN - 1) / GateUpPk::BN;
     const int64_t grid = splits * L.nblocks * ntiles;
     INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
@@ -757,8 +862,6 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
                             group_size, out, H, stream);
   }
   if (st != INTENT_OK) return st;
-  const int threads = 256;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((T * H + threads - 1) / threads)), dim3(threads), 0,
-                     (hipStream_t)stream, out, H, wts, (int)T, (int)top_k, y, (int)H, H, splits, R * H);
+  launch_combine(out, H, wts, T, top_k, y, H, H, splits, R * H, (hipStream_t)stream);
   return intent::launch_status("moe_combine");
 }
