@@ -62,7 +62,8 @@ int intent_amd_device_arch(int device, char* buf, int64_t buf_len);
  * I.matmul(acc_dtype=f32) -> scale (doc/dsl/core.en.md:246,
  * lib/Conversion/KIRToCPU/Contractions.cpp:12-41).
  * x f16 [M,K] (stride x_ld); w int8 [N,K] (w_ld); scales f16 [N]; y f16 [M,N].
- * Requires K % 64 == 0.
+ * Any K and strides: K % 64 == 0 with 16-byte aligned rows runs the tiled
+ * kernels, other shapes a generic kernel (same arithmetic, lower throughput).
  */
 int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld,
                         const int8_t* w, int64_t N, int64_t w_ld,
@@ -75,9 +76,13 @@ int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld,
  * Replaces weight_only_int4_matmul (examples/kernels/contraction/
  * weight_only_int4.py:18-51; CPU oracle experiments/cpu/baselines/pytorch/
  * cpu_runtime.py:97-102) for the asymmetric uint4, [N, K/2]-packed format.
- * Requires K % 128 == 0 and group % 32 == 0, K % group == 0.
+ * Requires K even and K % group == 0 (else INTENT_ERR_INVALID_ARGUMENT).
+ * K % 128 == 0, group % 32 == 0 and 16-byte aligned rows (x_ld % 8 == 0,
+ * packed_ld % 16 == 0) take the fast kernels, other shapes a generic kernel
+ * (same per-element dequantisation, f32 sums).
  * `intent_w4a16_matmul` picks the decode GEMV kernel for M <= 16 and the
- * MFMA tile kernel otherwise; the _gemv / _gemm entries force one kernel.
+ * MFMA tile kernel otherwise; the _gemv / _gemm entries force one kernel
+ * (the _gemv entry covers M <= 16).
  */
 int intent_w4a16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld,
                         const uint8_t* packed, int64_t N, int64_t packed_ld,
@@ -103,7 +108,8 @@ int intent_w4a16_gemm(const void* x, int64_t M, int64_t K, int64_t x_ld,
  * Replaces the integer contraction branch (lib/Conversion/KIRToCPU/
  * Contractions.cpp:30-35,79-80) plus per-token/per-channel scale epilogue
  * (examples/kernels/contraction/gemm.py:83-106 pattern).
- * Requires K % 64 == 0.
+ * Any K and strides (K % 64 == 0 with 16-byte aligned rows: the tiled
+ * kernels; else a generic kernel with the same exact sums and epilogue).
  */
 int intent_w8a8_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
                      const float* a_scales,
@@ -115,7 +121,7 @@ int intent_w8a8_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
  * int8 x int8 -> int32 contraction with optional int32 bias (nullable):
  * c[m,n] = sum_k i32(a[m,k]) * i32(w[n,k]) + bias[n], modulo 2^32.
  * Replaces gemm_i8 (examples/kernels/contraction/gemm.py:29-39), with the
- * weight given K-contiguous as [N, K]. Requires K % 64 == 0.
+ * weight given K-contiguous as [N, K]. Any K and strides, as intent_w8a8_gemm.
  */
 int intent_i8_gemm_i32(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
                        const int8_t* w, int64_t N, int64_t w_ld,
@@ -129,7 +135,8 @@ int intent_i8_gemm_i32(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
  * No reference counterpart exists (the reference takes topk_ids as an input,
  * experiments/_common/support.py:113-130); this is the producer of that input.
  * logits f32 [T,E]; topk_ids i32 [T,top_k]; topk_weights f32 [T,top_k].
- * Requires 1 <= top_k <= min(E, 8), E <= 256.
+ * Requires 1 <= top_k <= min(E, 8). E <= 256 runs one wave per token, larger E
+ * one thread per token (same selections and ties).
  */
 int intent_moe_route(const float* logits, int64_t T, int64_t E, int64_t top_k,
                      int renormalize, int32_t* topk_ids, float* topk_weights,

@@ -592,6 +592,12 @@ namespace intent {
 int w4a16_check(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t N,
                 int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld, int64_t gs,
                 const void* y, int64_t y_ld);
+bool w4a16_fast(const void* x, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t packed_ld, int64_t gs);
+int w4a16_generic_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t N,
+                         int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld, int64_t gs,
+                         void* y, int64_t y_ld, void* stream);
+int w8a16_generic_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const int8_t* w, int64_t N, int64_t w_ld,
+                         const void* scales, void* y, int64_t y_ld, void* stream);
 int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t N,
                       int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld, int64_t gs,
                       void* y, int64_t y_ld, void* stream);
@@ -603,8 +609,8 @@ int w4a16_gemm_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
                       int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld, int64_t gs,
                       void* y, int64_t y_ld, void* stream) {
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(gs == 32 || gs % 64 == 0, INTENT_ERR_UNSUPPORTED,
-                 "the tiled GEMM needs group_size 32 or a multiple of 64, got %lld", (long long)gs);
+  if (!w4a16_fast(x, K, x_ld, packed, packed_ld, gs) || !(gs == 32 || gs % 64 == 0))
+    return w4a16_generic_launch(x, M, K, x_ld, packed, N, packed_ld, scales, zeros, qparam_ld, gs, y, y_ld, stream);
   INTENT_REQUIRE(intent::fits_offset(N, packed_ld) && intent::fits_offset(N, qparam_ld * 2) &&
                      intent::fits_offset(256 + 1, x_ld * 2),
                  INTENT_ERR_UNSUPPORTED, "w4a16_gemm: operand too large for 31-bit buffer offsets");
@@ -621,7 +627,7 @@ extern "C" int intent_w4a16_matmul(const void* x, int64_t M, int64_t K, int64_t 
   intent::clear_error();
   int st = intent::w4a16_check(x, M, K, x_ld, packed, N, packed_ld, scales, zeros, qparam_ld, group_size, y, y_ld);
   if (st != INTENT_OK) return st;
-  if (M <= 16)
+  if (M <= 16 && intent::w4a16_fast(x, K, x_ld, packed, packed_ld, group_size))
     return intent::w4a16_gemv_launch(x, M, K, x_ld, packed, N, packed_ld, scales, zeros, qparam_ld, group_size, y,
                                      y_ld, stream);
   return intent::w4a16_gemm_launch(x, M, K, x_ld, packed, N, packed_ld, scales, zeros, qparam_ld, group_size, y, y_ld,
@@ -634,6 +640,11 @@ extern "C" int intent_w4a16_gemv(const void* x, int64_t M, int64_t K, int64_t x_
   intent::clear_error();
   int st = intent::w4a16_check(x, M, K, x_ld, packed, N, packed_ld, scales, zeros, qparam_ld, group_size, y, y_ld);
   if (st != INTENT_OK) return st;
+  INTENT_REQUIRE(M <= 16, INTENT_ERR_UNSUPPORTED, "the GEMV covers M <= 16, got M=%lld", (long long)M);
+  if (M == 0 || N == 0) return INTENT_OK;
+  if (!intent::w4a16_fast(x, K, x_ld, packed, packed_ld, group_size))
+    return intent::w4a16_generic_launch(x, M, K, x_ld, packed, N, packed_ld, scales, zeros, qparam_ld, group_size, y,
+                                        y_ld, stream);
   return intent::w4a16_gemv_launch(x, M, K, x_ld, packed, N, packed_ld, scales, zeros, qparam_ld, group_size, y, y_ld,
                                    stream);
 }
@@ -653,12 +664,12 @@ extern "C" int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t 
   intent::clear_error();
   INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0, INTENT_ERR_INVALID_ARGUMENT, "negative extent");
   INTENT_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "extent exceeds int32");
-  INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
   INTENT_REQUIRE(x && w && scales && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(x_ld >= K && w_ld >= K && y_ld >= N, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
-  INTENT_REQUIRE(intent::aligned16(x) && intent::aligned16(w) && x_ld % 8 == 0 && w_ld % 16 == 0, INTENT_ERR_ALIGNMENT,
-                 "x and w must be 16-byte aligned with 16-byte row strides");
+  // the tiled kernels take whole 64-k stages of 16-byte aligned rows; other shapes run the generic kernel
+  if (K == 0 || K % 64 != 0 || !intent::aligned16(x) || !intent::aligned16(w) || x_ld % 8 != 0 || w_ld % 16 != 0)
+    return intent::w8a16_generic_launch(x, M, K, x_ld, w, N, w_ld, scales, y, y_ld, stream);
   if (M <= 16) return intent::w8a16_gemv_launch(x, M, K, x_ld, w, N, w_ld, scales, y, y_ld, stream);
   INTENT_REQUIRE(intent::fits_offset(N, w_ld) && intent::fits_offset(256 + 1, x_ld * 2), INTENT_ERR_UNSUPPORTED,
                  "w8a16_matmul: operand too large for 31-bit buffer offsets");

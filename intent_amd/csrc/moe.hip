@@ -108,6 +108,51 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
   }
 }
 
+// Any E above the wave kernel's 256: one thread per token runs the scan itself
+// (the chosen experts, at most kMaxTopK, kept in registers).
+__global__ __launch_bounds__(256) void moe_route_seq_kernel(const float* __restrict__ logits, int T, int E, int top_k,
+                                                            int renorm, int32_t* __restrict__ ids,
+                                                            float* __restrict__ weights) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  const float* l = logits + (int64_t)t * E;
+  float mx = l[0];
+  for (int e = 1; e < E; ++e) mx = l[e] > mx ? l[e] : mx;
+  float sum = 0.f;
+  for (int e = 0; e < E; ++e) sum += expf(l[e] - mx);
+  int chosen[kMaxTopK];
+  float p[kMaxTopK];
+  float psum = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) {
+    chosen[j] = -1;
+    p[j] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j) {
+    if (j >= top_k) break;
+    int best = -1;
+    float bv = 0.f;
+    for (int e = 0; e < E; ++e) {
+      bool taken = false;
+#pragma unroll
+      for (int i = 0; i < kMaxTopK; ++i) taken |= chosen[i] == e;
+      if (taken) continue;
+      if (best < 0 || l[e] > bv) {
+        best = e;
+        bv = l[e];
+      }
+    }
+    chosen[j] = best;
+    ids[(int64_t)t * top_k + j] = best;
+    p[j] = expf(bv - mx) / sum;
+    psum += p[j];
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxTopK; ++j)
+    if (j < top_k) weights[(int64_t)t * top_k + j] = renorm ? p[j] / psum : p[j];
+}
+
 // ---- alignment --------------------------------------------------------------
 // One workgroup. Counts use LDS atomics (order-free). The scatter is stable:
 // routes are processed in chunks of 1024 in route order; inside a wave the rank
@@ -581,12 +626,17 @@ extern "C" int intent_moe_route(const float* logits, int64_t T, int64_t E, int64
                                 int32_t* topk_ids, float* topk_weights, void* stream) {
   intent::clear_error();
   INTENT_REQUIRE(T >= 0 && T <= INT32_MAX, INTENT_ERR_INVALID_ARGUMENT, "bad token count %lld", (long long)T);
-  INTENT_REQUIRE(E >= 1 && E <= kMaxRouteExperts, INTENT_ERR_UNSUPPORTED, "experts must be in [1, %d], got %lld",
-                 kMaxRouteExperts, (long long)E);
+  INTENT_REQUIRE(E >= 1 && E <= INT32_MAX, INTENT_ERR_INVALID_ARGUMENT, "experts must be at least 1, got %lld",
+                 (long long)E);
   INTENT_REQUIRE(top_k >= 1 && top_k <= E && top_k <= kMaxTopK, INTENT_ERR_UNSUPPORTED,
                  "top_k must be in [1, min(E, %d)], got %lld", kMaxTopK, (long long)top_k);
   if (T == 0) return INTENT_OK;
   INTENT_REQUIRE(logits && topk_ids && topk_weights, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  if (E > kMaxRouteExperts) {
+    hipLaunchKernelGGL(moe_route_seq_kernel, dim3((unsigned)((T + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       logits, (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights);
+    return intent::launch_status("moe_route_seq_kernel");
+  }
   hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0,
                      (hipStream_t)stream, logits, (int)T, (int)E, (int)top_k, renormalize, topk_ids, topk_weights);
   return intent::launch_status("moe_route");

@@ -793,24 +793,30 @@ void launch_gemv(const f16* x, int64_t ldx, int M, int K, const uint8_t* wq, int
 
 namespace intent {
 
+// Validity of a W4A16 call (any shape the operator defines: K even and a
+// multiple of the group size). The tiled kernels also need w4a16_fast.
 int w4a16_check(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t N,
                 int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld, int64_t gs,
                 const void* y, int64_t y_ld) {
   INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0, INTENT_ERR_INVALID_ARGUMENT, "negative extent (M=%lld N=%lld K=%lld)",
                  (long long)M, (long long)N, (long long)K);
   INTENT_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "extent exceeds int32");
-  INTENT_REQUIRE(gs > 0 && gs % 32 == 0, INTENT_ERR_UNSUPPORTED, "group_size must be a positive multiple of 32, got %lld",
-                 (long long)gs);
-  INTENT_REQUIRE(K % 128 == 0 && K % gs == 0, INTENT_ERR_UNSUPPORTED,
-                 "K must be a multiple of 128 and of group_size (K=%lld group=%lld)", (long long)K, (long long)gs);
+  INTENT_REQUIRE(gs > 0, INTENT_ERR_INVALID_ARGUMENT, "group_size must be positive, got %lld", (long long)gs);
+  INTENT_REQUIRE(K % 2 == 0 && K % gs == 0, INTENT_ERR_INVALID_ARGUMENT,
+                 "K must be even and a multiple of group_size (K=%lld group=%lld)", (long long)K, (long long)gs);
   if (M == 0 || N == 0) return INTENT_OK;
   INTENT_REQUIRE(x && packed && scales && zeros && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(x_ld >= K && packed_ld >= K / 2 && qparam_ld >= K / gs && y_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row (x_ld=%lld packed_ld=%lld qparam_ld=%lld y_ld=%lld)",
                  (long long)x_ld, (long long)packed_ld, (long long)qparam_ld, (long long)y_ld);
-  INTENT_REQUIRE(aligned16(x) && aligned16(packed) && x_ld % 8 == 0 && packed_ld % 16 == 0, INTENT_ERR_ALIGNMENT,
-                 "x and packed must be 16-byte aligned with 16-byte row strides");
   return INTENT_OK;
+}
+
+// Shapes the GEMV and tiled GEMM kernels take: whole 128-k steps, groups of
+// 32 k or more, 16-byte aligned activation and weight rows.
+bool w4a16_fast(const void* x, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t packed_ld, int64_t gs) {
+  return gs % 32 == 0 && K % 128 == 0 && K > 0 && aligned16(x) && aligned16(packed) && x_ld % 8 == 0 &&
+         packed_ld % 16 == 0;
 }
 
 int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t N,

@@ -8,6 +8,12 @@
 #include "internal.h"
 #include "mfma_pipe.h"
 
+namespace intent {
+int i8_generic_launch(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const int8_t* w, int64_t N, int64_t w_ld,
+                      const float* sa, const float* sw, const int32_t* bias, void* out, int64_t out_ld, bool scaled,
+                      void* stream);
+}  // namespace intent
+
 namespace {
 
 using T256 = mp::Tile<256, 256, 4, 2>;  // 8 waves of 64 x 128 (two per SIMD)
@@ -183,14 +189,16 @@ int check_i8(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const int8_t* 
              const void* out, int64_t out_ld) {
   INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0, INTENT_ERR_INVALID_ARGUMENT, "negative extent");
   INTENT_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "extent exceeds int32");
-  INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
   INTENT_REQUIRE(a && w && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(a_ld >= K && w_ld >= K && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row");
-  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(w) && a_ld % 16 == 0 && w_ld % 16 == 0,
-                 INTENT_ERR_ALIGNMENT, "a and w must be 16-byte aligned with 16-byte row strides");
   return INTENT_OK;
+}
+
+// The tiled kernels take whole 64-k stages of 16-byte aligned rows.
+bool i8_fast(const int8_t* a, int64_t K, int64_t a_ld, const int8_t* w, int64_t w_ld) {
+  return K > 0 && K % 64 == 0 && intent::aligned16(a) && intent::aligned16(w) && a_ld % 16 == 0 && w_ld % 16 == 0;
 }
 
 template <class T, Epi E>
@@ -232,6 +240,9 @@ extern "C" int intent_w8a8_gemm(const int8_t* a, int64_t M, int64_t K, int64_t a
   int st = check_i8(a, M, K, a_ld, w, N, w_ld, out, out_ld);
   if (st != INTENT_OK || M == 0 || N == 0) return st;
   INTENT_REQUIRE(a_scales && w_scales, INTENT_ERR_INVALID_ARGUMENT, "null scale pointer");
+  if (!i8_fast(a, K, a_ld, w, w_ld))
+    return intent::i8_generic_launch(a, M, K, a_ld, w, N, w_ld, a_scales, w_scales, nullptr, out, out_ld, true,
+                                     stream);
   return launch_i8<Epi::kBf16Scaled>(a, M, K, a_ld, a_scales, w, N, w_ld, w_scales, nullptr, out, out_ld, stream,
                                      "w8a8_gemm");
 }
@@ -241,6 +252,8 @@ extern "C" int intent_i8_gemm_i32(const int8_t* a, int64_t M, int64_t K, int64_t
   intent::clear_error();
   int st = check_i8(a, M, K, a_ld, w, N, w_ld, c, c_ld);
   if (st != INTENT_OK || M == 0 || N == 0) return st;
+  if (!i8_fast(a, K, a_ld, w, w_ld))
+    return intent::i8_generic_launch(a, M, K, a_ld, w, N, w_ld, nullptr, nullptr, bias, c, c_ld, false, stream);
   return launch_i8<Epi::kI32Bias>(a, M, K, a_ld, nullptr, w, N, w_ld, nullptr, bias, c, c_ld, stream, "i8_gemm_i32");
 }
 

@@ -40,19 +40,21 @@ FAKE = 0x1000  # a 16-byte aligned non-null address; never dereferenced by the c
 
 
 def test_w4a16_argument_checks():
-    # K not a multiple of 128
-    assert status("intent_w4a16_matmul", FAKE, 1, 100, 100, FAKE, 8, 50, FAKE, FAKE, 4, 32, FAKE, 8, None) == \
-        errors.INTENT_ERR_UNSUPPORTED
-    assert "multiple of 128" in _native.last_error()
-    # group not a multiple of 32
-    assert status("intent_w4a16_gemv", FAKE, 1, 256, 256, FAKE, 8, 128, FAKE, FAKE, 16, 16, FAKE, 8, None) == \
-        errors.INTENT_ERR_UNSUPPORTED
+    # Shapes outside the tiled kernels (K not a multiple of 128, groups of other sizes, unaligned
+    # rows) run the generic kernel (GPU tests); here only calls that are invalid, which fail before
+    # any launch. K odd:
+    assert status("intent_w4a16_matmul", FAKE, 1, 101, 101, FAKE, 8, 51, FAKE, FAKE, 1, 101, FAKE, 8, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT
+    assert "even" in _native.last_error()
+    # K not a multiple of the group size
+    assert status("intent_w4a16_gemv", FAKE, 1, 96, 96, FAKE, 8, 48, FAKE, FAKE, 2, 64, FAKE, 8, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT
+    # group size 0
+    assert status("intent_w4a16_gemm", FAKE, 4, 256, 256, FAKE, 8, 128, FAKE, FAKE, 2, 0, FAKE, 8, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT
     # null pointer
     assert status("intent_w4a16_gemm", None, 4, 256, 256, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None) == \
         errors.INTENT_ERR_INVALID_ARGUMENT
-    # misaligned activation
-    assert status("intent_w4a16_gemm", FAKE + 2, 4, 256, 256, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None) == \
-        errors.INTENT_ERR_ALIGNMENT
     # row stride smaller than the row
     assert status("intent_w4a16_gemm", FAKE, 4, 256, 128, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None) == \
         errors.INTENT_ERR_INVALID_ARGUMENT
@@ -64,20 +66,23 @@ def test_w4a16_argument_checks():
 
 
 def test_int8_and_w8a16_checks():
-    assert status("intent_w8a8_gemm", FAKE, 4, 100, 100, FAKE, FAKE, 4, 100, FAKE, FAKE, 4, None) == \
-        errors.INTENT_ERR_UNSUPPORTED
+    # any K and any alignment run (the generic kernel off the tiled shapes); invalid calls fail first
     assert status("intent_w8a8_gemm", FAKE, 4, 128, 128, None, FAKE, 4, 128, FAKE, FAKE, 4, None) == \
         errors.INTENT_ERR_INVALID_ARGUMENT
-    assert status("intent_i8_gemm_i32", FAKE, 4, 128, 136, FAKE, 4, 128, None, FAKE, 4, None) == \
-        errors.INTENT_ERR_ALIGNMENT
-    assert status("intent_w8a16_matmul", FAKE, 4, 96, 96, FAKE, 4, 96, FAKE, FAKE, 4, None) == \
-        errors.INTENT_ERR_UNSUPPORTED
+    assert status("intent_w8a8_gemm", FAKE, 4, 100, 90, FAKE, FAKE, 4, 100, FAKE, FAKE, 4, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT  # a_ld < K
+    assert status("intent_i8_gemm_i32", FAKE, 4, 128, 136, FAKE, 4, 100, None, FAKE, 4, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT  # w_ld < K
+    assert status("intent_w8a16_matmul", FAKE, 4, 96, 96, None, 4, 96, FAKE, FAKE, 4, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT
+    assert status("intent_w8a16_matmul", FAKE, 4, 96, 96, FAKE, 4, 96, FAKE, FAKE, 3, None) == \
+        errors.INTENT_ERR_INVALID_ARGUMENT  # y_ld < N
     assert status("intent_i8_gemm_i32", FAKE, 0, 128, 128, FAKE, 4, 128, None, FAKE, 4, None) == 0
 
 
 def test_moe_checks():
     assert status("intent_moe_route", FAKE, 8, 8, 9, 1, FAKE, FAKE, None) == errors.INTENT_ERR_UNSUPPORTED
-    assert status("intent_moe_route", FAKE, 8, 300, 2, 1, FAKE, FAKE, None) == errors.INTENT_ERR_UNSUPPORTED
+    assert status("intent_moe_route", FAKE, 8, 0, 1, 1, FAKE, FAKE, None) == errors.INTENT_ERR_INVALID_ARGUMENT
     assert status("intent_moe_route", FAKE, 0, 8, 2, 1, FAKE, FAKE, None) == 0
     # capacity below R + E*(B-1)
     assert status("intent_moe_align", FAKE, 16, 2, 4, 128, FAKE, 100, FAKE, 10, FAKE, FAKE, None) == \
@@ -120,5 +125,7 @@ def test_status_mapping():
     assert isinstance(errors.status_error(-3, "e", "m"), NotImplementedError)
     assert isinstance(errors.status_error(-4, "e", "m"), RuntimeError)
     assert isinstance(errors.status_error(-5, "e", "m"), ValueError)
-    with pytest.raises(NotImplementedError, match="multiple of 128"):
+    with pytest.raises(NotImplementedError, match="M <= 16"):
+        _native.call("intent_w4a16_gemv", FAKE, 17, 256, 256, FAKE, 8, 128, FAKE, FAKE, 2, 128, FAKE, 8, None)
+    with pytest.raises(ValueError, match="multiple of group_size"):
         _native.call("intent_w4a16_matmul", FAKE, 1, 100, 100, FAKE, 8, 50, FAKE, FAKE, 4, 32, FAKE, 8, None)

@@ -178,9 +178,63 @@ def test_i8_gemm_bias(gpu, threads, M, K, N):
     assert np.array_equal(host(c), oracle.i8_gemm_i32(a, w, bias, threads))
 
 
+# ---- shapes off the tiled kernels: the generic kernels ---------------------------------
+
+def _padded(arr, extra):
+    """A device copy of arr whose rows are `extra` elements longer (a leading stride that is
+    not a multiple of 16 bytes), sliced back to arr's shape."""
+    t = dev(np.ascontiguousarray(np.pad(arr, ((0, 0), (0, extra)))))
+    return t[:, :arr.shape[1]]
+
+
+@pytest.mark.parametrize("M,K,N,group,kernel", [(1, 96, 70, 32, "auto"), (3, 160, 33, 16, "gemv"),
+                                                (20, 96, 50, 48, "auto"), (40, 256, 64, 8, "gemm"),
+                                                (2, 4096, 300, 128, "strided")])
+def test_w4a16_generic_shapes(gpu, threads, M, K, N, group, kernel):
+    # K not a multiple of 128, groups not multiples of 32, rows not 16-byte aligned: the generic
+    # kernel, against the oracle and a float64 brute force
+    x, q, s, z = w4_case(6, M, K, N, group)
+    if kernel == "strided":
+        X, kern = _padded(x, 3), "auto"
+    else:
+        X, kern = dev(x), kernel
+    a = art(intent.weight_only_int4_asym_matmul, KERNEL=kern)
+    y = host(a.run(X, dev(q), dev(s), dev(z)))
+    assert a.observation.kernel == "w4a16_generic_kernel", a.observation.kernel
+    assert_close_rms(y, oracle.w4a16(x, q, s, z, threads), what=f"generic w4 {M}x{K}x{N} g{group}")
+    assert_close_rms(y, oracle.w4a16_f64(x, q, s, z), what="generic w4 vs f64")
+
+
+@pytest.mark.parametrize("M,K,N", [(3, 100, 50), (40, 200, 130), (17, 72, 9)])
+def test_w8a16_generic_shapes(gpu, threads, M, K, N):
+    d = inputs.config0_w8a16(1, M=M, K=K, N=N)
+    a = art(intent.weight_only_int8_matmul)
+    y = host(a.run(dev(d["x"]), dev(d["w"]), dev(d["scales"])))
+    assert a.observation.kernel == "w8a16_generic_kernel", a.observation.kernel
+    assert_close_rms(y, oracle.w8a16(d["x"], d["w"], d["scales"], threads), what="generic w8a16")
+
+
+@pytest.mark.parametrize("M,K,N", [(5, 200, 70), (64, 96, 33), (3, 1000, 8)])
+def test_int8_generic_shapes_exact(gpu, threads, M, K, N):
+    d = inputs.config3_w8a8(2, M=M, K=K, N=N)
+    o = art(intent.w8a8_scaled_matmul)
+    out = o.run(dev(d["a"]), dev(d["a_scales"]), dev(d["w"]), dev(d["w_scales"]))
+    assert o.observation.kernel == "i8_generic_kernel<scaled>", o.observation.kernel
+    bits = host(out.view(torch.int16)).view(np.uint16)
+    assert np.array_equal(bits, oracle.w8a8(d["a"], d["a_scales"], d["w"], d["w_scales"], threads))
+    rng = np.random.default_rng(M)
+    a, w = rng.integers(-128, 128, (M, K), dtype=np.int8), rng.integers(-128, 128, (N, K), dtype=np.int8)
+    bias = rng.integers(-2**31, 2**31 - 1, N, dtype=np.int64).astype(np.int32)
+    g = art(intent.gemm_i8_nt)
+    c = g.run(_padded(a, 5), _padded(w, 7), dev(bias))  # unaligned rows
+    assert g.observation.kernel == "i8_generic_kernel<i32>", g.observation.kernel
+    assert np.array_equal(host(c), oracle.i8_gemm_i32(a, w, bias, threads))
+
+
 # ---- MoE routing ------------------------------------------------------------------
 
-@pytest.mark.parametrize("T,E,k,renorm", [(512, 8, 2, True), (333, 64, 4, False), (7, 3, 3, True), (1, 256, 8, True)])
+@pytest.mark.parametrize("T,E,k,renorm", [(512, 8, 2, True), (333, 64, 4, False), (7, 3, 3, True), (1, 256, 8, True),
+                                         (100, 300, 4, True), (37, 1000, 8, False)])
 def test_moe_route(gpu, T, E, k, renorm):
     rng = np.random.default_rng(T + E)
     logits = rng.standard_normal((T, E), dtype=np.float32)
