@@ -176,7 +176,9 @@ int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_k, int64_t 
  * act f16 [num_blocks*block_size, F].
  * Replaces the first contraction + activation of moe_expert_ffn
  * (examples/kernels/ragged/moe.py:28-45) for SiLU-gated W4 experts.
- * Requires block_size 64 or 128, H % 128 == 0, F % 64 == 0.
+ * Requires H even and a multiple of group_size. Block size 64 or 128 with
+ * H % 128 == 0, F % 64 == 0, group 32 or a multiple of 64 and aligned rows
+ * runs the tiled kernels; any other block size or shape a generic kernel.
  */
 int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_t x_ld,
                           const int32_t* sorted_route_ids, const int32_t* expert_blocks,
@@ -191,7 +193,9 @@ int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_t x_ld,
  * Wd: packed [E][H, F/2], scales/zeros [E][H, F/g]; out f32 [R, H].
  * Replaces the second contraction of moe_expert_ffn
  * (examples/kernels/ragged/moe.py:46-53).
- * Requires block_size 64 or 128, F % 128 == 0.
+ * Requires F even and a multiple of group_size. Block size 64 or 128 with
+ * F % 128 == 0, group 32 or a multiple of 64 and aligned rows runs the
+ * tiled kernels; any other block size or shape a generic kernel.
  */
 int intent_moe_down_w4(const void* act, int64_t act_ld,
                        const int32_t* sorted_route_ids, const int32_t* expert_blocks,

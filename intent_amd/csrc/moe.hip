@@ -671,6 +671,66 @@ extern "C" int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_
 namespace {
 
 
+// ---- any block size / shape: one output element per thread -------------------
+// The same dequantisation (f16 (q - z) * s, one rounding), f32 sums of the
+// f16 products, SiLU gating and route scatter as the tiled kernels; used
+// where those do not apply (block sizes other than 64 and 128, dimensions
+// off their tiles, unaligned rows).
+INTENT_DEVICE float w4_dot_row(const f16* __restrict__ xr, const uint8_t* __restrict__ qr,
+                               const f16* __restrict__ sr, const uint8_t* __restrict__ zr, int K, int gs) {
+  float acc = 0.f;
+  for (int g0 = 0, g = 0; g0 < K; g0 += gs, ++g) {
+    const float s = (float)sr[g];
+    const float z = (float)zr[g];
+    for (int k = g0; k < g0 + gs; ++k) {
+      const uint32_t byte = qr[k >> 1];
+      const float q = (float)((k & 1) ? (byte >> 4) : (byte & 15u));
+      const f16 w = (f16)((float)(f16)(q - z) * s);
+      acc = __builtin_fmaf((float)xr[k], (float)w, acc);
+    }
+  }
+  return acc;
+}
+
+__global__ __launch_bounds__(256) void moe_gate_up_generic_kernel(
+    const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ blocks, int B, int R, int top_k, const uint8_t* __restrict__ wq,
+    const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int F, int gs, f16* __restrict__ act,
+    int64_t ld_act, int fchunks) {
+  const int row = blockIdx.x / fchunks;
+  const int f = (blockIdx.x % fchunks) * 256 + threadIdx.x;
+  if (f >= F) return;
+  const int e = blocks[row / B];
+  if (e < 0) return;
+  const int r = sorted[row];
+  f16 o = (f16)0.f;
+  if (r >= 0 && r < R) {
+    const int64_t ldq = H / 2, ldp = H / gs;
+    const int64_t gr = (int64_t)e * 2 * F + f, ur = gr + F;
+    const f16* xr = x + (int64_t)(r / top_k) * ldx;
+    const float gt = w4_dot_row(xr, wq + gr * ldq, ws + gr * ldp, wz + gr * ldp, H, gs);
+    const float up = w4_dot_row(xr, wq + ur * ldq, ws + ur * ldp, wz + ur * ldp, H, gs);
+    o = (f16)((gt / (1.0f + expf(-gt))) * up);
+  }
+  act[(int64_t)row * ld_act + f] = o;
+}
+
+__global__ __launch_bounds__(256) void moe_down_generic_kernel(
+    const f16* __restrict__ act, int64_t ld_act, const int32_t* __restrict__ sorted,
+    const int32_t* __restrict__ blocks, int B, int R, const uint8_t* __restrict__ wq, const f16* __restrict__ ws,
+    const uint8_t* __restrict__ wz, int H, int F, int gs, float* __restrict__ out, int64_t ldo, int dchunks) {
+  const int row = blockIdx.x / dchunks;
+  const int d = (blockIdx.x % dchunks) * 256 + threadIdx.x;
+  if (d >= H) return;
+  const int e = blocks[row / B];
+  const int r = sorted[row];
+  if (e < 0 || r < 0 || r >= R) return;
+  const int64_t ldq = F / 2, ldp = F / gs;
+  const int64_t wr = (int64_t)e * H + d;
+  out[(int64_t)r * ldo + d] = w4_dot_row(act + (int64_t)row * ld_act, wq + wr * ldq, ws + wr * ldp, wz + wr * ldp,
+                                         F, gs);
+}
+
 template <int B>
 int gate_up_launch(const void* x, int64_t T, int64_t H, int64_t x_ld, const int32_t* sorted, const int32_t* blocks,
                    int64_t num_blocks, int64_t top_k, const uint8_t* wq, const void* ws, const uint8_t* wz,
@@ -725,22 +785,32 @@ extern "C" int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_
                                      const uint8_t* w_zeros, int64_t E, int64_t F, int64_t group_size, void* act,
                                      int64_t act_ld, void* stream) {
   intent::clear_error();
-  INTENT_REQUIRE(supported_block(block_size), INTENT_ERR_UNSUPPORTED, "block_size must be 64 or 128, got %lld",
+  INTENT_REQUIRE(block_size >= 1 && block_size <= (1 << 20), INTENT_ERR_INVALID_ARGUMENT, "bad block_size %lld",
                  (long long)block_size);
-  INTENT_REQUIRE(H > 0 && H % 128 == 0 && H <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "H must be a positive multiple of 128");
-  INTENT_REQUIRE(F > 0 && F % 64 == 0 && F <= INT32_MAX / 2, INTENT_ERR_UNSUPPORTED, "F must be a positive multiple of 64");
-  INTENT_REQUIRE(group_size > 0 && (group_size == 32 || group_size % 64 == 0) && H % group_size == 0,
-                 INTENT_ERR_UNSUPPORTED, "group_size must be 32 or a multiple of 64 dividing H");
-  INTENT_REQUIRE(intent::fits_offset(2 * F, H / 2) && intent::fits_offset(2 * F, H / group_size * 2) &&
-                     intent::fits_offset(T, x_ld * 2) && intent::fits_offset(256 + 1, act_ld * 2),
-                 INTENT_ERR_UNSUPPORTED, "moe_gate_up_w4: operand too large for 31-bit buffer offsets");
+  INTENT_REQUIRE(H > 0 && H % 2 == 0 && H <= INT32_MAX && F > 0 && F <= INT32_MAX / 2, INTENT_ERR_INVALID_ARGUMENT,
+                 "H must be positive and even, F positive");
+  INTENT_REQUIRE(group_size > 0 && H % group_size == 0, INTENT_ERR_INVALID_ARGUMENT,
+                 "group_size must divide H (H=%lld group=%lld)", (long long)H, (long long)group_size);
   INTENT_REQUIRE(T >= 0 && top_k >= 1 && E >= 1 && num_blocks >= 0, INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   if (num_blocks == 0 || T == 0) return INTENT_OK;
   INTENT_REQUIRE(x && sorted_route_ids && expert_blocks && w_packed && w_scales && w_zeros && act,
                  INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(x_ld >= H && act_ld >= F, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
-  INTENT_REQUIRE(intent::aligned16(x) && x_ld % 8 == 0 && intent::aligned16(w_packed), INTENT_ERR_ALIGNMENT,
-                 "x and weights must be 16-byte aligned");
+  const bool fast = supported_block(block_size) && H % 128 == 0 && F % 64 == 0 &&
+                    (group_size == 32 || group_size % 64 == 0) && intent::fits_offset(2 * F, H / 2) &&
+                    intent::fits_offset(2 * F, H / group_size * 2) && intent::fits_offset(T, x_ld * 2) &&
+                    intent::fits_offset(256 + 1, act_ld * 2) && intent::aligned16(x) && x_ld % 8 == 0 &&
+                    intent::aligned16(w_packed);
+  if (!fast) {
+    const int64_t fchunks = (F + 255) / 256;
+    const int64_t grid = num_blocks * block_size * fchunks;
+    INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "moe_gate_up_w4: grid too large");
+    hipLaunchKernelGGL(moe_gate_up_generic_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                       (const f16*)x, x_ld, (int)H, sorted_route_ids, expert_blocks, (int)block_size,
+                       (int)(T * top_k), (int)top_k, w_packed, (const f16*)w_scales, w_zeros, (int)F, (int)group_size,
+                       (f16*)act, act_ld, (int)fchunks);
+    return intent::launch_status("moe_gate_up_generic_kernel");
+  }
   if (block_size == 64)
     return gate_up_launch<64>(x, T, H, x_ld, sorted_route_ids, expert_blocks, num_blocks, top_k, w_packed, w_scales,
                               w_zeros, F, group_size, act, act_ld, stream);
@@ -754,23 +824,39 @@ int down_check(const void* act, int64_t act_ld, const int32_t* sorted_route_ids,
                int64_t num_blocks, int64_t block_size, int64_t R, const uint8_t* w_packed, const void* w_scales,
                const uint8_t* w_zeros, int64_t E, int64_t H, int64_t F, int64_t group_size, const float* out,
                int64_t out_ld) {
-  INTENT_REQUIRE(supported_block(block_size), INTENT_ERR_UNSUPPORTED, "block_size must be 64 or 128, got %lld",
+  INTENT_REQUIRE(block_size >= 1 && block_size <= (1 << 20), INTENT_ERR_INVALID_ARGUMENT, "bad block_size %lld",
                  (long long)block_size);
-  INTENT_REQUIRE(F > 0 && F % 128 == 0 && F <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "F must be a positive multiple of 128");
-  INTENT_REQUIRE(H > 0 && H <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "bad H");
-  INTENT_REQUIRE(group_size > 0 && (group_size == 32 || group_size % 64 == 0) && F % group_size == 0,
-                 INTENT_ERR_UNSUPPORTED, "group_size must be 32 or a multiple of 64 dividing F");
-  INTENT_REQUIRE(intent::fits_offset(H, F / 2) && intent::fits_offset(H, F / group_size * 2) &&
-                     intent::fits_offset(256 + 1, act_ld * 2),
-                 INTENT_ERR_UNSUPPORTED, "moe_down_w4: operand too large for 31-bit buffer offsets");
+  INTENT_REQUIRE(F > 0 && F % 2 == 0 && F <= INT32_MAX && H > 0 && H <= INT32_MAX, INTENT_ERR_INVALID_ARGUMENT,
+                 "F must be positive and even, H positive");
+  INTENT_REQUIRE(group_size > 0 && F % group_size == 0, INTENT_ERR_INVALID_ARGUMENT,
+                 "group_size must divide F (F=%lld group=%lld)", (long long)F, (long long)group_size);
   INTENT_REQUIRE(R >= 0 && E >= 1 && num_blocks >= 0, INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   if (num_blocks == 0 || R == 0) return INTENT_OK;
   INTENT_REQUIRE(act && sorted_route_ids && expert_blocks && w_packed && w_scales && w_zeros && out,
                  INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(act_ld >= F && out_ld >= H, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
-  INTENT_REQUIRE(intent::aligned16(act) && act_ld % 8 == 0 && intent::aligned16(w_packed), INTENT_ERR_ALIGNMENT,
-                 "activations and weights must be 16-byte aligned");
   return INTENT_OK;
+}
+
+// Shapes the tiled down projections take.
+bool down_fast(const void* act, int64_t act_ld, int64_t block_size, const uint8_t* w_packed, int64_t H, int64_t F,
+               int64_t group_size) {
+  return supported_block(block_size) && F % 128 == 0 && (group_size == 32 || group_size % 64 == 0) &&
+         intent::fits_offset(H, F / 2) && intent::fits_offset(H, F / group_size * 2) &&
+         intent::fits_offset(256 + 1, act_ld * 2) && intent::aligned16(act) && act_ld % 8 == 0 &&
+         intent::aligned16(w_packed);
+}
+
+int down_generic(const void* act, int64_t act_ld, const int32_t* sorted, const int32_t* blocks, int64_t num_blocks,
+                 int64_t block_size, int64_t R, const uint8_t* wq, const void* ws, const uint8_t* wz, int64_t H,
+                 int64_t F, int64_t gs, float* out, int64_t out_ld, void* stream) {
+  const int64_t dchunks = (H + 255) / 256;
+  const int64_t grid = num_blocks * block_size * dchunks;
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "moe_down_w4: grid too large");
+  hipLaunchKernelGGL(moe_down_generic_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                     (const f16*)act, act_ld, sorted, blocks, (int)block_size, (int)R, wq, (const f16*)ws, wz, (int)H,
+                     (int)F, (int)gs, out, out_ld, (int)dchunks);
+  return intent::launch_status("moe_down_generic_kernel");
 }
 
 int down_dispatch(const void* act, int64_t act_ld, const int32_t* sorted, const int32_t* blocks, int64_t num_blocks,
@@ -791,6 +877,9 @@ extern "C" int intent_moe_down_w4(const void* act, int64_t act_ld, const int32_t
   int st = down_check(act, act_ld, sorted_route_ids, expert_blocks, num_blocks, block_size, R, w_packed, w_scales,
                       w_zeros, E, H, F, group_size, out, out_ld);
   if (st != INTENT_OK || num_blocks == 0 || R == 0) return st;
+  if (!down_fast(act, act_ld, block_size, w_packed, H, F, group_size))
+    return down_generic(act, act_ld, sorted_route_ids, expert_blocks, num_blocks, block_size, R, w_packed, w_scales,
+                        w_zeros, H, F, group_size, out, out_ld, stream);
   return down_dispatch(act, act_ld, sorted_route_ids, expert_blocks, num_blocks, block_size, R, w_packed, w_scales,
                        w_zeros, H, F, group_size, out, out_ld, stream);
 }
@@ -892,7 +981,8 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
   const int64_t R = T * top_k;
   const int64_t ldp = F / group_size;
   const int want = down_splits(F, group_size);
-  const bool pk = ldp % 4 == 0 && F % (want * 4 * group_size) == 0 && (F / want) % 64 == 0 &&
+  const bool pk = down_fast(act, F, B, wd_packed, H, F, group_size) && ldp % 4 == 0 &&
+                  F % (want * 4 * group_size) == 0 && (F / want) % 64 == 0 &&
                   intent::aligned4(wd_scales) && intent::aligned4(wd_zeros);
   int splits = 1;
   if (pk) {

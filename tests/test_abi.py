@@ -90,10 +90,13 @@ def test_moe_checks():
     assert "needs" in _native.last_error()
     assert status("intent_moe_align", FAKE, 16, 2, 1000, 128, FAKE, 10 ** 6, FAKE, 10 ** 4, FAKE, FAKE, None) == \
         errors.INTENT_ERR_UNSUPPORTED
-    assert status("intent_moe_gate_up_w4", FAKE, 4, 256, 256, FAKE, FAKE, 2, 32, 2, FAKE, FAKE, FAKE, 2, 128, 128,
-                  FAKE, 128, None) == errors.INTENT_ERR_UNSUPPORTED  # block size 32
-    assert status("intent_moe_down_w4", FAKE, 96, FAKE, FAKE, 2, 128, 8, FAKE, FAKE, FAKE, 2, 256, 96, 32,
-                  FAKE, 256, None) == errors.INTENT_ERR_UNSUPPORTED  # F % 128
+    # other block sizes and dimensions off the tiles run the generic kernels (GPU tests); invalid calls:
+    assert status("intent_moe_gate_up_w4", FAKE, 4, 256, 256, FAKE, FAKE, 2, 0, 2, FAKE, FAKE, FAKE, 2, 128, 128,
+                  FAKE, 128, None) == errors.INTENT_ERR_INVALID_ARGUMENT  # block size 0
+    assert status("intent_moe_gate_up_w4", FAKE, 4, 250, 256, FAKE, FAKE, 2, 32, 2, FAKE, FAKE, FAKE, 2, 128, 128,
+                  FAKE, 128, None) == errors.INTENT_ERR_INVALID_ARGUMENT  # group 128 does not divide H = 250
+    assert status("intent_moe_down_w4", FAKE, 95, FAKE, FAKE, 2, 128, 8, FAKE, FAKE, FAKE, 2, 256, 95, 32,
+                  FAKE, 256, None) == errors.INTENT_ERR_INVALID_ARGUMENT  # F odd
     assert _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 128) >= \
         16 * 128 * 14336 * 2 + 1024 * 4096 * 4  # block 128: padded activations + route outputs
     need = _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 0)  # composite plan

@@ -298,6 +298,38 @@ def test_moe_ffn_group_sizes(gpu, threads, group):
     assert_close_rms(got, ref, what=f"moe ffn group {group}")
 
 
+@pytest.mark.parametrize("B", [16, 32])
+def test_moe_stages_other_block_sizes(gpu, threads, B):
+    # align -> gate/up -> down -> combine at block sizes the tiled kernels do not take (the generic
+    # kernels), against the oracle's whole expert FFN
+    T, H, E, k, F = 45, 256, 4, 2, 128
+    d = moe_small(8, T, H, E, k, F)
+    ids, wts = oracle.moe_route(d["logits"], k, True)
+    sorted_ids, blocks, _, _ = art(intent.moe_align_block_size, EXPERTS=E, BLOCK_SIZE=B).run(dev(ids))
+    gu = art(intent.moe_gate_up_w4, TOP_K=k, BLOCK_SIZE=B)
+    act = gu.run(dev(d["x"]), sorted_ids, blocks, dev(d["wgu"]), dev(d["sgu"]), dev(d["zgu"]))
+    assert gu.observation.kernel == "moe_gate_up_generic_kernel", gu.observation.kernel
+    dn = art(intent.moe_down_w4, ROUTES=T * k, BLOCK_SIZE=B)
+    route_out = dn.run(act, sorted_ids, blocks, dev(d["wd"]), dev(d["sd"]), dev(d["zd"]))
+    assert dn.observation.kernel == "moe_down_generic_kernel", dn.observation.kernel
+    y = dev(np.zeros((T, H), np.float32))
+    art(intent.moe_combine).run(route_out, dev(wts), y)
+    ref = oracle.moe_ffn_w4(d["x"], ids, wts, d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"],
+                            threads=threads)
+    assert_close_rms(host(y), ref, what=f"moe stages B={B}")
+
+
+@pytest.mark.parametrize("T,H,E,k,F,group", [(30, 192, 3, 2, 96, 32), (9, 96, 2, 1, 200, 8)])
+def test_moe_ffn_off_tile_dims(gpu, threads, T, H, E, k, F, group):
+    # H not a multiple of 128, F not a multiple of 64 / 128, small groups: the composite runs the
+    # generic projections
+    d = moe_small(9, T, H, E, k, F, group=group)
+    got = run_ffn(d, np.zeros((T, H), np.float32))
+    ids, wts = oracle.moe_route(d["logits"], k, True)
+    ref = oracle.moe_ffn_w4(d["x"], ids, wts, d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"], threads=threads)
+    assert_close_rms(got, ref, what=f"moe ffn off-tile {T}x{H}x{F} g{group}")
+
+
 def test_moe_ffn_config4(gpu, threads):
     d = inputs.config4_moe(0)
     T, H = d["x"].shape
