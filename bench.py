@@ -415,7 +415,7 @@ def bench_i8_quant(steps: int, warmup: int) -> dict:
 def measured_traffic(kernel: str) -> int | None:
     """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE profile, if that
     profile covers `kernel` (the variant this run dispatched to); otherwise None."""
-    path = ROOT / "profiles" / "w4a16_gemv_dot_m1_traffic.md"
+    path = ROOT / "profiles" / "w4a16_gemv_decode_m1_traffic.md"
     if not path.exists():
         return None
     text = path.read_text().splitlines()
