@@ -17,47 +17,70 @@ namespace {
 // the list is the same on every run.
 constexpr int kListThreads = 1024;
 
+// Token counts and placement cursors live in LDS up to this many tokens
+// (64 KB), in the count array of the workspace beyond.
+constexpr int kListLdsTokens = 16384;
+
+// Inclusive sum of v over the workgroup's kListThreads threads, in thread
+// order (wave prefix by shuffles, then the wave totals); `wsum` holds one
+// slot per wave.
+INTENT_DEVICE int block_inclusive_scan(int v, int* wsum) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d);
+    if (lane >= d) v += o;
+  }
+  if (lane == 63) wsum[wave] = v;
+  __syncthreads();
+  if (wave == 0) {
+    int w = lane < kListThreads / 64 ? wsum[lane] : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(w, d);
+      if (lane >= d) w += o;
+    }
+    if (lane < kListThreads / 64) wsum[lane] = w;
+  }
+  __syncthreads();
+  return v + (wave > 0 ? wsum[wave - 1] : 0);
+}
+
+template <bool kLds>
 __global__ __launch_bounds__(kListThreads) void token_member_list_kernel(
     const int32_t* __restrict__ route_offsets, int E, const int32_t* __restrict__ members,
     const int32_t* __restrict__ route_token, int T, int R, int NR, int32_t* __restrict__ count,
     int32_t* __restrict__ start, int32_t* __restrict__ list) {
-  __shared__ int32_t part[kListThreads];
+  __shared__ int32_t lds_cnt[kLds ? kListLdsTokens : 1];
+  __shared__ int32_t wsum[kListThreads / 64];
+  int32_t* cnt = kLds ? lds_cnt : count;
   const int tid = threadIdx.x;
   const int m0 = clampi(route_offsets[0], 0, R);
   int m1 = m0;  // end of the last non-empty group, as find_tile clamps it
   for (int g = 0; g < E; ++g) m1 = clampi(route_offsets[g + 1], m1, R);
   auto token_of = [&](int i) { return clampi(route_token[clampi(members[i], 0, NR - 1)], 0, T - 1); };
-  for (int t = tid; t < T; t += kListThreads) count[t] = 0;
+  for (int t = tid; t < T; t += kListThreads) cnt[t] = 0;
   __syncthreads();
-  for (int i = m0 + tid; i < m1; i += kListThreads) atomicAdd(&count[token_of(i)], 1);
+  for (int i = m0 + tid; i < m1; i += kListThreads) atomicAdd(&cnt[token_of(i)], 1);
   __syncthreads();
-  // exclusive scan of count over T: each thread scans a contiguous slice
+  // exclusive scan of the counts: each thread takes a contiguous slice of tokens
   const int per = (T + kListThreads - 1) / kListThreads;
   const int t0 = tid * per;
   int sum = 0;
-  for (int t = t0; t < t0 + per && t < T; ++t) sum += count[t];
-  part[tid] = sum;
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int k = 0; k < kListThreads; ++k) {
-      const int v = part[k];
-      part[k] = run;
-      run += v;
-    }
-    start[T] = run;
-  }
-  __syncthreads();
-  int run = part[tid];
+  for (int t = t0; t < t0 + per && t < T; ++t) sum += cnt[t];
+  const int incl = block_inclusive_scan(sum, wsum);
+  int run = incl - sum;
+  if (tid == kListThreads - 1) start[T] = incl;
   for (int t = t0; t < t0 + per && t < T; ++t) {
     start[t] = run;
-    run += count[t];
-    count[t] = 0;  // reused as the placement cursor
+    run += cnt[t];
+    cnt[t] = 0;  // reused as the placement cursor
   }
   __syncthreads();
   for (int i = m0 + tid; i < m1; i += kListThreads) {
     const int t = token_of(i);
-    const int pos = atomicAdd(&count[t], 1);
+    const int pos = atomicAdd(&cnt[t], 1);
     list[start[t] + pos] = i;
   }
   __syncthreads();
@@ -174,7 +197,7 @@ extern "C" int intent_moe_expert_ffn(const void* x, int64_t T, int64_t D, int64_
                                                          D, s);
   st = intent::launch_status("grouped_kn_kernel<moe w2 weighted>");
   if (st != INTENT_OK) return st;
-  hipLaunchKernelGGL(token_member_list_kernel, dim3(1), dim3(kListThreads), 0, s, route_offsets, (int)E,
+  hipLaunchKernelGGL(T <= kListLdsTokens ? token_member_list_kernel<true> : token_member_list_kernel<false>, dim3(1), dim3(kListThreads), 0, s, route_offsets, (int)E,
                      member_routes, route_token, (int)T, (int)R, (int)NR, count, start, list);
   st = intent::launch_status("token_member_list");
   if (st != INTENT_OK) return st;
