@@ -157,7 +157,7 @@ int intent_moe_route(const float* logits, int64_t T, int64_t E, int64_t top_k,
  *     blocks past the padded total hold -1;
  *   expert_offsets i32 [E+1]; total_padded i32 [1].
  * Route ids whose expert is outside [0,E) are dropped.
- * Requires E <= 512.
+ * Requires E <= 2048 (its LDS holds 19 counters per expert).
  */
 int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_k, int64_t E,
                      int64_t block_size,

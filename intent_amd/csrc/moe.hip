@@ -13,7 +13,7 @@ constexpr int kMaxTopK = 8;
 constexpr int kMaxRouteExperts = 256;
 constexpr int kAlignThreads = 1024;
 constexpr int kAlignWaves = kAlignThreads / 64;
-constexpr int kMaxAlignExperts = 512;
+constexpr int kMaxAlignExperts = 2048;  // LDS: (3E + 1 + 16E) ints
 
 // ---- router ---------------------------------------------------------------
 // One wave per token; lane L holds the logits of experts 4L .. 4L+3. Every
@@ -164,10 +164,14 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t*
                                                                   int32_t* __restrict__ blocks, int nblocks,
                                                                   int32_t* __restrict__ offsets,
                                                                   int32_t* __restrict__ total) {
-  __shared__ int cnt[kMaxAlignExperts];
-  __shared__ int off[kMaxAlignExperts + 1];
-  __shared__ int base[kMaxAlignExperts];
-  __shared__ int wcnt[kAlignWaves][kMaxAlignExperts];
+  // LDS sized by E at launch: counts, offsets (E + 1), bases, then the
+  // per-wave counts of a chunk (kAlignWaves x E)
+  extern __shared__ int align_lds[];
+  int* cnt = align_lds;
+  int* off = cnt + E;
+  int* base = off + E + 1;
+  int* wcnt_flat = base + E;
+  auto wcnt = [&](int w, int e) -> int& { return wcnt_flat[w * E + e]; };
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -211,7 +215,7 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t*
 
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int c = 0; c < R; c += kAlignThreads) {
-    for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wcnt[i / E][i % E] = 0;
+    for (int i = tid; i < kAlignWaves * E; i += kAlignThreads) wcnt(i / E, i % E) = 0;
     const int r = c + tid;
     int e = r < R ? ids[r] : -1;
     const bool valid = e >= 0 && e < E;
@@ -224,21 +228,21 @@ __global__ __launch_bounds__(kAlignThreads) void moe_align_kernel(const int32_t*
       const int le = __shfl(e, leader);
       const uint64_t same = __ballot(e == le) & remaining;
       if (e == le) rank = __popcll(same & lt_mask);
-      if (lane == leader) wcnt[wave][le] = __popcll(same);
+      if (lane == leader) wcnt(wave, le) = __popcll(same);
       remaining &= ~same;
     }
     __syncthreads();
     for (int x = tid; x < E; x += kAlignThreads) {
       int run = base[x];
       for (int w = 0; w < kAlignWaves; ++w) {
-        const int n = wcnt[w][x];
-        wcnt[w][x] = run;
+        const int n = wcnt(w, x);
+        wcnt(w, x) = run;
         run += n;
       }
       base[x] = run;
     }
     __syncthreads();
-    if (valid) sorted[off[e] + wcnt[wave][e] + rank] = r;
+    if (valid) sorted[off[e] + wcnt(wave, e) + rank] = r;
     __syncthreads();
   }
 }
@@ -662,7 +666,14 @@ extern "C" int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_
   INTENT_REQUIRE(capacity <= INT32_MAX && num_blocks <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "capacity exceeds int32");
   INTENT_REQUIRE(sorted_route_ids && expert_blocks && expert_offsets && total_padded && (R == 0 || topk_ids),
                  INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), 0, (hipStream_t)stream, topk_ids, (int)R, (int)E,
+  const size_t lds = (size_t)(3 * E + 1 + kAlignWaves * E) * sizeof(int);
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute((const void*)moe_align_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)lds);
+    INTENT_REQUIRE(e == hipSuccess, INTENT_ERR_LAUNCH, "moe_align: %zu bytes of LDS refused (%s)", lds,
+                   hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(kAlignThreads), lds, (hipStream_t)stream, topk_ids, (int)R, (int)E,
                      (int)block_size, sorted_route_ids, (int)capacity, expert_blocks, (int)num_blocks,
                      expert_offsets, total_padded);
   return intent::launch_status("moe_align");

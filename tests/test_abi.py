@@ -88,8 +88,8 @@ def test_moe_checks():
     assert status("intent_moe_align", FAKE, 16, 2, 4, 128, FAKE, 100, FAKE, 10, FAKE, FAKE, None) == \
         errors.INTENT_ERR_INVALID_ARGUMENT
     assert "needs" in _native.last_error()
-    assert status("intent_moe_align", FAKE, 16, 2, 1000, 128, FAKE, 10 ** 6, FAKE, 10 ** 4, FAKE, FAKE, None) == \
-        errors.INTENT_ERR_UNSUPPORTED
+    assert status("intent_moe_align", FAKE, 16, 2, 3000, 128, FAKE, 10 ** 6, FAKE, 10 ** 4, FAKE, FAKE, None) == \
+        errors.INTENT_ERR_UNSUPPORTED  # more than 2048 experts
     # other block sizes and dimensions off the tiles run the generic kernels (GPU tests); invalid calls:
     assert status("intent_moe_gate_up_w4", FAKE, 4, 256, 256, FAKE, FAKE, 2, 0, 2, FAKE, FAKE, FAKE, 2, 128, 128,
                   FAKE, 128, None) == errors.INTENT_ERR_INVALID_ARGUMENT  # block size 0

@@ -246,7 +246,7 @@ def test_moe_route(gpu, T, E, k, renorm):
 
 
 @pytest.mark.parametrize("T,k,E,B", [(512, 2, 8, 128), (4096, 2, 64, 128), (100, 3, 5, 16), (1, 1, 1, 128),
-                                     (3000, 2, 512, 64)])
+                                     (3000, 2, 512, 64), (700, 3, 1500, 16), (64, 2, 2048, 32)])
 def test_moe_align(gpu, T, k, E, B):
     rng = np.random.default_rng(T * 7 + E)
     if T == 4096:
