@@ -7,6 +7,8 @@
 #include "mfma_pipe.h"
 #include "w4pk.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kMaxTopK = 8;
@@ -395,6 +397,12 @@ __global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_ker
 using GateUpPk = mp::Tile<128, 256, 1, 4>;
 constexpr int kGateUpPkStages = 3;
 
+// Group parameters per stage (gs == 32) or per window of four groups.
+template <bool kWin>
+using PkParams = std::conditional_t<kWin, mp::GroupWindowDma<GateUpPk::BN, GateUpPk::NW>,
+                                    mp::GroupParamsDma<GateUpPk::BN, GateUpPk::NW>>;
+
+template <bool kWin>
 __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
     const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ blocks, int mblocks, int R, int top_k, const uint8_t* __restrict__ wq,
@@ -402,7 +410,8 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
     int64_t ld_act) {
   using T = GateUpPk;
   constexpr int NB = kGateUpPkStages;
-  __shared__ __attribute__((aligned(16))) char smem[NB][mp::stage_bytes_pk<T>()];
+  __shared__ __attribute__((aligned(16))) char smem[NB][mp::stage_bytes_pk<T, kWin>()];
+  __shared__ __attribute__((aligned(16))) char pwin[kWin ? 2 * PkParams<true>::BYTES : 16];
   char* bufs[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) bufs[b] = smem[b];
@@ -420,7 +429,7 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
   aop.init(mp::GatherRows{x, ldx * 2, sorted, R, top_k}, m0, wave);
   mp::PackedRowsDma<T::BN, T::NW> bop;
   bop.init(wq + (int64_t)e * 2 * F * ldq, ldq, rows, wave);
-  mp::GroupParamsDma<T::BN, T::NW> pop;
+  PkParams<kWin> pop;
   pop.init(ws + (int64_t)e * 2 * F * ldp, wz + (int64_t)e * 2 * F * ldp, ldp, gs, rows, wave);
   f32x16 acc[T::TI][T::TJ];
   // An expert's padding rows (sentinel route R) sit at the end of its last
@@ -433,13 +442,13 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
   using BDma = decltype(bop);
   using PDma = decltype(pop);
   if (ta <= 1)
-    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 1>(aop, bop, pop, H / 64, bufs, acc);
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 1>(aop, bop, pop, H / 64, bufs, acc, pwin);
   else if (ta == 2)
-    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 2>(aop, bop, pop, H / 64, bufs, acc);
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 2>(aop, bop, pop, H / 64, bufs, acc, pwin);
   else if (ta == 3)
-    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 3>(aop, bop, pop, H / 64, bufs, acc);
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 3>(aop, bop, pop, H / 64, bufs, acc, pwin);
   else
-    mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, H / 64, bufs, acc);
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, H / 64, bufs, acc, pwin);
   store_gate_up<T>(acc, m0, f0, F, sorted, R, act, ld_act);
 }
 
@@ -509,6 +518,7 @@ __global__ __launch_bounds__(MoeTiles<B>::Down::NT_WS, 1) void moe_down_kernel(
 // combine adds the parts in order. Measured on config 4: 328 us for the
 // producer/consumer kernel below, which runs 384 workgroups of 128 x 128 with
 // the decode in separate waves.
+template <bool kWin>
 __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
     const f16* __restrict__ act, int64_t ld_act, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ blocks, int mblocks, int ntiles, int R, const uint8_t* __restrict__ wq,
@@ -516,7 +526,8 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
     float* __restrict__ out, int64_t ldo, int64_t part_stride) {
   using T = GateUpPk;
   constexpr int NB = kGateUpPkStages;
-  __shared__ __attribute__((aligned(16))) char smem[NB][mp::stage_bytes_pk<T>()];
+  __shared__ __attribute__((aligned(16))) char smem[NB][mp::stage_bytes_pk<T, kWin>()];
+  __shared__ __attribute__((aligned(16))) char pwin[kWin ? 2 * PkParams<true>::BYTES : 16];
   char* bufs[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) bufs[b] = smem[b];
@@ -538,7 +549,7 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
   aop.init(mp::DenseRows{act + k0, ld_act * 2, m0 + T::BM}, m0, wave);
   mp::PackedRowsDma<T::BN, T::NW> bop;
   bop.init(wq + (int64_t)e * H * ldq + k0 / 2, ldq, rows, wave);
-  mp::GroupParamsDma<T::BN, T::NW> pop;
+  PkParams<kWin> pop;
   pop.init(ws + (int64_t)e * H * ldp + k0 / gs, wz + (int64_t)e * H * ldp + k0 / gs, ldp, gs, rows, wave);
   f32x16 acc[T::TI][T::TJ];
   int ta = 0;
@@ -550,13 +561,13 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
   using PDma = decltype(pop);
   const int nk = kpart / 64;
   if (ta <= 1)
-    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 1>(aop, bop, pop, nk, bufs, acc);
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 1>(aop, bop, pop, nk, bufs, acc, pwin);
   else if (ta == 2)
-    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 2>(aop, bop, pop, nk, bufs, acc);
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 2>(aop, bop, pop, nk, bufs, acc, pwin);
   else if (ta == 3)
-    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 3>(aop, bop, pop, nk, bufs, acc);
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 3>(aop, bop, pop, nk, bufs, acc, pwin);
   else
-    mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, nk, bufs, acc);
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, nk, bufs, acc, pwin);
   store_down<T>(acc, m0, n0, H, sorted, R, out + part * part_stride, ldo);
 }
 
@@ -750,9 +761,10 @@ int gate_up_launch(const void* x, int64_t T, int64_t H, int64_t x_ld, const int3
   if (B == GateUpPk::BM && ldp % 4 == 0 && intent::aligned4(ws) && intent::aligned4(wz)) {
     const int64_t grid = num_blocks * ((F + GateUpPk::BN / 2 - 1) / (GateUpPk::BN / 2));
     INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
-    hipLaunchKernelGGL(moe_gate_up_pk_kernel, dim3((unsigned)grid), dim3(GateUpPk::NT), 0, (hipStream_t)stream,
-                       (const f16*)x, x_ld, (int)H, sorted, blocks, (int)num_blocks, (int)(T * top_k), (int)top_k, wq,
-                       (const f16*)ws, wz, (int)F, (int)gs, (f16*)act, act_ld);
+    auto kernel = gs % 64 == 0 ? moe_gate_up_pk_kernel<true> : moe_gate_up_pk_kernel<false>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(GateUpPk::NT), 0, (hipStream_t)stream, (const f16*)x, x_ld,
+                       (int)H, sorted, blocks, (int)num_blocks, (int)(T * top_k), (int)top_k, wq, (const f16*)ws, wz,
+                       (int)F, (int)gs, (f16*)act, act_ld);
     return intent::launch_status("moe_gate_up_w4");
   }
   using Tl = typename MoeTiles<B>::GateUp;
@@ -1004,7 +1016,8 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
     const int64_t ntiles = (H + GateUpPk::BN - 1) / GateUpPk::BN;
     const int64_t grid = splits * L.nblocks * ntiles;
     INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
-    hipLaunchKernelGGL(moe_down_pk_kernel, dim3((unsigned)grid), dim3(GateUpPk::NT), 0, (hipStream_t)stream,
+    auto kernel = group_size % 64 == 0 ? moe_down_pk_kernel<true> : moe_down_pk_kernel<false>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(GateUpPk::NT), 0, (hipStream_t)stream,
                        (const f16*)act, F, sorted, blocks, (int)L.nblocks, (int)ntiles, (int)R, wd_packed,
                        (const f16*)wd_scales, wd_zeros, (int)H, (int)F, (int)group_size, splits, out, H, R * H);
     st = intent::launch_status("moe_down_pk");

@@ -85,6 +85,7 @@ struct PackedRowsDma {
 // Requires 4-byte aligned rows of scales and zeros (checked by the caller).
 template <int ROWS, int NW>
 struct GroupParamsDma {
+  static constexpr bool kWindowed = false;
   static constexpr int TOTAL = ROWS / 64;
   static_assert(ROWS % 64 == 0, "weight tile rows must be a multiple of 64");
   static constexpr int N_INST = (TOTAL + NW - 1) / NW;  // per array
@@ -123,6 +124,59 @@ struct GroupParamsDma {
   }
 };
 
+// Group scales and zero points of a window of four groups, for group sizes
+// that are multiples of 64 (a window then spans gs / 16 >= 4 stages). A
+// window is loaded once into one of two LDS buffers outside the stage ring:
+// per tile row the two scale dwords (8 bytes) and the zero dword (4 bytes)
+// of groups 4w .. 4w + 3. The per-stage form above touches one cache line
+// per row and array in every stage; this one does so once per window.
+// Scale instruction t: lane i fills dword i % 2 of row 32t + i / 2; zero
+// instruction t: lane i fills row 64t + i. Requires ldp % 4 == 0, 4-byte
+// aligned rows, and K ranges that start on a window (checked by the caller).
+template <int ROWS, int NW>
+struct GroupWindowDma {
+  static constexpr bool kWindowed = true;
+  static_assert(ROWS % 64 == 0, "weight tile rows must be a multiple of 64");
+  static constexpr int S_TOTAL = ROWS / 32;
+  static constexpr int Z_TOTAL = ROWS / 64;
+  static constexpr int S_INST = (S_TOTAL + NW - 1) / NW;
+  static constexpr int Z_INST = (Z_TOTAL + NW - 1) / NW;
+  static constexpr int NVM = S_INST + Z_INST;
+  static constexpr int BYTES = 12 * ROWS;  // scale dword pairs, then zero dwords
+  Rsrc rs, rz;
+  uint32_t soff[S_INST], zoff[Z_INST];
+  int srow0[S_INST], zrow0[Z_INST];
+  int spg;  // stages per group: gs / 64
+  template <class RowMap>
+  INTENT_DEVICE void init(const f16* s, const uint8_t* z, int64_t ldp, int gsize, const RowMap& wrow, int wave) {
+    rs = make_rsrc(s);
+    rz = make_rsrc(z);
+    spg = gsize / 64;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < S_INST; ++j) {
+      const int t = j * NW + wave < S_TOTAL ? j * NW + wave : S_TOTAL - 1;
+      srow0[j] = t * 32;
+      soff[j] = (uint32_t)(wrow(t * 32 + (lane >> 1)) * ldp * 2 + (lane & 1) * 4);
+    }
+#pragma unroll
+    for (int j = 0; j < Z_INST; ++j) {
+      const int t = j * NW + wave < Z_TOTAL ? j * NW + wave : Z_TOTAL - 1;
+      zrow0[j] = t * 64;
+      zoff[j] = (uint32_t)(wrow(t * 64 + lane) * ldp);
+    }
+  }
+  INTENT_DEVICE void issue(char* lds_p, int w) const {
+#pragma unroll
+    for (int j = 0; j < S_INST; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_t*)(lds_p + srow0[j] * 8), 4, soff[j], (uint32_t)w * 8, 0, 0);
+#pragma unroll
+    for (int j = 0; j < Z_INST; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rz, (lds_t*)(lds_p + 8 * ROWS + zrow0[j] * 4), 4, zoff[j],
+                                               (uint32_t)w * 4, 0, 0);
+  }
+};
+
 // Per-stage register state: the stage's packed weight fragments with their
 // group parameters, and the A fragments and decoded weights of step 0.
 template <class T>
@@ -134,17 +188,18 @@ struct StagePk {
 
 // Reads of a stage that the first MFMA needs. sshift / zshift select the
 // lane's scale half and zero byte inside the staged dwords.
-template <class T, int TA>
-INTENT_DEVICE void stage_prologue(const char* buf, const uint32_t (&aaddr)[4], uint32_t baddr, uint32_t paddr,
-                                  int sshift, int zshift, StagePk<T>& st) {
+// ps / pz: the lane's scale and zero dwords for accumulator column block 0;
+// for block j they sit j * SJ and j * 128 bytes further.
+template <class T, int TA, int SJ>
+INTENT_DEVICE void stage_prologue(const char* buf, const uint32_t (&aaddr)[4], uint32_t baddr, const char* ps,
+                                  const char* pz, int sshift, int zshift, StagePk<T>& st) {
   const char* a = buf;
   const char* b = buf + T::A_BYTES;
-  const char* p = b + T::BN * 32;
 #pragma unroll
   for (int j = 0; j < T::TJ; ++j) {
     st.bq[j] = *reinterpret_cast<const u32x4*>(b + baddr + j * 32 * 32);
-    const uint32_t sw = *reinterpret_cast<const uint32_t*>(p + paddr + j * 32 * 4);
-    const uint32_t zw = *reinterpret_cast<const uint32_t*>(p + 4 * T::BN + paddr + j * 32 * 4);
+    const uint32_t sw = *reinterpret_cast<const uint32_t*>(ps + j * SJ);
+    const uint32_t zw = *reinterpret_cast<const uint32_t*>(pz + j * 32 * 4);
     st.zo[j] = splat2((f16)(float)(1024 + ((zw >> zshift) & 0xFFu)));
     st.sc[j] = splat2(bit_cast<f16>((uint16_t)(sw >> sshift)));
   }
@@ -209,19 +264,30 @@ INTENT_DEVICE void stage_body(const char* buf, const uint32_t (&aaddr)[4], const
 // same data into a buffer nobody reads again) and reads the first fragments
 // of stage kt + 1. Only DMA is in flight across steps, so the compiler's own
 // wait-count pass has nothing to wait for.
-template <class T>
+template <class T, bool kWindowed = false>
 constexpr int stage_bytes_pk() {
-  return T::A_BYTES + T::BN * 32 + GroupParamsDma<T::BN, T::NW>::BYTES;
+  return T::A_BYTES + T::BN * 32 + (kWindowed ? 0 : GroupParamsDma<T::BN, T::NW>::BYTES);
 }
 
 // TA <= T::TI: only the first TA 32-row blocks of the tile are computed (the
 // others are padding); their accumulators stay zero.
+//
+// With a windowed PDma (GroupWindowDma), pwin holds two window buffers of
+// PDma::BYTES. Windows 0 and 1 are loaded before the loop; the step whose
+// next stage opens window w loads window w + 1 into the buffer window w - 1
+// used, right after that step's stage group. Such a load sits between stage
+// groups in the vmcnt order, so the wait of each of the next two steps
+// allows its NVM instructions on top of one stage group; a window is read
+// at least three steps after its load was issued (a window spans >= 4
+// stages), by which time the stage group issued after it has been waited for.
 template <class T, int NB, class ADma, class BDma, class PDma, int TA = T::TI>
 INTENT_DEVICE void mainloop_pk(const ADma& aop, const BDma& bop, const PDma& pop, int nk, char* const (&bufs)[NB],
-                               f32x16 (&acc)[T::TI][T::TJ]) {
+                               f32x16 (&acc)[T::TI][T::TJ], char* pwin = nullptr) {
   static_assert(NB >= 2 && NB <= 8, "stage ring");
-  constexpr int NV = ADma::NVM + BDma::NVM + PDma::NVM;
-  static_assert(NB * NV < 64, "vmcnt range");
+  constexpr bool kWin = PDma::kWindowed;
+  constexpr int NV = ADma::NVM + BDma::NVM + (kWin ? 0 : PDma::NVM);
+  constexpr int NVP = kWin ? PDma::NVM : 0;
+  static_assert(NB * NV + NVP < 64, "vmcnt range");
 #pragma unroll
   for (int i = 0; i < T::TI; ++i)
 #pragma unroll
@@ -240,22 +306,43 @@ INTENT_DEVICE void mainloop_pk(const ADma& aop, const BDma& bop, const PDma& pop
   }
   const int brow = T::wave_n() * T::WTN + (lane & 31);
   const uint32_t baddr = (uint32_t)(brow * 32 + ((h ^ bswz(brow)) << 4));
-  const uint32_t paddr = (uint32_t)(brow * 4);
 
   auto issue = [&](auto J, int kt) {
     constexpr int j = decltype(J)::value;
     const int st = kt < nk ? kt : nk - 1;
     aop.issue(bufs[j], st);
     bop.issue(bufs[j] + T::A_BYTES, st);
-    pop.issue(bufs[j] + T::A_BYTES + T::BN * 32, st);
+    if constexpr (!kWin) pop.issue(bufs[j] + T::A_BYTES + T::BN * 32, st);
   };
-  // The lane's group is g0 + h for gs == 32, else g0; its scale is half
-  // (group & 1) of the dword at 2*(g0 & ~1), its zero byte (group & 3).
+  // Windowed: group pg and stage psg inside it of the next stage read.
+  int pg = 0, psg = 0, nwin = 0, pmask = 0;
+  if constexpr (kWin) nwin = (nk / pop.spg + 3) >> 2;
+  // Per-stage params: the lane's group is g0 + h for gs == 32, else g0; its
+  // scale is half (group & 1) of the dword at 2*(g0 & ~1), its zero byte
+  // (group & 3). Windowed: group gi = pg & 3 of the window, scale dword
+  // gi / 2, half gi & 1, zero byte gi.
   auto prologue = [&](auto J, int kt, StagePk<T>& st) {
-    const int g0 = pop.group(kt);
-    const int g = pop.gs == 32 ? g0 + h : g0;
-    stage_prologue<T, TA>(bufs[decltype(J)::value], aaddr, baddr, paddr, (g & 1) * 16, (g & 3) * 8, st);
+    constexpr int j = decltype(J)::value;
+    if constexpr (kWin) {
+      const int gi = pg & 3;
+      const char* pw = pwin + ((pg >> 2) & 1) * PDma::BYTES;
+      stage_prologue<T, TA, 32 * 8>(bufs[j], aaddr, baddr, pw + brow * 8 + (gi >> 1) * 4, pw + 8 * T::BN + brow * 4,
+                                    (gi & 1) * 16, gi * 8, st);
+      if (++psg == pop.spg) {
+        psg = 0;
+        ++pg;
+      }
+    } else {
+      const int g0 = pop.group(kt);
+      const int g = pop.gs == 32 ? g0 + h : g0;
+      const char* p = bufs[j] + T::A_BYTES + T::BN * 32 + brow * 4;
+      stage_prologue<T, TA, 32 * 4>(bufs[j], aaddr, baddr, p, p + 4 * T::BN, (g & 1) * 16, (g & 3) * 8, st);
+    }
   };
+  if constexpr (kWin) {
+    pop.issue(pwin, 0);
+    if (nwin > 1) pop.issue(pwin + PDma::BYTES, 1);
+  }
   static_for<0, NB>([&](auto S) { issue(S, decltype(S)::value); });
   StagePk<T> st;
   wait_vm_lgkm_barrier<(NB - 1) * NV>();
@@ -265,8 +352,23 @@ INTENT_DEVICE void mainloop_pk(const ADma& aop, const BDma& bop, const PDma& pop
     constexpr int j = decltype(J)::value;
     stage_body<T, TA>(bufs[j], aaddr, st, acc);
     if (kt + 1 < nk) {
-      wait_vm_lgkm_barrier<(NB - 2) * NV>();
+      if constexpr (kWin) {
+        if (pmask)
+          wait_vm_lgkm_barrier<(NB - 2) * NV + NVP>();
+        else
+          wait_vm_lgkm_barrier<(NB - 2) * NV>();
+      } else {
+        wait_vm_lgkm_barrier<(NB - 2) * NV>();
+      }
       issue(J, kt + NB);
+      if constexpr (kWin) {
+        pmask = (pmask << 1) & 3;
+        const int w1 = (pg >> 2) + 1;
+        if ((pg & 3) == 0 && psg == 0 && w1 < nwin) {
+          pop.issue(pwin + (w1 & 1) * PDma::BYTES, w1);
+          pmask |= 1;
+        }
+      }
       prologue(std::integral_constant<int, (j + 1) % NB>{}, kt + 1, st);
     }
   };

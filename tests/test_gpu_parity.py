@@ -298,6 +298,19 @@ def test_moe_ffn_group_sizes(gpu, threads, group):
     assert_close_rms(got, ref, what=f"moe ffn group {group}")
 
 
+# Group sizes that are multiples of 64 load scales and zeros in windows of
+# four groups; these shapes cross several windows in gate/up (H) and down (F),
+# including an odd window count and three stages per group.
+@pytest.mark.parametrize("group,H,F", [(64, 1024, 768), (128, 2048, 1536), (192, 3072, 2304), (128, 1536, 1024)])
+def test_moe_ffn_group_windows(gpu, threads, group, H, F):
+    T, E, k = 70, 4, 2
+    d = moe_small(6, T, H, E, k, F, group=group)
+    got = run_ffn(d, np.zeros((T, H), np.float32))
+    ids, wts = oracle.moe_route(d["logits"], k, True)
+    ref = oracle.moe_ffn_w4(d["x"], ids, wts, d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"], threads=threads)
+    assert_close_rms(got, ref, what=f"moe ffn group {group} H {H} F {F}")
+
+
 @pytest.mark.parametrize("B", [16, 32])
 def test_moe_stages_other_block_sizes(gpu, threads, B):
     # align -> gate/up -> down -> combine at block sizes the tiled kernels do not take (the generic
