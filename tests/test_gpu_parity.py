@@ -298,6 +298,19 @@ def test_moe_ffn_group_sizes(gpu, threads, group):
     assert_close_rms(got, ref, what=f"moe ffn group {group}")
 
 
+# Many routes per expert: experts of two and more 128-row blocks with light
+# last blocks, at group sizes 32, 64 and 128 and with F not a whole number
+# of four-group windows.
+@pytest.mark.parametrize("T,H,E,k,F,group", [(400, 1024, 4, 2, 1024, 128), (300, 512, 3, 2, 512, 64),
+                                             (512, 2048, 8, 2, 768, 128), (200, 512, 2, 1, 512, 32)])
+def test_moe_ffn_many_routes(gpu, threads, T, H, E, k, F, group):
+    d = moe_small(8, T, H, E, k, F, group=group)
+    got = run_ffn(d, np.zeros((T, H), np.float32))
+    ids, wts = oracle.moe_route(d["logits"], k, True)
+    ref = oracle.moe_ffn_w4(d["x"], ids, wts, d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"], threads=threads)
+    assert_close_rms(got, ref, what=f"moe ffn many routes T {T} H {H} E {E} F {F} group {group}")
+
+
 # Group sizes that are multiples of 64 load scales and zeros in windows of
 # four groups; these shapes cross several windows in gate/up (H) and down (F),
 # including an odd window count and three stages per group.
@@ -373,9 +386,12 @@ def test_moe_ffn_config4(gpu, threads):
     assert_close_rms(got, y.cpu().numpy(), what="moe config4 vs f64")
 
 
-@pytest.mark.parametrize("B,T,F", [(128, 48, 256), (64, 48, 256), (64, 100, 384)])
-def test_moe_stage_entries(gpu, threads, B, T, F):
-    H, E, k = 256, 4, 2
+# H = 512 at group 128 gives the tiled kernels whole four-group windows; block
+# size 192 is off the tiles and runs the generic kernels.
+@pytest.mark.parametrize("B,T,F,H", [(128, 48, 256, 256), (64, 48, 256, 256), (64, 100, 384, 256),
+                                     (128, 300, 512, 512), (192, 48, 256, 256)])
+def test_moe_stage_entries(gpu, threads, B, T, F, H):
+    E, k = 4, 2
     d = moe_small(9, T, H, E, k, F)
     ids, wts = art(intent.moe_route_topk, TOP_K=k).run(dev(d["logits"]))
     sorted_ids, blocks, offsets, total = art(intent.moe_align_block_size, EXPERTS=E, BLOCK_SIZE=B).run(ids)
