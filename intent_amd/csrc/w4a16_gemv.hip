@@ -490,9 +490,11 @@ __global__ __launch_bounds__(64 * WPB) void w4a16_gemv_dot_shared_kernel(
     qr[i] = r;
     qp[i] = p;
     const int n = (rbase + r < N ? r : N - 1 - rbase);
-    const bool ok = p < G2;
-    sq[i] = __builtin_amdgcn_raw_buffer_load_b32(srs, ok ? n * ldq * 2 + p * 4 : 0, 0, 0);
-    zq[i] = __builtin_amdgcn_raw_buffer_load_b16(zrs, ok ? n * ldq + p * 2 : 0, 0, 0);
+    // items past the records read offset 0; a mask rather than a select keeps
+    // the address math branch-free, so the weight loads issue sooner
+    const int keep = -(int)(p < G2);
+    sq[i] = __builtin_amdgcn_raw_buffer_load_b32(srs, (n * ldq * 2 + p * 4) & keep, 0, 0);
+    zq[i] = __builtin_amdgcn_raw_buffer_load_b16(zrs, (n * ldq + p * 2) & keep, 0, 0);
   }
 
   // Weight loads of this wave.
