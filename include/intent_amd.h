@@ -17,6 +17,12 @@
  * The library never allocates user-visible memory: outputs and workspaces
  * belong to the caller. No entry synchronises the stream.
  *
+ * Empty extents: M = 0 or N = 0 is a no-op. An empty K (K = 0, no groups or
+ * blocks) is a contraction that sums nothing (doc/dsl/core.en.md:213): the
+ * entry writes its epilogue of a zero accumulator to the whole output (zeros,
+ * the bias, quantized_gemm's epilogue, the in-place output plus zero) and
+ * reads no operand along K, whose pointers may then be null.
+ *
  * Quantized formats (row-major, K contiguous):
  *   W4 asymmetric group quant: packed uint8 [N, K/2]; byte j of row n holds
  *       k = 2j in its low nibble and k = 2j+1 in its high nibble; scales f16

@@ -266,6 +266,18 @@ __global__ void fill_u8_kernel(uint8_t* __restrict__ z, int rows, int cols, int6
 // the kQuantI8 instances, and kGemmBf16: c = bf16(acc) with bf16 operands.
 enum class DenseEpi { kQuantI8, kGemmBf16 };
 
+// quantized_gemm's epilogue of one element (gemm.py:83-106): relu(acc + bias)
+// plus the residual, divided by the output scale, clamped to [-128, 127] and
+// truncated to int8; each step rounds to f32 (NaN clamps to -128).
+INTENT_DEVICE uint32_t quant_i8_epilogue(float acc, float bias, f16 res, float scale) {
+  float v = __fadd_rn(acc, bias);
+  v = v < 0.f ? 0.f : v;
+  v = __fadd_rn(v, (float)res);
+  v = __fdiv_rn(v, scale);
+  v = fminf(fmaxf(v, -128.f), 127.f);
+  return (uint32_t)(int32_t)v & 255u;
+}
+
 // Epilogues of the dense f16 / bf16 GEMMs (lane holds m = row(i), n = col(j, g) + 0..3).
 template <class T, DenseEpi E>
 INTENT_DEVICE void dense_epilogue(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N,
@@ -355,12 +367,7 @@ INTENT_DEVICE void dense_epilogue(const f32x16 (&acc)[T::TI][T::TJ], int m0, int
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const f16 res = bit_cast<f16>((uint16_t)(rv[g][c >> 1] >> (16 * (c & 1))));
-          float v = __fadd_rn(acc[i][j][4 * g + c], bv[g][c]);
-          v = v < 0.f ? 0.f : v;
-          v = __fadd_rn(v, (float)res);
-          v = __fdiv_rn(v, sv[g][c]);
-          v = fminf(fmaxf(v, -128.f), 127.f);
-          packed |= ((uint32_t)(int32_t)v & 255u) << (8 * c);
+          packed |= quant_i8_epilogue(acc[i][j][4 * g + c], bv[g][c], res, sv[g][c]) << (8 * c);
         }
         if (vec && n + 3 < N) {
           *reinterpret_cast<uint32_t*>(o) = packed;
@@ -621,6 +628,59 @@ int w4a16_gemm_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
 
 }  // namespace intent
 
+namespace {
+
+// quantized_gemm over an empty K: every element is the epilogue of a zero sum.
+__global__ __launch_bounds__(256) void quantized_empty_k_kernel(const float* __restrict__ bias,
+                                                                const f16* __restrict__ residual, int64_t ldr,
+                                                                const float* __restrict__ oscale,
+                                                                int8_t* __restrict__ out, int64_t ldo, int64_t M,
+                                                                int64_t N) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  for (int64_t m = blockIdx.y; m < M; m += gridDim.y)
+    out[m * ldo + n] = (int8_t)quant_i8_epilogue(0.f, bias[n], residual[m * ldr + n], oscale[n]);
+}
+
+// Grouped GEMMs over an empty K: zeros in the rows the groups cover (output
+// row idx, or routes[idx] for routed rows, for offsets[g] <= idx < offsets[g + 1]).
+__global__ __launch_bounds__(256) void grouped_empty_k_kernel(const int32_t* __restrict__ offsets, int64_t G,
+                                                              const int32_t* __restrict__ routes, int64_t rows,
+                                                              uint16_t* __restrict__ out, int64_t ldo, int64_t N) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  for (int64_t g = blockIdx.y; g < G; g += gridDim.y) {
+    const int64_t lo = offsets[g] > 0 ? offsets[g] : 0;
+    const int64_t hi = offsets[g + 1] < rows ? offsets[g + 1] : rows;
+    for (int64_t idx = lo; idx < hi; ++idx) out[(routes ? (int64_t)routes[idx] : idx) * ldo + n] = 0;
+  }
+}
+
+int quantized_empty_k(const float* bias, const void* residual, int64_t residual_ld, const float* oscale, int8_t* out,
+                      int64_t out_ld, int64_t M, int64_t N, void* stream) {
+  INTENT_REQUIRE(bias && residual && oscale && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(residual_ld >= N && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  const dim3 grid((unsigned)((N + 255) / 256), (unsigned)(M < 65535 ? M : 65535));
+  hipLaunchKernelGGL(quantized_empty_k_kernel, grid, dim3(256), 0, (hipStream_t)stream, bias, (const f16*)residual,
+                     residual_ld, oscale, out, out_ld, M, N);
+  return intent::launch_status("quantized_empty_k_kernel");
+}
+
+}  // namespace
+
+namespace intent {
+
+int grouped_empty_k(const int32_t* offsets, int64_t G, const int32_t* routes, int64_t rows, void* out, int64_t out_ld,
+                    int64_t N, void* stream) {
+  INTENT_REQUIRE(offsets && out && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT, "null pointer or short output stride");
+  const dim3 grid((unsigned)((N + 255) / 256), (unsigned)(G < 4096 ? G : 4096));
+  hipLaunchKernelGGL(grouped_empty_k_kernel, grid, dim3(256), 0, (hipStream_t)stream, offsets, G, routes, rows,
+                     (uint16_t*)out, out_ld, N);
+  return launch_status("grouped_empty_k_kernel");
+}
+
+}  // namespace intent
+
 extern "C" int intent_w4a16_matmul(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t* packed, int64_t N,
                                    int64_t packed_ld, const void* scales, const uint8_t* zeros, int64_t qparam_ld,
                                    int64_t group_size, void* y, int64_t y_ld, void* stream) {
@@ -665,9 +725,10 @@ extern "C" int intent_w8a16_matmul(const void* x, int64_t M, int64_t K, int64_t 
   INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0, INTENT_ERR_INVALID_ARGUMENT, "negative extent");
   INTENT_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "extent exceeds int32");
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(x && w && scales && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(scales && y && (K == 0 || (x && w)), INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(x_ld >= K && w_ld >= K && y_ld >= N, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
-  // the tiled kernels take whole 64-k stages of 16-byte aligned rows; other shapes run the generic kernel
+  // the tiled kernels take whole 64-k stages of 16-byte aligned rows; other shapes (and an empty K,
+  // y = f16(0 * scale)) run the generic kernel
   if (K == 0 || K % 64 != 0 || !intent::aligned16(x) || !intent::aligned16(w) || x_ld % 8 != 0 || w_ld % 16 != 0)
     return intent::w8a16_generic_launch(x, M, K, x_ld, w, N, w_ld, scales, y, y_ld, stream);
   if (M <= 16) return intent::w8a16_gemv_launch(x, M, K, x_ld, w, N, w_ld, scales, y, y_ld, stream);
@@ -685,7 +746,7 @@ extern "C" int intent_fp4_bf16_matmul(const void* x, int64_t M, int64_t K, int64
                  INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "empty K");
+  if (K == 0) return intent::fill_launch(y, M, N, y_ld, 2, 0u, stream);  // bf16(0)
   INTENT_REQUIRE(x && packed && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(x_ld >= K && packed_ld >= K / 2 && y_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row");
@@ -762,6 +823,7 @@ extern "C" int intent_quantized_gemm(const void* a, int64_t M, int64_t K, int64_
                  INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
+  if (K == 0) return quantized_empty_k(bias, residual, residual_ld, output_scale, out, out_ld, M, N, stream);
   INTENT_REQUIRE(a && bt && bias && residual && output_scale && out, INTENT_ERR_INVALID_ARGUMENT,
                  "null pointer argument");
   INTENT_REQUIRE(a_ld >= K && bt_ld >= K && residual_ld >= N && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
@@ -805,7 +867,8 @@ extern "C" int intent_grouped_gemm(const void* x, int64_t rows, int64_t K, int64
                  INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
   if (rows == 0 || N == 0 || G == 0) return INTENT_OK;
-  INTENT_REQUIRE(K > 0 && (!routes || top_k >= 1), INTENT_ERR_INVALID_ARGUMENT, "bad K or top_k");
+  INTENT_REQUIRE(!routes || top_k >= 1, INTENT_ERR_INVALID_ARGUMENT, "bad top_k");
+  if (K == 0) return intent::grouped_empty_k(offsets, G, routes, rows, out, out_ld, N, stream);
   INTENT_REQUIRE(x && offsets && w && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(x_ld >= K && w_ld >= K && out_ld >= N && w_group_stride >= N * w_ld, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row");
@@ -850,6 +913,7 @@ extern "C" int intent_f16_gemm(const void* a, int64_t M, int64_t K, int64_t a_ld
                  "epilogue must be 0 (f16), 1 (f16 relu) or 2 (bf16)");
   INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 64, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
+  if (K == 0) return intent::fill_launch(c, M, N, c_ld, 2, 0u, stream);  // f16 / bf16 zero (relu(0) = 0)
   INTENT_REQUIRE(a && bt && c, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(a_ld >= K && bt_ld >= K && c_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row");
@@ -881,7 +945,7 @@ int gemm_kn_check(const void* a, int64_t M, int64_t K, int64_t a_ld, const void*
   INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "%s: K must be a multiple of 64, got %lld", what, (long long)K);
   INTENT_REQUIRE(N % 8 == 0, INTENT_ERR_UNSUPPORTED, "%s: N must be a multiple of 8 for the [K, N] operand, got %lld",
                  what, (long long)N);
-  if (M == 0 || N == 0) return INTENT_OK;
+  if (M == 0 || N == 0 || K == 0) return INTENT_OK;  // an empty K reads no operand
   INTENT_REQUIRE(a && b, INTENT_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
   INTENT_REQUIRE(a_ld >= K && b_ld >= N && c_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "%s: leading stride smaller than the row", what);
@@ -905,6 +969,7 @@ extern "C" int intent_quantized_gemm_kn(const void* a, int64_t M, int64_t K, int
   intent::clear_error();
   int st = gemm_kn_check(a, M, K, a_ld, b, N, b_ld, out_ld, "quantized_gemm_kn");
   if (st != INTENT_OK || M == 0 || N == 0) return st;
+  if (K == 0) return quantized_empty_k(bias, residual, residual_ld, output_scale, out, out_ld, M, N, stream);
   INTENT_REQUIRE(bias && residual && output_scale && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(residual_ld >= N, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
   using T = KNTile;
@@ -924,6 +989,7 @@ extern "C" int intent_f16_gemm_kn(const void* a, int64_t M, int64_t K, int64_t a
                  "epilogue must be 0 (f16), 1 (f16 relu) or 2 (bf16)");
   int st = gemm_kn_check(a, M, K, a_ld, b, N, b_ld, c_ld, "f16_gemm_kn");
   if (st != INTENT_OK || M == 0 || N == 0) return st;
+  if (K == 0) return intent::fill_launch(c, M, N, c_ld, 2, 0u, stream);  // f16 / bf16 zero (relu(0) = 0)
   INTENT_REQUIRE(c, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   using T = KNTile;
   const int mblocks = (int)((M + T::BM - 1) / T::BM);

@@ -9,8 +9,12 @@
 // these kernels; they keep the operator surface as wide as the reference's
 // (examples/kernels/contraction/weight_only_int4.py:18-51, gemm.py:29-39,
 // the W8 kernels of runtime/cpu_runtime.py), whose DSL kernels take any shape.
+// fill_launch writes a constant: the epilogue of an empty K, where a
+// contraction sums nothing (doc/dsl/core.en.md:213).
 #include "common.h"
 #include "internal.h"
+
+#include <type_traits>
 
 namespace {
 
@@ -84,6 +88,16 @@ __global__ __launch_bounds__(kThreads) void i8_generic_kernel(const int8_t* __re
 
 dim3 grid_for(int64_t M, int64_t N) { return dim3((unsigned)((N + kThreads - 1) / kThreads), (unsigned)M); }
 
+// out[r * ld + c] = bits for r < rows, c < cols; elements of EB bytes.
+template <int EB>
+__global__ __launch_bounds__(kThreads) void fill_kernel(void* __restrict__ out, int64_t rows, int64_t cols,
+                                                        int64_t ld, uint32_t bits) {
+  using E = std::conditional_t<EB == 1, uint8_t, std::conditional_t<EB == 2, uint16_t, uint32_t>>;
+  const int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (c >= cols) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) reinterpret_cast<E*>(out)[r * ld + c] = (E)bits;
+}
+
 }  // namespace
 
 namespace intent {
@@ -106,6 +120,21 @@ int w8a16_generic_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, cons
   hipLaunchKernelGGL(w8a16_generic_kernel, grid_for(M, N), dim3(kThreads), 0, (hipStream_t)stream, (const f16*)x,
                      x_ld, w, w_ld, (const f16*)scales, (int)K, (int)N, (f16*)y, y_ld);
   return launch_status("w8a16_generic_kernel");
+}
+
+int fill_launch(void* out, int64_t rows, int64_t cols, int64_t ld, int elem_bytes, uint32_t bits, void* stream) {
+  if (rows == 0 || cols == 0) return INTENT_OK;
+  INTENT_REQUIRE(out, INTENT_ERR_INVALID_ARGUMENT, "null output");
+  INTENT_REQUIRE(ld >= cols, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
+  INTENT_REQUIRE((cols + kThreads - 1) / kThreads < (1ll << 31), INTENT_ERR_UNSUPPORTED, "fill: row too long");
+  const dim3 grid((unsigned)((cols + kThreads - 1) / kThreads), (unsigned)(rows < 65535 ? rows : 65535));
+  if (elem_bytes == 1)
+    hipLaunchKernelGGL(fill_kernel<1>, grid, dim3(kThreads), 0, (hipStream_t)stream, out, rows, cols, ld, bits);
+  else if (elem_bytes == 2)
+    hipLaunchKernelGGL(fill_kernel<2>, grid, dim3(kThreads), 0, (hipStream_t)stream, out, rows, cols, ld, bits);
+  else
+    hipLaunchKernelGGL(fill_kernel<4>, grid, dim3(kThreads), 0, (hipStream_t)stream, out, rows, cols, ld, bits);
+  return launch_status("fill_kernel");
 }
 
 int i8_generic_launch(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const int8_t* w, int64_t N, int64_t w_ld,

@@ -4,6 +4,12 @@
 
 using namespace gkn;
 
+namespace intent {
+// zeros in the rows the groups cover (dense_gemm.hip)
+int grouped_empty_k(const int32_t* offsets, int64_t G, const int32_t* routes, int64_t rows, void* out, int64_t out_ld,
+                    int64_t N, void* stream);
+}  // namespace intent
+
 extern "C" int intent_grouped_gemm_kn(const void* x, int64_t rows, int64_t K, int64_t x_ld, const int32_t* offsets,
                                       int64_t G, const void* w, int64_t N, int64_t w_ld, int64_t w_group_stride,
                                       int bf16, void* out, int64_t out_ld, void* stream) {
@@ -12,6 +18,7 @@ extern "C" int intent_grouped_gemm_kn(const void* x, int64_t rows, int64_t K, in
                      G <= (1 << 20),
                  INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   if (rows == 0 || N == 0 || G == 0) return INTENT_OK;
+  if (K == 0) return intent::grouped_empty_k(offsets, G, nullptr, rows, out, out_ld, N, stream);
   int st = kn_shape_check(K, N, w_ld, w, "grouped_gemm_kn");
   if (st != INTENT_OK) return st;
   INTENT_REQUIRE(x && offsets && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");

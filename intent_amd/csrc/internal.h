@@ -30,6 +30,11 @@ int launch_status(const char* kernel);
 // Same, with a printf-formatted kernel name (template parameters).
 int launch_status_fmt(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 
+// Writes `bits` (the low elem_bytes = 1, 2 or 4 bytes) to every element of a
+// rows x cols matrix with a leading stride of ld elements: the output of a
+// contraction over an empty K, which is its epilogue applied to zero.
+int fill_launch(void* out, int64_t rows, int64_t cols, int64_t ld, int elem_bytes, uint32_t bits, void* stream);
+
 }  // namespace intent
 
 #define INTENT_REQUIRE(cond, code, ...)            \

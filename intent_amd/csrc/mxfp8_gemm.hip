@@ -448,6 +448,28 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
 // stays in registers: read once (kAccum) and written once.
 using TSk = mp::Tile<256, 128, 2, 2>;  // four waves of 128 x 64
 
+// The same output for an empty K: p = f16((0 * lhs_scale) * rhs_scale) (zero,
+// or NaN for a non-finite scale); splits == 0 stores p, else out = f16(out + p)
+// once per split.
+__global__ __launch_bounds__(256) void fp8_scaled_empty_k_kernel(f16* __restrict__ out, int64_t rows, int64_t cols,
+                                                                 int64_t ldo, float lhs_scale, float rhs_scale,
+                                                                 int splits) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  const float acc = 0.f;
+  const f16 p = (f16)((acc * lhs_scale) * rhs_scale);
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    f16* o = out + r * ldo + c;
+    if (splits == 0) {
+      *o = p;
+    } else {
+      f16 v = *o;
+      for (int s = 0; s < splits; ++s) v = v + p;
+      *o = v;
+    }
+  }
+}
+
 template <bool kAccum>
 __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
                                                                  const uint8_t* __restrict__ bt, int64_t ldb, int N,
@@ -715,6 +737,7 @@ extern "C" int intent_mxfp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t
                  INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 128, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
+  if (K == 0) return intent::fill_launch(out, M, N, out_ld, 4, 0u, stream);  // no scale blocks: 0.0f
   INTENT_REQUIRE(a && b && a_scales && b_scales && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(a_ld >= K && b_ld >= K && a_scales_ld >= K / 32 && b_scales_ld >= K / 32 && out_ld >= N,
                  INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
@@ -767,7 +790,13 @@ extern "C" int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, in
   else
     INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 128, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "empty K");
+  if (K == 0) {  // every split sums nothing: p = f16((0 * lhs_scale) * rhs_scale)
+    INTENT_REQUIRE(out && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT, "null output or short output stride");
+    const dim3 grid((unsigned)((N + 255) / 256), (unsigned)(M < 65535 ? M : 65535));
+    hipLaunchKernelGGL(fp8_scaled_empty_k_kernel, grid, dim3(256), 0, (hipStream_t)stream, (f16*)out, M, N, out_ld,
+                       a_scale, b_scale, accumulate ? (int)splits : 0);
+    return intent::launch_status("fp8_scaled_empty_k_kernel");
+  }
   INTENT_REQUIRE(a && bt && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(a_ld >= K && bt_ld >= K && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row");
@@ -797,7 +826,7 @@ extern "C" int intent_deepgemm_fp8(const uint8_t* a, int64_t M, int64_t K, int64
                  INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 128, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "empty K");
+  if (K == 0) return intent::fill_launch(out, M, N, out_ld, 2, 0u, stream);  // no K blocks: bf16(0)
   INTENT_REQUIRE(a && b && a_scales && b_scales && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(a_ld >= K && b_ld >= K && a_scales_ld >= K / 128 && b_scales_ld >= K / 128 && out_ld >= N,
                  INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
@@ -824,7 +853,7 @@ extern "C" int intent_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a
   INTENT_REQUIRE(format == 0 || format == 1, INTENT_ERR_INVALID_ARGUMENT, "format must be 0 (E4M3FN) or 1 (E5M2)");
   INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 128, got %lld", (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "empty K");
+  if (K == 0) return intent::fill_launch(out, M, N, out_ld, 1, 0u, stream);  // the FP8 code of +0
   INTENT_REQUIRE(a && bt && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(a_ld >= K && bt_ld >= K && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row");

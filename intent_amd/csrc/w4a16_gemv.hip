@@ -807,7 +807,9 @@ int w4a16_check(const void* x, int64_t M, int64_t K, int64_t x_ld, const uint8_t
   INTENT_REQUIRE(K % 2 == 0 && K % gs == 0, INTENT_ERR_INVALID_ARGUMENT,
                  "K must be even and a multiple of group_size (K=%lld group=%lld)", (long long)K, (long long)gs);
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(x && packed && scales && zeros && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  // an empty K reads no operand (y = 0, on the generic kernel): they may be null
+  INTENT_REQUIRE(y && (K == 0 || (x && packed && scales && zeros)), INTENT_ERR_INVALID_ARGUMENT,
+                 "null pointer argument");
   INTENT_REQUIRE(x_ld >= K && packed_ld >= K / 2 && qparam_ld >= K / gs && y_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row (x_ld=%lld packed_ld=%lld qparam_ld=%lld y_ld=%lld)",
                  (long long)x_ld, (long long)packed_ld, (long long)qparam_ld, (long long)y_ld);

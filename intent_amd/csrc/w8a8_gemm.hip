@@ -190,7 +190,8 @@ int check_i8(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const int8_t* 
   INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0, INTENT_ERR_INVALID_ARGUMENT, "negative extent");
   INTENT_REQUIRE(M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX, INTENT_ERR_UNSUPPORTED, "extent exceeds int32");
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(a && w && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  // an empty K reads no operand (the generic kernel applies the epilogue to zero)
+  INTENT_REQUIRE(out && (K == 0 || (a && w)), INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(a_ld >= K && w_ld >= K && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row");
   return INTENT_OK;
@@ -282,9 +283,12 @@ int lowbit_entry(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint
   INTENT_REQUIRE(K % 128 == 0, INTENT_ERR_UNSUPPORTED, "%s: K must be a multiple of 128, got %lld", name,
                  (long long)K);
   if (M == 0 || N == 0) return INTENT_OK;
-  INTENT_REQUIRE(a && w && out, INTENT_ERR_INVALID_ARGUMENT, "%s: null pointer argument", name);
+  INTENT_REQUIRE(out, INTENT_ERR_INVALID_ARGUMENT, "%s: null output", name);
   INTENT_REQUIRE(a_ld >= K && w_ld >= K / per_byte && out_ld >= (kBitNet ? N : M), INTENT_ERR_INVALID_ARGUMENT,
                  "%s: leading stride smaller than the row", name);
+  // empty K: int32 zeros ([N, M] for W4A8, [M, N] for BitNet)
+  if (K == 0) return intent::fill_launch(out, kBitNet ? M : N, kBitNet ? N : M, out_ld, 4, 0u, stream);
+  INTENT_REQUIRE(a && w, INTENT_ERR_INVALID_ARGUMENT, "%s: null pointer argument", name);
   INTENT_REQUIRE(intent::aligned16(a) && a_ld % 16 == 0 && (reinterpret_cast<uintptr_t>(w) % align) == 0 &&
                      w_ld % align == 0,
                  INTENT_ERR_ALIGNMENT, "%s: activations 16-byte aligned rows, packed weights %d-byte aligned rows",

@@ -108,9 +108,12 @@ def _ld(t) -> int:
 def _w4_check(env: dict) -> None:
     if env["P"] * 2 != env["K"]:
         raise ValueError(f"packed_weight.shape[1] ({env['P']}) must be K/2 ({env['K']}/2)")
-    if env["G"] <= 0 or env["K"] % env["G"]:
+    if env["K"] == 0 and env["G"] == 0:  # empty K: no groups, y = 0
+        env["GROUP"] = 128
+    elif env["G"] <= 0 or env["K"] % env["G"]:
         raise ValueError(f"K ({env['K']}) must be a multiple of the number of groups ({env['G']})")
-    env["GROUP"] = env["K"] // env["G"]
+    else:
+        env["GROUP"] = env["K"] // env["G"]
     if env["KERNEL"] not in ("auto", "gemv", "gemm"):
         raise ValueError("KERNEL must be 'auto', 'gemv' or 'gemm'")
 

@@ -1030,3 +1030,143 @@ def test_nvfp4_rejects_wider_scale_blocks(gpu):
     scales = torch.zeros(2, 3, 32, 4, 4, dtype=torch.uint8, device="cuda")   # NT 3 where N needs 2
     with pytest.raises(ValueError):
         art(intent.nvfp4_quantize).run(x, torch.tensor([1.0], device="cuda"), packed, scales)
+
+
+# ---- empty K -------------------------------------------------------------------------
+# A contraction over an empty K is zero-initialised and sums nothing
+# (doc/dsl/core.en.md:213, Contractions.cpp:12-41): every entry writes
+# epilogue(0) to its whole output - zeros, the bias, the in-place output
+# unchanged, or quantized_gemm's epilogue of a zero accumulator. Outputs are
+# given as buffers filled with a non-zero pattern so a skipped write shows.
+
+def _filled(shape, dtype, value=7):
+    return torch.full(shape, value, dtype=torch.int8 if dtype == torch.int8 else dtype, device="cuda") \
+        if dtype not in (torch.float8_e4m3fn, torch.float8_e5m2) else \
+        torch.full(shape, 0x38, dtype=torch.uint8, device="cuda").view(dtype)
+
+
+def _empty(shape, dtype):
+    return torch.empty(shape, dtype=dtype, device="cuda")
+
+
+M0, N0 = 37, 70
+
+
+def _k0_cases():
+    f16, bf16, i8, u8, i32, f32 = torch.float16, torch.bfloat16, torch.int8, torch.uint8, torch.int32, torch.float32
+    f8 = torch.float8_e4m3fn
+    bias = torch.arange(N0, dtype=i32, device="cuda") - 20
+    zeros = lambda shape, dt: torch.zeros(shape, dtype=dt, device="cuda")  # noqa: E731
+    cases = {
+        "w4a16_gemv": (intent.weight_only_int4_asym_matmul, {"KERNEL": "gemv"},
+                       (_empty((4, 0), f16), _empty((N0, 0), u8), _empty((N0, 0), f16), _empty((N0, 0), u8)),
+                       (_filled((4, N0), f16),), zeros((4, N0), f16)),
+        "w4a16_gemm": (intent.weight_only_int4_asym_matmul, {"KERNEL": "gemm"},
+                       (_empty((M0, 0), f16), _empty((N0, 0), u8), _empty((N0, 0), f16), _empty((N0, 0), u8)),
+                       (_filled((M0, N0), f16),), zeros((M0, N0), f16)),
+        "w8a16": (intent.weight_only_int8_matmul, {},
+                  (_empty((M0, 0), f16), _empty((N0, 0), i8), torch.ones(N0, dtype=f16, device="cuda")),
+                  (_filled((M0, N0), f16),), zeros((M0, N0), f16)),
+        "w8a8": (intent.w8a8_scaled_matmul, {},
+                 (_empty((M0, 0), i8), torch.ones(M0, dtype=f32, device="cuda"), _empty((N0, 0), i8),
+                  torch.ones(N0, dtype=f32, device="cuda")),
+                 (_filled((M0, N0), bf16),), zeros((M0, N0), bf16)),
+        "gemm_i8_nt": (intent.gemm_i8_nt, {}, (_empty((M0, 0), i8), _empty((N0, 0), i8), bias),
+                       (_filled((M0, N0), i32),), bias[None, :].expand(M0, N0)),
+        "gemm_i8": (intent.gemm_i8, {}, (_empty((M0, 0), i8), _empty((0, N0), i8), bias),
+                    (_filled((M0, N0), i32),), bias[None, :].expand(M0, N0)),
+        "w4a8": (intent.w4a8_packed_matmul, {}, (_empty((M0, 0), i8), _empty((N0, 0), u8)),
+                 (_filled((N0, M0), i32),), zeros((N0, M0), i32)),
+        "bitnet": (intent.bitnet_int2_matmul, {}, (_empty((M0, 0), i8), _empty((N0, 0), u8)),
+                   (_filled((M0, N0), i32),), zeros((M0, N0), i32)),
+        "block_scaled": (intent.block_scaled_matmul, {},
+                         (_empty((M0, 0, 32), f8), _empty((M0, 0), u8), _empty((0, 32, N0), f8), _empty((0, N0), u8)),
+                         (_filled((M0, N0), f32),), zeros((M0, N0), f32)),
+        "scaled_fp8": (intent.scaled_fp8_matmul, {}, (_empty((M0, 0), f8), _empty((0, N0), f8), 0.5, 2.0),
+                       (_filled((M0, N0), f16),), zeros((M0, N0), f16)),
+        "deepgemm_fp8": (intent.deepgemm_fp8_2xacc, {},
+                         (_empty((M0, 0, 128), f8), _empty((N0, 0, 128), f8), _empty((M0, 0), f32),
+                          _empty(((N0 + 127) // 128, 0), f32)),
+                         (_filled((M0, N0), bf16),), zeros((M0, N0), bf16)),
+        "fp8_e4m3": (intent.fp8_e4m3_matmul, {}, (_empty((M0, 0), f8), _empty((N0, 0), f8)),
+                     (_filled((M0, N0), f8),), zeros((M0, N0), f8)),
+        "fp4_bf16": (intent.dequant_bf16_fp4_matmul, {}, (_empty((M0, 0), bf16), _empty((N0, 0), u8)),
+                     (_filled((M0, N0), bf16),), zeros((M0, N0), bf16)),
+        "w4_sym": (intent.weight_only_int4_matmul, {}, (_empty((M0, 0), f16), _empty((0, N0), i32),
+                                                        _empty((0, N0), f16)),
+                   (_filled((M0, N0), f16),), zeros((M0, N0), f16)),
+        "gemm": (intent.gemm, {}, (_empty((M0, 0), f16), _empty((0, N0), f16)), (_filled((M0, N0), f16),),
+                 zeros((M0, N0), f16)),
+        "bf16_gemm": (intent.bf16_gemm, {}, (_empty((M0, 0), bf16), _empty((0, N0), bf16)),
+                      (_filled((M0, N0), bf16),), zeros((M0, N0), bf16)),
+        "ragged_grouped": (intent.ragged_grouped_gemm, {},
+                           (_empty((M0, 0), f16), torch.tensor([0, 10, 10, M0], dtype=i32, device="cuda"),
+                            _empty((3, 0, N0), f16)),
+                           (_filled((M0, N0), f16),), zeros((M0, N0), f16)),
+    }
+    return cases
+
+
+@pytest.mark.parametrize("name", ["w4a16_gemv", "w4a16_gemm", "w8a16", "w8a8", "gemm_i8_nt", "gemm_i8", "w4a8",
+                                  "bitnet", "block_scaled", "scaled_fp8", "deepgemm_fp8", "fp8_e4m3", "fp4_bf16",
+                                  "w4_sym", "gemm", "bf16_gemm", "ragged_grouped"])
+def test_empty_k(gpu, name):
+    defn, cx, ins, outs, expected = _k0_cases()[name]
+    art(defn, **cx).prepare(*ins, outputs=outs).launch()
+    got = outs[0]
+    torch.cuda.synchronize()
+    if got.dtype in (torch.float8_e4m3fn, torch.float8_e5m2):
+        assert torch.equal(got.view(torch.uint8), expected.view(torch.uint8)), name
+    else:
+        assert torch.equal(got, expected), name
+
+
+def test_empty_k_quantized_gemm(gpu, threads):
+    # epilogue(0) = trunc(clamp((relu(0 + bias) + residual) / scale)), not zero
+    M, N = 9, 40
+    g = torch.Generator().manual_seed(3)
+    bias = torch.randn((N,), generator=g) * 4
+    residual = (torch.randn((M, N), generator=g) * 4).half()
+    scale = torch.linspace(1.0 / 48.0, 1.0 / 24.0, N)
+    a, b = np.zeros((M, 0), np.float16), np.zeros((0, N), np.float16)
+    out = torch.full((M, N), 99, dtype=torch.int8, device="cuda")
+    art(intent.quantized_gemm).prepare(dev(a), dev(b), bias.cuda(), residual.cuda(), scale.cuda(),
+                                       outputs=(out,)).launch()
+    ref = oracle.quantized_gemm(a, b, bias.numpy(), residual.numpy(), scale.numpy(), threads)
+    assert np.array_equal(host(out), ref)
+
+
+def test_empty_k_more(gpu):
+    # split-K FP8 with no iterations: out = f16(out + p) per split with p = +0, so the
+    # output is unchanged except that -0 becomes +0
+    M, N, SP = 6, 40, 3
+    out0 = (torch.randn(M, N, generator=torch.Generator().manual_seed(1)) * 8).half()
+    out0[0, 0] = -0.0
+    out = out0.cuda()
+    f8 = torch.float8_e4m3fn
+    art(intent.scaled_fp8_splitk_matmul).run(_empty((M, 0, SP, 256), f8), _empty((0, SP, 256, N), f8), out, 0.5, 2.0)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu().view(torch.int16), (out0 + 0.0).view(torch.int16))
+    # a non-finite scale makes p = f16(0 * inf) = NaN, which the sum carries
+    out = out0.cuda()
+    art(intent.scaled_fp8_splitk_matmul).run(_empty((M, 0, SP, 256), f8), _empty((0, SP, 256, N), f8), out,
+                                             float("inf"), 2.0)
+    assert torch.isnan(out).all()
+    # routed bf16 projection over K = 0: every routed row is zero
+    T, TOP_K, E, Nr = 20, 2, 3, 24
+    experts = torch.arange(T * TOP_K) % E
+    member = torch.sort(experts, stable=True).indices.int().cuda()
+    offs = torch.zeros(E + 1, dtype=torch.int32)
+    offs[1:] = torch.cumsum(torch.bincount(experts, minlength=E), 0).int()
+    y = torch.full((T, TOP_K, Nr), 3.0, dtype=torch.bfloat16, device="cuda")
+    art(intent.routed_expert_projection_bf16).prepare(_empty((T, 0), torch.bfloat16), offs.cuda(), member,
+                                                      _empty((E, Nr, 0), torch.bfloat16), outputs=(y,)).launch()
+    torch.cuda.synchronize()
+    assert torch.equal(y, torch.zeros_like(y))
+    # Q4_K x Q8_K over zero blocks: +0 per row
+    w = _empty((9, 0, 144), torch.uint8)
+    q = _empty((0, 292), torch.uint8)
+    r = torch.full((9,), 5.0, device="cuda")
+    art(intent.q4_k_q8_k_dot).prepare(w, q, outputs=(r,)).launch()
+    torch.cuda.synchronize()
+    assert torch.equal(r, torch.zeros_like(r))
