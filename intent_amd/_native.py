@@ -8,13 +8,16 @@ There is no fallback: if the library is missing every call raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 from .errors import INTENT_OK, NativeLibraryError, status_error
 
 PACKAGE = Path(__file__).resolve().parent
-LIBRARY_PATH = PACKAGE / "_lib" / "libintent_amd.so"
+# INTENT_AMD_LIBRARY names another build of the same library (the host-side
+# AddressSanitizer build the sanitizer test loads); the in-tree build otherwise.
+LIBRARY_PATH = Path(os.environ.get("INTENT_AMD_LIBRARY") or PACKAGE / "_lib" / "libintent_amd.so")
 ABI_VERSION = 1
 
 P = ctypes.c_void_p

@@ -78,6 +78,34 @@ def build(verbose: bool = False) -> Path:
     return LIBRARY
 
 
+def build_host_sanitized(out_dir: Path) -> Path:
+    """The library with its host code (argument checks, dispatch, launch set-up)
+    compiled with AddressSanitizer, into out_dir/libintent_amd.so; the device
+    code is built as usual (-Xarch_host keeps the sanitizer off the gfx950
+    pass). Loaded under the sanitizer runtime through INTENT_AMD_LIBRARY."""
+    out_dir = Path(out_dir)
+    out_dir.mkdir(parents=True, exist_ok=True)
+    flags = [f for f in HIPCC_FLAGS if f not in ("-O3", "-Wall")] + [
+        "-O1", "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
+
+    def one(source: Path) -> Path:
+        obj = out_dir / (source.stem + ".o")
+        proc = subprocess.run([hipcc(), *flags, "-c", str(source), "-o", str(obj)], capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc (host ASan) failed for {source.name}:\n{proc.stderr}")
+        return obj
+
+    sources = sorted(CSRC.glob("*.hip"))
+    with ThreadPoolExecutor(max_workers=min(len(sources), os.cpu_count() or 1)) as pool:
+        objects = list(pool.map(one, sources))
+    lib = out_dir / "libintent_amd.so"
+    proc = subprocess.run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-fsanitize=address", "-o", str(lib),
+                           *map(str, objects)], capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link (host ASan) failed:\n{proc.stderr}")
+    return lib
+
+
 if __name__ == "__main__":
     build(verbose=True)
     sys.exit(0)

@@ -21,13 +21,16 @@ Parity status of every function is pinned by tests in ``tests/test_oracle.py``:
 from __future__ import annotations
 
 import ctypes
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIBRARY = HERE / "liboracle.so"
+# ORACLE_LIBRARY names another build of oracle.c (the sanitizer test's
+# AddressSanitizer / UBSan build); the in-tree liboracle.so otherwise.
+LIBRARY = Path(os.environ.get("ORACLE_LIBRARY") or HERE / "liboracle.so")
 
 _lib = None
 
