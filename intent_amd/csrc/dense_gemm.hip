@@ -42,6 +42,16 @@ struct WeightOp<T, W4Args> {
     op.init(w.q, w.ldq, w.s, w.z, w.ldp, w.gs, ClampRows{n0, N});
   }
 };
+// W4 with windowed group parameters (W4Operand kWin): group sizes that are
+// multiples of 64, scale and zero rows in whole dwords.
+struct W4WinArgs : W4Args {};
+template <class T>
+struct WeightOp<T, W4WinArgs> {
+  using Op = mp::W4Operand<T::BN, T::NT, true>;
+  INTENT_DEVICE static void init(Op& op, const W4WinArgs& w, int n0, int N) {
+    op.init(w.q, w.ldq, w.s, w.z, w.ldp, w.gs, ClampRows{n0, N});
+  }
+};
 template <class T>
 struct WeightOp<T, W8Args> {
   using Op = mp::W8Operand<T::BN, T::NT>;
@@ -622,6 +632,9 @@ int w4a16_gemm_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
                      intent::fits_offset(256 + 1, x_ld * 2),
                  INTENT_ERR_UNSUPPORTED, "w4a16_gemm: operand too large for 31-bit buffer offsets");
   W4Args w{packed, packed_ld, (const f16*)scales, zeros, qparam_ld, (int)gs};
+  if (gs % 64 == 0 && qparam_ld % 4 == 0 && intent::aligned4(scales) && intent::aligned4(zeros) && M > 128)
+    return launch_dense<W4WinArgs, false>((const f16*)x, x_ld, (int)M, (int)N, (int)K, W4WinArgs{w}, (f16*)y, y_ld,
+                                          nullptr, (hipStream_t)stream, "w4a16_gemm");
   return launch_dense<W4Args, false>((const f16*)x, x_ld, (int)M, (int)N, (int)K, w, (f16*)y, y_ld, nullptr,
                                        (hipStream_t)stream, "w4a16_gemm");
 }

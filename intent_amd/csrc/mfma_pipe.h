@@ -314,20 +314,31 @@ struct DmaRowsOperand {
 // Asymmetric group-quantized 4-bit weight rows (packed two per byte, low nibble
 // = even k), decoded to f16 (q - z) * s. A stage is 64 k = 32 packed bytes per
 // row, read as P = 2 pieces of 16 bytes (32 k each) or 4 pieces of 8 bytes.
-template <int ROWS, int NT = NTHREADS>
+// kWin (group sizes that are multiples of 64, scale and zero rows in whole
+// dwords): the scale dword of groups 2d, 2d + 1 and the zero dword of groups
+// 4e .. 4e + 3 are loaded only by the stage that opens a pair of groups, and
+// the decode keeps them in registers (ps, pz) for the stages that follow; the
+// per-stage form loads a 2-byte scale and a 1-byte zero per piece and stage,
+// one cache line per row each time. params_at(kt) says whether stage kt's
+// load carries them (vm_ops = NS or 3 * NS instructions).
+template <int ROWS, int NT = NTHREADS, bool kWin = false>
 struct W4Operand {
+  static constexpr bool kWinParams = kWin;
   static constexpr int PIECE = (ROWS * 2) % NT == 0 ? 16 : (ROWS * 4) % NT == 0 ? 8 : 4;  // bytes per load
   static constexpr int P = 32 / PIECE;                                                     // pieces per row per stage
   static constexpr int NS = ROWS * P / NT;                                                 // loads per thread per stage
   static_assert(NS * NT == ROWS * P, "W4 staging must divide evenly");
-  static constexpr int NVM = 3 * NS;            // vector memory instructions per stage
+  static constexpr int NVM = 3 * NS;            // vector memory instructions per stage (at most)
+  static constexpr int NVM_W = NS;              // ... of a windowed stage without group parameters
   static constexpr int NDS = NS * (PIECE / 4);  // LDS writes per stage
   typedef uint32_t Piece __attribute__((ext_vector_type(PIECE / 4 > 1 ? PIECE / 4 : 2)));
 
   Rsrc rq, rs, rz;
   uint32_t qoff[NS], soff[NS], zoff[NS];
   int lrow[NS], part[NS];
-  int gs;  // 32 or a multiple of 64
+  int gs;   // 32 or a multiple of 64
+  int spg;  // kWin: stages per group (gs / 64)
+  mutable uint32_t ps[NS], pz[NS];  // kWin: the parameter dwords in use
 
   // Scales and zeros stay in 32-bit registers: packing two 16-bit loads
   // into one VGPR would force a wait right after they are issued.
@@ -345,6 +356,7 @@ struct W4Operand {
     rs = make_rsrc(s);
     rz = make_rsrc(z);
     gs = gsize;
+    spg = gsize / 64;
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int c = (int)(threadIdx.x % NT) + i * NT;
@@ -352,14 +364,16 @@ struct W4Operand {
       part[i] = c % P;
       const int64_t w = wrow(lrow[i]);
       // gs == 32: a stage spans two groups; piece p starts at k = p * PIECE * 2.
-      const int extra = gsize == 32 ? (part[i] * PIECE * 2) / 32 : 0;
+      const int extra = !kWin && gsize == 32 ? (part[i] * PIECE * 2) / 32 : 0;
       qoff[i] = (uint32_t)(w * ldq + part[i] * PIECE);
       soff[i] = (uint32_t)((w * ldp + extra) * 2);
       zoff[i] = (uint32_t)(w * ldp + extra);
     }
   }
+  INTENT_DEVICE bool params_at(int kt) const { return !kWin || kt % (2 * spg) == 0; }
   INTENT_DEVICE void load(int kt, Regs& r) const {
-    const uint32_t g = gs == 32 ? 2 * kt : (kt * 64) / gs;
+    const uint32_t g = kWin ? (uint32_t)(kt / spg) : gs == 32 ? 2 * kt : (kt * 64) / gs;
+    const bool with_params = params_at(kt);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       if constexpr (PIECE == 16)
@@ -368,17 +382,35 @@ struct W4Operand {
         r.w[i] = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff[i], (uint32_t)kt * 32, 0);
       else
         r.w[i][0] = __builtin_amdgcn_raw_buffer_load_b32(rq, qoff[i], (uint32_t)kt * 32, 0);
-      r.s[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, soff[i], g * 2, 0);
-      r.z[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rz, zoff[i], g, 0);
+      if constexpr (kWin) {
+        if (with_params) {
+          r.s[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, soff[i], (g & ~1u) * 2, 0);
+          r.z[i] = __builtin_amdgcn_raw_buffer_load_b32(rz, zoff[i], g & ~3u, 0);
+        }
+      } else {
+        r.s[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, soff[i], g * 2, 0);
+        r.z[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rz, zoff[i], g, 0);
+      }
     }
   }
-  // Decode into the B region of a stage buffer (kAsm: see lds_store16).
+  // Decode stage kt into the B region of a stage buffer (kAsm: see lds_store16).
   template <bool kAsm = false>
-  INTENT_DEVICE void store(const Regs& r, char* lds_b) const {
+  INTENT_DEVICE void store(const Regs& r, char* lds_b, int kt = 0) const {
+    const int g = kWin ? kt / spg : 0;
+    const bool fresh = params_at(kt);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const f16x2 zo = splat2((f16)(float)(1024 + r.z[i]));
-      const f16x2 sc = splat2(bit_cast<f16>((uint16_t)r.s[i]));
+      uint32_t zq = r.z[i], sq = r.s[i];
+      if constexpr (kWin) {
+        if (fresh) {
+          ps[i] = r.s[i];
+          pz[i] = r.z[i];
+        }
+        zq = (pz[i] >> ((g & 3) * 8)) & 0xFFu;
+        sq = (ps[i] >> ((g & 1) * 16)) & 0xFFFFu;
+      }
+      const f16x2 zo = splat2((f16)(float)(1024 + zq));
+      const f16x2 sc = splat2(bit_cast<f16>((uint16_t)sq));
       char* row = lds_b + lrow[i] * ROWB;
       const int sw = swz(lrow[i]);
 #pragma unroll
@@ -393,6 +425,13 @@ struct W4Operand {
     }
   }
 };
+
+// WinParams<B>::value: B loads its group parameters only at some stages
+// (W4Operand<..., true>); mainloop_ws then picks the wait count per step.
+template <class B, class = void>
+struct WinParams : std::false_type {};
+template <class B>
+struct WinParams<B, std::void_t<decltype(B::kWinParams)>> : std::bool_constant<B::kWinParams> {};
 
 // Per-channel int8 weight rows converted exactly to f16 (scale applied in the
 // epilogue). A stage is 64 k = 64 bytes per row, loaded as 16-byte pieces
@@ -851,7 +890,12 @@ INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, co
 #pragma unroll
     for (int s = 0; s < NB; ++s)
       if (s < nk) bop.load(s, rb[s]);
-    bop.template store<true>(rb[0], bufs[0] + T::A_BYTES);
+    constexpr bool kWinB = WinParams<BOp>::value;
+    static_assert(!kWinB || NB == 2, "windowed group parameters: two stage buffers");
+    if constexpr (kWinB)
+      bop.template store<true>(rb[0], bufs[0] + T::A_BYTES, 0);
+    else
+      bop.template store<true>(rb[0], bufs[0] + T::A_BYTES);
     wait_vm_lgkm_barrier<0>();
     // Step kt publishes stage kt+1. Its DMA was issued NB-2 steps earlier;
     // vmcnt counts in issue order, so the wait leaves exactly the operations
@@ -868,11 +912,22 @@ INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, co
       aop.issue(bufs[(j + NB - 1) % NB], kt + NB - 1 < nk ? kt + NB - 1 : nk - 1);
       __builtin_amdgcn_sched_barrier(0);
       bop.load(full ? kt + NB : nk - 1, rb[j]);
-      bop.template store<true>(rb[(j + 1) % NB], bufs[(j + 1) % NB] + T::A_BYTES);
-      if (full)
-        wait_vm_lgkm_barrier<kAfter>();
-      else
-        wait_vm_lgkm_barrier<0>();
+      if constexpr (kWinB) {
+        bop.template store<true>(rb[(j + 1) % NB], bufs[(j + 1) % NB] + T::A_BYTES, kt + 1);
+        // in flight: stage kt + 2's loads, with or without its group parameters
+        if (full && bop.params_at(kt + NB))
+          wait_vm_lgkm_barrier<kAfter>();
+        else if (full)
+          wait_vm_lgkm_barrier<kAfter - (BOp::NVM - BOp::NVM_W)>();
+        else
+          wait_vm_lgkm_barrier<0>();
+      } else {
+        bop.template store<true>(rb[(j + 1) % NB], bufs[(j + 1) % NB] + T::A_BYTES);
+        if (full)
+          wait_vm_lgkm_barrier<kAfter>();
+        else
+          wait_vm_lgkm_barrier<0>();
+      }
     };
     for (int kt = 0; kt < nk - 1; kt += NB) {
       step(std::integral_constant<int, 0>{}, kt);

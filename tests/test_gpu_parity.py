@@ -113,9 +113,12 @@ def test_w4a16_gemv_strided_operands(gpu, threads, M, K, N, group):
     assert_close_rms(host(y), oracle.w4a16(x, q, s, z, threads), what="gemv strided")
 
 
+# M > 128 with group sizes that are multiples of 64 and K / group a multiple of 4 load scales
+# and zeros once per pair of groups (64, 128, 192 with three stages per group, 256);
+# (300, 384, 130, 192) has two groups per row and takes the per-stage loads.
 @pytest.mark.parametrize("M,K,N,group", [(16, 4096, 4096, 128), (17, 512, 200, 128), (130, 256, 64, 64),
                                          (256, 1024, 384, 128), (1, 128, 128, 32), (40, 512, 256, 32),
-                                         (300, 384, 130, 192)])
+                                         (300, 384, 130, 192), (300, 768, 130, 192), (200, 2048, 96, 256)])
 def test_w4a16_gemm_shapes(gpu, threads, M, K, N, group):
     x, q, s, z = w4_case(2, M, K, N, group)
     y = art(intent.weight_only_int4_asym_matmul, KERNEL="gemm").run(dev(x), dev(q), dev(s), dev(z))
