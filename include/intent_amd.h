@@ -184,7 +184,9 @@ int intent_moe_align(const int32_t* topk_ids, int64_t T, int64_t top_k, int64_t 
  * (examples/kernels/ragged/moe.py:28-45) for SiLU-gated W4 experts.
  * Requires H even and a multiple of group_size. Block size 64 or 128 with
  * H % 128 == 0, F % 64 == 0, group 32 or a multiple of 64 and aligned rows
- * runs the tiled kernels; any other block size or shape a generic kernel.
+ * runs the tiled kernels, block size 160 too when the group is a multiple of
+ * 64, H / group a multiple of 4 and scales/zeros 4-byte aligned; any other
+ * block size or shape a generic kernel.
  */
 int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_t x_ld,
                           const int32_t* sorted_route_ids, const int32_t* expert_blocks,
@@ -201,7 +203,9 @@ int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_t x_ld,
  * (examples/kernels/ragged/moe.py:46-53).
  * Requires F even and a multiple of group_size. Block size 64 or 128 with
  * F % 128 == 0, group 32 or a multiple of 64 and aligned rows runs the
- * tiled kernels; any other block size or shape a generic kernel.
+ * tiled kernels, block size 160 too when the group is a multiple of 64,
+ * F / group a multiple of 4 and scales/zeros 4-byte aligned; any other
+ * block size or shape a generic kernel.
  */
 int intent_moe_down_w4(const void* act, int64_t act_ld,
                        const int32_t* sorted_route_ids, const int32_t* expert_blocks,
@@ -228,9 +232,12 @@ int intent_moe_combine(const float* route_out, int64_t out_ld,
  * Replaces moe_expert_ffn (examples/kernels/ragged/moe.py:12-53) together
  * with its host alignment (examples/programs/composition.py:134-174).
  * `workspace` must hold intent_moe_workspace_size(T, top_k, E, H, F, 0) bytes
- * (16-byte aligned); the composite aligns routes to 128-row blocks.
+ * (16-byte aligned); the composite aligns routes to 160-row blocks when
+ * experts average at least 96 routes (T*top_k >= 96*E) and both projections
+ * take the 160-row tile, else to 128-row blocks.
  * intent_moe_workspace_size with block_size > 0 gives the staged pipeline's
- * buffers for that block size (block_size <= 0 means the composite's 128).
+ * buffers for that block size; block_size <= 0 gives the composite's, which
+ * covers either block size it may pick.
  * If topk_ids_out / topk_weights_out are non-null the routing results are
  * also copied there ([T,top_k] each).
  */

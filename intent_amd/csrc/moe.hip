@@ -396,20 +396,26 @@ __global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_ker
 // CU, 519 us at two 4-wave workgroups per CU.
 using GateUpPk = mp::Tile<128, 256, 1, 4>;
 constexpr int kGateUpPkStages = 3;
+// 160-row blocks (five row blocks per wave): an expert with 129..160 routes
+// is one block, not a full block plus a light one that streams and decodes
+// the expert's weights a second time. 160 x 128 B token rows make a 28 KB
+// stage, so two workgroups per CU hold a ring of two stages (a two-stage ring
+// measured the same as three on the 128-row tile); 15-17 VGPRs spill. Config
+// 4 (experts of 112..143 routes): gate/up 348 -> 334 us, down 213 -> 207 us.
+using Pk160 = mp::Tile<160, 256, 1, 4>;
+constexpr int kPk160Stages = 2;
 
 // Group parameters per stage (gs == 32) or per window of four groups.
 template <bool kWin>
 using PkParams = std::conditional_t<kWin, mp::GroupWindowDma<GateUpPk::BN, GateUpPk::NW>,
                                     mp::GroupParamsDma<GateUpPk::BN, GateUpPk::NW>>;
 
-template <bool kWin>
+template <bool kWin, class T = GateUpPk, int NB = kGateUpPkStages>
 __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
     const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ blocks, int mblocks, int R, int top_k, const uint8_t* __restrict__ wq,
     const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int F, int gs, f16* __restrict__ act,
     int64_t ld_act) {
-  using T = GateUpPk;
-  constexpr int NB = kGateUpPkStages;
   __shared__ __attribute__((aligned(16))) char smem[NB][mp::stage_bytes_pk<T, kWin>()];
   __shared__ __attribute__((aligned(16))) char pwin[kWin ? 2 * PkParams<true>::BYTES : 16];
   char* bufs[NB];
@@ -447,6 +453,8 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
     mp::mainloop_pk<T, NB, ADma, BDma, PDma, 2>(aop, bop, pop, H / 64, bufs, acc, pwin);
   else if (ta == 3)
     mp::mainloop_pk<T, NB, ADma, BDma, PDma, 3>(aop, bop, pop, H / 64, bufs, acc, pwin);
+  else if (ta == 4 || T::TI == 4)
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 4>(aop, bop, pop, H / 64, bufs, acc, pwin);
   else
     mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, H / 64, bufs, acc, pwin);
   store_gate_up<T>(acc, m0, f0, F, sorted, R, act, ld_act);
@@ -518,14 +526,12 @@ __global__ __launch_bounds__(MoeTiles<B>::Down::NT_WS, 1) void moe_down_kernel(
 // combine adds the parts in order. Measured on config 4: 328 us for the
 // producer/consumer kernel below, which runs 384 workgroups of 128 x 128 with
 // the decode in separate waves.
-template <bool kWin>
+template <bool kWin, class T = GateUpPk, int NB = kGateUpPkStages>
 __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
     const f16* __restrict__ act, int64_t ld_act, const int32_t* __restrict__ sorted,
     const int32_t* __restrict__ blocks, int mblocks, int ntiles, int R, const uint8_t* __restrict__ wq,
     const f16* __restrict__ ws, const uint8_t* __restrict__ wz, int H, int F, int gs, int splits,
     float* __restrict__ out, int64_t ldo, int64_t part_stride) {
-  using T = GateUpPk;
-  constexpr int NB = kGateUpPkStages;
   __shared__ __attribute__((aligned(16))) char smem[NB][mp::stage_bytes_pk<T, kWin>()];
   __shared__ __attribute__((aligned(16))) char pwin[kWin ? 2 * PkParams<true>::BYTES : 16];
   char* bufs[NB];
@@ -566,6 +572,8 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
     mp::mainloop_pk<T, NB, ADma, BDma, PDma, 2>(aop, bop, pop, nk, bufs, acc, pwin);
   else if (ta == 3)
     mp::mainloop_pk<T, NB, ADma, BDma, PDma, 3>(aop, bop, pop, nk, bufs, acc, pwin);
+  else if (ta == 4 || T::TI == 4)
+    mp::mainloop_pk<T, NB, ADma, BDma, PDma, 4>(aop, bop, pop, nk, bufs, acc, pwin);
   else
     mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, nk, bufs, acc, pwin);
   store_down<T>(acc, m0, n0, H, sorted, R, out + part * part_stride, ldo);
@@ -798,7 +806,13 @@ int combine_launch(const float* route_out, int64_t out_ld, const float* topk_wei
   return intent::launch_status("moe_combine");
 }
 
-bool supported_block(int64_t b) { return b == 64 || b == 128; }
+// The 160-row tile takes windowed group parameters only: group sizes that
+// are multiples of 64, K / group a multiple of 4, 4-byte aligned parameters.
+bool pk160_ok(int64_t K, int64_t gs, const void* scales, const void* zeros) {
+  return gs % 64 == 0 && (K / gs) % 4 == 0 && intent::aligned4(scales) && intent::aligned4(zeros);
+}
+
+bool supported_block(int64_t b) { return b == 64 || b == 128 || b == Pk160::BM; }
 
 }  // namespace
 
@@ -823,7 +837,8 @@ extern "C" int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_
                     (group_size == 32 || group_size % 64 == 0) && intent::fits_offset(2 * F, H / 2) &&
                     intent::fits_offset(2 * F, H / group_size * 2) && intent::fits_offset(T, x_ld * 2) &&
                     intent::fits_offset(256 + 1, act_ld * 2) && intent::aligned16(x) && x_ld % 8 == 0 &&
-                    intent::aligned16(w_packed);
+                    intent::aligned16(w_packed) &&
+                    (block_size != Pk160::BM || pk160_ok(H, group_size, w_scales, w_zeros));
   if (!fast) {
     const int64_t fchunks = (F + 255) / 256;
     const int64_t grid = num_blocks * block_size * fchunks;
@@ -833,6 +848,15 @@ extern "C" int intent_moe_gate_up_w4(const void* x, int64_t T, int64_t H, int64_
                        (int)(T * top_k), (int)top_k, w_packed, (const f16*)w_scales, w_zeros, (int)F, (int)group_size,
                        (f16*)act, act_ld, (int)fchunks);
     return intent::launch_status("moe_gate_up_generic_kernel");
+  }
+  if (block_size == Pk160::BM) {
+    const int64_t grid = num_blocks * ((F + Pk160::BN / 2 - 1) / (Pk160::BN / 2));
+    INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+    hipLaunchKernelGGL((moe_gate_up_pk_kernel<true, Pk160, kPk160Stages>), dim3((unsigned)grid), dim3(Pk160::NT), 0,
+                       (hipStream_t)stream, (const f16*)x, x_ld, (int)H, sorted_route_ids, expert_blocks,
+                       (int)num_blocks, (int)(T * top_k), (int)top_k, w_packed, (const f16*)w_scales, w_zeros, (int)F,
+                       (int)group_size, (f16*)act, act_ld);
+    return intent::launch_status("moe_gate_up_w4");
   }
   if (block_size == 64)
     return gate_up_launch<64>(x, T, H, x_ld, sorted_route_ids, expert_blocks, num_blocks, top_k, w_packed, w_scales,
@@ -882,9 +906,27 @@ int down_generic(const void* act, int64_t act_ld, const int32_t* sorted, const i
   return intent::launch_status("moe_down_generic_kernel");
 }
 
+// Down projection on the 160-row packed-weight tile, K split into `splits`
+// parts (part p at out + p * part_stride).
+int down_pk160_launch(const void* act, int64_t act_ld, const int32_t* sorted, const int32_t* blocks,
+                      int64_t num_blocks, int64_t R, const uint8_t* wq, const void* ws, const uint8_t* wz, int64_t H,
+                      int64_t F, int64_t gs, int splits, float* out, int64_t out_ld, int64_t part_stride,
+                      void* stream) {
+  const int64_t ntiles = (H + Pk160::BN - 1) / Pk160::BN;
+  const int64_t grid = splits * num_blocks * ntiles;
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
+  hipLaunchKernelGGL((moe_down_pk_kernel<true, Pk160, kPk160Stages>), dim3((unsigned)grid), dim3(Pk160::NT), 0,
+                     (hipStream_t)stream, (const f16*)act, act_ld, sorted, blocks, (int)num_blocks, (int)ntiles, (int)R,
+                     wq, (const f16*)ws, wz, (int)H, (int)F, (int)gs, splits, out, out_ld, part_stride);
+  return intent::launch_status("moe_down_pk");
+}
+
 int down_dispatch(const void* act, int64_t act_ld, const int32_t* sorted, const int32_t* blocks, int64_t num_blocks,
                   int64_t block_size, int64_t R, const uint8_t* wq, const void* ws, const uint8_t* wz, int64_t H,
                   int64_t F, int64_t gs, float* out, int64_t out_ld, void* stream) {
+  if (block_size == Pk160::BM)
+    return down_pk160_launch(act, act_ld, sorted, blocks, num_blocks, R, wq, ws, wz, H, F, gs, 1, out, out_ld, 0,
+                             stream);
   if (block_size == 64)
     return down_launch<64>(act, act_ld, sorted, blocks, num_blocks, R, wq, ws, wz, H, F, gs, out, out_ld, stream);
   return down_launch<128>(act, act_ld, sorted, blocks, num_blocks, R, wq, ws, wz, H, F, gs, out, out_ld, stream);
@@ -900,7 +942,8 @@ extern "C" int intent_moe_down_w4(const void* act, int64_t act_ld, const int32_t
   int st = down_check(act, act_ld, sorted_route_ids, expert_blocks, num_blocks, block_size, R, w_packed, w_scales,
                       w_zeros, E, H, F, group_size, out, out_ld);
   if (st != INTENT_OK || num_blocks == 0 || R == 0) return st;
-  if (!down_fast(act, act_ld, block_size, w_packed, H, F, group_size))
+  if (!down_fast(act, act_ld, block_size, w_packed, H, F, group_size) ||
+      (block_size == Pk160::BM && !pk160_ok(F, group_size, w_scales, w_zeros)))
     return down_generic(act, act_ld, sorted_route_ids, expert_blocks, num_blocks, block_size, R, w_packed, w_scales,
                         w_zeros, H, F, group_size, out, out_ld, stream);
   return down_dispatch(act, act_ld, sorted_route_ids, expert_blocks, num_blocks, block_size, R, w_packed, w_scales,
@@ -962,12 +1005,25 @@ MoEWorkspace moe_layout(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t 
 // did not help either.
 constexpr int64_t kCompositeBlock = 128;
 
+// The composite takes 160-row blocks (Pk160) when experts average at least 96
+// routes (with fewer, 160-row blocks mostly hold padding) and both
+// projections take windowed group parameters; else 128-row blocks.
+bool composite_wants_pk160(int64_t T, int64_t top_k, int64_t E) { return T * top_k >= 96 * E; }
+
+// Workspace for either block size the composite may pick.
+size_t composite_workspace(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t F) {
+  const size_t base = moe_layout(T, top_k, E, H, F, kCompositeBlock).bytes;
+  if (!composite_wants_pk160(T, top_k, E)) return base;
+  const size_t big = moe_layout(T, top_k, E, H, F, Pk160::BM).bytes;
+  return big > base ? big : base;
+}
+
 }  // namespace
 
 extern "C" size_t intent_moe_workspace_size(int64_t T, int64_t top_k, int64_t E, int64_t H, int64_t F,
                                             int64_t block_size) {
   if (T < 0 || top_k < 1 || E < 1 || H < 0 || F < 0) return 0;
-  return moe_layout(T, top_k, E, H, F, block_size > 0 ? block_size : kCompositeBlock).bytes;
+  return block_size > 0 ? moe_layout(T, top_k, E, H, F, block_size).bytes : composite_workspace(T, top_k, E, H, F);
 }
 
 extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* x, int64_t T, int64_t H, int64_t E,
@@ -977,12 +1033,16 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
                                         int64_t group_size, float* y, void* workspace, size_t workspace_bytes,
                                         int32_t* topk_ids_out, float* topk_weights_out, void* stream) {
   intent::clear_error();
-  const int64_t B = kCompositeBlock;
   INTENT_REQUIRE(T >= 0 && top_k >= 1 && E >= 1 && H > 0 && F > 0, INTENT_ERR_INVALID_ARGUMENT, "bad extents");
   if (T == 0) return INTENT_OK;
+  INTENT_REQUIRE(group_size > 0, INTENT_ERR_INVALID_ARGUMENT, "group_size must be positive");
+  const bool big = composite_wants_pk160(T, top_k, E) && pk160_ok(H, group_size, wgu_scales, wgu_zeros) &&
+                   pk160_ok(F, group_size, wd_scales, wd_zeros) && F % (down_splits(F, group_size) * 4 * group_size) == 0;
+  const int64_t B = big ? Pk160::BM : kCompositeBlock;
   const MoEWorkspace L = moe_layout(T, top_k, E, H, F, B);
-  INTENT_REQUIRE(workspace && workspace_bytes >= L.bytes, INTENT_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu",
-                 L.bytes, workspace_bytes);
+  const size_t need = composite_workspace(T, top_k, E, H, F);
+  INTENT_REQUIRE(workspace && workspace_bytes >= need, INTENT_ERR_WORKSPACE, "workspace needs %zu bytes, got %zu", need,
+                 workspace_bytes);
   INTENT_REQUIRE(intent::aligned16(workspace), INTENT_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
   INTENT_REQUIRE(y, INTENT_ERR_INVALID_ARGUMENT, "null output");
   char* ws = (char*)workspace;
@@ -1013,6 +1073,13 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
                     H);
     if (st != INTENT_OK) return st;
     splits = want;
+    if (B == Pk160::BM) {
+      st = down_pk160_launch(act, F, sorted, blocks, L.nblocks, R, wd_packed, wd_scales, wd_zeros, H, F, group_size,
+                             splits, out, H, R * H, stream);
+      if (st != INTENT_OK) return st;
+      launch_combine(out, H, wts, T, top_k, y, H, H, splits, R * H, (hipStream_t)stream);
+      return intent::launch_status("moe_combine");
+    }
     const int64_t ntiles = (H + GateUpPk::BN - 1) / GateUpPk::BN;
     const int64_t grid = splits * L.nblocks * ntiles;
     INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");

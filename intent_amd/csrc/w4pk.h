@@ -276,8 +276,9 @@ constexpr int stage_bytes_pk() {
 // PDma::BYTES. Windows 0 and 1 are loaded before the loop; the step whose
 // next stage opens window w loads window w + 1 into the buffer window w - 1
 // used, right after that step's stage group. Such a load sits between stage
-// groups in the vmcnt order, so the wait of each of the next two steps
-// allows its NVM instructions on top of one stage group; a window is read
+// groups in the vmcnt order, so the wait of each of the next NB - 1 steps
+// (whose target stage group was issued before it) allows its NVM
+// instructions on top of NB - 2 stage groups; a window is read
 // at least three steps after its load was issued (a window spans >= 4
 // stages), by which time the stage group issued after it has been waited for.
 template <class T, int NB, class ADma, class BDma, class PDma, int TA = T::TI>
@@ -362,7 +363,7 @@ INTENT_DEVICE void mainloop_pk(const ADma& aop, const BDma& bop, const PDma& pop
       }
       issue(J, kt + NB);
       if constexpr (kWin) {
-        pmask = (pmask << 1) & 3;
+        pmask = (pmask << 1) & ((1 << (NB - 1)) - 1);  // loads issued in the last NB - 1 steps
         const int w1 = (pg >> 2) + 1;
         if ((pg & 3) == 0 && psg == 0 && w1 < nwin) {
           pop.issue(pwin + (w1 & 1) * PDma::BYTES, w1);

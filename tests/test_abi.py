@@ -100,7 +100,11 @@ def test_moe_checks():
     assert _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 128) >= \
         16 * 128 * 14336 * 2 + 1024 * 4096 * 4  # block 128: padded activations + route outputs
     need = _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 0)  # composite plan
-    assert need == _native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, 128)
+    # 128 routes per expert: the composite may take 128- or 160-row blocks and sizes for either
+    assert need == max(_native.library().intent_moe_workspace_size(512, 2, 8, 4096, 14336, b) for b in (128, 160))
+    # 8 routes per expert: 128-row blocks only
+    assert _native.library().intent_moe_workspace_size(32, 2, 8, 4096, 14336, 0) == \
+        _native.library().intent_moe_workspace_size(32, 2, 8, 4096, 14336, 128)
     assert status("intent_moe_expert_ffn_w4", FAKE, FAKE, 512, 4096, 8, 2, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
                   14336, 128, FAKE, FAKE, need - 1, None, None, None) == errors.INTENT_ERR_WORKSPACE
     assert _native.library().intent_moe_workspace_size(-1, 2, 8, 64, 64, 128) == 0

@@ -390,9 +390,12 @@ def test_moe_ffn_config4(gpu, threads):
 
 
 # H = 512 at group 128 gives the tiled kernels whole four-group windows; block
-# size 192 is off the tiles and runs the generic kernels.
+# size 192 is off the tiles and runs the generic kernels. Block size 160 takes
+# the 160-row tile where K is whole four-group windows (H 512 for gate/up,
+# F 512 for down) and the generic kernels elsewhere (H 256, F 384).
 @pytest.mark.parametrize("B,T,F,H", [(128, 48, 256, 256), (64, 48, 256, 256), (64, 100, 384, 256),
-                                     (128, 300, 512, 512), (192, 48, 256, 256)])
+                                     (128, 300, 512, 512), (192, 48, 256, 256), (160, 300, 512, 512),
+                                     (160, 200, 384, 512), (160, 48, 512, 256)])
 def test_moe_stage_entries(gpu, threads, B, T, F, H):
     E, k = 4, 2
     d = moe_small(9, T, H, E, k, F)
