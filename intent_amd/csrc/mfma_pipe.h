@@ -53,6 +53,42 @@ INTENT_DEVICE void static_for_mp(F&& f) {
 
 using Rsrc = __amdgpu_buffer_rsrc_t;
 
+// Buffer load of BYTES (4 or 16) per lane straight into LDS: lane l's bytes
+// land at lds + l * BYTES (M0 holds the workgroup-relative LDS byte address)
+// and come from buffer base + voff + soff.
+//
+// kAsm = false: the compiler builtin. The compiler's wait insertion then makes
+// LDS reads that follow such a DMA wait for all outstanding loads (vmcnt 0),
+// the next stages' DMA included, whenever it cannot tell which LDS bytes the
+// DMA writes. kAsm = true: the same instructions as assembly, which that pass
+// does not track; a pipeline using it orders every read of DMA-written LDS
+// with its own vmcnt waits and barriers, and keeps the compiler's own vector
+// loads (spill reloads included) out of its loop, since their waits would
+// drain the DMA too. Which form is faster depends on the kernel's schedule,
+// so each pipeline picks the one measured faster.
+template <int BYTES, bool kAsm>
+INTENT_DEVICE void lds_dma(Rsrc rs, lds_t* lds, uint32_t voff, uint32_t soff) {
+  static_assert(BYTES == 4 || BYTES == 16, "dword or dwordx4");
+  if constexpr (!kAsm) {
+    if constexpr (BYTES == 16)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 16, voff, soff, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 4, voff, soff, 0, 0);
+  } else {
+    const uint32_t m = (uint32_t)(uintptr_t)lds;
+    if constexpr (BYTES == 16)
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                   :
+                   : "s"(m), "v"(voff), "s"(rs), "s"(soff)
+                   : "memory", "m0");
+    else
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                   :
+                   : "s"(m), "v"(voff), "s"(rs), "s"(soff)
+                   : "memory", "m0");
+  }
+}
+
 // s_waitcnt with only vmcnt constrained (expcnt 7, lgkmcnt 15 = no wait).
 template <int N>
 INTENT_DEVICE void wait_vm() {
@@ -138,6 +174,22 @@ struct DenseRows {  // rows m0.. of a row-major matrix; rows >= M clamp to M-1
     return (uint32_t)((m < M ? p : M - 1 - m0) * ld_bytes);
   }
 };
+
+// Rows m0.. of a row-major matrix whose tile rows all exist (no clamp): row p
+// sits p * ld_bytes after the tile base, so the DMA of consecutive row groups
+// differs by a uniform offset.
+struct LinearRows {
+  static constexpr bool kLinear = true;
+  const void* base;
+  int64_t ld_bytes;
+  INTENT_DEVICE const void* tile_base(int m0) const { return (const char*)base + (int64_t)m0 * ld_bytes; }
+  INTENT_DEVICE uint32_t off(int, int p) const { return (uint32_t)(p * ld_bytes); }
+};
+
+template <class R, class = void>
+struct IsLinearRows : std::false_type {};
+template <class R>
+struct IsLinearRows<R, std::void_t<decltype(R::kLinear)>> : std::bool_constant<R::kLinear> {};
 
 struct GatherRows {  // MoE gate/up: padded row p holds route sorted[p]; token = route / top_k
   const void* base;
@@ -284,13 +336,19 @@ struct LowBitRowsOperand {
 // Raw rows copied global -> LDS by DMA (buffer_load ... lds): no VGPRs and
 // no ds_write issue slots. Each wave instruction moves 8 rows x 128 bytes;
 // lane i writes slot i%8 of row i/8, fetching chunk slot ^ swz(row).
-template <int ROWS, class Rows, int NW = 4>
+// LinearRows: instruction j's rows sit j * NW * 8 rows after instruction 0's
+// with the same swizzle (NW even), so one offset register serves all and the
+// row step goes into the uniform offset.
+template <int ROWS, class Rows, int NW = 4, bool kAsm = false>
 struct DmaRowsOperand {
   static constexpr int N_INST = ROWS / (8 * NW);
   static_assert(N_INST * 8 * NW == ROWS, "tile rows must be a multiple of 8 per wave");
   static constexpr int NVM = N_INST;
+  static constexpr bool kLin = IsLinearRows<Rows>::value;
+  static_assert(!kLin || NW % 2 == 0, "linear rows keep one swizzle per lane only for an even wave count");
   Rsrc rs;
-  uint32_t voff[N_INST];
+  uint32_t voff[kLin ? 1 : N_INST];
+  uint32_t jstep = 0;  // LinearRows: bytes between the rows of instructions j and j + 1
   int lds_row0[N_INST];
   INTENT_DEVICE void init(const Rows& rows, int m0, int wave) {
     rs = make_rsrc(rows.tile_base(m0));
@@ -299,15 +357,16 @@ struct DmaRowsOperand {
     for (int j = 0; j < N_INST; ++j) {
       const int r0 = (j * NW + wave) * 8;
       const int r = r0 + (lane >> 3);
-      voff[j] = rows.off(m0, r) + (((lane & 7) ^ swz(r)) << 4);
+      if (!kLin || j == 0) voff[kLin ? 0 : j] = rows.off(m0, r) + (((lane & 7) ^ swz(r)) << 4);
       lds_row0[j] = r0;
     }
+    if constexpr (kLin) jstep = rows.off(m0, NW * 8);
   }
   INTENT_DEVICE void issue(char* lds_region, int kt) const {
 #pragma unroll
     for (int j = 0; j < N_INST; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_t*)(lds_region + lds_row0[j] * ROWB), 16, voff[j],
-                                               (uint32_t)kt * ROWB, 0, 0);
+      lds_dma<16, kAsm>(rs, (lds_t*)(lds_region + lds_row0[j] * ROWB), voff[kLin ? 0 : j],
+                        (uint32_t)kt * ROWB + (kLin ? j * jstep : 0u));
   }
 };
 
@@ -710,8 +769,7 @@ struct DmaKNOperand {
   INTENT_DEVICE void issue(char* lds_b, int kt) const {
 #pragma unroll
     for (int j = 0; j < N_INST; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_t*)(lds_b + lds_kb[j] * 1024), 16, voff[j],
-                                               (uint32_t)kt * kstep, 0, 0);
+      lds_dma<16, false>(rs, (lds_t*)(lds_b + lds_kb[j] * 1024), voff[j], (uint32_t)kt * kstep);
   }
 };
 

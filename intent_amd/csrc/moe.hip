@@ -431,7 +431,7 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
   const int m0 = mb * T::BM;
   const int wave = T::wave();
   const GateUpRowMap<T> rows{f0, F};
-  mp::DmaRowsOperand<T::BM, mp::GatherRows, T::NW> aop;
+  mp::DmaRowsOperand<T::BM, mp::GatherRows, T::NW, true> aop;
   aop.init(mp::GatherRows{x, ldx * 2, sorted, R, top_k}, m0, wave);
   mp::PackedRowsDma<T::BN, T::NW> bop;
   bop.init(wq + (int64_t)e * 2 * F * ldq, ldq, rows, wave);
@@ -551,8 +551,8 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
   const int m0 = mb * T::BM;
   const int wave = T::wave();
   const ClampRows rows{n0, H};
-  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
-  aop.init(mp::DenseRows{act + k0, ld_act * 2, m0 + T::BM}, m0, wave);
+  mp::DmaRowsOperand<T::BM, mp::LinearRows, T::NW, true> aop;
+  aop.init(mp::LinearRows{act + k0, ld_act * 2}, m0, wave);
   mp::PackedRowsDma<T::BN, T::NW> bop;
   bop.init(wq + (int64_t)e * H * ldq + k0 / 2, ldq, rows, wave);
   PkParams<kWin> pop;

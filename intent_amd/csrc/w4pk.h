@@ -73,8 +73,7 @@ struct PackedRowsDma {
   INTENT_DEVICE void issue(char* lds_b, int kt) const {
 #pragma unroll
     for (int j = 0; j < N_INST; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_t*)(lds_b + lds_row0[j] * 32), 16, voff[j],
-                                               (uint32_t)kt * 32, 0, 0);
+      lds_dma<16, true>(rq, (lds_t*)(lds_b + lds_row0[j] * 32), voff[j], (uint32_t)kt * 32);
   }
 };
 
@@ -117,9 +116,8 @@ struct GroupParamsDma {
     const uint32_t g = (uint32_t)group(kt);
 #pragma unroll
     for (int j = 0; j < N_INST; ++j) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_t*)(lds_p + row0[j] * 4), 4, soff[j], (2 * g) & ~3u, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rz, (lds_t*)(lds_p + 4 * ROWS + row0[j] * 4), 4, zoff[j], g & ~3u,
-                                               0, 0);
+      lds_dma<4, true>(rs, (lds_t*)(lds_p + row0[j] * 4), soff[j], (2 * g) & ~3u);
+      lds_dma<4, true>(rz, (lds_t*)(lds_p + 4 * ROWS + row0[j] * 4), zoff[j], g & ~3u);
     }
   }
 };
@@ -169,11 +167,10 @@ struct GroupWindowDma {
   INTENT_DEVICE void issue(char* lds_p, int w) const {
 #pragma unroll
     for (int j = 0; j < S_INST; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_t*)(lds_p + srow0[j] * 8), 4, soff[j], (uint32_t)w * 8, 0, 0);
+      lds_dma<4, true>(rs, (lds_t*)(lds_p + srow0[j] * 8), soff[j], (uint32_t)w * 8);
 #pragma unroll
     for (int j = 0; j < Z_INST; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rz, (lds_t*)(lds_p + 8 * ROWS + zrow0[j] * 4), 4, zoff[j],
-                                               (uint32_t)w * 4, 0, 0);
+      lds_dma<4, true>(rz, (lds_t*)(lds_p + 8 * ROWS + zrow0[j] * 4), zoff[j], (uint32_t)w * 4);
   }
 };
 
@@ -210,12 +207,17 @@ INTENT_DEVICE void stage_prologue(const char* buf, const uint32_t (&aaddr)[4], u
 }
 
 // The four MFMA steps of a stage; the A reads and weight decodes of step
-// kk + 1 are interleaved with the MFMAs of step kk.
+// kk + 1 are interleaved with the MFMAs of step kk. With five row blocks
+// (kSingleA) each row block's A fragment is reread right after its last MFMA
+// of the step, into the same registers: double-buffering all of them would
+// need 20 more VGPRs than the 256 that two workgroups per CU allow.
 template <class T, int TA>
 INTENT_DEVICE void stage_body(const char* buf, const uint32_t (&aaddr)[4], const StagePk<T>& st,
                               f32x16 (&acc)[T::TI][T::TJ]) {
+  constexpr bool kSingleA = T::TI >= 5;
+  constexpr int NAB = kSingleA ? 1 : 2;
   const char* a = buf;
-  f16x8 af[2][T::TI], bf[2][T::TJ];
+  f16x8 af[NAB][T::TI], bf[2][T::TJ];
 #pragma unroll
   for (int i = 0; i < TA; ++i) af[0][i] = st.af[i];
 #pragma unroll
@@ -223,21 +225,28 @@ INTENT_DEVICE void stage_body(const char* buf, const uint32_t (&aaddr)[4], const
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
     const int cb = kk & 1;
+    const int ca = kSingleA ? 0 : cb;
     if (kk + 1 < 4) {
+      if constexpr (!kSingleA) {
 #pragma unroll
-      for (int i = 0; i < TA; ++i)
-        af[cb ^ 1][i] = *reinterpret_cast<const f16x8*>(a + aaddr[kk + 1] + i * 32 * ROWB);
+        for (int i = 0; i < TA; ++i)
+          af[ca ^ 1][i] = *reinterpret_cast<const f16x8*>(a + aaddr[kk + 1] + i * 32 * ROWB);
+      }
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j) bf[cb ^ 1][j] = dequant8(st.bq[j][kk + 1], st.zo[j], st.sc[j]);
     }
 #pragma unroll
-    for (int i = 0; i < TA; ++i)
+    for (int i = 0; i < TA; ++i) {
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cb][j], af[cb][i], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cb][j], af[ca][i], acc[i][j], 0, 0, 0);
+      if constexpr (kSingleA)
+        if (kk + 1 < 4) af[0][i] = *reinterpret_cast<const f16x8*>(a + aaddr[kk + 1] + i * 32 * ROWB);
+    }
   }
   // Schedule (masks: 0x008 MFMA, 0x002 VALU, 0x100 DS read): per step one
-  // MFMA followed by its share of the next step's reads and decode VALU.
+  // MFMA followed by its share of the next step's reads and decode VALU
+  // (kSingleA: a row block's read after its last MFMA).
   constexpr int NM = TA * T::TJ;
   constexpr int VALU_STEP = T::TJ * 17;  // decode of one step (dequant8)
   static_for<0, 4>([&](auto KK) {
@@ -246,7 +255,8 @@ INTENT_DEVICE void stage_body(const char* buf, const uint32_t (&aaddr)[4], const
       constexpr int x = decltype(X)::value;
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       if constexpr (kk < 3) {
-        if constexpr (x < TA) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        constexpr bool rd = kSingleA ? x % T::TJ == T::TJ - 1 : x < TA;
+        if constexpr (rd) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         constexpr int v = (x + 1) * VALU_STEP / NM - x * VALU_STEP / NM;
         if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
       }
