@@ -314,6 +314,17 @@ def test_moe_ffn_many_routes(gpu, threads, T, H, E, k, F, group):
     assert_close_rms(got, ref, what=f"moe ffn many routes T {T} H {H} E {E} F {F} group {group}")
 
 
+# More than 64 row blocks of 160 rows (64 experts of ~128 routes): the
+# heavy-first block order of gate/up takes several wave-wide passes.
+def test_moe_ffn_many_blocks(gpu, threads):
+    T, H, E, k, F = 2048, 512, 64, 4, 512
+    d = moe_small(10, T, H, E, k, F)
+    got = run_ffn(d, np.zeros((T, H), np.float32))
+    ids, wts = oracle.moe_route(d["logits"], k, True)
+    ref = oracle.moe_ffn_w4(d["x"], ids, wts, d["wgu"], d["sgu"], d["zgu"], d["wd"], d["sd"], d["zd"], threads=threads)
+    assert_close_rms(got, ref, what="moe ffn many blocks")
+
+
 # Group sizes that are multiples of 64 load scales and zeros in windows of
 # four groups; these shapes cross several windows in gate/up (H) and down (F),
 # including an odd window count and three stages per group.
