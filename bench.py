@@ -496,7 +496,7 @@ def mfma_ceiling() -> dict:
     lib = _native.library()
     sink = torch.zeros(256, dtype=torch.int32, device="cuda")
     out = {}
-    wgs, iters = 2048, 64  # 8 waves per SIMD; about 35 ms per launch
+    wgs, iters = 2048, 256  # 8 waves per SIMD; about 0.15 ms per launch, so ramp-up and drain stay small
     for kind, label, per in ((0, "f16", 32768), (1, "i8", 65536)):
         def go():
             st = lib.intent_mfma_peak_probe(kind, iters, wgs, ctypes.c_void_p(sink.data_ptr()),
