@@ -48,34 +48,66 @@ def hipcc() -> str:
     return found
 
 
-def _compile(source: Path) -> Path:
-    obj = OBJDIR / (source.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(source), "-o", str(obj)]
+def _compile(source: Path, objdir: Path = OBJDIR, extra_flags=()) -> Path:
+    obj = objdir / (source.stem + ".o")
+    cmd = [hipcc(), *HIPCC_FLAGS, *extra_flags, "-c", str(source), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{proc.stdout}\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source and link the shared library; returns its path."""
-    OBJDIR.mkdir(parents=True, exist_ok=True)
-    LIBDIR.mkdir(parents=True, exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
+def check_objects(objects, workdir: Path) -> None:
+    """Run the code-object checks (``codeobj_check``) over the device code of
+    every object; every kernel named in ``UNTRACKED_DMA_KERNELS`` must be
+    among them, with its LDS DMA, when its source file is."""
+    from .codeobj_check import UNTRACKED_DMA_KERNELS, check_binary
+
+    seen = set()
+    for obj in objects:
+        if not _has_device_code(obj):
+            continue
+        for rep in check_binary(obj, workdir):
+            for k in UNTRACKED_DMA_KERNELS:
+                if k in rep.name and rep.dma:
+                    seen.add(k)
+    if any(Path(o).stem == "moe" for o in objects):
+        missing = set(UNTRACKED_DMA_KERNELS) - seen
+        if missing:
+            raise RuntimeError(f"code-object check: no LDS DMA found in {sorted(missing)}; update UNTRACKED_DMA_KERNELS")
+
+
+def _has_device_code(obj: Path) -> bool:
+    from .codeobj_check import _tool
+
+    proc = subprocess.run([_tool("llvm-readelf"), "-S", str(obj)], capture_output=True, text=True)
+    return ".hip_fatbin" in proc.stdout
+
+
+def build(verbose: bool = False, *, sources=None, extra_flags=(), library: Path = LIBRARY,
+          objdir: Path = OBJDIR) -> Path:
+    """Compile every HIP source (or ``sources``), check the device code
+    (``check_objects``) and link the shared library; returns its path."""
+    objdir = Path(objdir)
+    library = Path(library)
+    objdir.mkdir(parents=True, exist_ok=True)
+    library.parent.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip")) if sources is None else [Path(s) for s in sources]
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     workers = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(_compile, sources))
-    tmp = LIBRARY.with_suffix(".so.tmp")
+        objects = list(pool.map(lambda src: _compile(src, objdir, tuple(extra_flags)), sources))
+    check_objects(objects, objdir / "codeobj")
+    tmp = library.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIBRARY)
+    os.replace(tmp, library)
     if verbose:
-        print(f"built {LIBRARY}")
-    return LIBRARY
+        print(f"built {library}")
+    return library
 
 
 def build_host_sanitized(out_dir: Path) -> Path:

@@ -75,17 +75,23 @@ INTENT_DEVICE void lds_dma(Rsrc rs, lds_t* lds, uint32_t voff, uint32_t soff) {
     else
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, lds, 4, voff, soff, 0, 0);
   } else {
+    // M0 is an input operand ("{m0}"), so the compiler writes it and knows it
+    // is overwritten; the s_nop is the one wait state gfx9 needs between an
+    // SALU write of M0 and an LDS DMA that reads it (inline assembly gets no
+    // hazard padding). The resource and offset SGPRs must not be VALU results
+    // of the last 5 wait states; intent_amd/codeobj_check.py rejects a build
+    // where they are, or where such a kernel uses scratch.
     const uint32_t m = (uint32_t)(uintptr_t)lds;
     if constexpr (BYTES == 16)
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+      asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                    :
-                   : "s"(m), "v"(voff), "s"(rs), "s"(soff)
-                   : "memory", "m0");
+                   : "v"(voff), "s"(rs), "s"(soff), "{m0}"(m)
+                   : "memory");
     else
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+      asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
                    :
-                   : "s"(m), "v"(voff), "s"(rs), "s"(soff)
-                   : "memory", "m0");
+                   : "v"(voff), "s"(rs), "s"(soff), "{m0}"(m)
+                   : "memory");
   }
 }
 
