@@ -449,7 +449,9 @@ def traffic_probe() -> None:
 
 
 def read_probe(steps: int) -> None:
-    """Plain HBM read of the decode's bytes vs the decode GEMV, both rotated over the same copy count."""
+    """Plain HBM read of the decode's bytes, without and with one small store per wave (a
+    GEMV writes its outputs, and a kernel's end waits for its stores), against the decode
+    GEMV, all rotated over the same copy count."""
     import ctypes
 
     import torch
@@ -460,21 +462,25 @@ def read_probe(steps: int) -> None:
     nbytes = (work.bytes + 15) // 16 * 16
     n = copies_for(nbytes)
     bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(n)]
-    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    words = 8 * ((nbytes + 4095) // 4096)
+    sink = torch.zeros(words, dtype=torch.int32, device="cuda")
     lib = _native.library()
     results = {}
-    for unroll in (1, 2, 4, 8, 16):
-        def make(buf, u=unroll):
-            def go():
-                stream = torch.cuda.current_stream().cuda_stream
-                st = lib.intent_hbm_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes, u,
-                                               ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream))
-                if st != 0:
-                    raise RuntimeError(_native.last_error())
-            return go
-        ms = graph_time([make(b) for b in bufs], steps, 10)
-        results[f"hbm_read_probe_kernel<{unroll}>"] = ms
-        log(f"[probe] read unroll={unroll}: {ms * 1e3:.3f} us, {nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
+    for store in (0, 1):
+        for unroll in (1, 2, 4, 8, 16):
+            def make(buf, u=unroll, st_=store):
+                def go():
+                    stream = torch.cuda.current_stream().cuda_stream
+                    st = lib.intent_hbm_read_probe(ctypes.c_void_p(buf.data_ptr()), nbytes, u, st_,
+                                                   ctypes.c_void_p(sink.data_ptr()), words, ctypes.c_void_p(stream))
+                    if st != 0:
+                        raise RuntimeError(_native.last_error())
+                return go
+            ms = graph_time([make(b) for b in bufs], steps, 10)
+            name = f"hbm_read_probe_kernel<{unroll}, {'true' if store else 'false'}>"
+            results[name] = ms
+            log(f"[probe] read unroll={unroll} store={store}: {ms * 1e3:.3f} us, "
+                f"{nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")
     del bufs
     torch.cuda.empty_cache()
     dec = bench_w4a16(1, 4096, 4096, steps, 10)

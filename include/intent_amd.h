@@ -573,24 +573,6 @@ int intent_nvfp4_quantize(const void* x, int64_t M, int64_t N, int64_t x_ld, con
 int intent_i8_per_token_quantize(const void* x, int x_is_bf16, int64_t M, int64_t K, int64_t x_ld,
                                  int8_t* q, int64_t q_ld, float* scales, void* stream);
 
-/* Measurement support, no counterpart in the reference: reads `bytes` (a
- * multiple of 16) of `buf` once with the plainest coalesced 16-byte loads,
- * each workgroup of 256 lanes covering 256 * unroll * 16 contiguous bytes
- * (unroll in {1, 2, 4, 8, 16}). Its duration is the HBM read floor that a
- * streaming kernel over the same bytes is compared with. `sink` (256 uint32,
- * device) is written only on a hash coincidence.
- */
-int intent_hbm_read_probe(const void* buf, int64_t bytes, int unroll, uint32_t* sink, void* stream);
-
-/* Measurement support, no counterpart in the reference: `workgroups` groups of
- * four waves each issue `iters` rounds of four independent register-only
- * 32x32 MFMAs (kind 0: f16, 32768 flops each; kind 1: i8, 65536 ops each). The
- * rate it reaches is the matrix cores' sustained ceiling at the clock the chip
- * holds under that load, the practical bound for the compute-bound kernels.
- * `sink` (256 uint32, device) is written only on a value coincidence.
- */
-int intent_mfma_peak_probe(int kind, int64_t iters, int64_t workgroups, uint32_t* sink, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

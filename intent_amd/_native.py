@@ -72,7 +72,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_moe_expert_ffn_w4": ([P, P, I64, I64, I64, I64, INT, P, P, P, P, P, P, I64, I64, P, P, SIZE, P, P, P],
                                  INT),
     "intent_i8_per_token_quantize": ([P, INT, I64, I64, I64, P, I64, P, P], INT),
-    "intent_hbm_read_probe": ([P, I64, INT, P, P], INT),
+    "intent_hbm_read_probe": ([P, I64, INT, INT, P, I64, P], INT),
     "intent_mfma_peak_probe": ([INT, I64, I64, P, P], INT),
 }
 

@@ -126,6 +126,10 @@ extern "C" int intent_i8_per_token_quantize(const void* x, int x_is_bf16, int64_
   INTENT_REQUIRE(M >= 0 && K >= 0 && M <= INT32_MAX && K <= INT32_MAX, INTENT_ERR_INVALID_ARGUMENT,
                  "bad extents (M=%lld K=%lld)", (long long)M, (long long)K);
   INTENT_REQUIRE(K % 8 == 0, INTENT_ERR_UNSUPPORTED, "K must be a multiple of 8, got %lld", (long long)K);
+  // one 256-lane workgroup per row: the grid's work items stay below 2^32
+  INTENT_REQUIRE(M < ((int64_t)1 << 24), INTENT_ERR_UNSUPPORTED,
+                 "M=%lld rows exceed the %lld a launch covers (one 256-lane workgroup per row)", (long long)M,
+                 (long long)((int64_t)1 << 24));
   if (M == 0) return INTENT_OK;
   INTENT_REQUIRE(scales != nullptr, INTENT_ERR_INVALID_ARGUMENT, "null scales");
   if (K > 0) {  // empty rows read and write nothing but their zero scales

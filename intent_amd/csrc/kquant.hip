@@ -13,6 +13,7 @@
 // from +0. The kernels reproduce that order exactly, so results are bit-equal
 // to a sequential CPU evaluation.
 #include "common.h"
+#include <atomic>
 #include <mutex>
 
 #include "internal.h"
@@ -352,7 +353,7 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
-uint8_t* g_scratch_ptr[kMaxDevices] = {};
+std::atomic<uint8_t*> g_scratch_ptr[kMaxDevices] = {};
 
 // Device address of the current device's `scratch` (looked up once per device,
 // with that device current; the array's name is not a device address in host code).
@@ -361,16 +362,22 @@ int current_scratch(uint8_t** out) {
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return intent::fail(INTENT_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
   if (dev < 0 || dev >= kMaxDevices) return intent::fail(INTENT_ERR_UNSUPPORTED, "device %d out of range", dev);
-  std::lock_guard<std::mutex> lock(g_scratch_mutex);
-  if (g_scratch_ptr[dev] == nullptr) {
-    void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || p == nullptr)
-      return intent::fail(INTENT_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
-                          hipGetErrorString(e));
-    g_scratch_ptr[dev] = (uint8_t*)p;
+  // after the first call on a device the address is read without the lock
+  uint8_t* known = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (known == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    known = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (known == nullptr) {
+      void* p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || p == nullptr)
+        return intent::fail(INTENT_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                            hipGetErrorString(e));
+      known = (uint8_t*)p;
+      g_scratch_ptr[dev].store(known, std::memory_order_release);
+    }
   }
-  *out = g_scratch_ptr[dev];
+  *out = known;
   return INTENT_OK;
 }
 

@@ -6,12 +6,13 @@
 // 16 bytes at t, t + 256, ... (U loads, all issued before any is used). The
 // values are folded with XOR and stored only if they hit a magic word, which
 // keeps the loads live without writing anything in practice.
+#include "../../include/intent_amd_probes.h"
 #include "common.h"
 #include "internal.h"
 
 namespace {
 
-template <int U>
+template <int U, bool kStore>
 __global__ __launch_bounds__(256) void hbm_read_probe_kernel(const u32x4* __restrict__ src, int64_t n16,
                                                              uint32_t* __restrict__ sink) {
   const int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x;
@@ -24,14 +25,27 @@ __global__ __launch_bounds__(256) void hbm_read_probe_kernel(const u32x4* __rest
   uint32_t s = 0;
 #pragma unroll
   for (int i = 0; i < U; ++i) s ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
-  if (s == 0x9e3779b9u) sink[blockIdx.x & 255] = s;
+  if (kStore) {
+    // every lane's value decides whether it stores, so no lane's loads can
+    // be dropped; lane 0 always stores (a lane on a hash hit rewrites the
+    // second word of its wave's pair)
+    const int lane = threadIdx.x & 63;
+    const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (lane == 0) *reinterpret_cast<u32x2*>(sink + 2 * w) = u32x2{s, s ^ 1u};
+    else if (s == 0x9e3779b9u) sink[2 * w + 1] = s;
+  } else if (s == 0x9e3779b9u) {
+    sink[blockIdx.x & 255] = s;
+  }
 }
 
 template <int U>
-void launch_probe(const void* buf, int64_t n16, uint32_t* sink, hipStream_t st) {
+void launch_probe(const void* buf, int64_t n16, bool store, uint32_t* sink, hipStream_t st) {
   const int64_t per = 256 * U;
   const unsigned blocks = (unsigned)((n16 + per - 1) / per);
-  hipLaunchKernelGGL(hbm_read_probe_kernel<U>, dim3(blocks), dim3(256), 0, st, (const u32x4*)buf, n16, sink);
+  if (store)
+    hipLaunchKernelGGL((hbm_read_probe_kernel<U, true>), dim3(blocks), dim3(256), 0, st, (const u32x4*)buf, n16, sink);
+  else
+    hipLaunchKernelGGL((hbm_read_probe_kernel<U, false>), dim3(blocks), dim3(256), 0, st, (const u32x4*)buf, n16, sink);
 }
 
 // MFMA issue-rate probe: every wave runs `iters` rounds of four independent
@@ -85,19 +99,27 @@ extern "C" int intent_mfma_peak_probe(int kind, int64_t iters, int64_t workgroup
   return intent::launch_status_fmt("mfma_peak_probe_kernel<%d>", kind);
 }
 
-extern "C" int intent_hbm_read_probe(const void* buf, int64_t bytes, int unroll, uint32_t* sink, void* stream) {
+extern "C" int intent_hbm_read_probe(const void* buf, int64_t bytes, int unroll, int store, uint32_t* sink,
+                                     int64_t sink_words, void* stream) {
   INTENT_REQUIRE(buf && sink, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
   INTENT_REQUIRE(bytes > 0 && bytes % 16 == 0, INTENT_ERR_INVALID_ARGUMENT, "bytes must be a positive multiple of 16");
-  INTENT_REQUIRE(intent::aligned16(buf), INTENT_ERR_ALIGNMENT, "buffer must be 16-byte aligned");
+  INTENT_REQUIRE(intent::aligned16(buf) && intent::aligned4(sink), INTENT_ERR_ALIGNMENT,
+                 "buffer must be 16-byte aligned, sink 4-byte aligned");
+  INTENT_REQUIRE(unroll == 1 || unroll == 2 || unroll == 4 || unroll == 8 || unroll == 16, INTENT_ERR_UNSUPPORTED,
+                 "unroll must be 1, 2, 4, 8 or 16, got %d", unroll);
+  INTENT_REQUIRE(store == 0 || store == 1, INTENT_ERR_INVALID_ARGUMENT, "store must be 0 or 1, got %d", store);
+  const int64_t waves = 4 * ((bytes + 4096LL * unroll - 1) / (4096LL * unroll));
+  const int64_t need = store ? 2 * waves : 256;
+  INTENT_REQUIRE(sink_words >= need, INTENT_ERR_INVALID_ARGUMENT, "sink needs %lld words, got %lld", (long long)need,
+                 (long long)sink_words);
   const int64_t n16 = bytes / 16;
   hipStream_t st = (hipStream_t)stream;
   switch (unroll) {
-    case 1: launch_probe<1>(buf, n16, sink, st); break;
-    case 2: launch_probe<2>(buf, n16, sink, st); break;
-    case 4: launch_probe<4>(buf, n16, sink, st); break;
-    case 8: launch_probe<8>(buf, n16, sink, st); break;
-    case 16: launch_probe<16>(buf, n16, sink, st); break;
-    default: return intent::fail(INTENT_ERR_UNSUPPORTED, "unroll must be 1, 2, 4, 8 or 16, got %d", unroll);
+    case 1: launch_probe<1>(buf, n16, store, sink, st); break;
+    case 2: launch_probe<2>(buf, n16, store, sink, st); break;
+    case 4: launch_probe<4>(buf, n16, store, sink, st); break;
+    case 8: launch_probe<8>(buf, n16, store, sink, st); break;
+    default: launch_probe<16>(buf, n16, store, sink, st); break;
   }
-  return intent::launch_status_fmt("hbm_read_probe_kernel<%d>", unroll);
+  return intent::launch_status_fmt("hbm_read_probe_kernel<%d, %s>", unroll, store ? "true" : "false");
 }

@@ -64,10 +64,20 @@ def config3_w8a8(seed: int = 0, M: int = 4096, K: int = 8192, N: int = 8192) -> 
     return {"a": a, "a_scales": sa, "w": w, "w_scales": sw}
 
 
+def _config4_logits(rng, T: int, E: int) -> np.ndarray:
+    return rng.standard_normal((T, E), dtype=np.float32)
+
+
+def config4_logits(seed: int = 0, T: int = 512, E: int = 8) -> np.ndarray:
+    """The router logits of config4_moe(seed, T=T, E=E) (its first draw), without
+    drawing the expert weights."""
+    return _config4_logits(np.random.default_rng(seed), T, E)
+
+
 def config4_moe(seed: int = 0, T: int = 512, H: int = 4096, E: int = 8, top_k: int = 2, F: int = 14336,
                 group: int = 128) -> dict:
     rng = np.random.default_rng(seed)
-    logits = rng.standard_normal((T, E), dtype=np.float32)
+    logits = _config4_logits(rng, T, E)
     x = normal_f16(rng, (T, H))
     wgu = np.empty((E, 2 * F, H // 2), np.uint8)
     sgu = np.empty((E, 2 * F, H // group), np.float16)

@@ -1,4 +1,4 @@
-"""The C ABI: every symbol declared in include/intent_amd.h is exported, and the
+"""The C ABI: every symbol declared in include/*.h is exported, and the
 argument checks that run before any HIP call return the documented status codes.
 CPU only: no call here reaches a kernel launch."""
 import ctypes
@@ -10,11 +10,11 @@ import pytest
 from intent_amd import _native
 from intent_amd import errors
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "intent_amd.h"
+HEADERS = sorted((Path(__file__).resolve().parent.parent / "include").glob("*.h"))
 
 
 def declared_symbols():
-    text = HEADER.read_text()
+    text = "\n".join(h.read_text() for h in HEADERS)
     return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(intent_\w+)\s*\(", text, re.M)))
 
 
@@ -124,6 +124,19 @@ def test_kquant_checks():
     assert status("intent_q4k_q8k_gemv", FAKE, 0, 3, 432, FAKE, FAKE, None) == 0  # N = 0
     assert status("intent_q4k_projection", FAKE, 4, 3, 432, FAKE + 8, 256, FAKE, FAKE, None) == \
         errors.INTENT_ERR_ALIGNMENT
+
+
+def test_probe_checks():
+    e = errors
+    rp = "intent_hbm_read_probe"
+    assert status(rp, P(FAKE), 4095, 1, 0, P(FAKE), 256, None) == e.INTENT_ERR_INVALID_ARGUMENT  # bytes % 16
+    assert status(rp, P(FAKE), 4096, 3, 0, P(FAKE), 256, None) == e.INTENT_ERR_UNSUPPORTED  # unroll
+    assert status(rp, P(FAKE), 4096, 1, 2, P(FAKE), 256, None) == e.INTENT_ERR_INVALID_ARGUMENT  # store flag
+    assert status(rp, P(FAKE), 4096, 1, 0, P(FAKE), 255, None) == e.INTENT_ERR_INVALID_ARGUMENT  # sink < 256
+    # store mode: one workgroup of four waves per 4096 bytes at unroll 1, two words per wave
+    assert status(rp, P(FAKE), 65536, 1, 1, P(FAKE), 127, None) == e.INTENT_ERR_INVALID_ARGUMENT
+    assert status(rp, P(FAKE + 8), 4096, 1, 0, P(FAKE), 256, None) == e.INTENT_ERR_ALIGNMENT
+    assert status("intent_mfma_peak_probe", 0, 0, 1, P(FAKE), None) == e.INTENT_ERR_INVALID_ARGUMENT
 
 
 def test_status_mapping():

@@ -265,6 +265,24 @@ def test_moe_align(gpu, T, k, E, B):
         assert np.array_equal(host(got), ref), name
 
 
+@pytest.mark.parametrize("B", [128, 160])
+def test_moe_route_align_config4(gpu, B):
+    """Routing and alignment of BASELINE config 4's own router logits (seed 0,
+    T=512, E=8, top-2, renormalised): ids, sorted route ids, block map and
+    offsets equal the oracle's exactly; 160 is the block size the composite
+    uses at this shape."""
+    logits = inputs.config4_logits(0, T=512, E=8)
+    assert np.array_equal(logits, inputs.config4_moe(0, T=512, H=64, E=8, top_k=2, F=64)["logits"])
+    ids, wts = art(intent.moe_route_topk, TOP_K=2, RENORMALIZE=True).run(dev(logits))
+    rid, rw = oracle.moe_route(logits, 2, True)
+    assert np.array_equal(host(ids), rid)
+    np.testing.assert_allclose(host(wts), rw, rtol=2e-6, atol=1e-7)
+    outs = art(intent.moe_align_block_size, EXPERTS=8, BLOCK_SIZE=B).run(ids)
+    refs = oracle.moe_align(rid, 8, B)
+    for got, ref, name in zip(outs, refs, ("sorted", "blocks", "offsets", "total")):
+        assert np.array_equal(host(got), ref), name
+
+
 # ---- MoE expert FFN -----------------------------------------------------------------
 
 def moe_small(seed, T, H, E, k, F, group=128):

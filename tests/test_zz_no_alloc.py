@@ -45,3 +45,33 @@ def test_noalloc_rejects_oversize(gpu):
                                                              torch.cuda.current_stream().cuda_stream)
     assert status == errors.INTENT_ERR_UNSUPPORTED
     assert "allocation-free limit" in _native.last_error()
+
+
+@pytest.mark.parametrize("N,K", [(1000, 8192), (333, 32768)])
+def test_noalloc_under_graph_capture(gpu, N, K):
+    """The use the entry exists for: after one eager call on the device it is
+    captured in a HIP graph (nothing allocated inside the capture) and replayed,
+    with eager work and synchronisations between replays; every replay equals
+    the workspace entry."""
+    d = inputs.kquant_projection(11, N=N, K=K)
+    w = torch.from_numpy(d["w"]).cuda()
+    x = torch.from_numpy(d["x"]).cuda()
+    G = K // 256
+    ref = _reference(w, x, N, G)
+    y = torch.full((N,), float("nan"), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        _native.call("intent_q4k_projection_noalloc", w.data_ptr(), N, G, G * 144, x.data_ptr(), 256, y.data_ptr(),
+                     stream.cuda_stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        _native.call("intent_q4k_projection_noalloc", w.data_ptr(), N, G, G * 144, x.data_ptr(), 256, y.data_ptr(),
+                     stream.cuda_stream)
+    for rep in range(3):
+        y.fill_(float("nan"))
+        _reference(w, x, N // 2, G)  # eager work on the same entry family between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), ref.view(torch.int32)), rep
