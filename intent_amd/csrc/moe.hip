@@ -537,10 +537,17 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_down_pk_kernel(
   char* bufs[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) bufs[b] = smem[b];
-  const int per_part = mblocks * ntiles;
-  const int part = blockIdx.x / per_part;
-  int mb, ct;
-  moe_tile_order(blockIdx.x - part * per_part, mblocks, ntiles, mb, ct);
+  // XCD-owned (row block, K part) pairs: workgroup b runs on XCD b % 8, and
+  // an XCD runs every column tile of the pairs it owns (pair p = mb * splits
+  // + part goes to XCD p % 8), so each pair's activation rows are fetched
+  // into one L2 once, and each weight tile is still read by one workgroup.
+  // (Spreading every pair's column tiles over all eight XCDs fetched the
+  // activation rows, the larger operand of a down tile, eight times.)
+  const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
+  const int pidx = xcd + 8 * (local / ntiles);
+  if (pidx >= mblocks * splits) return;
+  const int ct = local % ntiles;
+  const int mb = pidx / splits, part = pidx % splits;
   const int n0 = ct * T::BN;
   const int e = blocks[mb];
   if (e < 0) return;
@@ -894,6 +901,12 @@ bool down_fast(const void* act, int64_t act_ld, int64_t block_size, const uint8_
          intent::aligned16(w_packed);
 }
 
+// Grid of moe_down_pk_kernel: every XCD runs ntiles column tiles for each
+// of the (row block, K part) pairs it owns, eight pairs per round of XCDs.
+int64_t down_pk_grid(int64_t splits, int64_t num_blocks, int64_t ntiles) {
+  return 8 * ntiles * ((splits * num_blocks + 7) / 8);
+}
+
 int down_generic(const void* act, int64_t act_ld, const int32_t* sorted, const int32_t* blocks, int64_t num_blocks,
                  int64_t block_size, int64_t R, const uint8_t* wq, const void* ws, const uint8_t* wz, int64_t H,
                  int64_t F, int64_t gs, float* out, int64_t out_ld, void* stream) {
@@ -913,7 +926,7 @@ int down_pk160_launch(const void* act, int64_t act_ld, const int32_t* sorted, co
                       int64_t F, int64_t gs, int splits, float* out, int64_t out_ld, int64_t part_stride,
                       void* stream) {
   const int64_t ntiles = (H + Pk160::BN - 1) / Pk160::BN;
-  const int64_t grid = splits * num_blocks * ntiles;
+  const int64_t grid = down_pk_grid(splits, num_blocks, ntiles);
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
   hipLaunchKernelGGL((moe_down_pk_kernel<true, Pk160, kPk160Stages>), dim3((unsigned)grid), dim3(Pk160::NT), 0,
                      (hipStream_t)stream, (const f16*)act, act_ld, sorted, blocks, (int)num_blocks, (int)ntiles, (int)R,
@@ -1081,7 +1094,7 @@ extern "C" int intent_moe_expert_ffn_w4(const float* router_logits, const void* 
       return intent::launch_status("moe_combine");
     }
     const int64_t ntiles = (H + GateUpPk::BN - 1) / GateUpPk::BN;
-    const int64_t grid = splits * L.nblocks * ntiles;
+    const int64_t grid = down_pk_grid(splits, L.nblocks, ntiles);
     INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "grid too large");
     auto kernel = group_size % 64 == 0 ? moe_down_pk_kernel<true> : moe_down_pk_kernel<false>;
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(GateUpPk::NT), 0, (hipStream_t)stream,
