@@ -120,32 +120,6 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
 }
 
 
-// 4 x 4 transpose of 16-byte pieces across the 16-lane rows of a wave: on
-// return, piece t of row g holds what piece g of row t held. v_permlane32_swap
-// exchanges the upper 32 lanes of its first operand with the lower 32 of its
-// second; v_permlane16_swap exchanges the odd 16-lane rows of the first with
-// the even rows of the second.
-INTENT_DEVICE void rows16_transpose4(u32x4 (&v)[4]) {
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const auto a = __builtin_amdgcn_permlane32_swap(v[0][d], v[2][d], false, false);
-    v[0][d] = a[0];
-    v[2][d] = a[1];
-    const auto b = __builtin_amdgcn_permlane32_swap(v[1][d], v[3][d], false, false);
-    v[1][d] = b[0];
-    v[3][d] = b[1];
-  }
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const auto a = __builtin_amdgcn_permlane16_swap(v[0][d], v[1][d], false, false);
-    v[0][d] = a[0];
-    v[1][d] = a[1];
-    const auto b = __builtin_amdgcn_permlane16_swap(v[2][d], v[3][d], false, false);
-    v[2][d] = b[0];
-    v[3][d] = b[1];
-  }
-}
-
 // ---- 4 <= M <= 16: MFMA GEMV with every load issued up front ------------------
 // Same split and MFMA operand roles as w4a16_gemv_kernel: 16 weight rows per
 // workgroup, KW waves taking 128-wide K steps in turn, lane (r, quad) holding
@@ -158,17 +132,18 @@ INTENT_DEVICE void rows16_transpose4(u32x4 (&v)[4]) {
 //    contiguous row segments (wave w: row w), packed into LDS records and read
 //    back after one barrier (per-lane scattered u16/u8 loads cost 1.6 us at
 //    M = 16, K = N = 4096);
-//  * activations are loaded as 64 contiguous bytes per row and instruction
-//    (instruction j, quad q: bytes j*64 + q*16 of the step) and moved into
-//    operand order by a 4 x 4 transpose across the 16-lane rows
-//    (rows16_transpose4), so an instruction touches 16 row segments, not 64.
+//  * activations are loaded as whole cache lines, four rows x 256 bytes per
+//    instruction, and moved into operand order through a wave-private LDS
+//    stage (one write and one read of 16 bytes per lane and piece).
 // Activation rows r >= M lie past the end of the x buffer resource (its size
 // is exactly the bytes of rows 0..M-1), so their loads return zeros without a
 // memory access. The product of a step is exact in fp32; the KW partial tiles
 // are summed through LDS in wave order and rounded to f16 once.
 constexpr int kFrontMaxGroups = 256;
+constexpr int kFrontXRow = 272;  // bytes per activation row in a wave's LDS stage (256 + 16)
+constexpr int kFrontWRow = 144;  // bytes per weight row in a wave's LDS stage (128 + 16)
 
-template <int KW, int SPW>
+template <int KW, int SPW, bool kPairRec>
 __global__ __launch_bounds__(64 * KW) void w4a16_gemv_front_kernel(
     const f16* __restrict__ x, int ldx, int x_bytes, const uint8_t* __restrict__ wq, int ldw,
     const f16* __restrict__ sc, const uint8_t* __restrict__ zp, int ldq, int nsteps, int G, float inv_cpg, int N,
@@ -176,17 +151,42 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_front_kernel(
   static_assert(KW == 16, "the record fetch gives wave w row w");
   __shared__ f32x4 red[KW][64];
   __shared__ uint32_t rec[16][kFrontMaxGroups];
+  __shared__ __attribute__((aligned(16))) uint8_t xstage[KW][16 * kFrontXRow];
+  // SPW == 2: a wave's two steps are adjacent, so its 16 weight rows are 128
+  // contiguous bytes each, loaded as whole lines and sorted through LDS.
+  constexpr bool kLineW = SPW == 2;
+  __shared__ __attribute__((aligned(16))) uint8_t wstage[kLineW ? KW : 1][kLineW ? 16 * kFrontWRow : 16];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15;
   const int quad = lane >> 4;
   const int n0 = blockIdx.x * 16;
   const int nr = n0 + r < N ? r : N - 1 - n0;  // tail rows compute on a valid row; their outputs are dropped
+  // Step i of a wave: adjacent steps with whole-line weight loads, else
+  // interleaved (wave w takes w, w + KW, ...).
+  auto step_of = [](int w, int i) { return kLineW ? SPW * w + i : w + KW * i; };
 
   // Records of row n0 + wave (clamped): groups lane, lane + 64, ...
-  constexpr int RPL = kFrontMaxGroups / 64;
+  // kPairRec (G even, 4-byte scale rows, 2-byte zero rows): item t of the
+  // workgroup = (row t / G2, group pair t % G2), a scale dword and a zero
+  // u16 per item, 16 * G2 items over the 1024 threads (8 instructions at
+  // G = 32 instead of 32).
+  constexpr int RPL = kPairRec ? (16 * kFrontMaxGroups / 2 + 64 * KW - 1) / (64 * KW) : kFrontMaxGroups / 64;
   uint32_t sq[RPL], zq[RPL];
-  {
+  const int G2 = G >> 1;
+  if constexpr (kPairRec) {
+#pragma unroll
+    for (int u = 0; u < RPL; ++u) {
+      const int t = threadIdx.x + 64 * KW * u;
+      if (64 * KW * u < 16 * G2) {  // uniform
+        const int row = min(t / G2, 15);
+        const int rn = n0 + row < N ? row : N - 1 - n0;
+        const int p = t < 16 * G2 ? t - row * G2 : 0;
+        sq[u] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(sc + (int64_t)n0 * ldq), (rn * ldq + 2 * p) * 2, 0, 0);
+        zq[u] = __builtin_amdgcn_raw_buffer_load_b16(make_rsrc(zp + (int64_t)n0 * ldq), rn * ldq + 2 * p, 0, 0);
+      }
+    }
+  } else {
     const int rn = n0 + wave < N ? wave : N - 1 - n0;
     const auto srs = make_rsrc(sc + (int64_t)(n0 + rn) * ldq);
     const auto zrs = make_rsrc(zp + (int64_t)(n0 + rn) * ldq);
@@ -204,21 +204,81 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_front_kernel(
   const auto wrs = make_rsrc(wq + (int64_t)n0 * ldw);
   const auto xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(x), (short)0, x_bytes, 0x00020000);
   const int wvo = nr * ldw + quad * 16;
-  const int xvo = r * ldx * 2 + quad * 16;
-  u32x4 wv[SPW], xv[SPW][4];
+  // Activations of a step: load j covers rows 4j .. 4j + 3 x 256 contiguous
+  // bytes (lane l: row 4j + l / 16, bytes (l % 16) * 16), eight whole cache
+  // lines per instruction. (Loading each lane's own 64-byte row segment
+  // directly, 16 rows x 64 bytes per instruction, took 2.3 us longer at
+  // M = 16, K = N = 4096: the same bytes, twice the lines per instruction.)
+  const int xvo = (lane >> 4) * ldx * 2 + (lane & 15) * 16;
+  // All activation loads (L2 hits after the first workgroups) go out before
+  // the weight loads (HBM): behind the weight misses they waited for slots.
+  u32x4 wv[SPW], xl[SPW][4];
 #pragma unroll
   for (int i = 0; i < SPW; ++i) {
-    const int s = min(wave + KW * i, nsteps - 1);
-    wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo, s * 64, 0);
+    const int s = min(step_of(wave, i), nsteps - 1);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) xv[i][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo, s * 256 + j * 64, 0);
+    for (int j = 0; j < 4; ++j)
+      xl[i][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvo, 4 * j * ldx * 2 + s * 256, 0);
+  }
+  u32x4 wl[2];
+  if constexpr (kLineW) {
+    // load h: rows 8h .. 8h + 7 x 128 bytes (lane l: row 8h + l / 8, step
+    // 2 * wave + (l % 8) / 4, bytes (l % 4) * 16 of it)
+    const int ls = min(2 * wave + ((lane & 7) >> 2), nsteps - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int row = 8 * h + (lane >> 3);
+      const int rr = n0 + row < N ? row : N - 1 - n0;
+      wl[h] = __builtin_amdgcn_raw_buffer_load_b128(wrs, rr * ldw + ls * 64 + (lane & 3) * 16, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      const int s = min(step_of(wave, i), nsteps - 1);
+      wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo, s * 64, 0);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 
+  if constexpr (kPairRec) {
 #pragma unroll
-  for (int u = 0; u < RPL; ++u)
-    if (u * 64 < G && lane + u * 64 < G) rec[wave][lane + u * 64] = (sq[u] & 0xffffu) | ((zq[u] & 0xffu) << 16);
+    for (int u = 0; u < RPL; ++u) {
+      const int t = threadIdx.x + 64 * KW * u;
+      if (t < 16 * G2) {
+        const int row = t / G2, p = t - row * G2;
+        rec[row][2 * p] = (sq[u] & 0xffffu) | ((zq[u] & 0xffu) << 16);
+        rec[row][2 * p + 1] = (sq[u] >> 16) | ((zq[u] & 0xff00u) << 8);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < RPL; ++u)
+      if (u * 64 < G && lane + u * 64 < G) rec[wave][lane + u * 64] = (sq[u] & 0xffffu) | ((zq[u] & 0xffu) << 16);
+  }
   __syncthreads();
+
+  // Into operand order through the wave's own LDS rows (no barrier: a wave's
+  // LDS operations complete in order): lane (r, quad) then reads piece t =
+  // k step*128 + quad*32 + t*8 .. + 8 of row r. Rows are 272 bytes apart, so
+  // the 16 rows of a read fall into different banks.
+  uint8_t* xw = xstage[wave];
+  u32x4 xv[SPW][4];
+#pragma unroll
+  for (int i = 0; i < SPW; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4*>(xw + (4 * j + (lane >> 4)) * kFrontXRow + (lane & 15) * 16) = xl[i][j];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) xv[i][t] = *reinterpret_cast<const u32x4*>(xw + r * kFrontXRow + quad * 64 + t * 16);
+  }
+  if constexpr (kLineW) {
+    uint8_t* ww = wstage[wave];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      *reinterpret_cast<u32x4*>(ww + (8 * h + (lane >> 3)) * kFrontWRow + (lane & 7) * 16) = wl[h];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) wv[i] = *reinterpret_cast<const u32x4*>(ww + r * kFrontWRow + i * 64 + quad * 16);
+  }
 
   // No branch on a step's validity (a branch lets the compiler sink that
   // step's loads behind the first wait): a step past K, a repeat of the last
@@ -226,11 +286,10 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_front_kernel(
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < SPW; ++i) {
-    const int sraw = wave + KW * i;
+    const int sraw = step_of(wave, i);
     const int s = min(sraw, nsteps - 1);
     const int g = (int)(((float)(s * 4 + quad) + 0.5f) * inv_cpg);  // chunk -> group (exact for these magnitudes)
     const uint32_t rq = rec[r][g];
-    rows16_transpose4(xv[i]);
     const f16x2 zoff = splat2((f16)(float)(1024 + (rq >> 16)));
     const f16x2 scale = splat2(sraw < nsteps ? bit_cast<f16>((uint16_t)rq) : (f16)0.0f);
 #pragma unroll
@@ -791,8 +850,15 @@ template <int SPW>
 void launch_front(const f16* x, int64_t ldx, int M, int K, const uint8_t* wq, int64_t ldw, const f16* sc,
                   const uint8_t* zp, int64_t ldq, int gs, f16* y, int64_t ldy, int N, hipStream_t st) {
   const int x_bytes = (int)(((int64_t)(M - 1) * ldx + K) * 2);
-  hipLaunchKernelGGL((w4a16_gemv_front_kernel<16, SPW>), dim3((N + 15) / 16), dim3(1024), 0, st, x, (int)ldx, x_bytes,
-                     wq, (int)ldw, sc, zp, (int)ldq, K / 128, K / gs, 32.0f / (float)gs, N, y, (int)ldy, M);
+  const bool pair = (K / gs) % 2 == 0 && ldq % 2 == 0 && (reinterpret_cast<uintptr_t>(sc) & 3) == 0 &&
+                    (reinterpret_cast<uintptr_t>(zp) & 1) == 0;
+  if (pair)
+    hipLaunchKernelGGL((w4a16_gemv_front_kernel<16, SPW, true>), dim3((N + 15) / 16), dim3(1024), 0, st, x, (int)ldx,
+                       x_bytes, wq, (int)ldw, sc, zp, (int)ldq, K / 128, K / gs, 32.0f / (float)gs, N, y, (int)ldy, M);
+  else
+    hipLaunchKernelGGL((w4a16_gemv_front_kernel<16, SPW, false>), dim3((N + 15) / 16), dim3(1024), 0, st, x,
+                       (int)ldx, x_bytes, wq, (int)ldw, sc, zp, (int)ldq, K / 128, K / gs, 32.0f / (float)gs, N, y,
+                       (int)ldy, M);
 }
 
 template <int NT, int KW>
@@ -880,7 +946,10 @@ int w4a16_gemv_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, const u
       launch_front<2>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
     else
       launch_front<4>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
-    return launch_status_fmt("w4a16_gemv_front_kernel<16, %d>", steps <= 16 ? 1 : steps <= 32 ? 2 : 4);
+    const bool pair = (K / gs) % 2 == 0 && qparam_ld % 2 == 0 && (reinterpret_cast<uintptr_t>(ss) & 3) == 0 &&
+                      (reinterpret_cast<uintptr_t>(zeros) & 1) == 0;
+    return launch_status_fmt("w4a16_gemv_front_kernel<16, %d, %s>", steps <= 16 ? 1 : steps <= 32 ? 2 : 4,
+                             pair ? "true" : "false");
   }
   if (steps >= 16)
     launch_gemv<1, 16>(xx, x_ld, (int)M, (int)K, packed, packed_ld, ss, zeros, qparam_ld, (int)gs, yy, y_ld, (int)N, st);
