@@ -49,13 +49,14 @@ def parse():
                     help="'decode' times only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--probe", choices=["traffic", "read", "mfma"], default=None,
+    ap.add_argument("--probe", choices=["traffic", "read", "mfma", "kn"], default=None,
                     help="'traffic': only run 40 decode launches over distinct weight copies, then four 64 MiB "
                          "device copies (run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE; the copies calibrate "
                          "the counters). 'read': time the plain HBM read of the decode's byte count (the floor "
                          "of any kernel streaming those bytes) beside the decode GEMV itself. 'mfma': three "
                          "launches each of the compute-bound lines (prefill, W8A8, MoE), for rocprofv3 --pmc "
-                         "MFMA-busy counters")
+                         "MFMA-busy counters. 'kn': the scaled FP8 GEMM (N=14336, K=4096) with its [K, N] "
+                         "operand read in place against the transposed copy plus the row-form kernel, over M")
     return ap.parse_args()
 
 
@@ -234,7 +235,7 @@ def bench_w4a8(steps: int, warmup: int) -> dict:
 def bench_sfp8_splitk(steps: int, warmup: int) -> dict:
     """The reference's split-K FP8 case (experiments/gpu/providers/triton/contraction.py:174-186):
     M=4096, N=14336, K=4096 as [IT=4, SP=4, 256], E4M3FN, scales 1, f16 InOut output. The
-    timed operator includes the transpose of the [K, N] right operand."""
+    [K, N] right operand is read in place."""
     import torch
 
     import intent_amd as intent
@@ -562,6 +563,46 @@ def mfma_probe() -> None:
     log("[probe] moe done")
 
 
+def kn_probe() -> None:
+    """Scaled FP8 GEMM, N=14336, K=4096, plain and split-K (SP 4): the [K, N] operand
+    read in place (intent_scaled_fp8_gemm_kn) against intent_fp8_transpose followed by
+    the row-form kernel, one JSON line per M (graph-timed, operands resident)."""
+    import torch
+
+    from intent_amd import _native
+
+    N, K = 14336, 4096
+    g = torch.Generator(device="cuda").manual_seed(0)
+    b = torch.randn((K, N), device="cuda", generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+    bt = torch.empty((N, K), dtype=torch.uint8, device="cuda")
+
+    def stream():
+        return torch.cuda.current_stream().cuda_stream
+
+    for M in (256, 512, 1024, 2048, 4096):
+        a = torch.randn((M, K), device="cuda", generator=g).to(torch.float8_e4m3fn).view(torch.uint8)
+        o = torch.zeros((M, N), device="cuda", dtype=torch.float16)
+        for sp in (1, 4):
+            def in_place(a=a, o=o, sp=sp, M=M):
+                _native.call("intent_scaled_fp8_gemm_kn", a.data_ptr(), M, K, K, b.data_ptr(), N, N, 1.0, 1.0, sp,
+                             int(sp > 1), o.data_ptr(), N, stream())
+
+            def transpose():
+                _native.call("intent_fp8_transpose", b.data_ptr(), K, N, N, bt.data_ptr(), K, stream())
+
+            def copy_rows(a=a, o=o, sp=sp, M=M):
+                transpose()
+                _native.call("intent_scaled_fp8_gemm", a.data_ptr(), M, K, K, bt.data_ptr(), N, K, 1.0, 1.0, sp,
+                             int(sp > 1), o.data_ptr(), N, stream())
+
+            row = {"probe": "fp8_kn", "M": M, "N": N, "K": K, "splits": sp,
+                   "in_place_us": round(graph_time([in_place], 30, 3) * 1e3, 1),
+                   "copy_plus_rows_us": round(graph_time([copy_rows], 30, 3) * 1e3, 1)}
+            if M == 256 and sp == 1:
+                row["copy_alone_us"] = round(graph_time([transpose], 30, 3) * 1e3, 1)
+            print(json.dumps(row), flush=True)
+
+
 def _numa_physical_cores(limit: int = 16) -> list[int]:
     """Up to `limit` physical cores (one hardware thread each) of one NUMA node, within this
     process's affinity: the node holding the most allowed cores."""
@@ -681,6 +722,9 @@ def main() -> int:
         return 0
     if args.probe == "mfma":
         mfma_probe()
+        return 0
+    if args.probe == "kn":
+        kn_probe()
         return 0
     arch = _native.device_arch(0)
     log(f"[bench] device 0: {arch}; decode M=1 steps={args.steps} warmup={args.warmup}")

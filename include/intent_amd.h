@@ -135,6 +135,18 @@ int intent_i8_gemm_i32(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
                        int32_t* c, int64_t c_ld, void* stream);
 
 /*
+ * The same contraction with the weight as the reference's gemm_i8 passes it
+ * (examples/kernels/contraction/gemm.py:29-39, b [K, N], N contiguous, b_ld
+ * bytes), read in place (no transposed copy):
+ * c[m,n] = sum_k i32(a[m,k]) * i32(b[k,n]) + bias[n], modulo 2^32.
+ * K a positive multiple of 128, N % 16 == 0, 16-byte aligned rows.
+ */
+int intent_i8_gemm_i32_kn(const int8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                          const int8_t* b, int64_t N, int64_t b_ld,
+                          const int32_t* bias,
+                          int32_t* c, int64_t c_ld, void* stream);
+
+/*
  * MoE router: per token, top_k experts by logit (ties -> lower expert index)
  * and their softmax probabilities (fp32, over all E experts; renormalised
  * over the selected top_k when `renormalize` != 0).
@@ -391,6 +403,17 @@ int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
                            const uint8_t* bt, int64_t N, int64_t bt_ld,
                            float a_scale, float b_scale, int64_t splits, int accumulate,
                            void* out, int64_t out_ld, void* stream);
+
+/* intent_scaled_fp8_gemm with the right operand as the reference passes it:
+ * b [K, N] E4M3FN (N contiguous, b_ld bytes), read in place (no transposed
+ * copy). Same semantics, splits and K rules; additionally N % 16 == 0.
+ * Replaces the same functions (block_scaled.py:42-63 and :66-98, whose rhs is
+ * [K, N] and [IT, SP, 256, N]).
+ */
+int intent_scaled_fp8_gemm_kn(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
+                              const uint8_t* b, int64_t N, int64_t b_ld,
+                              float a_scale, float b_scale, int64_t splits, int accumulate,
+                              void* out, int64_t out_ld, void* stream);
 
 /* DeepGEMM-style FP8 GEMM with f32 block scales. Replaces deepgemm_fp8_2xacc
  * (examples/kernels/contraction/block_scaled.py:101-122; CPU baseline

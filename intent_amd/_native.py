@@ -38,6 +38,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_w4a16_gemm": ([P, I64, I64, I64, P, I64, I64, P, P, I64, I64, P, I64, P], INT),
     "intent_w8a8_gemm": ([P, I64, I64, I64, P, P, I64, I64, P, P, I64, P], INT),
     "intent_i8_gemm_i32": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P], INT),
+    "intent_i8_gemm_i32_kn": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P], INT),
     "intent_moe_route": ([P, I64, I64, I64, INT, P, P, P], INT),
     "intent_moe_align": ([P, I64, I64, I64, I64, P, I64, P, I64, P, P, P], INT),
     "intent_moe_gate_up_w4": ([P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, P], INT),
@@ -53,6 +54,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_mxfp8_gemm": ([P, I64, I64, I64, P, I64, P, I64, I64, P, I64, P, I64, P], INT),
     "intent_fp8_transpose": ([P, I64, I64, I64, P, I64, P], INT),
     "intent_scaled_fp8_gemm": ([P, I64, I64, I64, P, I64, I64, F32, F32, I64, INT, P, I64, P], INT),
+    "intent_scaled_fp8_gemm_kn": ([P, I64, I64, I64, P, I64, I64, F32, F32, I64, INT, P, I64, P], INT),
     "intent_w4_sym_repack": ([P, I64, I64, I64, P, I64, I64, P, I64, P, P, I64, P], INT),
     "intent_f16_transpose": ([P, I64, I64, I64, P, I64, P], INT),
     "intent_quantized_gemm": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P, P, I64, P], INT),

@@ -231,6 +231,7 @@ struct SplitK {
 
 template <int ROWS, int NW, bool kScales>
 struct Rows {
+  static constexpr bool kKN = false;
   static constexpr int N_INST = ROWS / 8 / NW;  // data instructions per wave
   static_assert(N_INST * 8 * NW == ROWS && ROWS % 64 == 0, "tile rows must split evenly");
   // Scale dwords: 64 rows per instruction; a wave with none left repeats the
@@ -278,6 +279,84 @@ struct Rows {
   }
 };
 
+// The right operand as [K][N] bytes (N contiguous), read in place: no
+// transposed copy. A stage is 128 k-rows of the tile's 128 columns, 128 bytes
+// each (the size of the row form's stage). DMA instruction t fills LDS
+// kilobyte t, k-rows 8t..8t+7: lane i moves 16-byte slot i % 8 of k-row
+// 8t + i / 8, which holds column chunk (i % 8) ^ kn8_swz(k-row). Fragments
+// are read with ds_read_b64_tr_b8: inside a group of 16 lanes, lane j
+// addresses k-row k0 + j / 2, columns c0 + 8 (j % 2) .. + 7, and lane t
+// receives column c0 + t at k-rows k0 .. k0 + 7. Four such reads give a lane
+// the 32 k of one column that read_frag gives a row (chunks c and c + 2 of
+// the stage). One read touches, per half wave, 8 k-rows x 32 bytes; with the
+// swizzle the four k-rows of each parity hit four distinct 32-byte windows,
+// so those 16 pieces cover the 64 banks once.
+INTENT_DEVICE constexpr int kn8_swz(int krow) { return 2 * ((krow >> 1) & 3); }
+
+template <int COLS, int NW>
+struct KNBytes {
+  static constexpr bool kKN = true;
+  static_assert(COLS == 128, "128 columns: one 128-byte LDS row per k-row");
+  static constexpr int TOTAL = 16;  // kilobyte DMA instructions per stage
+  static constexpr int N_INST = TOTAL / NW;
+  static constexpr int NVM = N_INST;
+  static_assert(N_INST * NW == TOTAL, "stage instructions split evenly over the waves");
+  mp::Rsrc rd;
+  uint32_t voff[N_INST];
+  uint32_t ld;  // bytes per k-row
+  int wave;
+  // b: element (0, 0) of [K][N]; ldb bytes per k-row; n0: first column of the
+  // tile. Requires N % 16 == 0: column chunks past N re-read the last valid
+  // chunk (their products land in output columns that are never stored).
+  INTENT_DEVICE void init(const uint8_t* b, int64_t ldb, int N, int n0, int w) {
+    wave = w;
+    ld = (uint32_t)ldb;
+    rd = make_rsrc(b + n0);
+    const int lane = threadIdx.x & 63;
+    const int valid = N - n0;
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j) {
+      const int r = (j * NW + w) * 8 + (lane >> 3);
+      int col = ((lane & 7) ^ kn8_swz(r)) * 16;
+      col = col + 16 <= valid ? col : valid - 16;
+      voff[j] = (uint32_t)(r * ldb + col);
+    }
+  }
+  // koff: the stage's first k (the row form's byte offset inside a row).
+  INTENT_DEVICE void issue(char* rows, char*, uint32_t koff, int) const {
+#pragma unroll
+    for (int j = 0; j < N_INST; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (mp::lds_t*)(rows + (j * NW + wave) * 1024), 16, voff[j],
+                                               koff * ld, 0, 0);
+  }
+};
+
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2_t;
+
+INTENT_DEVICE i32x2 read_tr8(const char* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_t*)(__attribute__((address_space(3))) char*)p);
+}
+
+// Per-lane base of the transpose reads of column block j (wave-tile column
+// wn0 + 32 j): the lane's k-row inside an 8-row group is t / 2 (t = lane %
+// 16), so its swizzle is the same for every read.
+INTENT_DEVICE uint32_t kn8_base(int wn0, int j) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, t = lane & 15;
+  const int cc = wn0 / 16 + 2 * j + (g & 1);
+  const int kr = t >> 1;
+  return (uint32_t)(kr * 128 + ((cc ^ kn8_swz(kr)) << 4) + 8 * (t & 1) + (g >> 1) * 16 * 128);
+}
+
+// The lane's 32 bytes of step s (chunks 4s + h and 4s + 2 + h in k units of
+// 16, h = lane / 32, already in base): k-rows 64 s + {0, 8, 32, 40} + ...
+INTENT_DEVICE i32x8 read_frag_kn(const char* b, uint32_t base, int s) {
+  const char* p = b + base + s * 64 * 128;
+  const i32x2 q0 = read_tr8(p), q1 = read_tr8(p + 8 * 128), q2 = read_tr8(p + 32 * 128), q3 = read_tr8(p + 40 * 128);
+  return i32x8{q0[0], q0[1], q1[0], q1[1], q2[0], q2[1], q3[0], q3[1]};
+}
+
 // How a stage's per-row scale dwords are used.
 enum class ScaleMode {
   kNone,     // no scales: every block scale is E8M0 127 (2^0)
@@ -287,17 +366,20 @@ enum class ScaleMode {
              // folds it into the caller's own accumulators
   kHook,     // no scales; hook(acc, -, -, kt) runs after every stage (and may
              // consume and clear acc)
+  kInt8,     // no scales; int8 operands, exact int32 sums: each 64-k step is
+             // two v_mfma_i32_32x32x32_i8 over the two 16-byte halves
 };
 
 // acc += A·B over nk stages (stage kt at byte offset koff(kt) of every row).
 // T: a 4-wave tile whose rows are multiples of 64. Starts with a barrier, so
 // that it can run again on the same LDS, and ends with no DMA in flight.
 // kFmt: the operands' format code for the f8f6f4 MFMA (0 E4M3, 1 E5M2).
-template <class T, ScaleMode kMode, class KOff, class Hook, int kFmt = 0>
+// BOp: Rows (B as [N][K] rows) or KNBytes (B as [K][N], no scales).
+template <class T, ScaleMode kMode, class KOff, class Hook, int kFmt = 0,
+          class BOp = Rows<T::BN, T::NW, kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote>>
 INTENT_DEVICE void dma_mainloop(char* smem,
                                 const Rows<T::BM, T::NW, kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote>& aop,
-                                const Rows<T::BN, T::NW, kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote>& bop,
-                                int nk, KOff koff,
+                                const BOp& bop, int nk, KOff koff,
                                 i32x16 (&acc)[T::TI][T::TJ], Hook&& hook) {
   constexpr bool kScales = kMode == ScaleMode::kE8M0 || kMode == ScaleMode::kPromote;
   constexpr bool kHooked = kMode == ScaleMode::kPromote || kMode == ScaleMode::kHook;
@@ -305,7 +387,8 @@ INTENT_DEVICE void dma_mainloop(char* smem,
   constexpr int SB = ROWBYTES + (T::BM + T::BN) * 4;
   constexpr int A_SC = ROWBYTES;
   constexpr int B_SC = A_SC + T::BM * 4;
-  constexpr int NV = Rows<T::BM, T::NW, kScales>::NVM + Rows<T::BN, T::NW, kScales>::NVM;
+  constexpr int NV = Rows<T::BM, T::NW, kScales>::NVM + BOp::NVM;
+  static_assert(!(BOp::kKN && kScales), "the [K][N] operand carries no scales");
   static_assert(2 * NV < 64, "vmcnt range");
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5;
@@ -323,11 +406,18 @@ INTENT_DEVICE void dma_mainloop(char* smem,
   // stage's end.
   i32x8 af[2][T::TI], bf[2][T::TJ];
   uint32_t csa[T::TI], csb[T::TJ], nsa[T::TI], nsb[T::TJ];
+  uint32_t knb[T::TJ];
+  if constexpr (BOp::kKN) {
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j) knb[j] = kn8_base(T::wave_n() * T::WTN, j);
+  }
   auto read = [&](const char* base, int s, int set) {
 #pragma unroll
     for (int i = 0; i < T::TI; ++i) af[set][i] = read_frag(base, ra + 32 * i, 4 * s + h);
 #pragma unroll
-    for (int j = 0; j < T::TJ; ++j) bf[set][j] = read_frag(base + T::A_BYTES, rb + 32 * j, 4 * s + h);
+    for (int j = 0; j < T::TJ; ++j)
+      bf[set][j] = BOp::kKN ? read_frag_kn(base + T::A_BYTES, knb[j], s)
+                            : read_frag(base + T::A_BYTES, rb + 32 * j, 4 * s + h);
   };
   auto read_scales = [&](const char* base, uint32_t (&xa)[T::TI], uint32_t (&xb)[T::TJ]) {
 #pragma unroll
@@ -343,6 +433,14 @@ INTENT_DEVICE void dma_mainloop(char* smem,
     for (int i = 0; i < T::TI; ++i)
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j) {
+        if constexpr (kMode == ScaleMode::kInt8) {
+          const i32x8 x = bf[s][j], y = af[s][i];
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(i32x4{x[0], x[1], x[2], x[3]}, i32x4{y[0], y[1], y[2], y[3]},
+                                                           acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(i32x4{x[4], x[5], x[6], x[7]}, i32x4{y[4], y[5], y[6], y[7]},
+                                                           acc[i][j], 0, 0, 0);
+          continue;
+        }
         f32x16 c = bit_cast<f32x16>(acc[i][j]);
         if (kMode == ScaleMode::kPromote && s == 0) c = f32x16{};  // a fresh sum per stage
         const int sb_ = kMode == ScaleMode::kE8M0 ? (int)((csb[j] >> sh) & 255u) : 127;
@@ -352,16 +450,17 @@ INTENT_DEVICE void dma_mainloop(char* smem,
       }
   };
   // Schedule hint: each MFMA followed by its share of NR LDS reads (0x100).
+  constexpr int NMF = T::TI * T::TJ * (kMode == ScaleMode::kInt8 ? 2 : 1);  // MFMAs per step
   auto interleave = [&](auto NR) {
-    mp::static_for<0, T::TI * T::TJ>([&](auto X) {
+    mp::static_for<0, NMF>([&](auto X) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       constexpr int x = decltype(X)::value;
       constexpr int nr = decltype(NR)::value;
-      constexpr int r = (x + 1) * nr / (T::TI * T::TJ) - x * nr / (T::TI * T::TJ);
+      constexpr int r = (x + 1) * nr / NMF - x * nr / NMF;
       if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
     });
   };
-  constexpr int NR = 2 * (T::TI + T::TJ);  // ds_read_b128 per step
+  constexpr int NR = 2 * T::TI + (BOp::kKN ? 4 : 2) * T::TJ;  // LDS reads per step
 
   __syncthreads();  // a previous pass over this LDS is fully read
   issue(0, 0);
@@ -470,9 +569,11 @@ __global__ __launch_bounds__(256) void fp8_scaled_empty_k_kernel(f16* __restrict
   }
 }
 
-template <bool kAccum>
+// kKN: b is the [K][N] operand itself (N % 16 == 0), read in place
+// (mxdma::KNBytes); otherwise its [N][K] rows.
+template <bool kAccum, bool kKN>
 __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
-                                                                 const uint8_t* __restrict__ bt, int64_t ldb, int N,
+                                                                 const uint8_t* __restrict__ b, int64_t ldb, int N,
                                                                  int K, int splits, float ls, float rs,
                                                                  f16* __restrict__ out, int64_t ldo, int mblocks) {
   using T = TSk;
@@ -481,9 +582,12 @@ __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* 
   const int m0 = (blockIdx.x % mblocks) * T::BM;
   const int n0 = (blockIdx.x / mblocks) * T::BN;
   mxdma::Rows<T::BM, T::NW, false> aop;
-  mxdma::Rows<T::BN, T::NW, false> bop;
+  std::conditional_t<kKN, mxdma::KNBytes<T::BN, T::NW>, mxdma::Rows<T::BN, T::NW, false>> bop;
   aop.init(a, lda, M, nullptr, 0, m0, T::wave());
-  bop.init(bt, ldb, N, nullptr, 0, n0, T::wave());
+  if constexpr (kKN)
+    bop.init(b, ldb, N, n0, T::wave());
+  else
+    bop.init(b, ldb, N, nullptr, 0, n0, T::wave());
   const int nks = K / mp::ROWB / splits;
   // The lane's outputs: m = row(i), n = col(j, g) + q, as packed f16 pairs
   // o[i][j][2g + q/2] (64 registers).
@@ -552,6 +656,53 @@ __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* 
           if (n + 1 < N) dst[1] = lo[1];
           if (n + 2 < N) dst[2] = hi[0];
           if (n + 3 < N) dst[3] = hi[1];
+        }
+      }
+  }
+}
+
+// int8 GEMM with b [K][N] read in place (gemm_i8, examples/kernels/contraction/
+// gemm.py:29-39): c[m, n] = sum_k a[m, k] * b[k, n] + bias[n], int32 modulo
+// 2^32. The scaled-FP8 tiles (TSk) and DMA main loop with the int8 MFMA;
+// K % 128 == 0, N % 16 == 0.
+__global__ __launch_bounds__(256, 1) void i8_gemm_kn_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                            const uint8_t* __restrict__ b, int64_t ldb, int N, int K,
+                                                            const int32_t* __restrict__ bias, int32_t* __restrict__ c,
+                                                            int64_t ldc, int mblocks) {
+  using T = TSk;
+  constexpr int SB = (T::BM + T::BN) * (mp::ROWB + 4);
+  __shared__ __attribute__((aligned(1024))) char smem[2 * SB];
+  const int m0 = (blockIdx.x % mblocks) * T::BM;
+  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  mxdma::Rows<T::BM, T::NW, false> aop;
+  mxdma::KNBytes<T::BN, T::NW> bop;
+  aop.init(a, lda, M, nullptr, 0, m0, T::wave());
+  bop.init(b, ldb, N, n0, T::wave());
+  i32x16 acc[T::TI][T::TJ];
+  mxdma::zero(acc);
+  mxdma::dma_mainloop<T, mxdma::ScaleMode::kInt8>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, acc,
+                                                  mxdma::NoHook{});
+  const bool vec = (ldc & 3) == 0 && (((uintptr_t)c) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        int32_t* o = c + (int64_t)m * ldc + n;
+        uint32_t v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          v[q] = (uint32_t)acc[i][j][4 * g + q] + (uint32_t)(bias && n + q < N ? bias[n + q] : 0);
+        if (vec && n + 3 < N) {
+          *reinterpret_cast<i32x4*>(o) = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < N) o[q] = (int32_t)v[q];
         }
       }
   }
@@ -710,6 +861,52 @@ __global__ __launch_bounds__(256) void byte_transpose_kernel(const uint8_t* __re
   }
 }
 
+// Byte-matrix transpose of whole 128 x 128 tiles (R, C multiples of 128,
+// 16-byte aligned rows): dst[c][r] = src[r][c]. Each thread loads four
+// 16-byte row pieces into LDS (128-byte rows, 16-byte slot q of row r holding
+// column chunk q ^ tsw(r)), then builds four 16-byte pieces of output rows
+// from two ds_read_b64_tr_b8 each: inside a group of 16 lanes, lane j
+// addresses row k0 + j / 2, columns 16 cg + 8 (j % 2) .. + 7, and lane t
+// receives column 16 cg + t at rows k0 .. k0 + 7. Piece p = 16 w + 4 i + g
+// (wave w, step i, lane group g) is output rows 16 cg + t, cg = p / 8, at
+// source rows 16 rb .. + 15, rb = p % 8: the four groups of one store cover
+// 64 contiguous bytes of 16 output rows. In the 64 banks, the 16 pieces of
+// each half wave (8 rows of a group x 2 groups, rows 16 apart) fall on
+// distinct (row parity, slot) pairs thanks to the (r >> 4) term.
+INTENT_DEVICE constexpr int tsw(int r) { return (r & 7) ^ ((r >> 4) & 1); }
+
+__global__ __launch_bounds__(256) void byte_transpose128_kernel(const uint8_t* __restrict__ src, int64_t sld,
+                                                                uint8_t* __restrict__ dst, int64_t dld) {
+  __shared__ __attribute__((aligned(16))) uint8_t t[128 * 128];
+  const int64_t r0 = (int64_t)blockIdx.y * 128, c0 = (int64_t)blockIdx.x * 128;
+  const int tid = threadIdx.x;
+  u32x4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = i * 32 + (tid >> 3);
+    v[i] = *reinterpret_cast<const u32x4*>(src + (r0 + r) * sld + c0 + (tid & 7) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = i * 32 + (tid >> 3);
+    *reinterpret_cast<u32x4*>(&t[r * 128 + (((tid & 7) ^ tsw(r)) << 4)]) = v[i];
+  }
+  __syncthreads();
+  const int lane = tid & 63, w = tid >> 6, g = lane >> 4, j = lane & 15;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = 16 * w + 4 * i + g;
+    const int cg = p >> 3, rb = p & 7;
+    mxdma::i32x2 q[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = 16 * rb + 8 * h + (j >> 1);
+      q[h] = mxdma::read_tr8((const char*)t + r * 128 + ((cg ^ tsw(r)) << 4) + 8 * (j & 1));
+    }
+    *reinterpret_cast<i32x4*>(dst + (c0 + 16 * cg + j) * dld + r0 + 16 * rb) = i32x4{q[0][0], q[0][1], q[1][0], q[1][1]};
+  }
+}
+
 // 128 x 128 tiles, four waves of 64 x 64 (a 256 x 256 tile does not fit the
 // registers of eight waves once the 32-byte scaled-MFMA fragments are counted).
 using TMx128 = mp::Tile<128, 128, 2, 2>;
@@ -770,14 +967,21 @@ extern "C" int intent_fp8_transpose(const uint8_t* src, int64_t rows, int64_t co
   INTENT_REQUIRE(src_ld >= cols && dst_ld >= rows, INTENT_ERR_INVALID_ARGUMENT, "leading stride smaller than the row");
   const int64_t gx = (cols + 63) / 64, gy = (rows + 63) / 64;
   INTENT_REQUIRE(gx < (1ll << 31) && gy < 65536, INTENT_ERR_UNSUPPORTED, "fp8_transpose: grid too large");
+  if (rows % 128 == 0 && cols % 128 == 0 && intent::aligned16(src) && intent::aligned16(dst) && src_ld % 16 == 0 &&
+      dst_ld % 16 == 0) {
+    hipLaunchKernelGGL(byte_transpose128_kernel, dim3((unsigned)(cols / 128), (unsigned)(rows / 128)), dim3(256), 0,
+                       (hipStream_t)stream, src, src_ld, dst, dst_ld);
+    return intent::launch_status("fp8_transpose");
+  }
   hipLaunchKernelGGL(byte_transpose_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, (hipStream_t)stream, src,
                      (int)rows, (int)cols, src_ld, dst, dst_ld);
   return intent::launch_status("fp8_transpose");
 }
 
-extern "C" int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* bt,
-                                      int64_t N, int64_t bt_ld, float a_scale, float b_scale, int64_t splits,
-                                      int accumulate, void* out, int64_t out_ld, void* stream) {
+// b: [N][K] rows (kn false, K contiguous) or the [K][N] matrix (kn true).
+static int scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* b, int64_t N,
+                           int64_t b_ld, bool kn, float a_scale, float b_scale, int64_t splits, int accumulate,
+                           void* out, int64_t out_ld, void* stream) {
   intent::clear_error();
   INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
                  INTENT_ERR_INVALID_ARGUMENT, "bad extents");
@@ -797,24 +1001,60 @@ extern "C" int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, in
                        a_scale, b_scale, accumulate ? (int)splits : 0);
     return intent::launch_status("fp8_scaled_empty_k_kernel");
   }
-  INTENT_REQUIRE(a && bt && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
-  INTENT_REQUIRE(a_ld >= K && bt_ld >= K && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+  INTENT_REQUIRE(a && b && out, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(a_ld >= K && b_ld >= (kn ? N : K) && out_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
                  "leading stride smaller than the row");
-  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(bt) && a_ld % 16 == 0 && bt_ld % 16 == 0,
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(b) && a_ld % 16 == 0 && b_ld % 16 == 0,
                  INTENT_ERR_ALIGNMENT, "operand rows must be 16-byte aligned");
-  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(N, bt_ld), INTENT_ERR_UNSUPPORTED,
+  if (kn) INTENT_REQUIRE(N % 16 == 0, INTENT_ERR_UNSUPPORTED, "[K, N] operand: N must be a multiple of 16");
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(kn ? K : N, b_ld), INTENT_ERR_UNSUPPORTED,
                  "scaled_fp8_gemm: operand too large for 31-bit buffer offsets");
   const int mblocks = (int)((M + TSk::BM - 1) / TSk::BM);
   const int64_t grid = (int64_t)mblocks * ((N + TSk::BN - 1) / TSk::BN);
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "scaled_fp8_gemm: grid too large");
-  if (accumulate)
-    hipLaunchKernelGGL(fp8_scaled_gemm_kernel<true>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a, a_ld,
-                       (int)M, bt, bt_ld, (int)N, (int)K, (int)splits, a_scale, b_scale, (f16*)out, out_ld, mblocks);
-  else
-    hipLaunchKernelGGL(fp8_scaled_gemm_kernel<false>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a,
-                       a_ld, (int)M, bt, bt_ld, (int)N, (int)K, (int)splits, a_scale, b_scale, (f16*)out, out_ld,
-                       mblocks);
+  auto kernel = accumulate ? (kn ? fp8_scaled_gemm_kernel<true, true> : fp8_scaled_gemm_kernel<true, false>)
+                           : (kn ? fp8_scaled_gemm_kernel<false, true> : fp8_scaled_gemm_kernel<false, false>);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a, a_ld, (int)M, b, b_ld,
+                     (int)N, (int)K, (int)splits, a_scale, b_scale, (f16*)out, out_ld, mblocks);
   return intent::launch_status("scaled_fp8_gemm");
+}
+
+extern "C" int intent_scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* bt,
+                                      int64_t N, int64_t bt_ld, float a_scale, float b_scale, int64_t splits,
+                                      int accumulate, void* out, int64_t out_ld, void* stream) {
+  return scaled_fp8_gemm(a, M, K, a_ld, bt, N, bt_ld, false, a_scale, b_scale, splits, accumulate, out, out_ld,
+                         stream);
+}
+
+extern "C" int intent_scaled_fp8_gemm_kn(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint8_t* b,
+                                         int64_t N, int64_t b_ld, float a_scale, float b_scale, int64_t splits,
+                                         int accumulate, void* out, int64_t out_ld, void* stream) {
+  return scaled_fp8_gemm(a, M, K, a_ld, b, N, b_ld, true, a_scale, b_scale, splits, accumulate, out, out_ld, stream);
+}
+
+extern "C" int intent_i8_gemm_i32_kn(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const int8_t* b,
+                                     int64_t N, int64_t b_ld, const int32_t* bias, int32_t* c, int64_t c_ld,
+                                     void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(K > 0 && K % 128 == 0, INTENT_ERR_UNSUPPORTED, "K must be a positive multiple of 128, got %lld",
+                 (long long)K);
+  INTENT_REQUIRE(N % 16 == 0, INTENT_ERR_UNSUPPORTED, "[K, N] operand: N must be a multiple of 16");
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(a && b && c, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(a_ld >= K && b_ld >= N && c_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(a) && intent::aligned16(b) && a_ld % 16 == 0 && b_ld % 16 == 0,
+                 INTENT_ERR_ALIGNMENT, "operand rows must be 16-byte aligned");
+  INTENT_REQUIRE(intent::fits_offset(M, a_ld) && intent::fits_offset(K, b_ld), INTENT_ERR_UNSUPPORTED,
+                 "i8_gemm_i32_kn: operand too large for 31-bit buffer offsets");
+  const int mblocks = (int)((M + TSk::BM - 1) / TSk::BM);
+  const int64_t grid = (int64_t)mblocks * ((N + TSk::BN - 1) / TSk::BN);
+  INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "i8_gemm_i32_kn: grid too large");
+  hipLaunchKernelGGL(i8_gemm_kn_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)a,
+                     a_ld, (int)M, (const uint8_t*)b, b_ld, (int)N, (int)K, bias, c, c_ld, mblocks);
+  return intent::launch_status("i8_gemm_i32_kn");
 }
 
 extern "C" int intent_deepgemm_fp8(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld, const float* a_scales,

@@ -216,11 +216,35 @@ gemm_i8_nt = KernelDefinition(
 )
 
 
+def _gemm_i8_kn_direct(env: dict, a, b) -> bool:
+    """b [K, N] feeds the kernel in place when K is a positive multiple of 128, N and
+    both row strides multiples of 16 bytes, and both operands 16-byte aligned."""
+    return (env["K"] > 0 and env["K"] % 128 == 0 and env["N"] % 16 == 0 and a.stride(0) % 16 == 0
+            and b.stride(0) % 16 == 0 and a.data_ptr() % 16 == 0 and b.data_ptr() % 16 == 0)
+
+
+def _gemm_i8_kn_workspace(env: dict) -> int:
+    # the transposed copy of b is needed only off the in-place shapes
+    if env["K"] > 0 and env["K"] % 128 == 0 and env["N"] % 16 == 0:
+        return 0
+    return env["N"] * (-(-env["K"] // 16) * 16)
+
+
 def _gemm_i8_kn_launch(v: dict, env: dict, stream: int, workspace) -> str:
     a, b, bias, c = v["a"], v["b"], v["bias"], v["c"]
     M, K, N = env["M"], env["K"], env["N"]
+    if _gemm_i8_kn_direct(env, a, b):
+        _native.call("intent_i8_gemm_i32_kn", _ptr(a), M, K, _ld(a), _ptr(b), N, b.stride(0), _ptr(bias), _ptr(c),
+                     _ld(c), stream)
+        return "intent_i8_gemm_i32_kn"
+    Kp = -(-K // 16) * 16
+    if workspace is None or workspace.numel() < N * Kp:
+        import torch
+
+        workspace = torch.empty(N * Kp, dtype=torch.uint8, device=b.device)
+        workspace.record_stream(torch.cuda.ExternalStream(stream, device=b.device))
     bt = workspace.data_ptr()  # b [K, N] -> [N, K] rows
-    _native.call("intent_fp8_transpose", _ptr(b), K, N, b.stride(0), bt, -(-K // 16) * 16, stream)
+    _native.call("intent_fp8_transpose", _ptr(b), K, N, b.stride(0), bt, Kp, stream)
     _native.call("intent_i8_gemm_i32", _ptr(a), M, K, _ld(a), bt, N, -(-K // 16) * 16, _ptr(bias), _ptr(c), _ld(c),
                  stream)
     return "intent_i8_gemm_i32"
@@ -235,9 +259,10 @@ gemm_i8 = KernelDefinition(
         Param("c", "i32", ("M", "N"), OUT, leading_stride=True),
     ),
     launch=_gemm_i8_kn_launch,
-    workspace=lambda env: env["N"] * (-(-env["K"] // 16) * 16),
+    workspace=_gemm_i8_kn_workspace,
     reference="examples/kernels/contraction/gemm.py:29-39",
-    doc="c = a @ b + bias in int32 (modulo 2^32); b [K, N] is transposed into the workspace first",
+    doc="c = a @ b + bias in int32 (modulo 2^32); b [K, N] read in place (K % 128 == 0, N % 16 == 0), "
+        "else transposed into the workspace first",
 )
 
 
@@ -709,23 +734,59 @@ block_scaled_matmul = KernelDefinition(
 
 # ---- per-tensor scaled FP8 GEMM and its split-K form ---------------------------
 
+# Largest M read in place. The in-place kernel spends four transpose reads of LDS per
+# 32-byte fragment where the row form spends two plain ones; on MI355X
+# (N=14336, K=4096) it wins up to M=512 (54 vs 59 us with the copy) and loses from
+# M=1024 (116 vs 101 us; 355 vs 312 us at M=4096), where the copy is amortised.
+FP8_KN_MAX_M = 768
+
+
+def _fp8_kn_shape(env: dict) -> bool:
+    return env["N"] % 16 == 0 and env["M"] <= FP8_KN_MAX_M
+
+
+def _fp8_kn_direct(env: dict, lhs, rhs_kn) -> bool:
+    """rhs [K, N] feeds the kernel in place (no transposed copy) when M is at most
+    FP8_KN_MAX_M, N and its row stride are multiples of 16 bytes and both operands are
+    16-byte aligned."""
+    return (_fp8_kn_shape(env) and rhs_kn.stride(0) % 16 == 0 and rhs_kn.data_ptr() % 16 == 0
+            and lhs.data_ptr() % 16 == 0)
+
+
 def _fp8_rhs_rows(rhs_kn, K: int, N: int, workspace, stream: int):
-    """The [K, N] right operand transposed into the workspace as [N, K] rows."""
+    """The [K, N] right operand transposed into [N, K] rows (the fallback when it cannot
+    be read in place): in the workspace, or in a scratch buffer whose memory the caching
+    allocator holds back until the launch stream has passed it."""
+    if workspace is None or workspace.numel() < K * N:
+        import torch
+
+        workspace = torch.empty(K * N, dtype=torch.uint8, device=rhs_kn.device)
+        workspace.record_stream(torch.cuda.ExternalStream(stream, device=rhs_kn.device))
     _native.call("intent_fp8_transpose", _ptr(rhs_kn), K, N, rhs_kn.stride(0), workspace.data_ptr(), K, stream)
     return workspace.data_ptr()
 
 
 def _sfp8_workspace(env: dict) -> int:
-    return env["K"] * env["N"]
+    # the transposed copy of rhs is not needed on the in-place shapes
+    return 0 if _fp8_kn_shape(env) else env["K"] * env["N"]
+
+
+def _sfp8_gemm(lhs, rhs_kn, env: dict, M: int, K: int, N: int, lhs_ld: int, splits: int, accumulate: int, out,
+               stream: int, workspace) -> str:
+    scales = (float(env["lhs_scale"]), float(env["rhs_scale"]))
+    if _fp8_kn_direct(env, lhs, rhs_kn):
+        _native.call("intent_scaled_fp8_gemm_kn", _ptr(lhs), M, K, lhs_ld, _ptr(rhs_kn), N, rhs_kn.stride(0), *scales,
+                     splits, accumulate, _ptr(out), _ld(out), stream)
+        return "intent_scaled_fp8_gemm_kn"
+    bt = _fp8_rhs_rows(rhs_kn, K, N, workspace, stream)
+    _native.call("intent_scaled_fp8_gemm", _ptr(lhs), M, K, lhs_ld, bt, N, K, *scales, splits, accumulate, _ptr(out),
+                 _ld(out), stream)
+    return "intent_scaled_fp8_gemm"
 
 
 def _sfp8_launch(v: dict, env: dict, stream: int, workspace) -> str:
     lhs, rhs, out = v["lhs"], v["rhs"], v["output"]
-    M, K, N = env["M"], env["K"], env["N"]
-    bt = _fp8_rhs_rows(rhs, K, N, workspace, stream)
-    _native.call("intent_scaled_fp8_gemm", _ptr(lhs), M, K, _ld(lhs), bt, N, K, float(env["lhs_scale"]),
-                 float(env["rhs_scale"]), 1, 0, _ptr(out), _ld(out), stream)
-    return "intent_scaled_fp8_gemm"
+    return _sfp8_gemm(lhs, rhs, env, env["M"], env["K"], env["N"], _ld(lhs), 1, 0, out, stream, workspace)
 
 
 def _sfp8_check(env: dict) -> None:
@@ -751,17 +812,14 @@ scaled_fp8_matmul = KernelDefinition(
 
 
 def _sfp8_splitk_workspace(env: dict) -> int:
-    return env["IT"] * env["SP"] * 256 * env["N"]
+    return 0 if _fp8_kn_shape(env) else env["IT"] * env["SP"] * 256 * env["N"]
 
 
 def _sfp8_splitk_launch(v: dict, env: dict, stream: int, workspace) -> str:
     lhs, rhs, out = v["lhs"], v["rhs"], v["output"]
     M, N, SP = env["M"], env["N"], env["SP"]
     K = env["IT"] * SP * 256
-    bt = _fp8_rhs_rows(rhs.view(K, N), K, N, workspace, stream)
-    _native.call("intent_scaled_fp8_gemm", _ptr(lhs), M, K, K, bt, N, K, float(env["lhs_scale"]),
-                 float(env["rhs_scale"]), SP, 1, _ptr(out), _ld(out), stream)
-    return "intent_scaled_fp8_gemm"
+    return _sfp8_gemm(lhs, rhs.view(K, N), env, M, K, N, K, SP, 1, out, stream, workspace)
 
 
 scaled_fp8_splitk_matmul = KernelDefinition(

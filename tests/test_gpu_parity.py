@@ -749,6 +749,62 @@ def test_scaled_fp8_splitk(gpu, threads, M, IT, SP, N):
     _f16_close(host(out)[rows], ref, f"splitk {M}x{K}x{N}/{SP}")
 
 
+@pytest.mark.parametrize("M,K,N,ldb,splits", [(300, 512, 4096, 4096, 1), (257, 384, 144, 160, 1),
+                                              (130, 1024, 272, 288, 2), (64, 128, 16, 16, 1)])
+def test_scaled_fp8_kn_in_place(gpu, threads, M, K, N, ldb, splits):
+    """intent_scaled_fp8_gemm_kn reads b [K, N] in place, with a row stride past N and
+    a last column tile that is partly outside N; against the oracle and against the
+    transposed-copy entry on the same inputs (bit-equal: same tile, same sum order)."""
+    from intent_amd import _native
+    a, bfull = _fp8_bits(M + K, (M, K)), _fp8_bits(N + K, (K, ldb))
+    b = np.ascontiguousarray(bfull[:, :N])
+    out0 = (torch.randn(M, N, generator=torch.Generator().manual_seed(5)) * 4).half()
+    ad, bd = dev(a), dev(bfull)
+    outs = []
+    for kn in (True, False):
+        out = out0.cuda()
+        if kn:
+            _native.call("intent_scaled_fp8_gemm_kn", ad.data_ptr(), M, K, K, bd.data_ptr(), N, ldb, 0.5, 1.5,
+                         splits, int(splits > 1), out.data_ptr(), N, 0)
+        else:
+            bt = dev(np.ascontiguousarray(b.T))
+            _native.call("intent_scaled_fp8_gemm", ad.data_ptr(), M, K, K, bt.data_ptr(), N, K, 0.5, 1.5, splits,
+                         int(splits > 1), out.data_ptr(), N, 0)
+        torch.cuda.synchronize()
+        outs.append(host(out))
+    assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16)), f"kn vs rows {M}x{K}x{N}"
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    ref = oracle.scaled_fp8_gemm(a[rows], b, 0.5, 1.5, splits=splits,
+                                 out=out0.numpy()[rows] if splits > 1 else None, threads=threads)
+    _f16_close(outs[0][rows], ref, f"scaled_fp8_kn {M}x{K}x{N}/{splits}")
+
+
+@pytest.mark.parametrize("R,C,sld,dld", [(256, 384, 384, 256), (128, 128, 144, 160), (4096, 1024, 1024, 4096),
+                                         (100, 70, 80, 112), (300, 128, 128, 304)])
+def test_fp8_transpose(gpu, R, C, sld, dld):
+    """intent_fp8_transpose (whole 128 x 128 tiles, and the general path) against numpy;
+    bytes of dst outside [C, R] stay untouched."""
+    from intent_amd import _native
+    src = np.random.default_rng(R * C).integers(0, 256, (R, sld), dtype=np.uint8)
+    dst = torch.full((C, dld), 0xA5, dtype=torch.uint8, device="cuda")
+    sd = dev(src)
+    _native.call("intent_fp8_transpose", sd.data_ptr(), R, C, sld, dst.data_ptr(), dld, 0)
+    torch.cuda.synchronize()
+    got = host(dst)
+    assert np.array_equal(got[:, :R], src[:, :C].T)
+    assert np.all(got[:, R:] == 0xA5)
+
+
+def test_scaled_fp8_kn_rejects_ragged_n(gpu):
+    from intent_amd import _native
+    a = torch.zeros((64, 128), dtype=torch.uint8, device="cuda")
+    b = torch.zeros((128, 40), dtype=torch.uint8, device="cuda")
+    out = torch.zeros((64, 40), dtype=torch.float16, device="cuda")
+    with pytest.raises(Exception, match="multiple of 16"):
+        _native.call("intent_scaled_fp8_gemm_kn", a.data_ptr(), 64, 128, 128, b.data_ptr(), 40, 48, 1.0, 1.0, 1, 0,
+                     out.data_ptr(), 40, 0)
+
+
 def test_scaled_fp8_splitk_reference_size(gpu):
     # The reference's split-K case (experiments/gpu/providers/triton/contraction.py:174-186:
     # 4096 x 4096 x 14336, IT 4, SP 4, scales 1), checked against its CPU formula
@@ -886,7 +942,8 @@ def test_quantized_gemm(gpu, threads, M, K, N):
     assert np.mean(got == ref) >= 0.99
 
 
-@pytest.mark.parametrize("M,K,N", [(100, 192, 77), (129, 640, 257), (4000, 192, 4100)])
+@pytest.mark.parametrize("M,K,N", [(100, 192, 77), (129, 640, 257), (4000, 192, 4100),
+                                   (300, 1024, 4096), (257, 384, 144), (64, 128, 16)])
 def test_gemm_i8_reference_layout(gpu, threads, M, K, N):
     # gemm.py:29-39 with b as [K, N], exact int32 against the oracle
     rng = np.random.default_rng(M + K)
@@ -896,6 +953,27 @@ def test_gemm_i8_reference_layout(gpu, threads, M, K, N):
     c = art(intent.gemm_i8).run(dev(a), dev(b), dev(bias))
     rows = np.r_[0:min(M, 8), max(0, M - 8):M]
     assert np.array_equal(host(c)[rows], oracle.i8_gemm_i32(a[rows], np.ascontiguousarray(b.T), bias, threads))
+
+
+@pytest.mark.parametrize("M,K,N,ldb", [(512, 2048, 1024, 1024), (257, 384, 144, 176)])
+def test_gemm_i8_kn_in_place_whole_matrix(gpu, M, K, N, ldb):
+    """The in-place [K, N] entry against the [N, K] entry on the transposed operand,
+    every element (both exact int32); b with a row stride past N."""
+    from intent_amd import _native
+    rng = np.random.default_rng(M * K)
+    a = rng.integers(-128, 128, (M, K), dtype=np.int8)
+    bfull = rng.integers(-128, 128, (K, ldb), dtype=np.int8)
+    bias = rng.integers(-2**31, 2**31 - 1, N, dtype=np.int64).astype(np.int32)
+    ad, bd, biasd = dev(a), dev(bfull), dev(bias)
+    bt = dev(np.ascontiguousarray(bfull[:, :N].T))
+    c_kn = torch.full((M, N), 7, dtype=torch.int32, device="cuda")
+    c_nt = torch.zeros((M, N), dtype=torch.int32, device="cuda")
+    _native.call("intent_i8_gemm_i32_kn", ad.data_ptr(), M, K, K, bd.data_ptr(), N, ldb, biasd.data_ptr(),
+                 c_kn.data_ptr(), N, 0)
+    _native.call("intent_i8_gemm_i32", ad.data_ptr(), M, K, K, bt.data_ptr(), N, K, biasd.data_ptr(), c_nt.data_ptr(),
+                 N, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(c_kn, c_nt)
 
 
 # ---- f16 / bf16 grouped GEMMs (ragged, routed) -------------------------------------------
