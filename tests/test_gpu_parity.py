@@ -142,6 +142,22 @@ def test_w4a16_prefill_config2(gpu, threads):
     assert_close_rms(yh, full, what="prefill full vs f64")
 
 
+@pytest.mark.parametrize("M,K,N,group", [(8192, 256, 2000, 128), (4096, 512, 3400, 64)])
+def test_w4a16_gemm_many_row_tiles(gpu, threads, M, K, N, group):
+    """The windowed W4 GEMM with 16 and 32 row tiles of 256 and a last column tile partly
+    outside N: every output against a float64 restatement on the GPU, sampled rows
+    against the oracle."""
+    x, q, s, z = w4_case(3, M, K, N, group)
+    X, Q, S, Z = dev(x), dev(q), dev(s), dev(z)
+    y = art(intent.weight_only_int4_asym_matmul, KERNEL="gemm").run(X, Q, S, Z)
+    yh = host(y)
+    rows = np.r_[0:16, M - 16:M]
+    assert_close_rms(yh[rows], oracle.w4a16(x[rows], q, s, z, threads), what="row tiles vs oracle")
+    nib = torch.stack((Q & 15, Q >> 4), dim=-1).reshape(Q.shape[0], -1).double()
+    deq = (nib - Z.double().repeat_interleave(group, 1)) * S.double().repeat_interleave(group, 1)
+    assert_close_rms(yh, (X.double() @ deq.T).cpu().numpy(), what="row tiles full vs f64")
+
+
 # ---- W8A16 --------------------------------------------------------------------------
 
 @pytest.mark.parametrize("M,K,N", [(16, 1024, 1024), (1, 64, 10), (200, 320, 130)])
