@@ -49,14 +49,16 @@ def parse():
                     help="'decode' times only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--probe", choices=["traffic", "read", "mfma", "kn"], default=None,
+    ap.add_argument("--probe", choices=["traffic", "read", "mfma", "kn", "ablation"], default=None,
                     help="'traffic': only run 40 decode launches over distinct weight copies, then four 64 MiB "
                          "device copies (run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE; the copies calibrate "
                          "the counters). 'read': time the plain HBM read of the decode's byte count (the floor "
                          "of any kernel streaming those bytes) beside the decode GEMV itself. 'mfma': three "
                          "launches each of the compute-bound lines (prefill, W8A8, MoE), for rocprofv3 --pmc "
                          "MFMA-busy counters. 'kn': the scaled FP8 GEMM (N=14336, K=4096) with its [K, N] "
-                         "operand read in place against the transposed copy plus the row-form kernel, over M")
+                         "operand read in place against the transposed copy plus the row-form kernel, over M. "
+                         "'ablation': the W8A8 line (config 3) with the product library and with each "
+                         "measurement-only library of `python -m intent_amd.build --ablations`")
     return ap.parse_args()
 
 
@@ -603,6 +605,50 @@ def kn_probe() -> None:
             print(json.dumps(row), flush=True)
 
 
+def ablation_probe(steps: int, warmup: int) -> None:
+    """Config 3 (W8A8, M=4096, N=K=8192) through `intent_w8a8_gemm` of the product library
+    and of each ablation library (intent_amd.build.ABLATIONS) that has been built: one
+    JSON line each, HIP-graph timed over the same rotation of input copies as the bench."""
+    import ctypes
+
+    import torch
+
+    from intent_amd import _native, build as B
+    from intent_amd import inputs
+
+    h = inputs.config3_w8a8(0)
+    M, K = h["a"].shape
+    N = h["w"].shape[0]
+    work = 2 * M * N * K
+    n = copies_for(M * K + N * K + 2 * M * N, minimum=2)
+    sets = []
+    for _ in range(n):
+        d = inputs.to_device(h)
+        d["out"] = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        sets.append(d)
+    libs = [("product", B.LIBRARY)] + [(name, B.ablation_library(name)) for name in B.ABLATIONS]
+    for name, path in libs:
+        if not path.exists():
+            print(json.dumps({"probe": "ablation", "variant": name, "missing": str(path)}), flush=True)
+            continue
+        lib = ctypes.CDLL(str(path))
+        fn = lib.intent_w8a8_gemm
+        args, _ = _native.SIGNATURES["intent_w8a8_gemm"]
+        fn.argtypes, fn.restype = args, ctypes.c_int
+
+        def make(d, fn=fn):
+            def go():
+                rc = fn(d["a"].data_ptr(), M, K, K, d["a_scales"].data_ptr(), d["w"].data_ptr(), N, K,
+                        d["w_scales"].data_ptr(), d["out"].data_ptr(), N, torch.cuda.current_stream().cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"{name}: intent_w8a8_gemm returned {rc}")
+            return go
+
+        ms = graph_time([make(d) for d in sets], steps, warmup)
+        print(json.dumps({"probe": "ablation", "variant": name, "library": path.name, "us": round(ms * 1e3, 1),
+                          "TOP/s": round(work / ms / 1e9, 1)}), flush=True)
+
+
 def _numa_physical_cores(limit: int = 16) -> list[int]:
     """Up to `limit` physical cores (one hardware thread each) of one NUMA node, within this
     process's affinity: the node holding the most allowed cores."""
@@ -725,6 +771,9 @@ def main() -> int:
         return 0
     if args.probe == "kn":
         kn_probe()
+        return 0
+    if args.probe == "ablation":
+        ablation_probe(args.steps, args.warmup)
         return 0
     arch = _native.device_arch(0)
     log(f"[bench] device 0: {arch}; decode M=1 steps={args.steps} warmup={args.warmup}")

@@ -138,6 +138,28 @@ def build_host_sanitized(out_dir: Path) -> Path:
     return lib
 
 
+# Measurement-only builds (INTENT_ABLATE in csrc/mfma_pipe.h): name -> bit mask.
+ABLATIONS = {"no_loads": 1, "no_loads_no_lds_writes": 3, "no_epilogue_stores": 4}
+ABLATION_DIR = LIBRARY.parent / "ablation"
+
+
+def ablation_library(name: str) -> Path:
+    return ABLATION_DIR / f"libintent_amd_{name}.so"
+
+
+def build_ablations(verbose: bool = False) -> list:
+    """The libraries `bench.py --probe ablation` times beside the product one (never
+    loaded by the package itself)."""
+    out = []
+    for name, mask in ABLATIONS.items():
+        out.append(build(verbose, extra_flags=[f"-DINTENT_ABLATE={mask}"], library=ablation_library(name),
+                         objdir=OBJDIR.parent / f"obj_ablate_{name}"))
+    return out
+
+
 if __name__ == "__main__":
-    build(verbose=True)
+    if "--ablations" in sys.argv[1:]:
+        build_ablations(verbose=True)
+    else:
+        build(verbose=True)
     sys.exit(0)

@@ -95,6 +95,14 @@ INTENT_DEVICE uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// Two f32 -> bf16 conversions in one v_cvt_pk_bf16_f32 (round to nearest
+// even; a NaN stays a NaN): lo in bits 0..15, hi in 16..31. Pinned against
+// f32_to_bf16_rne bit for bit by the W8A8 special-value test.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+INTENT_DEVICE uint32_t bf16x2_rne(float lo, float hi) {
+  return bit_cast<uint32_t>(__builtin_convertvector(f32x2{lo, hi}, bf16x2_t));
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (blockIdx % 8 picks
 // the XCD). Renumber so that consecutive logical tiles land on one XCD and
 // share its L2. Tiles beyond the last full group of 8 keep their id.

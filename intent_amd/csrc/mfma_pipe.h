@@ -29,6 +29,18 @@
 // which lets epilogues store 4 (f16/bf16) or 4 (f32/i32) adjacent outputs.
 #pragma once
 
+// Measurement-only switches, 0 in the product build. `python -m intent_amd.build
+// --ablations` links separate libraries with them set, which `bench.py --probe
+// ablation` times beside the product library to split a kernel's time:
+//   bit 0: the int8/f16 main loop (mainloop) issues no global loads after its
+//          first two stages (later stages compute on stale register data);
+//   bit 1: ... and writes nothing to its LDS stage buffers after the first;
+//   bit 2: the W8A8 epilogue stores nothing (the accumulators stay live).
+// Results are meaningless with any bit set; only the timing is of interest.
+#ifndef INTENT_ABLATE
+#define INTENT_ABLATE 0
+#endif
+
 #include <type_traits>
 
 #include "common.h"
@@ -700,11 +712,15 @@ INTENT_DEVICE void mainloop(const AOp& aop, const BOp& bop, int nk, char* buf0, 
   auto step = [&](int kt, char* cur, char* nxt, typename AOp::Regs& ran, typename BOp::Regs& rbn,
                   typename AOp::Regs& raf, typename BOp::Regs& rbf) {
     const int kn = kidx(kt + 2 < nk ? kt + 2 : nk - 1);
-    aop.load(kn, raf);
-    bop.load(kn, rbf);
+    if constexpr (!(INTENT_ABLATE & 1)) {
+      aop.load(kn, raf);
+      bop.load(kn, rbf);
+    }
     compute_stage<T, Math, 4, false>(cur, aaddr, baddr, acc);
-    aop.store(ran, nxt);
-    bop.store(rbn, nxt + T::A_BYTES);
+    if constexpr (!(INTENT_ABLATE & 2)) {
+      aop.store(ran, nxt);
+      bop.store(rbn, nxt + T::A_BYTES);
+    }
     sched_step<T::TI * T::TJ, T::TI + T::TJ, AOp::NVM + BOp::NVM, AOp::NDS + BOp::NDS>();
     wait_vm_lgkm_barrier<AOp::NVM + BOp::NVM>();
   };

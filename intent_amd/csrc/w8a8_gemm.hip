@@ -26,6 +26,8 @@ template <class T, Epi E>
 INTENT_DEVICE void store_tile(const i32x16 (&acc)[T::TI][T::TJ], int m0, int n0, int M, int N,
                               const float* __restrict__ a_scales, const float* __restrict__ w_scales,
                               const int32_t* __restrict__ bias, void* __restrict__ out, int64_t ldo) {
+  if constexpr ((INTENT_ABLATE & 4) != 0)
+    if (ldo > 0) return;  // measurement build: no stores (ldo is unknown here, so the sums stay live)
   const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
@@ -41,16 +43,15 @@ INTENT_DEVICE void store_tile(const i32x16 (&acc)[T::TI][T::TJ], int m0, int n0,
           uint16_t* o = reinterpret_cast<uint16_t*>(out) + (int64_t)m * ldo + n;
           if (vec && n + 3 < N) {
             const f32x4 ws = *reinterpret_cast<const f32x4*>(w_scales + n);
-            uint32_t lo = 0, hi = 0;
-            lo = f32_to_bf16_rne(((float)acc[i][j][4 * g] * sa) * ws[0]) |
-                 ((uint32_t)f32_to_bf16_rne(((float)acc[i][j][4 * g + 1] * sa) * ws[1]) << 16);
-            hi = f32_to_bf16_rne(((float)acc[i][j][4 * g + 2] * sa) * ws[2]) |
-                 ((uint32_t)f32_to_bf16_rne(((float)acc[i][j][4 * g + 3] * sa) * ws[3]) << 16);
+            const uint32_t lo = bf16x2_rne(((float)acc[i][j][4 * g] * sa) * ws[0],
+                                           ((float)acc[i][j][4 * g + 1] * sa) * ws[1]);
+            const uint32_t hi = bf16x2_rne(((float)acc[i][j][4 * g + 2] * sa) * ws[2],
+                                           ((float)acc[i][j][4 * g + 3] * sa) * ws[3]);
             *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
           } else {
 #pragma unroll
             for (int c = 0; c < 4; ++c)
-              if (n + c < N) o[c] = f32_to_bf16_rne(((float)acc[i][j][4 * g + c] * sa) * w_scales[n + c]);
+              if (n + c < N) o[c] = (uint16_t)bf16x2_rne(((float)acc[i][j][4 * g + c] * sa) * w_scales[n + c], 0.f);
           }
         } else {
           int32_t* o = reinterpret_cast<int32_t*>(out) + (int64_t)m * ldo + n;
@@ -61,6 +62,71 @@ INTENT_DEVICE void store_tile(const i32x16 (&acc)[T::TI][T::TJ], int m0, int n0,
       }
   }
 
+}
+
+// The scaled bf16 epilogue through LDS (a stage buffer is free after the main
+// loop): each wave converts its 32-row blocks one at a time into a private
+// [32][128] bf16 block (256-byte rows, 16-byte piece p of row r in slot
+// p ^ (r % 16), so the 8-byte writes of 16 rows and the 16-byte reads of one
+// row fall in distinct banks), reads it back as 16-byte row pieces and stores
+// whole 256-byte row segments, where the register layout would store 16-byte
+// pieces of 32 rows per instruction. lds: NW * 8 KB no longer read by any wave.
+template <class T>
+INTENT_DEVICE void store_bf16_lds(const i32x16 (&acc)[T::TI][T::TJ], char* lds, int m0, int n0, int M, int N,
+                                  const float* __restrict__ a_scales, const float* __restrict__ w_scales,
+                                  uint16_t* __restrict__ out, int64_t ldo) {
+  static_assert(T::WTN == 128, "128-column wave tiles");
+  constexpr int RS = 256;  // LDS row bytes
+  const int lane = threadIdx.x & 63;
+  char* blk = lds + T::wave() * 32 * RS;
+  const int wm = m0 + T::wave_m() * T::WTM, wn = n0 + T::wave_n() * T::WTN;
+  const bool vec_out = (ldo & 7) == 0 && (((uintptr_t)out) & 15) == 0;
+  f32x4 ws[T::TJ][4];
+#pragma unroll
+  for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int n = n0 + T::col(j, g);
+      if (n + 3 < N) {
+        ws[j][g] = *reinterpret_cast<const f32x4*>(w_scales + n);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ws[j][g][c] = n + c < N ? w_scales[n + c] : 0.f;
+      }
+    }
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int m = m0 + T::row(i);
+    const float sa = m < M ? a_scales[m] : 0.f;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t lo = bf16x2_rne(((float)acc[i][j][4 * g] * sa) * ws[j][g][0],
+                                       ((float)acc[i][j][4 * g + 1] * sa) * ws[j][g][1]);
+        const uint32_t hi = bf16x2_rne(((float)acc[i][j][4 * g + 2] * sa) * ws[j][g][2],
+                                       ((float)acc[i][j][4 * g + 3] * sa) * ws[j][g][3]);
+        const int cb = (T::col(j, g) - T::wave_n() * T::WTN) * 2;  // byte in the row
+        const int r = lane & 31;
+        *reinterpret_cast<u32x2*>(blk + r * RS + ((((cb >> 4) ^ (r & 15))) << 4) + (cb & 15)) = u32x2{lo, hi};
+      }
+    // rows r = 4q + lane / 16 of the block, 16-byte piece lane % 16
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int r = 4 * q + (lane >> 4), c8 = (lane & 15) * 8;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(blk + r * RS + (((lane & 15) ^ (r & 15)) << 4));
+      const int gm = wm + i * 32 + r, gn = wn + c8;
+      if (gm >= M) continue;
+      uint16_t* dst = out + (int64_t)gm * ldo + gn;
+      if (vec_out && gn + 7 < N) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (gn + c < N) dst[c] = (uint16_t)(v[c >> 1] >> (16 * (c & 1)));
+      }
+    }
+  }
 }
 
 // One workgroup per output tile; 128 k per LDS stage, the last one possibly 64.
@@ -86,6 +152,12 @@ __global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restr
   aop.init(mp::DenseRows{a, lda, M}, m0, wave, half ? nk - 1 : -1);
   mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc, half);
 
+  if constexpr (E == Epi::kBf16Scaled && T::WTN == 128 && T::NW * 32 * 256 <= T::STAGE_BYTES &&
+                (INTENT_ABLATE & 4) == 0) {
+    __syncthreads();  // every wave's last fragment reads are done
+    store_bf16_lds<T>(acc, buf0, m0, n0, M, N, a_scales, w_scales, reinterpret_cast<uint16_t*>(out), ldo);
+    return;
+  }
   store_tile<T, E>(acc, m0, n0, M, N, a_scales, w_scales, bias, out, ldo);
 }
 

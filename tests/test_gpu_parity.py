@@ -187,6 +187,46 @@ def test_w8a8_config3(gpu, threads):
     assert torch.equal(out.view(torch.int16), f.to(torch.bfloat16).view(torch.int16)), "bf16 epilogue not exact"
 
 
+def _f32(bits):
+    return np.array(bits, np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("M,N", [(256, 256), (4096, 4096)])
+def test_w8a8_special_values(gpu, threads, M, N):
+    """The bf16 epilogue (hardware v_cvt_pk_bf16_f32) bit for bit against the oracle's
+    round-to-nearest-even where the products are NaN (quiet and signalling payloads, both
+    signs), +-inf, +-0, f32 subnormals, bf16 overflow and exact rounding ties: A has one
+    non-zero column, so acc = a[m, 0] * w[n, 0] exactly. (256 x 256: the 128-row tiles;
+    4096 x 4096: the 256 x 256 tiles.)"""
+    K = 64
+    rng = np.random.default_rng(11)
+    a = np.zeros((M, K), np.int8)
+    a[:, 0] = rng.integers(-128, 128, M, dtype=np.int8)
+    w = rng.integers(-128, 128, (N, K), dtype=np.int8)
+    sa_pool = np.concatenate([_f32([0x7fc00000, 0xffc00001, 0x7fa00001, 0xff812345, 0x7f800000, 0xff800000,
+                                    0x00000000, 0x80000000, 0x00000001, 0x807fffff, 0x00400000, 0x7f7fffff,
+                                    0x3f808000, 0x3f818000, 0xbf808000, 0x3f800000]),
+                              rng.uniform(-2, 2, 16).astype(np.float32)])
+    sw_pool = np.concatenate([_f32([0x3f800000, 0x3f808000, 0x3f7f8000, 0x40000000, 0x00800000, 0x00000002,
+                                    0x7f000000, 0x7fbfffff, 0x3c008000, 0xbc018000]),
+                              rng.uniform(-1, 1, 22).astype(np.float32)])
+    sa = sa_pool[np.arange(M) % sa_pool.size]
+    sw = sw_pool[np.arange(N) % sw_pool.size]
+    out = art(intent.w8a8_scaled_matmul).run(dev(a), dev(sa), dev(w), dev(sw))
+    bits = host(out.view(torch.int16)).view(np.uint16)
+    rows = np.r_[0:64, M - 64:M]
+    ref = oracle.w8a8(a[rows], sa[rows], w, sw, threads)
+    got = bits[rows]
+    # Where both scales are NaN, IEEE 754 leaves the payload of the product to the
+    # implementation (v_mul_f32 returns its first source's, and which scale that is
+    # is the compiler's choice): a NaN is required there, the exact bits elsewhere.
+    both = np.isnan(sa[rows])[:, None] & np.isnan(sw)[None, :]
+    assert np.all((got[both] & 0x7f80) == 0x7f80) and np.all((got[both] & 0x7f) != 0)
+    bad = np.argwhere((got != ref) & ~both)
+    assert bad.size == 0, f"{len(bad)} bf16 outputs differ, first at {bad[0]}: got {got[tuple(bad[0])]:#06x} " \
+                          f"want {ref[tuple(bad[0])]:#06x}"
+
+
 @pytest.mark.parametrize("M,K,N", [(100, 192, 77), (1, 64, 1), (129, 640, 257), (4000, 192, 4100), (4096, 64, 4096)])
 def test_i8_gemm_bias(gpu, threads, M, K, N):
     rng = np.random.default_rng(5)
