@@ -71,10 +71,11 @@ INTENT_DEVICE void store_tile(const i32x16 (&acc)[T::TI][T::TJ], int m0, int n0,
 // row fall in distinct banks), reads it back as 16-byte row pieces and stores
 // whole 256-byte row segments, where the register layout would store 16-byte
 // pieces of 32 rows per instruction. lds: NW * 8 KB no longer read by any wave.
+// scales: the tile's BM row scales, then its BN column scales (LDS; zero past
+// M and N).
 template <class T>
-INTENT_DEVICE void store_bf16_lds(const i32x16 (&acc)[T::TI][T::TJ], char* lds, int m0, int n0, int M, int N,
-                                  const float* __restrict__ a_scales, const float* __restrict__ w_scales,
-                                  uint16_t* __restrict__ out, int64_t ldo) {
+INTENT_DEVICE void store_bf16_lds(const i32x16 (&acc)[T::TI][T::TJ], char* lds, const float* scales, int m0, int n0,
+                                  int M, int N, uint16_t* __restrict__ out, int64_t ldo) {
   static_assert(T::WTN == 128, "128-column wave tiles");
   constexpr int RS = 256;  // LDS row bytes
   const int lane = threadIdx.x & 63;
@@ -85,19 +86,10 @@ INTENT_DEVICE void store_bf16_lds(const i32x16 (&acc)[T::TI][T::TJ], char* lds, 
 #pragma unroll
   for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int n = n0 + T::col(j, g);
-      if (n + 3 < N) {
-        ws[j][g] = *reinterpret_cast<const f32x4*>(w_scales + n);
-      } else {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) ws[j][g][c] = n + c < N ? w_scales[n + c] : 0.f;
-      }
-    }
+    for (int g = 0; g < 4; ++g) ws[j][g] = *reinterpret_cast<const f32x4*>(scales + T::BM + T::col(j, g));
 #pragma unroll
   for (int i = 0; i < T::TI; ++i) {
-    const int m = m0 + T::row(i);
-    const float sa = m < M ? a_scales[m] : 0.f;
+    const float sa = scales[T::row(i)];
 #pragma unroll
     for (int j = 0; j < T::TJ; ++j)
 #pragma unroll
@@ -150,12 +142,24 @@ __global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restr
   i32x16 acc[T::TI][T::TJ];
   mp::RegRowsOperand<T::BM, mp::DenseRows, kHalf, T::NW> aop;
   aop.init(mp::DenseRows{a, lda, M}, m0, wave, half ? nk - 1 : -1);
+  constexpr bool kLdsEpi = E == Epi::kBf16Scaled && T::WTN == 128 && T::NW * 32 * 256 <= T::STAGE_BYTES &&
+                           T::NT == T::BM + T::BN && (INTENT_ABLATE & 4) == 0;
+  // kLdsEpi: thread t's scale (row t, or column t - BM), loaded before the main
+  // loop, whose first wait retires it
+  __shared__ float scales[kLdsEpi ? T::BM + T::BN : 1];
+  float my_scale = 0.f;
+  if constexpr (kLdsEpi) {
+    const int t = threadIdx.x;
+    const int idx = t < T::BM ? m0 + t : n0 + (t - T::BM);
+    const int lim = t < T::BM ? M : N;
+    my_scale = idx < lim ? (t < T::BM ? a_scales : w_scales)[idx] : 0.f;
+  }
   mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc, half);
 
-  if constexpr (E == Epi::kBf16Scaled && T::WTN == 128 && T::NW * 32 * 256 <= T::STAGE_BYTES &&
-                (INTENT_ABLATE & 4) == 0) {
-    __syncthreads();  // every wave's last fragment reads are done
-    store_bf16_lds<T>(acc, buf0, m0, n0, M, N, a_scales, w_scales, reinterpret_cast<uint16_t*>(out), ldo);
+  if constexpr (kLdsEpi) {
+    scales[threadIdx.x] = my_scale;
+    __syncthreads();  // every wave's last fragment reads are done; the scales are in
+    store_bf16_lds<T>(acc, buf0, scales, m0, n0, M, N, reinterpret_cast<uint16_t*>(out), ldo);
     return;
   }
   store_tile<T, E>(acc, m0, n0, M, N, a_scales, w_scales, bias, out, ldo);
