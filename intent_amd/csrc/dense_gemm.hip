@@ -553,6 +553,59 @@ INTENT_DEVICE void store_dense(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0
 
 }
 
+// store_dense through LDS: each consumer wave converts one 32-row block of
+// its tile at a time into a private block of 32 rows (WTN f16 + 16 bytes of
+// padding each: the 8-byte writes of 16 rows fall in distinct bank groups),
+// reads it back as 16-byte row pieces and stores whole row segments, where the
+// register layout would store 8 bytes in each of 32 rows per instruction.
+// lds: NC * 32 * (2 * WTN + 16) bytes that no wave reads or writes any more.
+template <class T, bool kColScale>
+INTENT_DEVICE void store_dense_lds(const f32x16 (&acc)[T::TI][T::TJ], char* lds, int m0, int n0, int M, int N,
+                                   f16* __restrict__ y, int64_t ldy, const f16* __restrict__ colscale) {
+  constexpr int RS = 2 * T::WTN + 16;  // LDS row bytes
+  constexpr int CH = T::WTN / 8;       // 16-byte pieces per row
+  constexpr int NP = 32 * CH / 64;     // pieces per lane and block
+  static_assert(NP * 64 == 32 * CH, "whole pieces per lane");
+  const int lane = threadIdx.x & 63;
+  char* blk = lds + T::wave() * 32 * RS;
+  const int wm = m0 + T::wave_m() * T::WTM, wn = n0 + T::wave_n() * T::WTN;
+  const bool vec = (ldy & 7) == 0 && (((uintptr_t)y) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + T::col(j, g);
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          v[c] = acc[i][j][4 * g + c];
+          if (kColScale) v[c] *= n + c < N ? (float)colscale[n + c] : 0.f;
+        }
+        const f16x2 lo = __builtin_convertvector(f32x2{v[0], v[1]}, f16x2);
+        const f16x2 hi = __builtin_convertvector(f32x2{v[2], v[3]}, f16x2);
+        *reinterpret_cast<u32x2*>(blk + (lane & 31) * RS + (n - wn) * 2) =
+            u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+      }
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int p = q * 64 + lane, r = p / CH, c8 = (p % CH) * 8;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(blk + r * RS + c8 * 2);
+      const int gm = wm + i * 32 + r, gn = wn + c8;
+      if (gm >= M) continue;
+      f16* dst = y + (int64_t)gm * ldy + gn;
+      if (vec && gn + 7 < N) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (gn + c < N) reinterpret_cast<uint16_t*>(dst)[c] = (uint16_t)(v[c >> 1] >> (16 * (c & 1)));
+      }
+    }
+  }
+}
+
 // y[m, n] = f16(sum_k x[m, k] * deq(W)[n, k] (* colscale[n])).
 template <class T, class WArgs, bool kColScale>
 __global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __restrict__ x, int64_t ldx, int M,
@@ -572,6 +625,13 @@ __global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __re
   aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave() % T::NW);
   if (!mp::mainloop_ws<T, mp::F16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
 
+  // After the main loop's last barrier the stage buffer of stage nk - 2 (of
+  // none, for nk = 1) is neither read nor written again: the producers drained
+  // their DMA before that barrier and issue nothing after it.
+  if constexpr (T::NW * 32 * (2 * T::WTN + 16) <= T::STAGE_BYTES) {
+    store_dense_lds<T, kColScale>(acc, ((K / 64) & 1) ? buf1 : buf0, m0, n0, M, N, y, ldy, colscale);
+    return;
+  }
   store_dense<T, kColScale>(acc, m0, n0, M, N, y, ldy, colscale);
 }
 
