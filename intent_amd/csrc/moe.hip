@@ -318,6 +318,15 @@ struct ClampRows {
 
 // acc[i][j][4g + c]: row(i), feature f0 + feature(wave_n, j*32 + g*8 + h*4 + c);
 // j < TJ/2 are gate columns, j + TJ/2 the up columns of the same features.
+// silu(g) * u = g / (1 + e^-g) * u with v_exp_f32 and v_rcp_f32 (about one
+// ulp each, so a few f32 ulps in all, far below the f16 rounding of the
+// result; g = -inf gives NaN and g = +inf gives inf, as the quotient does,
+// and a large negative g gives -0).
+INTENT_DEVICE float silu_mul(float g, float u) {
+  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+}
+
 template <class T>
 INTENT_DEVICE void store_gate_up(const f32x16 (&acc)[T::TI][T::TJ], int m0, int f0, int F,
                                  const int32_t* __restrict__ sorted, int R, f16* __restrict__ act, int64_t ld_act) {
@@ -337,7 +346,7 @@ INTENT_DEVICE void store_gate_up(const f32x16 (&acc)[T::TI][T::TJ], int m0, int 
         for (int c = 0; c < 4; ++c) {
           const float gt = acc[i][j][4 * g + c];
           const float up = acc[i][j + T::TJ / 2][4 * g + c];
-          o[c] = valid ? (f16)((gt / (1.0f + expf(-gt))) * up) : (f16)0.f;
+          o[c] = valid ? (f16)silu_mul(gt, up) : (f16)0.f;
         }
         f16* dst = act + (int64_t)row * ld_act + f;
         if (vec && f + 3 < F) {
