@@ -366,6 +366,60 @@ INTENT_DEVICE void store_gate_up(const f32x16 (&acc)[T::TI][T::TJ], int m0, int 
 
 }
 
+// store_gate_up through LDS for the packed-weight tiles (one wave row, NW
+// waves of WTN / 2 features each): the tile's BM rows x NW * WTN / 2 features
+// are gathered in LDS (rows padded by 16 bytes, so the 8-byte writes of 16
+// rows fall in distinct bank groups), then stored as 16-byte pieces of whole
+// row segments. lds: BM * (NW * WTN + 16) bytes that no wave reads any more
+// once the workgroup barrier inside has passed.
+template <class T>
+INTENT_DEVICE void store_gate_up_lds(const f32x16 (&acc)[T::TI][T::TJ], char* lds, int m0, int f0, int F,
+                                     const int32_t* __restrict__ sorted, int R, f16* __restrict__ act,
+                                     int64_t ld_act) {
+  static_assert(T::WM == 1, "one wave row");
+  constexpr int FW = T::WTN / 2;   // features per wave
+  constexpr int FT = T::NW * FW;   // features per tile
+  constexpr int RS = 2 * FT + 16;  // LDS row bytes
+  constexpr int NP = T::BM * (FT / 8) / T::NT;  // 16-byte pieces per thread
+  static_assert(NP * T::NT == T::BM * (FT / 8), "whole pieces per thread");
+  const int lane = threadIdx.x & 63;
+  const int w = T::wave_n();
+  __syncthreads();  // every wave is done with the stage buffers
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int row = T::row(i);
+    const int r = sorted[m0 + row];
+    const bool valid = r >= 0 && r < R;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = valid ? silu_mul(acc[i][0][4 * g + c], acc[i][T::TJ / 2][4 * g + c]) : 0.f;
+      const f16x2 lo = __builtin_convertvector(f32x2{o[0], o[1]}, f16x2);
+      const f16x2 hi = __builtin_convertvector(f32x2{o[2], o[3]}, f16x2);
+      const int fl = w * FW + (T::col(0, g) - w * T::WTN);
+      *reinterpret_cast<u32x2*>(lds + row * RS + fl * 2) = u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+    }
+  }
+  __syncthreads();
+  const bool vec = (ld_act & 7) == 0 && (((uintptr_t)act) & 15) == 0;
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const int p = q * T::NT + (int)threadIdx.x;
+    const int row = p / (FT / 8), c8 = (p % (FT / 8)) * 8;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(lds + row * RS + c8 * 2);
+    const int f = f0 + c8;
+    f16* dst = act + (int64_t)(m0 + row) * ld_act + f;
+    if (vec && f + 7 < F) {
+      *reinterpret_cast<u32x4*>(dst) = v;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (f + c < F) reinterpret_cast<uint16_t*>(dst)[c] = (uint16_t)(v[c >> 1] >> (16 * (c & 1)));
+    }
+  }
+}
+
 template <int B>
 __global__ __launch_bounds__(MoeTiles<B>::GateUp::NT_WS, 1) void moe_gate_up_kernel(
     const f16* __restrict__ x, int64_t ldx, int H, const int32_t* __restrict__ sorted,
@@ -466,6 +520,10 @@ __global__ __launch_bounds__(GateUpPk::NT, 2) void moe_gate_up_pk_kernel(
     mp::mainloop_pk<T, NB, ADma, BDma, PDma, 4>(aop, bop, pop, H / 64, bufs, acc, pwin);
   else
     mp::mainloop_pk<T, NB, ADma, BDma, PDma, T::TI>(aop, bop, pop, H / 64, bufs, acc, pwin);
+  if constexpr (T::WM == 1 && T::BM * (T::NW * T::WTN + 16) <= (int)sizeof(smem)) {
+    store_gate_up_lds<T>(acc, &smem[0][0], m0, f0, F, sorted, R, act, ld_act);
+    return;
+  }
   store_gate_up<T>(acc, m0, f0, F, sorted, R, act, ld_act);
 }
 
