@@ -71,6 +71,84 @@ enum class GEpi {
   kRouteWeight,  // out32[row] = route_weights[members[row]] * acc (f32) (MoE second projection)
 };
 
+// The epilogue through LDS: after a workgroup barrier (the stage buffers are
+// then free) each wave passes its 32-row blocks one at a time through a
+// private LDS block (rows of WTN outputs plus 16 bytes of padding, so the
+// writes of 16 rows fall in distinct bank groups) and stores whole row
+// segments (WTN outputs) per row, where the register layout would store 8 or
+// 16 bytes of each of 32 rows per instruction. lds0 / lds1: the two stage
+// buffers; waves NW/2.. use lds1 when one buffer cannot hold all waves.
+template <class T, GEpi E, bool kBf16>
+INTENT_DEVICE void grouped_store_lds(const f32x16 (&acc)[T::TI][T::TJ], char* lds0, char* lds1,
+                                     const GroupTile& tile, int n0, int N, const int32_t* __restrict__ members,
+                                     int nroutes, const float* __restrict__ route_weights, void* __restrict__ out,
+                                     int64_t ldo) {
+  constexpr int EB = E == GEpi::kRouteWeight ? 4 : 2;  // output bytes
+  constexpr int RS = T::WTN * EB + 16;                  // LDS row bytes
+  constexpr int CH = T::WTN * EB / 16;                  // 16-byte pieces per row
+  constexpr int PE = 16 / EB;                           // outputs per piece
+  constexpr int NP = 32 * CH / 64;                      // pieces per lane and block
+  static_assert(NP * 64 == 32 * CH, "whole pieces per lane");
+  constexpr bool kOne = T::NW * 32 * RS <= T::STAGE_BYTES;
+  static_assert(kOne || (T::NW / 2) * 32 * RS <= T::STAGE_BYTES, "wave blocks fit the stage buffers");
+  const int lane = threadIdx.x & 63;
+  const int wv = T::wave();
+  char* blk = kOne ? lds0 + wv * 32 * RS : (wv < T::NW / 2 ? lds0 + wv * 32 * RS : lds1 + (wv - T::NW / 2) * 32 * RS);
+  const int wn = n0 + T::wave_n() * T::WTN;
+  const bool vec = ((ldo * EB) & 15) == 0 && (((uintptr_t)out) & 15) == 0;
+  __syncthreads();  // every wave is done with the stage buffers
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+    const int rb = tile.start + T::wave_m() * T::WTM + i * 32;
+    if (rb >= tile.end) break;  // wave-uniform
+    const int row = rb + (lane & 31);
+    float rw = 1.f;
+    if constexpr (E == GEpi::kRouteWeight)
+      rw = row < tile.end ? route_weights[clampi(members[row], 0, nroutes - 1)] : 0.f;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        char* dst = blk + (lane & 31) * RS + (T::col(j, gq) - T::wave_n() * T::WTN) * EB;
+        if constexpr (E == GEpi::kRouteWeight) {
+          *reinterpret_cast<f32x4*>(dst) =
+              f32x4{__fmul_rn(rw, acc[i][j][4 * gq]), __fmul_rn(rw, acc[i][j][4 * gq + 1]),
+                    __fmul_rn(rw, acc[i][j][4 * gq + 2]), __fmul_rn(rw, acc[i][j][4 * gq + 3])};
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            float v = acc[i][j][4 * gq + c];
+            if constexpr (E == GEpi::kReluF16) v = v < 0.f ? 0.f : v;  // NaN stays NaN
+            h[c] = kBf16 ? f32_to_bf16_rne(v) : bit_cast<uint16_t>((f16)v);
+          }
+          *reinterpret_cast<u32x2*>(dst) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        }
+      }
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int p = q * 64 + lane, r = p / CH, c = (p % CH) * PE;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(blk + r * RS + c * EB);
+      const int gm = rb + r;
+      if (gm >= tile.end) continue;
+      const int n = wn + c;
+      char* o = reinterpret_cast<char*>(out) + ((int64_t)gm * ldo + n) * EB;
+      if (vec && n + PE - 1 < N) {
+        *reinterpret_cast<u32x4*>(o) = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < PE; ++e) {
+          if (n + e >= N) continue;
+          if constexpr (EB == 4)
+            reinterpret_cast<uint32_t*>(o)[e] = v[e];
+          else
+            reinterpret_cast<uint16_t*>(o)[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+        }
+      }
+    }
+  }
+}
+
 template <class T, class Math, bool kGather, GEpi E>
 __global__ __launch_bounds__(T::NT, 1) void grouped_kn_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const int32_t* __restrict__ offsets, int G, int rows,
@@ -98,47 +176,7 @@ __global__ __launch_bounds__(T::NT, 1) void grouped_kn_kernel(
   mp::mainloop_kn<T, Math, mp::DmaRowsOperand<T::BM, Rows, T::NW>, mp::DmaKNOperand<T::BN, T::NW>, true>(
       aop, bop, K / 64, buf0, buf1, acc);
   constexpr bool kBf16 = std::is_same<Math, mp::BF16Math>::value;
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
-    const int row = tile.start + T::row(i);
-    if (row >= tile.end) continue;
-    float rw = 1.f;
-    if constexpr (E == GEpi::kRouteWeight) rw = route_weights[clampi(members[row], 0, nroutes - 1)];
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
-        const int n = n0 + T::col(j, gq);
-        if constexpr (E == GEpi::kRouteWeight) {
-          float* o = reinterpret_cast<float*>(out) + (int64_t)row * ldo + n;
-          const f32x4 v = {__fmul_rn(rw, acc[i][j][4 * gq]), __fmul_rn(rw, acc[i][j][4 * gq + 1]),
-                           __fmul_rn(rw, acc[i][j][4 * gq + 2]), __fmul_rn(rw, acc[i][j][4 * gq + 3])};
-          if (n + 3 < N && (ldo & 3) == 0) {
-            *reinterpret_cast<f32x4*>(o) = v;
-          } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              if (n + c < N) o[c] = v[c];
-          }
-        } else {
-          uint16_t* o = reinterpret_cast<uint16_t*>(out) + (int64_t)row * ldo + n;
-          uint32_t h[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            float v = acc[i][j][4 * gq + c];
-            if constexpr (E == GEpi::kReluF16) v = v < 0.f ? 0.f : v;  // NaN stays NaN
-            h[c] = kBf16 ? f32_to_bf16_rne(v) : bit_cast<uint16_t>((f16)v);
-          }
-          if (n + 3 < N && (ldo & 3) == 0) {
-            *reinterpret_cast<u32x2*>(o) = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-          } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-              if (n + c < N) o[c] = (uint16_t)h[c];
-          }
-        }
-      }
-  }
+  grouped_store_lds<T, E, kBf16>(acc, buf0, buf1, tile, n0, N, members, nroutes, route_weights, out, ldo);
 }
 
 inline int kn_shape_check(int64_t K, int64_t N, int64_t w_ld, const void* w, const char* what) {
