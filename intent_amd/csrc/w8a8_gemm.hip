@@ -239,6 +239,47 @@ __global__ __launch_bounds__(T::NT_WS, 1) void lowbit_ws_kernel(const int8_t* __
   // acc[i][j][4g + c]: n = col j, lane % 32; m = row block i, 8g + 4h + c.
   const int lane = threadIdx.x & 63;
   const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 15) == 0;
+  // Through LDS: after the main loop's last barrier the stage buffer of
+  // stage nk - 2 (none, for nk = 1) is neither read nor written again (the
+  // producers drained their DMA before it and issue nothing after it). Each
+  // consumer wave passes 32 n x 64 m blocks through a private part of it
+  // (rows padded by 16 bytes: the 16-byte writes of 16 rows fall in distinct
+  // bank groups) and stores 256-byte row segments, where the register layout
+  // stores 32 bytes of each of 32 rows per instruction.
+  constexpr int RS = 64 * 4 + 16;
+  if constexpr (T::TI % 2 == 0 && T::NW * 32 * RS <= T::STAGE_BYTES) {
+    char* blk = (((K / mp::ROWB) & 1) ? buf1 : buf0) + T::wave() * 32 * RS;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int ih = 0; ih < T::TI / 2; ++ih) {
+#pragma unroll
+        for (int i2 = 0; i2 < 2; ++i2)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int i = 2 * ih + i2;
+            *reinterpret_cast<i32x4*>(blk + (lane & 31) * RS + (i2 * 32 + g * 8 + (lane >> 5) * 4) * 4) =
+                i32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+          }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int p = q * 64 + lane, r = p / 16, c = (p % 16) * 4;
+          const i32x4 v = *reinterpret_cast<const i32x4*>(blk + r * RS + c * 4);
+          const int n = n0 + T::wave_n() * T::WTN + j * 32 + r;
+          const int m = m0 + T::wave_m() * T::WTM + ih * 64 + c;
+          if (n >= N) continue;
+          int32_t* dst = out + (int64_t)n * ldo + m;
+          if (vec && m + 3 < M) {
+            *reinterpret_cast<i32x4*>(dst) = v;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (m + e < M) dst[e] = v[e];
+          }
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < T::TJ; ++j) {
     const int n = n0 + T::wave_n() * T::WTN + j * 32 + (lane & 31);
