@@ -49,7 +49,7 @@ def parse():
                     help="'decode' times only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU-baseline sample budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--probe", choices=["traffic", "read", "mfma", "kn", "ablation"], default=None,
+    ap.add_argument("--probe", choices=["traffic", "read", "mfma", "kn", "ablation", "decode"], default=None,
                     help="'traffic': only run 40 decode launches over distinct weight copies, then four 64 MiB "
                          "device copies (run under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE; the copies calibrate "
                          "the counters). 'read': time the plain HBM read of the decode's byte count (the floor "
@@ -58,7 +58,9 @@ def parse():
                          "MFMA-busy counters. 'kn': the scaled FP8 GEMM (N=14336, K=4096) with its [K, N] "
                          "operand read in place against the transposed copy plus the row-form kernel, over M. "
                          "'ablation': the W8A8 line (config 3) with the product library and with each "
-                         "measurement-only library of `python -m intent_amd.build --ablations`")
+                         "measurement-only library of `python -m intent_amd.build --ablations`. 'decode': 40 "
+                         "launches each of the decode GEMV at M=1 and M=16 over distinct weight copies (run "
+                         "under rocprofv3 --pmc for per-dispatch L1 / address-unit counters)")
     return ap.parse_args()
 
 
@@ -451,6 +453,25 @@ def traffic_probe() -> None:
     torch.cuda.synchronize()
 
 
+def decode_probe() -> None:
+    """40 plain launches each of config 1's decode at M = 1 and M = 16, every launch on its own
+    copy of the weights (so each reads them from HBM), for per-dispatch PMC counters."""
+    import torch
+
+    import intent_amd as intent
+    from intent_amd import inputs
+
+    art = intent.compile(intent.weight_only_int4_asym_matmul, target=intent.MI355XTarget(0))
+    for M in (1, 16):
+        d = inputs.to_device(inputs.config1_w4a16_decode(0, M=M))
+        sets = [(d["x"].clone(), d["packed"].clone(), d["scales"].clone(), d["zeros"].clone()) for _ in range(40)]
+        for call in [art.prepare(*s) for s in sets]:
+            call.launch()
+        torch.cuda.synchronize()
+        log(f"[probe] decode M={M}: {art.observation.kernel}")
+        del sets, d
+
+
 def read_probe(steps: int) -> None:
     """Plain HBM read of the decode's bytes, without and with one small store per wave (a
     GEMV writes its outputs, and a kernel's end waits for its stores), against the decode
@@ -771,6 +792,9 @@ def main() -> int:
         return 0
     if args.probe == "kn":
         kn_probe()
+        return 0
+    if args.probe == "decode":
+        decode_probe()
         return 0
     if args.probe == "ablation":
         ablation_probe(args.steps, args.warmup)
