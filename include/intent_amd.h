@@ -468,6 +468,20 @@ int intent_w4_sym_repack(const int32_t* packed, int64_t P, int64_t N, int64_t pa
                          uint8_t* q_out, int64_t q_ld, void* s_out, uint8_t* z_out, int64_t sz_ld,
                          void* stream);
 
+/* weight_only_int4_matmul (examples/kernels/contraction/weight_only_int4.py:18-51)
+ * for M <= 5, reading the reference's layout in place (no repack):
+ *   y[m, n] = f16(sum_k x[m, k] * (signed nibble (k, n) * scales[k / 64, n]))
+ * x: f16 [M, K] (x_ld elements); packed: int32 [K/8, N] (packed_ld elements),
+ * word (r, n) holding k = 8r .. 8r+7 at nibble k % 8; scales: f16 [K/64, N]
+ * (scales_ld elements); y: f16 [M, N] (y_ld elements).
+ * K % 64 == 0 and K <= 8192, N % 4 == 0, x and packed rows 16-byte aligned,
+ * scale rows 8-byte aligned.
+ */
+int intent_w4a16_sym_gemv(const void* x, int64_t M, int64_t K, int64_t x_ld,
+                          const int32_t* packed, int64_t N, int64_t packed_ld,
+                          const void* scales, int64_t scales_ld,
+                          void* y, int64_t y_ld, void* stream);
+
 /* f16 matrix transpose: dst[c * dst_ld + r] = src[r * src_ld + c] (elements).
  * Plumbing for quantized_gemm, whose right operand the reference passes as
  * [K, N]. Replaces no reference function.

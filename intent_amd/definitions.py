@@ -943,6 +943,9 @@ def _w4sym_layout(env: dict) -> tuple:
 
 
 def _w4sym_workspace(env: dict) -> int:
+    # the repacked copy is not needed on the in-place decode shapes (alignment permitting)
+    if env["M"] <= 5 and env["K"] <= 8192 and env["N"] % 4 == 0:
+        return 0
     return _w4sym_layout(env)[3]
 
 
@@ -955,9 +958,26 @@ def _w4sym_check(env: dict) -> None:
         raise NotImplementedError(f"K ({env['K']}) must be a multiple of 64")
 
 
+def _w4sym_in_place(v: dict, env: dict) -> bool:
+    """Decode shapes the in-place kernel (intent_w4a16_sym_gemv) takes."""
+    x, packed, scales = v["activation"], v["packed_weight"], v["scales"]
+    return (env["M"] <= 5 and env["K"] <= 8192 and env["N"] % 4 == 0 and x.data_ptr() % 16 == 0
+            and x.stride(0) % 8 == 0 and packed.data_ptr() % 16 == 0 and packed.stride(0) % 4 == 0
+            and scales.data_ptr() % 8 == 0 and scales.stride(0) % 4 == 0)
+
+
 def _w4sym_launch(v: dict, env: dict, stream: int, workspace) -> str:
     x, packed, scales, y = v["activation"], v["packed_weight"], v["scales"], v["output"]
     M, K, N, G = env["M"], env["K"], env["N"], env["G"]
+    if _w4sym_in_place(v, env):
+        _native.call("intent_w4a16_sym_gemv", _ptr(x), M, K, x.stride(0), _ptr(packed), N, packed.stride(0),
+                     _ptr(scales), scales.stride(0), _ptr(y), _ld(y), stream)
+        return "intent_w4a16_sym_gemv"
+    if workspace is None or workspace.numel() < _w4sym_layout(env)[3]:
+        import torch
+
+        workspace = torch.empty(_w4sym_layout(env)[3], dtype=torch.uint8, device=x.device)
+        workspace.record_stream(torch.cuda.ExternalStream(stream, device=x.device))
     oq, os_, oz, _ = _w4sym_layout(env)
     base = workspace.data_ptr()
     _native.call("intent_w4_sym_repack", _ptr(packed), env["P"], N, packed.stride(0), _ptr(scales), G,
@@ -980,7 +1000,8 @@ weight_only_int4_matmul = KernelDefinition(
     check=_w4sym_check,
     workspace=_w4sym_workspace,
     reference="examples/kernels/contraction/weight_only_int4.py:18-51",
-    doc="the reference's symmetric signed-nibble W4 (int32 [K/8, N], f16 scales [K/64, N]) on the W4A16 kernels",
+    doc="the reference's symmetric signed-nibble W4 (int32 [K/8, N], f16 scales [K/64, N]): read in place up to "
+        "M = 5, repacked for the W4A16 kernels above",
 )
 
 

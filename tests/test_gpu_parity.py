@@ -963,7 +963,8 @@ def test_dequant_bf16_fp4_matmul(gpu, threads, M, K, N):
 
 # ---- the reference's own weight_only_int4_matmul layout --------------------------------
 
-@pytest.mark.parametrize("M,K,N", [(512, 2048, 4096), (1, 2048, 4096), (3, 256, 100), (40, 128, 33)])
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 4096), (1, 2048, 4096), (3, 256, 100), (40, 128, 33),
+                                   (1, 4096, 4096), (2, 8192, 260), (4, 64, 4), (5, 4160, 1028), (16, 4096, 512)])
 def test_weight_only_int4_matmul_reference_layout(gpu, threads, M, K, N):
     # (512, 2048, 4096) is the reference's own example size (weight_only_int4.py:6-8)
     rng = np.random.default_rng(M + N)
@@ -974,6 +975,22 @@ def test_weight_only_int4_matmul_reference_layout(gpu, threads, M, K, N):
     rows = np.r_[0:min(M, 8), max(0, M - 8):M]
     ref = oracle.w4_sym(x[rows], packed, scales, threads)
     assert_close_rms(host(y)[rows], ref.astype(np.float32), what=f"w4 sym {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (3, 1024, 64), (5, 8192, 132)])
+def test_weight_only_int4_matmul_in_place_strided(gpu, threads, M, K, N):
+    """The in-place decode entry (intent_w4a16_sym_gemv) on strided x, packed words and
+    scales, against the oracle; and the entry the operator picked for these shapes."""
+    rng = np.random.default_rng(K + N)
+    x = rng.standard_normal((M, K + 8)).astype(np.float16)
+    packed = rng.integers(-2**31, 2**31, (K // 8, N + 4), dtype=np.int64).astype(np.int32)
+    scales = rng.uniform(0.005, 0.02, (K // 64, N + 8)).astype(np.float16)
+    a = art(intent.weight_only_int4_matmul)
+    y = a.run(dev(x)[:, :K], dev(packed)[:, :N], dev(scales)[:, :N])
+    assert a.observation.entry == "intent_w4a16_sym_gemv"
+    ref = oracle.w4_sym(np.ascontiguousarray(x[:, :K]), np.ascontiguousarray(packed[:, :N]),
+                        np.ascontiguousarray(scales[:, :N]), threads)
+    assert_close_rms(host(y), ref.astype(np.float32), what=f"w4 sym in place {M}x{K}x{N}")
 
 
 # ---- quantized_gemm -------------------------------------------------------------------
