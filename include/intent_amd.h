@@ -482,6 +482,15 @@ int intent_w4a16_sym_gemv(const void* x, int64_t M, int64_t K, int64_t x_ld,
                           const void* scales, int64_t scales_ld,
                           void* y, int64_t y_ld, void* stream);
 
+/* The same function for any M on the tiled W4 GEMM (producer waves decode the
+ * reference's words in place into the f16 LDS tile; no repack). K % 64 == 0,
+ * x rows 16-byte aligned.
+ */
+int intent_w4a16_sym_gemm(const void* x, int64_t M, int64_t K, int64_t x_ld,
+                          const int32_t* packed, int64_t N, int64_t packed_ld,
+                          const void* scales, int64_t scales_ld,
+                          void* y, int64_t y_ld, void* stream);
+
 /* f16 matrix transpose: dst[c * dst_ld + r] = src[r * src_ld + c] (elements).
  * Plumbing for quantized_gemm, whose right operand the reference passes as
  * [K, N]. Replaces no reference function.

@@ -57,6 +57,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "intent_scaled_fp8_gemm_kn": ([P, I64, I64, I64, P, I64, I64, F32, F32, I64, INT, P, I64, P], INT),
     "intent_w4_sym_repack": ([P, I64, I64, I64, P, I64, I64, P, I64, P, P, I64, P], INT),
     "intent_w4a16_sym_gemv": ([P, I64, I64, I64, P, I64, I64, P, I64, P, I64, P], INT),
+    "intent_w4a16_sym_gemm": ([P, I64, I64, I64, P, I64, I64, P, I64, P, I64, P], INT),
     "intent_f16_transpose": ([P, I64, I64, I64, P, I64, P], INT),
     "intent_quantized_gemm": ([P, I64, I64, I64, P, I64, I64, P, P, I64, P, P, I64, P], INT),
     "intent_f16_transpose_batched": ([P, I64, I64, I64, I64, I64, P, I64, I64, P], INT),

@@ -52,6 +52,18 @@ struct WeightOp<T, W4WinArgs> {
     op.init(w.q, w.ldq, w.s, w.z, w.ldp, w.gs, ClampRows{n0, N});
   }
 };
+// The reference's own W4 layout (int32 [K/8, N] words, f16 [K/64, N] scales).
+struct W4SymArgs {
+  const int32_t* q;
+  int64_t ldq;
+  const f16* s;
+  int64_t lds;
+};
+template <class T>
+struct WeightOp<T, W4SymArgs> {
+  using Op = mp::W4SymOperand<T::BN, T::NT>;
+  INTENT_DEVICE static void init(Op& op, const W4SymArgs& w, int n0, int N) { op.init(w.q, w.ldq, w.s, w.lds, n0, N); }
+};
 template <class T>
 struct WeightOp<T, W8Args> {
   using Op = mp::W8Operand<T::BN, T::NT>;
@@ -1077,4 +1089,28 @@ extern "C" int intent_f16_gemm_kn(const void* a, int64_t M, int64_t K, int64_t a
                        0, (hipStream_t)stream, (const f16*)a, a_ld, (int)M, (const f16*)b, b_ld, (int)N, (int)K,
                        nullptr, nullptr, 0, nullptr, (int8_t*)c, c_ld, mblocks, epilogue + 1);
   return intent::launch_status(epilogue == 2 ? "gemm_kn_kernel<bf16>" : "gemm_kn_kernel<f16>");
+}
+
+extern "C" int intent_w4a16_sym_gemm(const void* x, int64_t M, int64_t K, int64_t x_ld, const int32_t* packed,
+                                     int64_t N, int64_t packed_ld, const void* scales, int64_t scales_ld, void* y,
+                                     int64_t y_ld, void* stream) {
+  intent::clear_error();
+  INTENT_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M <= INT32_MAX && N <= INT32_MAX && K <= INT32_MAX,
+                 INTENT_ERR_INVALID_ARGUMENT, "bad extents");
+  INTENT_REQUIRE(K % 64 == 0, INTENT_ERR_UNSUPPORTED, "w4a16_sym_gemm: K must be a multiple of 64, got %lld",
+                 (long long)K);
+  if (M == 0 || N == 0) return INTENT_OK;
+  INTENT_REQUIRE(K > 0, INTENT_ERR_UNSUPPORTED, "w4a16_sym_gemm: K must be positive");
+  INTENT_REQUIRE(x && packed && scales && y, INTENT_ERR_INVALID_ARGUMENT, "null pointer argument");
+  INTENT_REQUIRE(x_ld >= K && packed_ld >= N && scales_ld >= N && y_ld >= N, INTENT_ERR_INVALID_ARGUMENT,
+                 "leading stride smaller than the row");
+  INTENT_REQUIRE(intent::aligned16(x) && x_ld % 8 == 0 && intent::aligned4(packed) &&
+                     (reinterpret_cast<uintptr_t>(scales) & 1) == 0,
+                 INTENT_ERR_ALIGNMENT, "w4a16_sym_gemm: 16-byte aligned activation rows, aligned words and scales");
+  INTENT_REQUIRE(intent::fits_offset(K / 8, packed_ld * 4) && intent::fits_offset(K / 64, scales_ld * 2) &&
+                     intent::fits_offset(256 + 1, x_ld * 2),
+                 INTENT_ERR_UNSUPPORTED, "w4a16_sym_gemm: operand too large for 31-bit buffer offsets");
+  W4SymArgs w{packed, packed_ld, (const f16*)scales, scales_ld};
+  return launch_dense<W4SymArgs, false>((const f16*)x, x_ld, (int)M, (int)N, (int)K, w, (f16*)y, y_ld, nullptr,
+                                        (hipStream_t)stream, "w4a16_sym_gemm");
 }

@@ -503,6 +503,72 @@ struct W4Operand {
   }
 };
 
+// The reference's own W4 layout as a B operand (weight_only_int4_matmul,
+// examples/kernels/contraction/weight_only_int4.py:18-51): int32 words
+// [K/8, N] (word (r, n): k = 8r .. 8r+7 of column n, signed nibble k % 8) and
+// f16 scales [K/64, N]. A stage (64 k) is one scale group and eight k-rows of
+// words; item i = thread + NT j takes column i % ROWS of k-row i / ROWS, so a
+// wave loads 64 consecutive columns (256 bytes) of one k-row per instruction.
+// A word has the nibble order of a [N, K/2] dword, so w ^ 0x88888888 (nibble
+// + 8) decodes through dequant8 with zero point 8 into 16 bytes of f16: chunk
+// r of B row (column) i % ROWS.
+template <int ROWS, int NT = NTHREADS>
+struct W4SymOperand {
+  static constexpr bool kWinParams = false;
+  static constexpr int NS = 8 * ROWS / NT;  // words per thread per stage
+  static_assert(NS * NT == 8 * ROWS, "W4 word staging must divide evenly");
+  static constexpr int NVM = 2 * NS;
+  static constexpr int NDS = NS;
+  Rsrc rq, rs;
+  uint32_t qoff[NS], soff[NS];
+  int lcol[NS], krow[NS];
+  uint32_t ldq_stage;  // bytes of eight k-rows of words
+  uint32_t lds_stage;  // bytes of one scale row
+  struct Regs {
+    uint32_t w[NS];
+    uint32_t s[NS];
+  };
+  // q: word (0, 0); ldq / lds: words / scales per row; the tile's columns are
+  // n0 .. n0 + ROWS - 1, those past N re-read column N - 1.
+  INTENT_DEVICE void init(const int32_t* q, int64_t ldq, const f16* s, int64_t lds, int n0, int N) {
+    rq = make_rsrc(q);
+    rs = make_rsrc(s);
+    ldq_stage = (uint32_t)(8 * ldq * 4);
+    lds_stage = (uint32_t)(lds * 2);
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const int i = (int)(threadIdx.x % NT) + NT * j;
+      lcol[j] = i % ROWS;
+      krow[j] = i / ROWS;
+      const int n = n0 + lcol[j] < N ? n0 + lcol[j] : N - 1;
+      qoff[j] = (uint32_t)((krow[j] * ldq + n) * 4);
+      soff[j] = (uint32_t)(n * 2);
+    }
+  }
+  INTENT_DEVICE bool params_at(int) const { return true; }
+  INTENT_DEVICE void load(int kt, Regs& r) const {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      r.w[j] = __builtin_amdgcn_raw_buffer_load_b32(rq, qoff[j], (uint32_t)kt * ldq_stage, 0);
+      r.s[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, soff[j], (uint32_t)kt * lds_stage, 0);
+    }
+  }
+  template <bool kAsm = false>
+  INTENT_DEVICE void store(const Regs& r, char* lds_b, int = 0) const {
+    const f16x2 zo = splat2((f16)1032.0f);
+#pragma unroll
+    for (int j = 0; j < NS; ++j) {
+      const f16x2 sc = splat2(bit_cast<f16>((uint16_t)r.s[j]));
+      const f16x8 v = dequant8(r.w[j] ^ 0x88888888u, zo, sc);
+      char* dst = lds_b + lcol[j] * ROWB + ((krow[j] ^ swz(lcol[j])) << 4);
+      if constexpr (kAsm)
+        lds_store16(dst, bit_cast<u32x4>(v));
+      else
+        *reinterpret_cast<f16x8*>(dst) = v;
+    }
+  }
+};
+
 // WinParams<B>::value: B loads its group parameters only at some stages
 // (W4Operand<..., true>); mainloop_ws then picks the wait count per step.
 template <class B, class = void>

@@ -943,8 +943,8 @@ def _w4sym_layout(env: dict) -> tuple:
 
 
 def _w4sym_workspace(env: dict) -> int:
-    # the repacked copy is not needed on the in-place decode shapes (alignment permitting)
-    if env["M"] <= 5 and env["K"] <= 8192 and env["N"] % 4 == 0:
+    # the repacked copy is not needed on the in-place shapes (alignment permitting)
+    if (env["M"] <= 5 and env["K"] <= 8192 and env["N"] % 4 == 0) or env["M"] > 16:
         return 0
     return _w4sym_layout(env)[3]
 
@@ -973,6 +973,10 @@ def _w4sym_launch(v: dict, env: dict, stream: int, workspace) -> str:
         _native.call("intent_w4a16_sym_gemv", _ptr(x), M, K, x.stride(0), _ptr(packed), N, packed.stride(0),
                      _ptr(scales), scales.stride(0), _ptr(y), _ld(y), stream)
         return "intent_w4a16_sym_gemv"
+    if M > 16 and x.data_ptr() % 16 == 0 and x.stride(0) % 8 == 0 and packed.data_ptr() % 4 == 0:
+        _native.call("intent_w4a16_sym_gemm", _ptr(x), M, K, x.stride(0), _ptr(packed), N, packed.stride(0),
+                     _ptr(scales), scales.stride(0), _ptr(y), _ld(y), stream)
+        return "intent_w4a16_sym_gemm"
     if workspace is None or workspace.numel() < _w4sym_layout(env)[3]:
         import torch
 
@@ -1001,7 +1005,7 @@ weight_only_int4_matmul = KernelDefinition(
     workspace=_w4sym_workspace,
     reference="examples/kernels/contraction/weight_only_int4.py:18-51",
     doc="the reference's symmetric signed-nibble W4 (int32 [K/8, N], f16 scales [K/64, N]): read in place up to "
-        "M = 5, repacked for the W4A16 kernels above",
+        "M = 5 and above M = 16, repacked for the W4A16 GEMV in between",
 )
 
 

@@ -977,20 +977,23 @@ def test_weight_only_int4_matmul_reference_layout(gpu, threads, M, K, N):
     assert_close_rms(host(y)[rows], ref.astype(np.float32), what=f"w4 sym {M}x{K}x{N}")
 
 
-@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (3, 1024, 64), (5, 8192, 132)])
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (3, 1024, 64), (5, 8192, 132), (17, 64, 20), (300, 1024, 390),
+                                   (2048, 4096, 1100)])
 def test_weight_only_int4_matmul_in_place_strided(gpu, threads, M, K, N):
-    """The in-place decode entry (intent_w4a16_sym_gemv) on strided x, packed words and
-    scales, against the oracle; and the entry the operator picked for these shapes."""
+    """The in-place entries (intent_w4a16_sym_gemv up to M = 5, intent_w4a16_sym_gemm above
+    M = 16) on strided x, packed words and scales, against the oracle; and the entry the
+    operator picked for these shapes."""
     rng = np.random.default_rng(K + N)
     x = rng.standard_normal((M, K + 8)).astype(np.float16)
     packed = rng.integers(-2**31, 2**31, (K // 8, N + 4), dtype=np.int64).astype(np.int32)
     scales = rng.uniform(0.005, 0.02, (K // 64, N + 8)).astype(np.float16)
     a = art(intent.weight_only_int4_matmul)
     y = a.run(dev(x)[:, :K], dev(packed)[:, :N], dev(scales)[:, :N])
-    assert a.observation.entry == "intent_w4a16_sym_gemv"
-    ref = oracle.w4_sym(np.ascontiguousarray(x[:, :K]), np.ascontiguousarray(packed[:, :N]),
+    assert a.observation.entry == ("intent_w4a16_sym_gemv" if M <= 5 else "intent_w4a16_sym_gemm")
+    rows = np.r_[0:min(M, 16), max(0, M - 16):M]
+    ref = oracle.w4_sym(np.ascontiguousarray(x[rows, :K]), np.ascontiguousarray(packed[:, :N]),
                         np.ascontiguousarray(scales[:, :N]), threads)
-    assert_close_rms(host(y), ref.astype(np.float32), what=f"w4 sym in place {M}x{K}x{N}")
+    assert_close_rms(host(y)[rows], ref.astype(np.float32), what=f"w4 sym in place {M}x{K}x{N}")
 
 
 # ---- quantized_gemm -------------------------------------------------------------------
