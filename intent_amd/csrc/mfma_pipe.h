@@ -35,7 +35,8 @@
 //   bit 0: the int8/f16 main loop (mainloop) issues no global loads after its
 //          first two stages (later stages compute on stale register data);
 //   bit 1: ... and writes nothing to its LDS stage buffers after the first;
-//   bit 2: the W8A8 epilogue stores nothing (the accumulators stay live).
+//   bit 2: the W8A8 epilogue stores nothing (the accumulators stay live);
+//   bit 3: the FP4 x bf16 producers copy the packed words instead of decoding.
 // Results are meaningless with any bit set; only the timing is of interest.
 #ifndef INTENT_ABLATE
 #define INTENT_ABLATE 0

@@ -644,6 +644,34 @@ def test_fp4_decode_matches_reference_recipe():
     assert set(np.unique(np.abs(got)).tolist()) == {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0}
 
 
+def test_fp4_nibble_gather_in_kernel_source():
+    # The FP4 kernel gathers each dword's eight codes into standard E2M1 nibbles
+    # (sign, e1, e0, m0) with rotate-and-mask terms, then converts nibble pairs
+    # from bytes 2, 1, 0, 3. Read those terms from the kernel source and check
+    # them, with the OCP E2M1 value table, against the oracle on every word.
+    import re
+    src = (Path(__file__).resolve().parents[1] / "intent_amd" / "csrc" / "dense_gemm.hip").read_text()
+    body = src[src.index("INTENT_DEVICE u32x4 fp4x8_to_bf16"):]
+    body = body[:body.index("u32x4 out;")]
+    terms = [(0, int(m, 16)) for m in re.findall(r"\(d & (0x[0-9a-f]+)u\)", body)]
+    terms += [(int(r), int(m, 16)) for r, m in re.findall(r"rotl32\(d, (\d+)\) & (0x[0-9a-f]+)u", body)]
+    sels = [int(v) for v in re.findall(r"cvt_scalef32_pk_bf16_fp4\(n, 1\.0f, (\d)\)", src)]
+    assert len(terms) == 9 and sels == [2, 1, 0, 3]
+    e2m1 = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6, -0.0, -0.5, -1, -1.5, -2, -3, -4, -6], np.float32)
+    words = np.arange(65536, dtype=np.uint32)
+    for shift in (0, 1):  # every word in the low and in the high half of a dword
+        w = np.roll(words, shift)
+        packed = np.stack(((w >> 8) & 255, w & 255), axis=1).astype(np.uint8).reshape(-1)
+        d = packed.view("<u4").astype(np.uint64)
+        n = np.zeros_like(d)
+        for r, m in terms:
+            n |= (((d << r) | (d >> ((32 - r) % 32))) & 0xFFFFFFFF) & m
+        nib = np.stack([(n >> (8 * s + 4 * h)) & 15 for s in sels for h in (0, 1)], axis=1)
+        got = e2m1[nib.astype(np.int64)].reshape(-1)
+        assert np.array_equal(got, oracle.fp4_decode_row(packed))
+        assert np.array_equal(np.signbit(got), np.signbit(oracle.fp4_decode_row(packed)))
+
+
 def test_fp4_bf16_matmul_closed_form():
     g = torch.Generator().manual_seed(32)
     M, K, N = 5, 256, 7
