@@ -627,9 +627,10 @@ def kn_probe() -> None:
 
 
 def ablation_probe(steps: int, warmup: int) -> None:
-    """Config 3 (W8A8, M=4096, N=K=8192) through `intent_w8a8_gemm` of the product library
-    and of each ablation library (intent_amd.build.ABLATIONS) that has been built: one
-    JSON line each, HIP-graph timed over the same rotation of input copies as the bench."""
+    """Config 3 (W8A8, M=4096, N=K=8192) through `intent_w8a8_gemm` and the FP4 x bf16 case
+    (M=N=K=4096) through `intent_fp4_bf16_matmul`, each in the product library and in every
+    ablation library (intent_amd.build.ABLATIONS) that has been built: one JSON line per
+    (library, entry), HIP-graph timed over rotations of input copies as in the bench."""
     import ctypes
 
     import torch
@@ -640,34 +641,53 @@ def ablation_probe(steps: int, warmup: int) -> None:
     h = inputs.config3_w8a8(0)
     M, K = h["a"].shape
     N = h["w"].shape[0]
-    work = 2 * M * N * K
     n = copies_for(M * K + N * K + 2 * M * N, minimum=2)
-    sets = []
+    w8_sets = []
     for _ in range(n):
         d = inputs.to_device(h)
         d["out"] = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-        sets.append(d)
+        w8_sets.append(d)
+    F = 4096
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = (torch.randn((F, F), device="cuda", generator=g) * 0.125).bfloat16()
+    wq = torch.randint(0, 256, (F, F // 2), device="cuda", generator=g, dtype=torch.uint8)
+    fp4_sets = [(x.clone(), wq.clone(), torch.empty((F, F), dtype=torch.bfloat16, device="cuda"))
+                for _ in range(copies_for(F * F * 2 + F * F // 2 + F * F * 2, minimum=2))]
+
+    def w8a8_calls(fn):
+        def make(d):
+            return lambda: fn(d["a"].data_ptr(), M, K, K, d["a_scales"].data_ptr(), d["w"].data_ptr(), N, K,
+                              d["w_scales"].data_ptr(), d["out"].data_ptr(), N,
+                              torch.cuda.current_stream().cuda_stream)
+        return [make(d) for d in w8_sets], 2 * M * N * K
+
+    def fp4_calls(fn):
+        def make(xs, ws, ys):
+            return lambda: fn(xs.data_ptr(), F, F, F, ws.data_ptr(), F, F // 2, ys.data_ptr(), F,
+                              torch.cuda.current_stream().cuda_stream)
+        return [make(*s) for s in fp4_sets], 2 * F * F * F
+
     libs = [("product", B.LIBRARY)] + [(name, B.ablation_library(name)) for name in B.ABLATIONS]
     for name, path in libs:
         if not path.exists():
             print(json.dumps({"probe": "ablation", "variant": name, "missing": str(path)}), flush=True)
             continue
         lib = ctypes.CDLL(str(path))
-        fn = lib.intent_w8a8_gemm
-        args, _ = _native.SIGNATURES["intent_w8a8_gemm"]
-        fn.argtypes, fn.restype = args, ctypes.c_int
+        for entry, calls_for in (("intent_w8a8_gemm", w8a8_calls), ("intent_fp4_bf16_matmul", fp4_calls)):
+            fn = getattr(lib, entry)
+            fn.argtypes, fn.restype = _native.SIGNATURES[entry][0], ctypes.c_int
 
-        def make(d, fn=fn):
-            def go():
-                rc = fn(d["a"].data_ptr(), M, K, K, d["a_scales"].data_ptr(), d["w"].data_ptr(), N, K,
-                        d["w_scales"].data_ptr(), d["out"].data_ptr(), N, torch.cuda.current_stream().cuda_stream)
-                if rc != 0:
-                    raise RuntimeError(f"{name}: intent_w8a8_gemm returned {rc}")
-            return go
+            def checked(f, entry=entry):
+                def go():
+                    rc = f()
+                    if rc != 0:
+                        raise RuntimeError(f"{name}: {entry} returned {rc}")
+                return go
 
-        ms = graph_time([make(d) for d in sets], steps, warmup)
-        print(json.dumps({"probe": "ablation", "variant": name, "library": path.name, "us": round(ms * 1e3, 1),
-                          "TOP/s": round(work / ms / 1e9, 1)}), flush=True)
+            calls, work = calls_for(fn)
+            ms = graph_time([checked(c) for c in calls], steps, warmup)
+            print(json.dumps({"probe": "ablation", "variant": name, "library": path.name, "entry": entry,
+                              "us": round(ms * 1e3, 1), "TOP/s": round(work / ms / 1e9, 1)}), flush=True)
 
 
 def _numa_physical_cores(limit: int = 16) -> list[int]:

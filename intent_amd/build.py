@@ -139,7 +139,7 @@ def build_host_sanitized(out_dir: Path) -> Path:
 
 
 # Measurement-only builds (INTENT_ABLATE in csrc/mfma_pipe.h): name -> bit mask.
-ABLATIONS = {"no_loads": 1, "no_loads_no_lds_writes": 3, "no_epilogue_stores": 4}
+ABLATIONS = {"no_loads": 1, "no_loads_no_lds_writes": 3, "no_epilogue_stores": 4, "fp4_no_decode": 8}
 ABLATION_DIR = LIBRARY.parent / "ablation"
 
 

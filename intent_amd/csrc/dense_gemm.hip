@@ -159,49 +159,6 @@ struct Fp4Operand {
   }
 };
 
-// y[m, n] = bf16(sum_k x[m, k] * fp4(W)[n, k]), bf16 activations, f32 accumulation.
-template <class T>
-__global__ __launch_bounds__(T::NT_WS, 1) void fp4_bf16_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
-                                                                    int M, const uint8_t* __restrict__ wq,
-                                                                    int64_t ldw, int N, int K,
-                                                                    uint16_t* __restrict__ y, int64_t ldy,
-                                                                    int mblocks) {
-  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  char* const bufs[2] = {buf0, buf1};
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
-  Fp4Operand<T::BN, T::NT> bop;
-  bop.init(wq, ldw, ClampRows{n0, N});
-  f32x16 acc[T::TI][T::TJ];
-  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
-  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave() % T::NW);
-  if (!mp::mainloop_ws<T, mp::BF16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
-  const bool vec = (ldy & 3) == 0 && (((uintptr_t)y) & 7) == 0;
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
-    const int m = m0 + T::row(i);
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + T::col(j, g);
-        uint16_t* o = y + (int64_t)m * ldy + n;
-        if (vec && n + 3 < N) {
-          const uint32_t lo = f32_to_bf16_rne(acc[i][j][4 * g]) | ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * g + 1]) << 16);
-          const uint32_t hi =
-              f32_to_bf16_rne(acc[i][j][4 * g + 2]) | ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * g + 3]) << 16);
-          *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
-        } else {
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (n + c < N) o[c] = f32_to_bf16_rne(acc[i][j][4 * g + c]);
-        }
-      }
-  }
-}
 
 // ---- the reference's own W4 layout -> the asymmetric nibble layout --------------
 // weight_only_int4_matmul (weight_only_int4.py:18-51) packs eight signed nibbles
@@ -575,7 +532,7 @@ INTENT_DEVICE void store_dense(const f32x16 (&acc)[T::TI][T::TJ], int m0, int n0
 // reads it back as 16-byte row pieces and stores whole row segments, where the
 // register layout would store 8 bytes in each of 32 rows per instruction.
 // lds: NC * 32 * (2 * WTN + 16) bytes that no wave reads or writes any more.
-template <class T, bool kColScale>
+template <class T, bool kColScale, bool kBf16 = false>
 INTENT_DEVICE void store_dense_lds(const f32x16 (&acc)[T::TI][T::TJ], char* lds, int m0, int n0, int M, int N,
                                    f16* __restrict__ y, int64_t ldy, const f16* __restrict__ colscale) {
   constexpr int RS = 2 * T::WTN + 16;  // LDS row bytes
@@ -599,10 +556,14 @@ INTENT_DEVICE void store_dense_lds(const f32x16 (&acc)[T::TI][T::TJ], char* lds,
           v[c] = acc[i][j][4 * g + c];
           if (kColScale) v[c] *= n + c < N ? (float)colscale[n + c] : 0.f;
         }
-        const f16x2 lo = __builtin_convertvector(f32x2{v[0], v[1]}, f16x2);
-        const f16x2 hi = __builtin_convertvector(f32x2{v[2], v[3]}, f16x2);
-        *reinterpret_cast<u32x2*>(blk + (lane & 31) * RS + (n - wn) * 2) =
-            u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+        u32x2 pk;
+        if constexpr (kBf16) {
+          pk = u32x2{bf16x2_rne(v[0], v[1]), bf16x2_rne(v[2], v[3])};
+        } else {
+          pk = u32x2{bit_cast<uint32_t>(__builtin_convertvector(f32x2{v[0], v[1]}, f16x2)),
+                     bit_cast<uint32_t>(__builtin_convertvector(f32x2{v[2], v[3]}, f16x2))};
+        }
+        *reinterpret_cast<u32x2*>(blk + (lane & 31) * RS + (n - wn) * 2) = pk;
       }
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
@@ -620,6 +581,31 @@ INTENT_DEVICE void store_dense_lds(const f32x16 (&acc)[T::TI][T::TJ], char* lds,
       }
     }
   }
+}
+
+// y[m, n] = bf16(sum_k x[m, k] * fp4(W)[n, k]), bf16 activations, f32 accumulation.
+template <class T>
+__global__ __launch_bounds__(T::NT_WS, 1) void fp4_bf16_gemm_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                    int M, const uint8_t* __restrict__ wq,
+                                                                    int64_t ldw, int N, int K,
+                                                                    uint16_t* __restrict__ y, int64_t ldy,
+                                                                    int mblocks) {
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  char* const bufs[2] = {buf0, buf1};
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  Fp4Operand<T::BN, T::NT> bop;
+  bop.init(wq, ldw, ClampRows{n0, N});
+  f32x16 acc[T::TI][T::TJ];
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{x, ldx * 2, M}, m0, T::wave() % T::NW);
+  if (!mp::mainloop_ws<T, mp::BF16Math, 2>(aop, bop, K / 64, bufs, acc)) return;
+  // The stage buffer of stage nk - 2 is free after the main loop, as in dense_gemm_kernel.
+  static_assert(T::NW * 32 * (2 * T::WTN + 16) <= T::STAGE_BYTES, "FP4 tiles stage their epilogue in LDS");
+  store_dense_lds<T, false, true>(acc, ((K / 64) & 1) ? buf1 : buf0, m0, n0, M, N, reinterpret_cast<f16*>(y), ldy,
+                                  nullptr);
 }
 
 // y[m, n] = f16(sum_k x[m, k] * deq(W)[n, k] (* colscale[n])).

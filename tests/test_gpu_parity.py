@@ -961,6 +961,40 @@ def test_dequant_bf16_fp4_matmul(gpu, threads, M, K, N):
     assert np.max(np.abs(g64 - r64)) <= 1e-2 * np.abs(r64).max()
 
 
+def _fp4_decode_torch(packed):
+    """E2M1 weights as f32 by the reference's recipe (cpu_runtime.py:117-124), on packed's device."""
+    word = (packed[:, 0::2].int() << 8) | packed[:, 1::2].int()
+    bits = torch.stack((word & 0x81C0, (word << 3) & 0x81C0, (word << 6) & 0x81C0,
+                        ((word << 1) & 0x8000) | ((word >> 3) & 0x0180) | ((word >> 7) & 0x0040)),
+                       dim=-1).flatten(1).to(torch.int16)
+    return (bits.view(torch.bfloat16).float() * (2.0 ** 126)).bfloat16().float()
+
+
+@pytest.mark.parametrize("M,K,N,y_pad", [(1000, 512, 520, 0), (700, 256, 300, 3), (4096, 1024, 1032, 8)])
+def test_fp4_whole_matrix_and_strided_output(gpu, M, K, N, y_pad):
+    """Every output element of intent_fp4_bf16_matmul (middle row and column tiles included)
+    against an f32 product of the decoded weights, on a contiguous or padded (odd stride:
+    element stores) output whose padding columns must stay untouched."""
+    from intent_amd import _native
+
+    g = torch.Generator().manual_seed(M + N + y_pad)
+    x = (torch.randn(M, K, generator=g) * 0.125).bfloat16()
+    packed = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
+    dec = _fp4_decode_torch(packed)
+    for r in (0, N - 1):  # the recipe is the oracle's decode
+        assert np.array_equal(dec[r].numpy(), oracle.fp4_decode_row(packed[r].numpy()))
+    xd, pd = x.cuda(), packed.cuda()
+    ld = N + y_pad
+    y = torch.full((M, ld), -7.0, dtype=torch.bfloat16, device="cuda")
+    _native.call("intent_fp4_bf16_matmul", xd.data_ptr(), M, K, K, pd.data_ptr(), N, K // 2, y.data_ptr(), ld, 0)
+    torch.cuda.synchronize()
+    ref = xd.float() @ dec.cuda().t()
+    err = (y[:, :N].float() - ref).abs().max().item()
+    assert err <= 1e-2 * ref.abs().max().item(), err
+    if y_pad:
+        assert torch.all(y[:, N:] == -7.0)
+
+
 # ---- the reference's own weight_only_int4_matmul layout --------------------------------
 
 @pytest.mark.parametrize("M,K,N", [(512, 2048, 4096), (1, 2048, 4096), (3, 256, 100), (40, 128, 33),
