@@ -514,6 +514,69 @@ INTENT_DEVICE void zero(i32x16 (&acc)[TI][TJ]) {
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0;  // the bits of +0.0f
 }
 
+
+// Output staging through LDS for the kernels fed by dma_mainloop. After its
+// last stage every wave has waited for its own DMA, so one workgroup barrier
+// leaves the whole stage ring free. Each wave then owns 32 x (WTN * EB + 16)
+// bytes and moves its WTM x WTN tile 32 rows at a time: lanes write their
+// accumulator layout (row lane % 32, four consecutive columns, packed by
+// pack(i, j, g) into EB dwords: one output element is EB bytes), then read
+// back whole 16-byte row pieces, so a store instruction covers whole row
+// segments instead of 4 * EB bytes in each of 32 rows. Rows past M are
+// skipped; pieces past N, or an output without 16-byte aligned rows, store
+// element by element.
+template <int EB>
+struct Piece {
+  uint32_t w[EB];
+};
+template <class T, int EB, class Pack>
+INTENT_DEVICE void store_rows_lds(char* smem, int m0, int n0, int M, int N, char* __restrict__ out, int64_t ldo_bytes,
+                                  Pack&& pack) {
+  constexpr int RS = T::WTN * EB + 16;  // LDS row bytes
+  constexpr int CH = T::WTN * EB / 16;  // 16-byte pieces per row
+  constexpr int NP = 32 * CH / 64;      // pieces per lane and block
+  constexpr int EPP = 16 / EB;          // elements per piece
+  static_assert(NP * 64 == 32 * CH, "whole pieces per lane");
+  static_assert(T::NW * 32 * RS <= 2 * ((T::BM + T::BN) * mp::ROWB), "staging fits the stage ring");
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  char* blk = smem + T::wave() * 32 * RS;
+  const int wm = m0 + T::wave_m() * T::WTM, wn = n0 + T::wave_n() * T::WTN;
+  const bool vec = (ldo_bytes & 15) == 0 && (((uintptr_t)out) & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const Piece<EB> v = pack(i, j, g);
+        char* d = blk + (lane & 31) * RS + (n0 + T::col(j, g) - wn) * EB;
+        if constexpr (EB == 4)
+          *reinterpret_cast<u32x4*>(d) = u32x4{v.w[0], v.w[1], v.w[2], v.w[3]};
+        else if constexpr (EB == 2)
+          *reinterpret_cast<u32x2*>(d) = u32x2{v.w[0], v.w[1]};
+        else
+          *reinterpret_cast<uint32_t*>(d) = v.w[0];
+      }
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int p = q * 64 + lane, r = p / CH, cb = (p % CH) * 16;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(blk + r * RS + cb);
+      const int gm = wm + i * 32 + r, gn = wn + cb / EB;
+      if (gm >= M) continue;
+      char* dst = out + (int64_t)gm * ldo_bytes + (int64_t)gn * EB;
+      if (vec && gn + EPP <= N) {
+        *reinterpret_cast<u32x4*>(dst) = v;
+      } else {
+        uint8_t b[16];
+        __builtin_memcpy(b, &v, 16);
+#pragma unroll
+        for (int e = 0; e < EPP; ++e)
+          if (gn + e < N) __builtin_memcpy(dst + e * EB, b + e * EB, EB);
+      }
+    }
+  }
+}
 }  // namespace mxdma
 
 __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
@@ -533,7 +596,10 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
   mxdma::zero(acc);
   mxdma::dma_mainloop<T, mxdma::ScaleMode::kE8M0>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, acc,
                                                   mxdma::NoHook{});
-  store_mx<T>(acc, m0, n0, M, N, out, ldo);
+  mxdma::store_rows_lds<T, 4>(smem, m0, n0, M, N, reinterpret_cast<char*>(out), ldo * 4, [&](int i, int j, int g) {
+    return mxdma::Piece<4>{{(uint32_t)acc[i][j][4 * g], (uint32_t)acc[i][j][4 * g + 1], (uint32_t)acc[i][j][4 * g + 2],
+                            (uint32_t)acc[i][j][4 * g + 3]}};
+  });
 }
 
 // Per-tensor scaled FP8 GEMM with an f16 result (block_scaled.py:42-63 and,
@@ -638,27 +704,9 @@ __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* 
   };
   const auto koff = [nks, splits](int kt) { return mxdma::SplitK{splits, kt / nks}(kt % nks); };
   mxdma::dma_mainloop<T, mxdma::ScaleMode::kHook>(smem, aop, bop, nks * splits, koff, acc, fold);
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
-    const int m = m0 + T::row(i);
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + T::col(j, g);
-        f16* dst = out + (int64_t)m * ldo + n;
-        const f16x2 lo = o[i][j][2 * g], hi = o[i][j][2 * g + 1];
-        if (vec && n + 3 < N) {
-          *reinterpret_cast<u32x2*>(dst) = u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
-        } else {
-          if (n < N) dst[0] = lo[0];
-          if (n + 1 < N) dst[1] = lo[1];
-          if (n + 2 < N) dst[2] = hi[0];
-          if (n + 3 < N) dst[3] = hi[1];
-        }
-      }
-  }
+  mxdma::store_rows_lds<T, 2>(smem, m0, n0, M, N, reinterpret_cast<char*>(out), ldo * 2, [&](int i, int j, int g) {
+    return mxdma::Piece<2>{{bit_cast<uint32_t>(o[i][j][2 * g]), bit_cast<uint32_t>(o[i][j][2 * g + 1])}};
+  });
 }
 
 // int8 GEMM with b [K][N] read in place (gemm_i8, examples/kernels/contraction/
@@ -682,30 +730,14 @@ __global__ __launch_bounds__(256, 1) void i8_gemm_kn_kernel(const uint8_t* __res
   mxdma::zero(acc);
   mxdma::dma_mainloop<T, mxdma::ScaleMode::kInt8>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, acc,
                                                   mxdma::NoHook{});
-  const bool vec = (ldc & 3) == 0 && (((uintptr_t)c) & 15) == 0;
+  mxdma::store_rows_lds<T, 4>(smem, m0, n0, M, N, reinterpret_cast<char*>(c), ldc * 4, [&](int i, int j, int g) {
+    mxdma::Piece<4> v;
+    const int n = n0 + T::col(j, g);
 #pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
-    const int m = m0 + T::row(i);
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + T::col(j, g);
-        int32_t* o = c + (int64_t)m * ldc + n;
-        uint32_t v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          v[q] = (uint32_t)acc[i][j][4 * g + q] + (uint32_t)(bias && n + q < N ? bias[n + q] : 0);
-        if (vec && n + 3 < N) {
-          *reinterpret_cast<i32x4*>(o) = i32x4{(int)v[0], (int)v[1], (int)v[2], (int)v[3]};
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (n + q < N) o[q] = (int32_t)v[q];
-        }
-      }
-  }
+    for (int q = 0; q < 4; ++q)
+      v.w[q] = (uint32_t)acc[i][j][4 * g + q] + (uint32_t)(bias && n + q < N ? bias[n + q] : 0);
+    return v;
+  });
 }
 
 // DeepGEMM-style FP8 GEMM with f32 block scales (deepgemm_fp8_2xacc,
@@ -755,30 +787,11 @@ __global__ __launch_bounds__(256, 1) void deepgemm_fp8_kernel(const uint8_t* __r
   };
   mxdma::dma_mainloop<T, mxdma::ScaleMode::kPromote>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, fresh,
                                                      promote);
-  // Lane holds m = row(i) and n = col(j, g) + 0..3 in acc[i][j][4g..4g+3].
-  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 7) == 0;
-#pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
-    const int m = m0 + T::row(i);
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + T::col(j, g);
-        uint16_t* o = out + (int64_t)m * ldo + n;
-        if (vec && n + 3 < N) {
-          const uint32_t lo = f32_to_bf16_rne(acc[i][j][4 * g]) | ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * g + 1]) << 16);
-          const uint32_t hi =
-              f32_to_bf16_rne(acc[i][j][4 * g + 2]) | ((uint32_t)f32_to_bf16_rne(acc[i][j][4 * g + 3]) << 16);
-          *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (n + q < N) o[q] = f32_to_bf16_rne(acc[i][j][4 * g + q]);
-        }
-      }
-  }
+  mxdma::store_rows_lds<T, 2>(smem, m0, n0, M, N, reinterpret_cast<char*>(out), ldo * 2, [&](int i, int j, int g) {
+    const f32x16& v = acc[i][j];
+    return mxdma::Piece<2>{{f32_to_bf16_rne(v[4 * g]) | ((uint32_t)f32_to_bf16_rne(v[4 * g + 1]) << 16),
+                            f32_to_bf16_rne(v[4 * g + 2]) | ((uint32_t)f32_to_bf16_rne(v[4 * g + 3]) << 16)}};
+  });
 }
 
 // FP8 x FP8 -> FP8 GEMM (fp8_e4m3_matmul, fp8_e5m2_matmul,
@@ -802,30 +815,13 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_kernel(const uint8_t* __restr
   mxdma::zero(acc);
   mxdma::dma_mainloop<T, mxdma::ScaleMode::kNone, mxdma::SplitK, mxdma::NoHook, kFmt>(
       smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, acc, mxdma::NoHook{});
-  const bool vec = (ldo & 3) == 0 && (((uintptr_t)out) & 3) == 0;
+  mxdma::store_rows_lds<T, 1>(smem, m0, n0, M, N, reinterpret_cast<char*>(out), ldo, [&](int i, int j, int g) {
+    const f32x16 c = bit_cast<f32x16>(acc[i][j]);
+    uint32_t q[4];
 #pragma unroll
-  for (int i = 0; i < T::TI; ++i) {
-    const int m = m0 + T::row(i);
-    if (m >= M) continue;
-#pragma unroll
-    for (int j = 0; j < T::TJ; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + T::col(j, g);
-        const f32x16 c = bit_cast<f32x16>(acc[i][j]);
-        uint32_t q[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) q[e] = kFmt == 0 ? f32_to_e4m3fn(c[4 * g + e]) : f32_to_e5m2(c[4 * g + e]);
-        uint8_t* o = out + (int64_t)m * ldo + n;
-        if (vec && n + 3 < N) {
-          *reinterpret_cast<uint32_t*>(o) = q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < N) o[e] = (uint8_t)q[e];
-        }
-      }
-  }
+    for (int e = 0; e < 4; ++e) q[e] = kFmt == 0 ? f32_to_e4m3fn(c[4 * g + e]) : f32_to_e5m2(c[4 * g + e]);
+    return mxdma::Piece<1>{{q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24)}};
+  });
 }
 
 // Byte-matrix transpose through a 64 x 64 LDS tile: dst[c][r] = src[r][c].

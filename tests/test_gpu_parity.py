@@ -46,6 +46,13 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
+def _sample_rows(M):
+    """Output rows checked against the oracle when a whole matrix would take it too long: the
+    first and last 40 (every lane row of the first and last 32-row blocks) and every 37th
+    between them (coprime with 32, so every row position of a block in some middle tile)."""
+    return np.unique(np.r_[0:min(M, 40), max(0, M - 40):M, np.arange(40, max(40, M - 40), 37)])
+
+
 def host(t):
     torch.cuda.synchronize()
     return t.cpu().numpy()
@@ -786,7 +793,7 @@ def test_scaled_fp8_matmul(gpu, threads, M, K, N):
     lhs = dev(a).view(torch.float8_e4m3fn)
     rhs = dev(b).view(torch.float8_e4m3fn)
     out = art(intent.scaled_fp8_matmul).run(lhs, rhs, 0.5, 1.5)
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     ref = oracle.scaled_fp8_gemm(a[rows], b, 0.5, 1.5, threads=threads)
     _f16_close(host(out)[rows], ref, f"scaled_fp8 {M}x{K}x{N}")
 
@@ -800,7 +807,7 @@ def test_scaled_fp8_splitk(gpu, threads, M, IT, SP, N):
     rhs = dev(b).view(torch.float8_e4m3fn).view(IT, SP, 256, N)
     out = out0.cuda()
     art(intent.scaled_fp8_splitk_matmul).run(lhs, rhs, out, 0.25, 2.0)
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     ref = oracle.scaled_fp8_gemm(a[rows], b, 0.25, 2.0, splits=SP, out=out0.numpy()[rows], threads=threads)
     _f16_close(host(out)[rows], ref, f"splitk {M}x{K}x{N}/{SP}")
 
@@ -829,7 +836,7 @@ def test_scaled_fp8_kn_in_place(gpu, threads, M, K, N, ldb, splits):
         torch.cuda.synchronize()
         outs.append(host(out))
     assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16)), f"kn vs rows {M}x{K}x{N}"
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     ref = oracle.scaled_fp8_gemm(a[rows], b, 0.5, 1.5, splits=splits,
                                  out=out0.numpy()[rows] if splits > 1 else None, threads=threads)
     _f16_close(outs[0][rows], ref, f"scaled_fp8_kn {M}x{K}x{N}/{splits}")
@@ -895,7 +902,7 @@ def test_deepgemm_fp8(gpu, threads, M, KB, N):
     lhs = dev(a).view(torch.float8_e4m3fn).view(M, KB, 128)
     rhs = dev(b).view(torch.float8_e4m3fn).view(N, KB, 128)
     out = art(intent.deepgemm_fp8_2xacc).run(lhs, rhs, dev(sa), dev(sb))
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     ref = _bf16_bits_to_f64(oracle.deepgemm_fp8(a[rows], sa[rows], b, sb, threads))
     got = host(out.view(torch.int16)).view(np.uint16)[rows]
     # bf16 output: one rounding of ~2^-8 relative on either side
@@ -933,7 +940,7 @@ def test_fp8_out_matmul(gpu, threads, fmt, M, K, N):
     b = (torch.randn(N, K, generator=g) * 0.25).to(tdt)
     defn = intent.fp8_e4m3_matmul if fmt == "e4m3fn" else intent.fp8_e5m2_matmul
     out = art(defn).run(a.cuda(), b.cuda())
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     ref = oracle.fp8_gemm(a.view(torch.uint8).numpy()[rows], b.view(torch.uint8).numpy(), fmt, threads)
     got = host(out.view(torch.uint8))[rows]
     # identical codes except where the two f32 sums (different order) straddle a
@@ -953,7 +960,7 @@ def test_dequant_bf16_fp4_matmul(gpu, threads, M, K, N):
     x = (torch.randn(M, K, generator=g) * 0.125).bfloat16()   # the reference's input scale
     packed = torch.randint(0, 256, (N, K // 2), generator=g, dtype=torch.uint8)
     out = art(intent.dequant_bf16_fp4_matmul).run(x.cuda(), packed.cuda())
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = np.r_[0:min(M, 8), max(0, M - 8):M]  # every element: test_fp4_whole_matrix_and_strided_output
     ref = oracle.fp4_bf16_matmul(x.view(torch.int16).numpy().view(np.uint16)[rows], packed.numpy(), threads)
     got = host(out.view(torch.int16)).view(np.uint16)[rows]
     r64 = torch.from_numpy(ref.view(np.int16)).view(torch.bfloat16).double().numpy()
@@ -1006,7 +1013,7 @@ def test_weight_only_int4_matmul_reference_layout(gpu, threads, M, K, N):
     packed = rng.integers(-2**31, 2**31, (K // 8, N), dtype=np.int64).astype(np.int32)
     scales = rng.uniform(0.005, 0.02, (K // 64, N)).astype(np.float16)
     y = art(intent.weight_only_int4_matmul).run(dev(x), dev(packed), dev(scales))
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     ref = oracle.w4_sym(x[rows], packed, scales, threads)
     assert_close_rms(host(y)[rows], ref.astype(np.float32), what=f"w4 sym {M}x{K}x{N}")
 
@@ -1043,7 +1050,7 @@ def test_quantized_gemm(gpu, threads, M, K, N):
     residual = (torch.randn((M, N), generator=g) * 0.25).half()
     scale = torch.linspace(1.0 / 48.0, 1.0 / 24.0, N)
     out = art(intent.quantized_gemm).run(a.cuda(), b.cuda(), bias.cuda(), residual.cuda(), scale.cuda())
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     ref = oracle.quantized_gemm(a.numpy()[rows], b.numpy(), bias.numpy(), residual.numpy()[rows], scale.numpy(),
                                 threads)
     got = host(out)[rows]
@@ -1061,7 +1068,7 @@ def test_gemm_i8_reference_layout(gpu, threads, M, K, N):
     b = rng.integers(-128, 128, (K, N), dtype=np.int8)
     bias = rng.integers(-2**31, 2**31 - 1, N, dtype=np.int64).astype(np.int32)
     c = art(intent.gemm_i8).run(dev(a), dev(b), dev(bias))
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     assert np.array_equal(host(c)[rows], oracle.i8_gemm_i32(a[rows], np.ascontiguousarray(b.T), bias, threads))
 
 
@@ -1213,7 +1220,7 @@ def test_float_gemm(gpu, threads, kind, M, K, N, bpad):
     c = art_.run(a.cuda(), bdev)
     direct = N % 8 == 0 and bpad % 8 == 0
     assert art_.observation.entry == ("intent_f16_gemm_kn" if direct else "intent_f16_gemm")
-    rows = np.r_[0:min(M, 8), max(0, M - 8):M]
+    rows = _sample_rows(M)
     ref = oracle.float_gemm(_bits16(a)[rows], _bits16(b), kind == "bf16", kind == "f16_relu", threads)
     r64 = torch.from_numpy(ref.view(np.int16)).view(tdt).double().numpy()
     g64 = torch.from_numpy(_bits16(c.cpu())[rows].view(np.int16)).view(tdt).double().numpy()
