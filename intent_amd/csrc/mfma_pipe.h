@@ -178,6 +178,26 @@ struct I8Math {
   using Frag = i32x4;
   INTENT_DEVICE static Acc mfma(Frag b, Frag a, Acc c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(b, a, c, 0, 0, 0); }
 };
+// E4M3 x E4M3 -> f32 on the f8f6f4 MFMA (32 x 32 x 64, block scales 2^0).
+// Its operands are 32 bytes per lane, so the main loops feed it pairs of the
+// 16-byte fragments the other maths use (kPairs): steps 2s and 2s + 1 of a
+// stage together. A and B take the same k positions, so only the summation
+// order within an MFMA differs from the row order.
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+struct F8Math {
+  using Acc = f32x16;
+  using Frag = i32x4;
+  static constexpr bool kPairs = true;
+  INTENT_DEVICE static Acc mfma2(Frag b0, Frag b1, Frag a0, Frag a1, Acc c) {
+    const i32x8 b{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+    const i32x8 a{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b, a, c, 0, 0, 0, 127, 0, 127);
+  }
+};
+template <class Math, class = void>
+struct PairedFrags : std::false_type {};
+template <class Math>
+struct PairedFrags<Math, std::void_t<decltype(Math::kPairs)>> : std::bool_constant<Math::kPairs> {};
 
 // ---- row sources: byte offset of tile row p from a per-tile base --------------
 // Rows that hold no data map to some valid row; loads stay unpredicated and
@@ -698,6 +718,47 @@ INTENT_DEVICE void compute_stage(const char* buf, const uint32_t (&aaddr)[4], co
   }
 }
 
+// compute_stage for a Math with paired fragments (PairedFrags): two MFMA
+// steps per 128-byte stage, step s on the fragments of steps 2s and 2s + 1;
+// the reads of step 1 are interleaved with the MFMAs of step 0.
+template <class T, class Math>
+INTENT_DEVICE void compute_stage_pairs(const char* buf, const uint32_t (&aaddr)[4], const uint32_t (&baddr)[4],
+                                       typename Math::Acc (&acc)[T::TI][T::TJ]) {
+  using Frag = typename Math::Frag;
+  constexpr int NR = 2 * (T::TI + T::TJ);
+  constexpr int NM = T::TI * T::TJ;
+  Frag af[2][2][T::TI], bf[2][2][T::TJ];
+  const char* a = buf;
+  const char* b = buf + T::A_BYTES;
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int i = 0; i < T::TI; ++i)
+        af[s][h][i] = *reinterpret_cast<const Frag*>(a + aaddr[2 * s + h] + i * 32 * ROWB);
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j)
+        bf[s][h][j] = *reinterpret_cast<const Frag*>(b + baddr[2 * s + h] + j * 32 * ROWB);
+    }
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j)
+        acc[i][j] = Math::mfma2(bf[s][0][j], bf[s][1][j], af[s][0][i], af[s][1][i], acc[i][j]);
+  __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+  constexpr int PAIRS = NR < NM ? NR : NM;
+  static_for<0, PAIRS>([&](auto X) {
+    constexpr int x = decltype(X)::value;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, (x + 1) * NR / PAIRS - x * NR / PAIRS, 0);
+  });
+  if (NM > PAIRS) __builtin_amdgcn_sched_group_barrier(0x008, NM - PAIRS, 0);
+  __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+}
+
 // Instruction schedule of one pipelined step: 4*NM MFMA slots. The fragment
 // reads of step kk+1 ride on the first NR slots of step kk; NV buffer loads
 // are spread over the first half of the slots and NW LDS writes over the
@@ -1016,9 +1077,21 @@ INTENT_DEVICE void mainloop_kn(const ADma& aop, const BDma& bop, int nk, char* b
 // each). Operands must be built with NT = T::NT (producer thread index =
 // threadIdx.x % NT) and the producer wave index. Returns true in consumer
 // waves, which then hold acc.
-template <class T, class Math, int NB, class Rows, class BOp, bool kSwap = false>
+// kmap: the k block (128 bytes of each A row) that stage kt reads, the same
+// for A and B (identity: stage kt reads block kt). hook(acc, kt) runs in the
+// consumer waves after stage kt's MFMAs.
+struct StageIdentity {
+  INTENT_DEVICE int operator()(int kt) const { return kt; }
+};
+struct StageNoHook {
+  template <class A>
+  INTENT_DEVICE void operator()(A&, int) const {}
+};
+template <class T, class Math, int NB, class Rows, class BOp, bool kSwap = false, class KMap = StageIdentity,
+          class Hook = StageNoHook>
 INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, const BOp& bop, int nk,
-                               char* const (&bufs)[NB], typename Math::Acc (&acc)[T::TI][T::TJ]) {
+                               char* const (&bufs)[NB], typename Math::Acc (&acc)[T::TI][T::TJ], KMap kmap = {},
+                               Hook&& hook = {}) {
   static_assert(NB == 2 || NB == 3, "two or three stage buffers");
   using ADma = DmaRowsOperand<T::BM, Rows, T::NW>;
   const bool consumer = T::wave() < T::NW;
@@ -1033,12 +1106,13 @@ INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, co
     typename BOp::Regs rb[NB];
 #pragma unroll
     for (int s = 0; s < NB - 1; ++s)
-      if (s < nk) aop.issue(bufs[s], s);
+      if (s < nk) aop.issue(bufs[s], kmap(s));
 #pragma unroll
     for (int s = 0; s < NB; ++s)
-      if (s < nk) bop.load(s, rb[s]);
+      if (s < nk) bop.load(kmap(s), rb[s]);
     constexpr bool kWinB = WinParams<BOp>::value;
     static_assert(!kWinB || NB == 2, "windowed group parameters: two stage buffers");
+    static_assert(!kWinB || std::is_same_v<KMap, StageIdentity>, "windowed group parameters: stages in order");
     if constexpr (kWinB)
       bop.template store<true>(rb[0], bufs[0] + T::A_BYTES, 0);
     else
@@ -1056,9 +1130,9 @@ INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, co
     auto step = [&](auto J, int kt) {
       constexpr int j = decltype(J)::value;  // kt % NB
       const bool full = kt + NB < nk;
-      aop.issue(bufs[(j + NB - 1) % NB], kt + NB - 1 < nk ? kt + NB - 1 : nk - 1);
+      aop.issue(bufs[(j + NB - 1) % NB], kmap(kt + NB - 1 < nk ? kt + NB - 1 : nk - 1));
       __builtin_amdgcn_sched_barrier(0);
-      bop.load(full ? kt + NB : nk - 1, rb[j]);
+      bop.load(kmap(full ? kt + NB : nk - 1), rb[j]);
       if constexpr (kWinB) {
         bop.template store<true>(rb[(j + 1) % NB], bufs[(j + 1) % NB] + T::A_BYTES, kt + 1);
         // in flight: stage kt + 2's loads, with or without its group parameters
@@ -1101,7 +1175,11 @@ INTENT_DEVICE bool mainloop_ws(const DmaRowsOperand<T::BM, Rows, T::NW>& aop, co
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
       if (kt + j < nk) {
-        compute_stage<T, Math, 4, true, kSwap>(bufs[j], aaddr, baddr, acc);
+        if constexpr (PairedFrags<Math>::value)
+          compute_stage_pairs<T, Math>(bufs[j], aaddr, baddr, acc);
+        else
+          compute_stage<T, Math, 4, true, kSwap>(bufs[j], aaddr, baddr, acc);
+        hook(acc, kt + j);
         if (kt + j < nk - 1) wait_vm_lgkm_barrier<0>();
       }
     }

@@ -635,9 +635,8 @@ __global__ __launch_bounds__(256) void fp8_scaled_empty_k_kernel(f16* __restrict
   }
 }
 
-// kKN: b is the [K][N] operand itself (N % 16 == 0), read in place
-// (mxdma::KNBytes); otherwise its [N][K] rows.
-template <bool kAccum, bool kKN>
+// b: the right operand's [N][K] rows (the [K][N] form goes to fp8_scaled_ws_kernel).
+template <bool kAccum>
 __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
                                                                  const uint8_t* __restrict__ b, int64_t ldb, int N,
                                                                  int K, int splits, float ls, float rs,
@@ -648,12 +647,9 @@ __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* 
   const int m0 = (blockIdx.x % mblocks) * T::BM;
   const int n0 = (blockIdx.x / mblocks) * T::BN;
   mxdma::Rows<T::BM, T::NW, false> aop;
-  std::conditional_t<kKN, mxdma::KNBytes<T::BN, T::NW>, mxdma::Rows<T::BN, T::NW, false>> bop;
+  mxdma::Rows<T::BN, T::NW, false> bop;
   aop.init(a, lda, M, nullptr, 0, m0, T::wave());
-  if constexpr (kKN)
-    bop.init(b, ldb, N, n0, T::wave());
-  else
-    bop.init(b, ldb, N, nullptr, 0, n0, T::wave());
+  bop.init(b, ldb, N, nullptr, 0, n0, T::wave());
   const int nks = K / mp::ROWB / splits;
   // The lane's outputs: m = row(i), n = col(j, g) + q, as packed f16 pairs
   // o[i][j][2g + q/2] (64 registers).
@@ -707,6 +703,209 @@ __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* 
   mxdma::store_rows_lds<T, 2>(smem, m0, n0, M, N, reinterpret_cast<char*>(out), ldo * 2, [&](int i, int j, int g) {
     return mxdma::Piece<2>{{bit_cast<uint32_t>(o[i][j][2 * g]), bit_cast<uint32_t>(o[i][j][2 * g + 1])}};
   });
+}
+
+// [K][N] bytes (N contiguous: the reference's right operand, block_scaled.py
+// :62-93) read in place by producer waves and transposed on the way to LDS:
+// k block kb (128 bytes of k) of columns n0 .. n0 + 127 becomes 128 LDS rows,
+// one per column, of 128 k-bytes in the row form's chunk order (chunk c of
+// row n at c ^ swz(n)), so that the consumers read it like an [N][K] operand.
+// Producer thread t of NT: column quad q = t % 32 (columns 4q .. 4q + 3),
+// k-rows 16 (t / 32) .. + 15. Per stage it issues 16 dword loads (a wave
+// reads two 128-byte row segments per load), transposes each 4 x 4 byte
+// block with v_perm_b32 and writes one 16-byte chunk per column. Lanes whose
+// bit 2 of q is set write their columns in the order 2 3 0 1, so that any 8
+// consecutive lanes write 8 distinct chunk positions (no bank conflicts).
+// Columns past N re-read the last valid quad (their products land in output
+// columns that are never stored): N % 4 == 0.
+template <int NT>
+struct KNTransposeOperand {
+  static_assert(NT == 256, "eight k-row groups of 32 column quads");
+  static constexpr bool kWinParams = false;
+  static constexpr int NVM = 16;  // loads per stage
+  struct Regs {
+    uint32_t d[16];
+  };
+  mp::Rsrc rb;
+  uint32_t voff;
+  uint32_t ld;
+  int kb, q;
+  uint32_t sel_lo, sel_hi;  // first-level perm selectors (swapped for the rotated lanes)
+  INTENT_DEVICE void init(const uint8_t* b, int64_t ldb, int N, int n0) {
+    const int t = (int)(threadIdx.x % NT);
+    q = t & 31;
+    kb = t >> 5;
+    const int valid = N - n0;
+    const int col = 4 * q + 4 <= valid ? 4 * q : valid - 4;
+    rb = make_rsrc(b + n0);
+    ld = (uint32_t)ldb;
+    voff = (uint32_t)(kb * 16 * ldb + col);
+    const bool rot = (q >> 2) & 1;
+    // (d_even, d_odd) -> {e.b0, o.b0, e.b1, o.b1} and {e.b2, o.b2, e.b3, o.b3}
+    sel_lo = rot ? 0x07030602u : 0x05010400u;
+    sel_hi = rot ? 0x05010400u : 0x07030602u;
+  }
+  // blk: the k block of the stage (128 k-rows of [K][N]).
+  INTENT_DEVICE void load(int blk, Regs& r) const {
+    const uint32_t base = (uint32_t)blk * 128u * ld;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r.d[i] = __builtin_amdgcn_raw_buffer_load_b32(rb, voff, base + (uint32_t)i * ld, 0);
+  }
+  template <bool kAsm = false>
+  INTENT_DEVICE void store(const Regs& r, char* lds_b) const {
+    // col[c][g]: k-bytes 4g .. 4g + 3 of column slot c (slot c holds column c
+    // for unrotated lanes, c ^ 2 for rotated ones).
+    uint32_t col[4][4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t d0 = r.d[4 * g], d1 = r.d[4 * g + 1], d2 = r.d[4 * g + 2], d3 = r.d[4 * g + 3];
+      const uint32_t lo01 = __builtin_amdgcn_perm(d1, d0, sel_lo), hi01 = __builtin_amdgcn_perm(d1, d0, sel_hi);
+      const uint32_t lo23 = __builtin_amdgcn_perm(d3, d2, sel_lo), hi23 = __builtin_amdgcn_perm(d3, d2, sel_hi);
+      col[0][g] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+      col[1][g] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+      col[2][g] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+      col[3][g] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
+    }
+    const int rot = ((q >> 2) & 1) << 1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int n = 4 * q + (c ^ rot);
+      char* dst = lds_b + n * mp::ROWB + ((kb ^ mp::swz(n)) << 4);
+      const u32x4 v{col[c][0], col[c][1], col[c][2], col[c][3]};
+      if constexpr (kAsm)
+        mp::lds_store16(dst, v);
+      else
+        *reinterpret_cast<u32x4*>(dst) = v;
+    }
+  }
+};
+
+// The per-tensor scaled FP8 GEMM (and split-K) with the [K][N] operand read in
+// place, on the producer/consumer core (mp::mainloop_ws): four consumer waves
+// of 128 x 64 and four producer waves per 256 x 128 tile; producers copy the
+// A rows by LDS DMA and transpose the B bytes into LDS. Split s's stages run
+// in order, and at the end of each the consumers fold the split's f32 sum
+// into the f16 output tile, which lives in LDS (64 KB beside the two 48 KB
+// stage buffers: the registers of two waves per SIMD do not hold it beside
+// the accumulators and fragments): o = f16(o + f16((acc * ls) * rs)), o read
+// from out first (kAccum), else o = the one split's product.
+// Consumer wave c's region: 128 rows of 128 bytes (its 64 columns); 16-byte
+// unit u (columns 8u .. 8u + 7) of row r sits at unit u ^ (r & 7). With
+// 16-byte aligned output rows, producer wave c fills region c from out by LDS
+// DMA before the main loop (the prologue's wait covers it); otherwise the
+// consumer loads it.
+INTENT_DEVICE int ounit(int r, int u) { return u ^ (r & 7); }
+
+template <bool kAccum>
+__global__ __launch_bounds__(TSk::NT_WS, 1) void fp8_scaled_ws_kernel(const uint8_t* __restrict__ a, int64_t lda,
+                                                                      int M, const uint8_t* __restrict__ b,
+                                                                      int64_t ldb, int N, int K, int splits, float ls,
+                                                                      float rs, f16* __restrict__ out, int64_t ldo,
+                                                                      int mblocks) {
+  using T = TSk;
+  constexpr int ORB = T::WTN * 2;  // bytes per row of an output region
+  static_assert(ORB == 128 && T::WTM == 128, "output regions of 128 x 64");
+  __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) char otile[T::NW * T::WTM * ORB];
+  char* const bufs[2] = {buf0, buf1};
+  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int m0 = (bid % mblocks) * T::BM;
+  const int n0 = (bid / mblocks) * T::BN;
+  const int nks = K / mp::ROWB / splits;
+  const int lane = threadIdx.x & 63;
+  const bool consumer = T::wave() < T::NW;
+  const int region = T::wave() % T::NW;  // consumer: its own; producer: the one it fills
+  char* const ot = otile + region * T::WTM * ORB;
+  const int wm = m0 + (region % T::WM) * T::WTM, wn = n0 + (region / T::WM) * T::WTN;
+  const bool dma_out = (ldo & 7) == 0 && (((uintptr_t)out) & 15) == 0 && (int64_t)M * ldo * 2 < (1ll << 31);
+  if (kAccum && !consumer && dma_out) {
+    // 16 DMA instructions of 8 rows x 128 bytes; lane l fills unit l % 8 of
+    // row 8 j + l / 8, i.e. logical unit (l % 8) ^ (row & 7). Rows past M
+    // re-read row M - 1 and units past N the last valid one (never stored).
+    const mp::Rsrc ro = make_rsrc(out);
+#pragma unroll
+    for (int j = 0; j < T::WTM / 8; ++j) {
+      const int r = 8 * j + (lane >> 3);
+      const int gm = wm + r < M ? wm + r : M - 1;
+      const int gn0 = wn + 8 * ounit(r, lane & 7);
+      const int gn = gn0 + 8 <= N ? gn0 : N - 8;
+      mp::lds_dma<16, false>(ro, (mp::lds_t*)(ot + j * 8 * ORB), (uint32_t)(((int64_t)gm * ldo + gn) * 2), 0u);
+    }
+  }
+  if (kAccum && consumer && !dma_out) {
+#pragma unroll 4
+    for (int p = lane; p < T::WTM * 16; p += 64) {  // 8-byte pieces: row p / 16, columns 4 (p % 16) ..
+      const int r = p >> 4, sl = p & 15, gm = wm + r, gn = wn + 4 * sl;
+      uint16_t e[4] = {0, 0, 0, 0};
+      if (gm < M) {
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(out + (int64_t)gm * ldo + gn);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (gn + c < N) e[c] = src[c];
+      }
+      *reinterpret_cast<u32x2*>(ot + r * ORB + (ounit(r, sl >> 1) << 4) + ((sl & 1) << 3)) =
+          u32x2{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16)};
+    }
+  }
+  KNTransposeOperand<T::NT> bop;
+  bop.init(b, ldb, N, n0);
+  mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
+  aop.init(mp::DenseRows{a, lda, M}, m0, T::wave() % T::NW);
+  f32x16 acc[T::TI][T::TJ];
+  auto fold = [&](f32x16 (&c)[T::TI][T::TJ], int kt) {
+    if ((kt + 1) % nks) return;  // wave-uniform: only at the end of a split
+    const int h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i) {
+      const int r = i * 32 + (lane & 31);
+      char* row = ot + r * ORB + (h << 3);
+      // The lane's 4 columns of group (j, g) are unit 4 j + g, half h.
+      u32x2 o[T::TJ][4];
+      if constexpr (kAccum) {
+#pragma unroll
+        for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) o[j][g] = *reinterpret_cast<const u32x2*>(row + (ounit(r, 4 * j + g) << 4));
+      }
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          f16 p[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) p[e] = (f16)__fmul_rn(__fmul_rn(c[i][j][4 * g + e], ls), rs);
+          f16x2 lo{p[0], p[1]}, hi{p[2], p[3]};
+          if constexpr (kAccum) {
+            const f16x2 olo = bit_cast<f16x2>(o[j][g][0]), ohi = bit_cast<f16x2>(o[j][g][1]);
+            lo = f16x2{(f16)__fadd_rn((float)olo[0], (float)p[0]), (f16)__fadd_rn((float)olo[1], (float)p[1])};
+            hi = f16x2{(f16)__fadd_rn((float)ohi[0], (float)p[2]), (f16)__fadd_rn((float)ohi[1], (float)p[3])};
+          }
+          *reinterpret_cast<u32x2*>(row + (ounit(r, 4 * j + g) << 4)) =
+              u32x2{bit_cast<uint32_t>(lo), bit_cast<uint32_t>(hi)};
+        }
+        c[i][j] = f32x16{};
+      }
+    }
+  };
+  const auto kmap = [nks, splits](int kt) { return (int)(mxdma::SplitK{splits, kt / nks}(kt % nks) / mp::ROWB); };
+  if (!mp::mainloop_ws<T, mp::F8Math, 2>(aop, bop, nks * splits, bufs, acc, kmap, fold)) return;
+  // The wave's region -> out: 8 lanes (128 bytes) per row segment.
+  const bool vec = (ldo & 7) == 0 && (((uintptr_t)out) & 15) == 0;
+#pragma unroll 4
+  for (int p = lane; p < T::WTM * 8; p += 64) {
+    const int r = p >> 3, u = p & 7, gm = wm + r, gn = wn + 8 * u;
+    if (gm >= M) continue;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(ot + r * ORB + (ounit(r, u) << 4));
+    f16* dst = out + (int64_t)gm * ldo + gn;
+    if (vec && gn + 7 < N) {
+      *reinterpret_cast<u32x4*>(dst) = v;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (gn + c < N) reinterpret_cast<uint16_t*>(dst)[c] = (uint16_t)(v[c >> 1] >> (16 * (c & 1)));
+    }
+  }
 }
 
 // int8 GEMM with b [K][N] read in place (gemm_i8, examples/kernels/contraction/
@@ -1008,8 +1207,13 @@ static int scaled_fp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t a_ld,
   const int mblocks = (int)((M + TSk::BM - 1) / TSk::BM);
   const int64_t grid = (int64_t)mblocks * ((N + TSk::BN - 1) / TSk::BN);
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "scaled_fp8_gemm: grid too large");
-  auto kernel = accumulate ? (kn ? fp8_scaled_gemm_kernel<true, true> : fp8_scaled_gemm_kernel<true, false>)
-                           : (kn ? fp8_scaled_gemm_kernel<false, true> : fp8_scaled_gemm_kernel<false, false>);
+  if (kn) {  // producer waves transpose [K][N] on its way to LDS
+    hipLaunchKernelGGL(accumulate ? fp8_scaled_ws_kernel<true> : fp8_scaled_ws_kernel<false>, dim3((unsigned)grid),
+                       dim3(TSk::NT_WS), 0, (hipStream_t)stream, a, a_ld, (int)M, b, b_ld, (int)N, (int)K,
+                       (int)splits, a_scale, b_scale, (f16*)out, out_ld, mblocks);
+    return intent::launch_status("scaled_fp8_gemm");
+  }
+  auto kernel = accumulate ? fp8_scaled_gemm_kernel<true> : fp8_scaled_gemm_kernel<false>;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a, a_ld, (int)M, b, b_ld,
                      (int)N, (int)K, (int)splits, a_scale, b_scale, (f16*)out, out_ld, mblocks);
   return intent::launch_status("scaled_fp8_gemm");

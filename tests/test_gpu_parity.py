@@ -812,29 +812,38 @@ def test_scaled_fp8_splitk(gpu, threads, M, IT, SP, N):
     _f16_close(host(out)[rows], ref, f"splitk {M}x{K}x{N}/{SP}")
 
 
-@pytest.mark.parametrize("M,K,N,ldb,splits", [(300, 512, 4096, 4096, 1), (257, 384, 144, 160, 1),
-                                              (130, 1024, 272, 288, 2), (64, 128, 16, 16, 1)])
-def test_scaled_fp8_kn_in_place(gpu, threads, M, K, N, ldb, splits):
+@pytest.mark.parametrize("M,K,N,ldb,splits,out_pad", [(300, 512, 4096, 4096, 1, 0), (257, 384, 144, 160, 1, 0),
+                                                      (130, 1024, 272, 288, 2, 0), (64, 128, 16, 16, 1, 0),
+                                                      (130, 1024, 272, 288, 2, 4), (520, 2048, 400, 400, 4, 8),
+                                                      (600, 1536, 160, 176, 3, 2), (1, 256, 32, 32, 1, 0)])
+def test_scaled_fp8_kn_in_place(gpu, threads, M, K, N, ldb, splits, out_pad):
     """intent_scaled_fp8_gemm_kn reads b [K, N] in place, with a row stride past N and
-    a last column tile that is partly outside N; against the oracle and against the
-    transposed-copy entry on the same inputs (bit-equal: same tile, same sum order)."""
+    a last column tile that is partly outside N, into outputs with 16-byte aligned rows
+    or not (out_pad 2, 4: the output tile is then loaded and stored element-wise);
+    against the oracle and against the transposed-copy entry on the same inputs (bit-equal:
+    same tile, same k pairing per MFMA), and the padding columns stay untouched."""
     from intent_amd import _native
     a, bfull = _fp8_bits(M + K, (M, K)), _fp8_bits(N + K, (K, ldb))
     b = np.ascontiguousarray(bfull[:, :N])
     out0 = (torch.randn(M, N, generator=torch.Generator().manual_seed(5)) * 4).half()
+    ld = N + out_pad
     ad, bd = dev(a), dev(bfull)
     outs = []
     for kn in (True, False):
-        out = out0.cuda()
+        full = torch.full((M, ld), -3.0, dtype=torch.float16)
+        full[:, :N] = out0
+        out = full.cuda()
         if kn:
             _native.call("intent_scaled_fp8_gemm_kn", ad.data_ptr(), M, K, K, bd.data_ptr(), N, ldb, 0.5, 1.5,
-                         splits, int(splits > 1), out.data_ptr(), N, 0)
+                         splits, int(splits > 1), out.data_ptr(), ld, 0)
         else:
             bt = dev(np.ascontiguousarray(b.T))
             _native.call("intent_scaled_fp8_gemm", ad.data_ptr(), M, K, K, bt.data_ptr(), N, K, 0.5, 1.5, splits,
-                         int(splits > 1), out.data_ptr(), N, 0)
+                         int(splits > 1), out.data_ptr(), ld, 0)
         torch.cuda.synchronize()
-        outs.append(host(out))
+        got = host(out)
+        assert np.all(got[:, N:] == -3.0)
+        outs.append(np.ascontiguousarray(got[:, :N]))
     assert np.array_equal(outs[0].view(np.uint16), outs[1].view(np.uint16)), f"kn vs rows {M}x{K}x{N}"
     rows = _sample_rows(M)
     ref = oracle.scaled_fp8_gemm(a[rows], b, 0.5, 1.5, splits=splits,
