@@ -113,6 +113,21 @@ INTENT_DEVICE int xcd_swizzle(int bid, int nblocks) {
   return (bid & 7) * per_xcd + (bid >> 3);
 }
 
+// Tile (row block, column block) of logical tile id bid, in groups of gm row
+// blocks: inside a group the row block varies fastest. After xcd_swizzle an
+// XCD's co-resident workgroups hold consecutive ids, so with gm = 4 the 32 of
+// a round cover 4 row blocks x 8 column blocks, and the operand blocks they
+// stream at one time fit its L2 (row-block-fastest over 16 row blocks would
+// stream a column block's whole left operand through every XCD).
+INTENT_DEVICE void grouped_tile(int bid, int mblocks, int nblocks, int gm, int& mb, int& nb) {
+  const int group = bid / (gm * nblocks);
+  const int first = group * gm;
+  const int rows = mblocks - first < gm ? mblocks - first : gm;
+  const int local = bid - group * gm * nblocks;
+  mb = first + local % rows;
+  nb = local / rows;
+}
+
 // f32 -> E4M3FN bits, round half to even; |f| >= 448 saturates to 448 (inputs
 // past the format's range are outside the cast's contract), NaN -> NaN.
 INTENT_DEVICE uint32_t f32_to_e4m3fn(float f) {

@@ -809,9 +809,10 @@ __global__ __launch_bounds__(TSk::NT_WS, 1) void fp8_scaled_ws_kernel(const uint
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char otile[T::NW * T::WTM * ORB];
   char* const bufs[2] = {buf0, buf1};
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
+  int mb, nb;
+  grouped_tile(xcd_swizzle(blockIdx.x, gridDim.x), mblocks, (int)gridDim.x / mblocks, 4, mb, nb);
+  const int m0 = mb * T::BM;
+  const int n0 = nb * T::BN;
   const int nks = K / mp::ROWB / splits;
   const int lane = threadIdx.x & 63;
   const bool consumer = T::wave() < T::NW;
