@@ -128,6 +128,12 @@ INTENT_DEVICE void grouped_tile(int bid, int mblocks, int nblocks, int gm, int& 
   nb = local / rows;
 }
 
+// This workgroup's tile in a grid of mblocks x (gridDim.x / mblocks) tiles:
+// xcd_swizzle, then groups of gm row blocks (grouped_tile).
+INTENT_DEVICE void grid_tile(int mblocks, int gm, int& mb, int& nb) {
+  grouped_tile(xcd_swizzle(blockIdx.x, gridDim.x), mblocks, (int)gridDim.x / mblocks, gm, mb, nb);
+}
+
 // f32 -> E4M3FN bits, round half to even; |f| >= 448 saturates to 448 (inputs
 // past the format's range are outside the cast's contract), NaN -> NaN.
 INTENT_DEVICE uint32_t f32_to_e4m3fn(float f) {

@@ -372,9 +372,10 @@ __global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   char* const bufs[2] = {buf0, buf1};
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   const int pw = T::wave() % T::NW;
   mp::RegRowsOperand<T::BN, mp::DenseRows, false, T::NW> bop;
   bop.init(mp::DenseRows{bt, ldb * 2, N}, n0, pw);
@@ -397,9 +398,10 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_kn_kernel(
     int8_t* __restrict__ out, int64_t ldo, int mblocks, int f16_epi = 0) {
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   const int wave = T::wave();
   mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
   aop.init(mp::DenseRows{a, lda * 2, M}, m0, wave);
@@ -593,9 +595,10 @@ __global__ __launch_bounds__(T::NT_WS, 1) void fp4_bf16_gemm_kernel(const uint16
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   char* const bufs[2] = {buf0, buf1};
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   Fp4Operand<T::BN, T::NT> bop;
   bop.init(wq, ldw, ClampRows{n0, N});
   f32x16 acc[T::TI][T::TJ];
@@ -617,9 +620,10 @@ __global__ __launch_bounds__(T::NT_WS, 1) void dense_gemm_kernel(const f16* __re
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   char* const bufs[2] = {buf0, buf1};
-  const int bid = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int m0 = (bid % mblocks) * T::BM;
-  const int n0 = (bid / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   typename WeightOp<T, WArgs>::Op bop;
   WeightOp<T, WArgs>::init(bop, w, n0, N);
   f32x16 acc[T::TI][T::TJ];

@@ -150,8 +150,10 @@ __global__ __launch_bounds__(T::NT, 1) void mxfp8_gemm_kernel(const uint8_t* __r
   using L = MxLayout<T>;
   __shared__ __attribute__((aligned(16))) char buf0[L::STAGE];
   __shared__ __attribute__((aligned(16))) char buf1[L::STAGE];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   const int wave = T::wave();
   const int nk = K / mp::ROWB;
   ScaledRows<T::BM, T::NW> aop;
@@ -586,8 +588,10 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
                                                                 float* __restrict__ out, int64_t ldo, int mblocks) {
   using T = mxdma::Tile;
   __shared__ __attribute__((aligned(1024))) char smem[2 * mxdma::kStage];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   mxdma::Rows<T::BM, T::NW, true> aop;
   mxdma::Rows<T::BN, T::NW, true> bop;
   aop.init(a, lda, M, sa, ld_sa, m0, T::wave());
@@ -644,8 +648,10 @@ __global__ __launch_bounds__(256, 1) void fp8_scaled_gemm_kernel(const uint8_t* 
   using T = TSk;
   constexpr int SB = (T::BM + T::BN) * (mp::ROWB + 4);
   __shared__ __attribute__((aligned(1024))) char smem[2 * SB];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   mxdma::Rows<T::BM, T::NW, false> aop;
   mxdma::Rows<T::BN, T::NW, false> bop;
   aop.init(a, lda, M, nullptr, 0, m0, T::wave());
@@ -920,8 +926,10 @@ __global__ __launch_bounds__(256, 1) void i8_gemm_kn_kernel(const uint8_t* __res
   using T = TSk;
   constexpr int SB = (T::BM + T::BN) * (mp::ROWB + 4);
   __shared__ __attribute__((aligned(1024))) char smem[2 * SB];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   mxdma::Rows<T::BM, T::NW, false> aop;
   mxdma::KNBytes<T::BN, T::NW> bop;
   aop.init(a, lda, M, nullptr, 0, m0, T::wave());
@@ -958,8 +966,10 @@ __global__ __launch_bounds__(256, 1) void deepgemm_fp8_kernel(const uint8_t* __r
   using T = TDg;
   constexpr int SB = (T::BM + T::BN) * (mp::ROWB + 4);
   __shared__ __attribute__((aligned(1024))) char smem[2 * SB];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   mxdma::Rows<T::BM, T::NW, true> aop;
   mxdma::Rows<T::BN, T::NW, true> bop;
   aop.init(a, lda, M, reinterpret_cast<const uint8_t*>(sa), ld_sa * 4, m0, T::wave(), 1);
@@ -1005,8 +1015,10 @@ __global__ __launch_bounds__(256, 1) void fp8_gemm_kernel(const uint8_t* __restr
                                                           uint8_t* __restrict__ out, int64_t ldo, int mblocks) {
   using T = mxdma::Tile;
   __shared__ __attribute__((aligned(1024))) char smem[2 * mxdma::kStage];
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   mxdma::Rows<T::BM, T::NW, false> aop;
   mxdma::Rows<T::BN, T::NW, false> bop;
   aop.init(a, lda, M, nullptr, 0, m0, T::wave());

@@ -131,9 +131,12 @@ __global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restr
                                                                 void* __restrict__ out, int64_t ldo, int mblocks) {
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
-  // Plain dispatch order (m fastest): measured faster here than the XCD-grouped order.
-  const int m0 = (blockIdx.x % mblocks) * T::BM;
-  const int n0 = (blockIdx.x / mblocks) * T::BN;
+  // XCD-grouped tile order (4 row blocks x 8 column blocks per XCD round): 1% faster here
+  // than plain m-fastest dispatch, which beat xcd_swizzle alone.
+  int tmb, tnb;
+  grid_tile(mblocks, 4, tmb, tnb);
+  const int m0 = tmb * T::BM;
+  const int n0 = tnb * T::BN;
   const int wave = T::wave();
   const int nk = (K + mp::ROWB - 1) / mp::ROWB;
   const bool half = kHalf;
@@ -222,6 +225,7 @@ __global__ __launch_bounds__(T::NT_WS, 1) void lowbit_ws_kernel(const int8_t* __
   __shared__ __attribute__((aligned(16))) char buf0[T::STAGE_BYTES];
   __shared__ __attribute__((aligned(16))) char buf1[T::STAGE_BYTES];
   char* const bufs[2] = {buf0, buf1};
+  // Plain m-fastest order: the XCD-grouped order (grid_tile) measured 0.7% slower here.
   const int m0 = (blockIdx.x % mblocks) * T::BM;
   const int n0 = (blockIdx.x / mblocks) * T::BN;
   const int pw = T::wave() % T::NW;
