@@ -408,6 +408,22 @@ INTENT_DEVICE void dma_mainloop(char* smem,
   // stage's end.
   i32x8 af[2][T::TI], bf[2][T::TJ];
   uint32_t csa[T::TI], csb[T::TJ], nsa[T::TI], nsb[T::TJ];
+  // kPromote: hook(i, j, fresh, xa, xb) folds one tile's stage sum. Stage
+  // kt's sums are folded tile by tile just before stage kt + 1's first MFMA
+  // of the tile overwrites them, with stage kt's scale dwords kept in psa /
+  // psb, so each fold's VALU work overlaps the MFMAs in flight; the first
+  // fold adds zeros, the last stage is folded after the loop.
+  uint32_t psa[T::TI], psb[T::TJ];
+  if constexpr (kMode == ScaleMode::kPromote) {
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i) psa[i] = 0u;
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j) psb[j] = 0u;
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j) acc[i][j] = i32x16{};
+  }
   uint32_t knb[T::TJ];
   if constexpr (BOp::kKN) {
 #pragma unroll
@@ -443,6 +459,8 @@ INTENT_DEVICE void dma_mainloop(char* smem,
                                                            acc[i][j], 0, 0, 0);
           continue;
         }
+        if constexpr (kMode == ScaleMode::kPromote)
+          if (s == 0) hook(i, j, acc[i][j], psa, psb);  // fold the previous stage's sum of this tile
         f32x16 c = bit_cast<f32x16>(acc[i][j]);
         if (kMode == ScaleMode::kPromote && s == 0) c = f32x16{};  // a fresh sum per stage
         const int sb_ = kMode == ScaleMode::kE8M0 ? (int)((csb[j] >> sh) & 255u) : 127;
@@ -486,14 +504,28 @@ INTENT_DEVICE void dma_mainloop(char* smem,
       read(nb, 0, 0);
       mfmas(1);
       interleave(std::integral_constant<int, NR + (kScales ? 4 : 0)>{});
-      if constexpr (kHooked) hook(acc, csa, csb, kt);
+      if constexpr (kMode == ScaleMode::kPromote) {
+#pragma unroll
+        for (int i = 0; i < T::TI; ++i) psa[i] = csa[i];
+#pragma unroll
+        for (int j = 0; j < T::TJ; ++j) psb[j] = csb[j];
+      } else if constexpr (kHooked) {
+        hook(acc, csa, csb, kt);
+      }
 #pragma unroll
       for (int i = 0; i < T::TI; ++i) csa[i] = nsa[i];
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j) csb[j] = nsb[j];
     } else {
       mfmas(1);
-      if constexpr (kHooked) hook(acc, csa, csb, kt);
+      if constexpr (kMode == ScaleMode::kPromote) {
+#pragma unroll
+        for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+          for (int j = 0; j < T::TJ; ++j) hook(i, j, acc[i][j], csa, csb);
+      } else if constexpr (kHooked) {
+        hook(acc, csa, csb, kt);
+      }
     }
   };
   for (int kt = 0; kt < nk - 1; ++kt) stage(kt, std::true_type{});
@@ -982,18 +1014,11 @@ __global__ __launch_bounds__(256, 1) void deepgemm_fp8_kernel(const uint8_t* __r
     for (int j = 0; j < T::TJ; ++j) acc[i][j] = f32x16{};
   // The wave's B rows all lie in one 128-row block (BN = 128), so one rhs
   // scale serves the stage.
-  auto promote = [&](const i32x16 (&f)[T::TI][T::TJ], const uint32_t (&xa)[T::TI], const uint32_t (&xb)[T::TJ], int) {
-    const float rs = bit_cast<float>(xb[0]);
+  auto promote = [&](int i, int j, const i32x16& f, const uint32_t (&xa)[T::TI], const uint32_t (&xb)[T::TJ]) {
+    const float w = __fmul_rn(bit_cast<float>(xa[i]), bit_cast<float>(xb[0]));
+    const f32x16 v = bit_cast<f32x16>(f);
 #pragma unroll
-    for (int i = 0; i < T::TI; ++i) {
-      const float w = __fmul_rn(bit_cast<float>(xa[i]), rs);
-#pragma unroll
-      for (int j = 0; j < T::TJ; ++j) {
-        const f32x16 v = bit_cast<f32x16>(f[i][j]);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(v[e], w, acc[i][j][e]);
-      }
-    }
+    for (int e = 0; e < 16; ++e) acc[i][j][e] = __builtin_fmaf(v[e], w, acc[i][j][e]);
   };
   mxdma::dma_mainloop<T, mxdma::ScaleMode::kPromote>(smem, aop, bop, K / mp::ROWB, mxdma::SplitK{1, 0}, fresh,
                                                      promote);
