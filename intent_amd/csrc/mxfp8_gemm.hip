@@ -437,16 +437,20 @@ INTENT_DEVICE void dma_mainloop(char* smem,
       bf[set][j] = BOp::kKN ? read_frag_kn(base + T::A_BYTES, knb[j], s)
                             : read_frag(base + T::A_BYTES, rb + 32 * j, 4 * s + h);
   };
+  // E8M0 scale dwords are shifted right by 8h as they are read: lane half h
+  // then finds group 2s + h's byte at byte 2s, which the MFMA's scale byte
+  // select picks (no byte extraction per MFMA).
+  const uint32_t sc_shift = kMode == ScaleMode::kE8M0 ? 8u * (uint32_t)h : 0u;
   auto read_scales = [&](const char* base, uint32_t (&xa)[T::TI], uint32_t (&xb)[T::TJ]) {
 #pragma unroll
     for (int i = 0; i < T::TI; ++i)
-      xa[i] = kScales ? *reinterpret_cast<const uint32_t*>(base + A_SC + (ra + 32 * i) * 4) : 0x7F7F7F7Fu;
+      xa[i] = kScales ? *reinterpret_cast<const uint32_t*>(base + A_SC + (ra + 32 * i) * 4) >> sc_shift : 0x7F7F7F7Fu;
 #pragma unroll
     for (int j = 0; j < T::TJ; ++j)
-      xb[j] = kScales ? *reinterpret_cast<const uint32_t*>(base + B_SC + (rb + 32 * j) * 4) : 0x7F7F7F7Fu;
+      xb[j] = kScales ? *reinterpret_cast<const uint32_t*>(base + B_SC + (rb + 32 * j) * 4) >> sc_shift : 0x7F7F7F7Fu;
   };
-  auto mfmas = [&](int s) {
-    const int sh = 8 * (2 * s + h);
+  auto mfmas = [&](auto S) {
+    constexpr int s = decltype(S)::value;
 #pragma unroll
     for (int i = 0; i < T::TI; ++i)
 #pragma unroll
@@ -463,9 +467,11 @@ INTENT_DEVICE void dma_mainloop(char* smem,
           if (s == 0) hook(i, j, acc[i][j], psa, psb);  // fold the previous stage's sum of this tile
         f32x16 c = bit_cast<f32x16>(acc[i][j]);
         if (kMode == ScaleMode::kPromote && s == 0) c = f32x16{};  // a fresh sum per stage
-        const int sb_ = kMode == ScaleMode::kE8M0 ? (int)((csb[j] >> sh) & 255u) : 127;
-        const int sa_ = kMode == ScaleMode::kE8M0 ? (int)((csa[i] >> sh) & 255u) : 127;
-        c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[s][j], af[s][i], c, kFmt, kFmt, 0, sb_, 0, sa_);
+        if constexpr (kMode == ScaleMode::kE8M0)
+          c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[s][j], af[s][i], c, kFmt, kFmt, 2 * s, (int)csb[j],
+                                                              2 * s, (int)csa[i]);
+        else
+          c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bf[s][j], af[s][i], c, kFmt, kFmt, 0, 127, 0, 127);
         acc[i][j] = bit_cast<i32x16>(c);
       }
   };
@@ -494,7 +500,7 @@ INTENT_DEVICE void dma_mainloop(char* smem,
     const int slot = kt & 1;
     const char* base = smem + slot * SB;
     read(base, 1, 1);
-    mfmas(0);
+    mfmas(std::integral_constant<int, 0>{});
     interleave(std::integral_constant<int, NR>{});
     if constexpr (decltype(more)::value) {
       mp::wait_vm_lgkm_barrier<0>();  // stage kt+1 landed everywhere; stage kt fully read
@@ -502,7 +508,7 @@ INTENT_DEVICE void dma_mainloop(char* smem,
       const char* nb = smem + (slot ^ 1) * SB;
       read_scales(nb, nsa, nsb);
       read(nb, 0, 0);
-      mfmas(1);
+      mfmas(std::integral_constant<int, 1>{});
       interleave(std::integral_constant<int, NR + (kScales ? 4 : 0)>{});
       if constexpr (kMode == ScaleMode::kPromote) {
 #pragma unroll
@@ -517,7 +523,7 @@ INTENT_DEVICE void dma_mainloop(char* smem,
 #pragma unroll
       for (int j = 0; j < T::TJ; ++j) csb[j] = nsb[j];
     } else {
-      mfmas(1);
+      mfmas(std::integral_constant<int, 1>{});
       if constexpr (kMode == ScaleMode::kPromote) {
 #pragma unroll
         for (int i = 0; i < T::TI; ++i)
