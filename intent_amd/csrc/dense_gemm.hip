@@ -364,6 +364,88 @@ INTENT_DEVICE void dense_epilogue(const f32x16 (&acc)[T::TI][T::TJ], int m0, int
   }
 }
 
+// quantized_gemm's int8 epilogue through LDS for the 8-wave [K, N] kernel
+// (T::NW = 8 waves of 128 x 64): after a barrier the two stage buffers are
+// free; wave w stages one 32-row block of f32 sums at a time in its own
+// 32 x (64 * 4 + 16)-byte block (waves 0-3 in buf0, 4-7 in buf1), then lane
+// l takes 8 consecutive columns (l % 8) of rows l / 8 + 8 q: 16-byte residual
+// loads and 8-byte int8 stores, eight lanes per 128-byte row segment, instead
+// of 8-byte residual pieces of 32 rows. Bias and scale are per column: each
+// lane loads its 8 once. Same arithmetic per element as dense_epilogue.
+template <class T>
+INTENT_DEVICE void quant_epilogue_lds(const f32x16 (&acc)[T::TI][T::TJ], char* buf0, char* buf1, int m0, int n0,
+                                      int M, int N, const float* __restrict__ bias, const f16* __restrict__ residual,
+                                      int64_t ldr, const float* __restrict__ oscale, int8_t* __restrict__ out,
+                                      int64_t ldo) {
+  static_assert(T::NW == 8 && T::WTN == 64, "eight waves of 64 columns");
+  constexpr int RS = T::WTN * 4 + 16;
+  static_assert(4 * 32 * RS <= T::STAGE_BYTES, "four wave blocks per stage buffer");
+  __syncthreads();  // every wave's DMA has drained (mainloop_kn) and its last fragments are read
+  const int lane = threadIdx.x & 63;
+  const int w = T::wave();
+  char* blk = (w < 4 ? buf0 : buf1) + (w & 3) * 32 * RS;
+  const int wm = m0 + T::wave_m() * T::WTM, wn = n0 + T::wave_n() * T::WTN;
+  const int c8 = (lane & 7) * 8;
+  const int gn = wn + c8;
+  const bool full = gn + 7 < N;
+  const bool vec = full && (ldr & 7) == 0 && (((uintptr_t)residual) & 15) == 0 && (ldo & 7) == 0 &&
+                   (((uintptr_t)out) & 7) == 0 && ((((uintptr_t)bias) | ((uintptr_t)oscale)) & 15) == 0;
+  float bv[8], sv[8];
+  if (vec) {
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + gn), b1 = *reinterpret_cast<const f32x4*>(bias + gn + 4);
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(oscale + gn), s1 = *reinterpret_cast<const f32x4*>(oscale + gn + 4);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) bv[c] = b0[c], bv[4 + c] = b1[c], sv[c] = s0[c], sv[4 + c] = s1[c];
+  } else {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      bv[c] = gn + c < N ? bias[gn + c] : 0.f;
+      sv[c] = gn + c < N ? oscale[gn + c] : 1.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(blk + (lane & 31) * RS + (j * 32 + g * 8 + (lane >> 5) * 4) * 4) =
+            f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = (lane >> 3) + 8 * q;
+      const int gm = wm + i * 32 + r;
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(blk + r * RS + c8 * 4);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(blk + r * RS + c8 * 4 + 16);
+      if (gm >= M) continue;
+      const f16* rp = residual + (int64_t)gm * ldr + gn;
+      uint16_t e[8];
+      if (vec) {
+        const u32x4 rv = *reinterpret_cast<const u32x4*>(rp);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) e[c] = (uint16_t)(rv[c >> 1] >> (16 * (c & 1)));
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) e[c] = gn + c < N ? bit_cast<uint16_t>(rp[c]) : (uint16_t)0;
+      }
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        lo |= quant_i8_epilogue(a0[c], bv[c], bit_cast<f16>(e[c]), sv[c]) << (8 * c);
+        hi |= quant_i8_epilogue(a1[c], bv[4 + c], bit_cast<f16>(e[4 + c]), sv[4 + c]) << (8 * c);
+      }
+      int8_t* o = out + (int64_t)gm * ldo + gn;
+      if (vec) {
+        *reinterpret_cast<u32x2*>(o) = u32x2{lo, hi};
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (gn + c < N) o[c] = (int8_t)(((c < 4 ? lo : hi) >> (8 * (c & 3))) & 255u);
+      }
+    }
+  }
+}
+
 template <class T, DenseEpi E = DenseEpi::kQuantI8, class Math = mp::F16Math>
 __global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
     const f16* __restrict__ a, int64_t lda, int M, const f16* __restrict__ bt, int64_t ldb, int N, int K,
@@ -410,6 +492,12 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_kn_kernel(
   f32x16 acc[T::TI][T::TJ];
   mp::mainloop_kn<T, Math, mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW>, mp::DmaKNOperand<T::BN, T::NW>, kSched>(
       aop, bop, K / 64, buf0, buf1, acc);
+  if constexpr (E == DenseEpi::kQuantI8 && T::NW == 8 && T::WTN == 64) {
+    if (f16_epi == 0) {  // workgroup-uniform
+      quant_epilogue_lds<T>(acc, buf0, buf1, m0, n0, M, N, bias, residual, ldr, oscale, out, ldo);
+      return;
+    }
+  }
   dense_epilogue<T, E>(acc, m0, n0, M, N, bias, residual, ldr, oscale, out, ldo, f16_epi);
 }
 

@@ -1068,6 +1068,37 @@ def test_quantized_gemm(gpu, threads, M, K, N):
     assert np.mean(got == ref) >= 0.99
 
 
+@pytest.mark.parametrize("res_pad,out_pad", [(3, 5), (8, 8), (0, 0)])
+def test_quantized_gemm_kn_strided(gpu, threads, res_pad, out_pad):
+    """intent_quantized_gemm_kn (b [K, N] in place, int8 epilogue staged through LDS) with
+    residual and output row strides that break the 16-/8-byte paths (odd pads) or keep
+    them, over several row and column tiles with a partial last column tile; every sampled
+    row against the oracle, padding columns untouched."""
+    from intent_amd import _native
+    M, K, N = 1000, 512, 520
+    g = torch.Generator().manual_seed(N + res_pad)
+    a = torch.randn((M, K), generator=g).half() / (K ** 0.5)
+    b = torch.randn((K, N), generator=g).half()
+    bias = torch.randn((N,), generator=g) * 0.25
+    residual = (torch.randn((M, N), generator=g) * 0.25).half()
+    scale = torch.linspace(1.0 / 48.0, 1.0 / 24.0, N)
+    rfull = torch.zeros((M, N + res_pad), dtype=torch.float16)
+    rfull[:, :N] = residual
+    ofull = torch.full((M, N + out_pad), 77, dtype=torch.int8)
+    ad, bd, biasd, rd, sd, od = a.cuda(), b.cuda(), bias.cuda(), rfull.cuda(), scale.cuda(), ofull.cuda()
+    _native.call("intent_quantized_gemm_kn", ad.data_ptr(), M, K, K, bd.data_ptr(), N, N, biasd.data_ptr(),
+                 rd.data_ptr(), N + res_pad, sd.data_ptr(), od.data_ptr(), N + out_pad, 0)
+    torch.cuda.synchronize()
+    got_full = host(od)
+    assert np.all(got_full[:, N:] == 77)
+    rows = _sample_rows(M)
+    ref = oracle.quantized_gemm(a.numpy()[rows], b.numpy(), bias.numpy(), residual.numpy()[rows], scale.numpy(),
+                                threads)
+    got = got_full[rows, :N]
+    assert np.max(np.abs(got.astype(np.int32) - ref.astype(np.int32))) <= 2
+    assert np.mean(got == ref) >= 0.99
+
+
 @pytest.mark.parametrize("M,K,N", [(100, 192, 77), (129, 640, 257), (4000, 192, 4100),
                                    (300, 1024, 4096), (257, 384, 144), (64, 128, 16)])
 def test_gemm_i8_reference_layout(gpu, threads, M, K, N):
