@@ -446,6 +446,62 @@ INTENT_DEVICE void quant_epilogue_lds(const f32x16 (&acc)[T::TI][T::TJ], char* b
   }
 }
 
+// The f16 / bf16 outputs of the same kernel (gemm, bf16_gemm) staged the
+// same way: lane l converts 8 consecutive columns of a row (f16, optionally
+// max(v, 0) with NaN kept, or bf16 round-to-nearest-even) and stores them as
+// one 16-byte piece.
+template <class T, DenseEpi E>
+INTENT_DEVICE void half_epilogue_lds(const f32x16 (&acc)[T::TI][T::TJ], char* buf0, char* buf1, int m0, int n0,
+                                     int M, int N, uint16_t* __restrict__ y, int64_t ldy, bool relu) {
+  static_assert(T::NW == 8 && T::WTN == 64, "eight waves of 64 columns");
+  constexpr int RS = T::WTN * 4 + 16;
+  static_assert(4 * 32 * RS <= T::STAGE_BYTES, "four wave blocks per stage buffer");
+  __syncthreads();  // every wave's DMA has drained (mainloop_kn) and its last fragments are read
+  const int lane = threadIdx.x & 63;
+  const int w = T::wave();
+  char* blk = (w < 4 ? buf0 : buf1) + (w & 3) * 32 * RS;
+  const int wm = m0 + T::wave_m() * T::WTM, wn = n0 + T::wave_n() * T::WTN;
+  const int c8 = (lane & 7) * 8;
+  const int gn = wn + c8;
+  const bool vec = gn + 7 < N && (ldy & 7) == 0 && (((uintptr_t)y) & 15) == 0;
+  auto cvt = [relu](float v) -> uint32_t {
+    if constexpr (E == DenseEpi::kGemmBf16) {
+      (void)relu;
+      return f32_to_bf16_rne(v);
+    } else {
+      if (relu) v = v < 0.f ? 0.f : v;
+      return bit_cast<uint16_t>((f16)v);
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < T::TI; ++i) {
+#pragma unroll
+    for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(blk + (lane & 31) * RS + (j * 32 + g * 8 + (lane >> 5) * 4) * 4) =
+            f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r = (lane >> 3) + 8 * q;
+      const int gm = wm + i * 32 + r;
+      const f32x4 a0 = *reinterpret_cast<const f32x4*>(blk + r * RS + c8 * 4);
+      const f32x4 a1 = *reinterpret_cast<const f32x4*>(blk + r * RS + c8 * 4 + 16);
+      if (gm >= M) continue;
+      const u32x4 v{cvt(a0[0]) | (cvt(a0[1]) << 16), cvt(a0[2]) | (cvt(a0[3]) << 16), cvt(a1[0]) | (cvt(a1[1]) << 16),
+                    cvt(a1[2]) | (cvt(a1[3]) << 16)};
+      uint16_t* o = y + (int64_t)gm * ldy + gn;
+      if (vec) {
+        *reinterpret_cast<u32x4*>(o) = v;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (gn + c < N) o[c] = (uint16_t)(v[c >> 1] >> (16 * (c & 1)));
+      }
+    }
+  }
+}
+
 template <class T, DenseEpi E = DenseEpi::kQuantI8, class Math = mp::F16Math>
 __global__ __launch_bounds__(T::NT_WS, 1) void quantized_gemm_kernel(
     const f16* __restrict__ a, int64_t lda, int M, const f16* __restrict__ bt, int64_t ldb, int N, int K,
@@ -492,11 +548,12 @@ __global__ __launch_bounds__(T::NT, 1) void gemm_kn_kernel(
   f32x16 acc[T::TI][T::TJ];
   mp::mainloop_kn<T, Math, mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW>, mp::DmaKNOperand<T::BN, T::NW>, kSched>(
       aop, bop, K / 64, buf0, buf1, acc);
-  if constexpr (E == DenseEpi::kQuantI8 && T::NW == 8 && T::WTN == 64) {
-    if (f16_epi == 0) {  // workgroup-uniform
+  if constexpr (T::NW == 8 && T::WTN == 64) {
+    if (E == DenseEpi::kQuantI8 && f16_epi == 0)  // workgroup-uniform
       quant_epilogue_lds<T>(acc, buf0, buf1, m0, n0, M, N, bias, residual, ldr, oscale, out, ldo);
-      return;
-    }
+    else
+      half_epilogue_lds<T, E>(acc, buf0, buf1, m0, n0, M, N, reinterpret_cast<uint16_t*>(out), ldo, f16_epi == 2);
+    return;
   }
   dense_epilogue<T, E>(acc, m0, n0, M, N, bias, residual, ldr, oscale, out, ldo, f16_epi);
 }

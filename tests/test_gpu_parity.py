@@ -1271,6 +1271,28 @@ def test_float_gemm(gpu, threads, kind, M, K, N, bpad):
     assert (c.double() - full).abs().max().item() <= 1e-2 * full.abs().max().item()
 
 
+@pytest.mark.parametrize("epi", [0, 1, 2])
+@pytest.mark.parametrize("c_pad", [3, 8])
+def test_float_gemm_kn_strided_output(gpu, epi, c_pad):
+    """intent_f16_gemm_kn (output staged through LDS, 8 columns per lane) into an output with
+    row stride N + 3 (element stores) or N + 8, over several row and column tiles and a
+    partial last column tile: every element against a float64 product, padding untouched."""
+    from intent_amd import _native
+    M, K, N = 600, 256, 520
+    tdt = torch.bfloat16 if epi == 2 else torch.float16
+    g = torch.Generator().manual_seed(epi * 10 + c_pad)
+    a = (torch.randn(M, K, generator=g) / (K ** 0.5)).to(tdt).cuda()
+    b = torch.randn(K, N, generator=g).to(tdt).cuda()
+    c = torch.full((M, N + c_pad), -5.0, dtype=tdt, device="cuda")
+    _native.call("intent_f16_gemm_kn", a.data_ptr(), M, K, K, b.data_ptr(), N, N, epi, c.data_ptr(), N + c_pad, 0)
+    torch.cuda.synchronize()
+    assert torch.all(c[:, N:] == -5.0)
+    full = a.double() @ b.double()
+    if epi == 1:
+        full = full.clamp_min(0.0)
+    assert (c[:, :N].double() - full).abs().max().item() <= 1e-2 * full.abs().max().item()
+
+
 # ---- NVFP4 quantizer --------------------------------------------------------------------
 
 @pytest.mark.parametrize("M,N,gsv", [(256, 128, 1.25), (300, 80, 1.25), (1, 16, 1.25), (8192, 4096, 1.25),
