@@ -302,8 +302,14 @@ struct RegRowsOperand {
 //     as two's complement (n - 2*(n & 8)) (weight_only_int4.py:54-91);
 //   kInt2: four 2-bit values (0..3) per byte, interleaved: k lives in byte
 //     (k/16)*4 + k%4 at bit 2*((k/4)%4) (weight_only_int4.py:94-124), so the
-//     16-k chunk c is packed dword c and output dword a is (d >> 2a) & 3s.
-enum class LowBit { kSignedNibble, kInt2 };
+//     16-k chunk c is packed dword c and output dword a is (d >> 2a) & 3s;
+//   kSignedNibbleX16: the signed nibbles of kSignedNibble placed in the high
+//     half of their bytes, i.e. decoded as 16 * value: no sign extension, and
+//     the int32 products are exact multiples of 16, so the accumulator shifted
+//     right by 4 is kSignedNibble's as long as it does not wrap
+//     (16 * 128 * 8 * K < 2^31, K <= kX16MaxK).
+enum class LowBit { kSignedNibble, kInt2, kSignedNibbleX16 };
+constexpr int64_t kX16MaxK = 131071;
 
 template <int ROWS, LowBit F, int NW = 4>
 struct LowBitRowsOperand {
@@ -311,7 +317,7 @@ struct LowBitRowsOperand {
   static_assert(N_INST * 8 * NW == ROWS, "tile rows must be a multiple of 8 per wave");
   static constexpr int NVM = N_INST;
   static constexpr int NDS = N_INST;
-  static constexpr int CHUNK_BYTES = F == LowBit::kSignedNibble ? 8 : 4;  // packed bytes per 16 k
+  static constexpr int CHUNK_BYTES = F == LowBit::kInt2 ? 4 : 8;  // packed bytes per 16 k
   static constexpr int STAGE_BYTES = 8 * CHUNK_BYTES;                     // per row per 128-k stage
   Rsrc rs;
   uint32_t voff[N_INST];
@@ -335,7 +341,7 @@ struct LowBitRowsOperand {
   INTENT_DEVICE void load(int kt, Regs& r) const {
 #pragma unroll
     for (int j = 0; j < N_INST; ++j) {
-      if constexpr (F == LowBit::kSignedNibble) {
+      if constexpr (F != LowBit::kInt2) {
         r.v[j] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff[j], (uint32_t)kt * STAGE_BYTES, 0);
       } else {
         r.v[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff[j], (uint32_t)kt * STAGE_BYTES, 0);
@@ -353,6 +359,15 @@ struct LowBitRowsOperand {
         hi |= ((hi >> 3) & 0x01010101u) * 0xF0u;
         out[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);      // k = 0, 1, 2, 3 of the dword
         out[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);  // k = 4, 5, 6, 7
+      }
+      return out;
+    } else if constexpr (F == LowBit::kSignedNibbleX16) {
+      u32x4 out;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t lo = (v[h] << 4) & 0xF0F0F0F0u, hi = v[h] & 0xF0F0F0F0u;
+        out[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+        out[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
       }
       return out;
     } else {

@@ -174,8 +174,11 @@ __global__ __launch_bounds__(T::NT, 1) void i8_gemm_kernel(const int8_t* __restr
 // BitNet int2 (weight_only_int4.py:94-124): out[m, n] = sum_k a[m, k] * W2[n, k]
 //   with weights 0..3 in the interleaved 2-bit packing.
 // The packed weights are decoded to int8 while staged into LDS; the rest is
-// the int8 pipeline above (128 k per stage, K % 128 == 0).
-template <class T, bool kBitNet>
+// the int8 pipeline above (128 k per stage, K % 128 == 0). For K <= kX16MaxK
+// the W4A8 nibbles are staged as 16 * value (LowBit::kSignedNibbleX16: two
+// logic ops per packed dword instead of a sign extension) and the int32
+// accumulators shifted right by 4 before the store.
+template <class T, bool kBitNet, bool kX16 = false>
 __global__ __launch_bounds__(T::NT, 1) void lowbit_gemm_kernel(const int8_t* __restrict__ act, int64_t ld_act,
                                                                int M, const uint8_t* __restrict__ wq,
                                                                int64_t ld_w, int N, int K,
@@ -198,11 +201,19 @@ __global__ __launch_bounds__(T::NT, 1) void lowbit_gemm_kernel(const int8_t* __r
     bop.init(wq, ld_w, N, c0, wave);
     mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc);
   } else {
-    mp::LowBitRowsOperand<T::BM, mp::LowBit::kSignedNibble, T::NW> aop;
+    mp::LowBitRowsOperand<T::BM, kX16 ? mp::LowBit::kSignedNibbleX16 : mp::LowBit::kSignedNibble, T::NW> aop;
     aop.init(wq, ld_w, N, r0, wave);
     mp::RegRowsOperand<T::BN, mp::DenseRows, false, T::NW> bop;
     bop.init(mp::DenseRows{act, ld_act, M}, c0, wave);
     mp::mainloop<T, mp::I8Math>(aop, bop, nk, buf0, buf1, acc);
+    if constexpr (kX16) {
+#pragma unroll
+      for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+        for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] >>= 4;  // exact: every product is a multiple of 16
+    }
   }
   store_tile<T, Epi::kI32Bias>(acc, r0, c0, rows, cols, nullptr, nullptr, nullptr, out, ldo);
 }
@@ -217,7 +228,7 @@ __global__ __launch_bounds__(T::NT, 1) void lowbit_gemm_kernel(const int8_t* __r
 // int32 of the output; BitNet's output is [M, N], the usual lane layout.
 using TWs = mp::Tile<256, 192, 2, 2>;  // consumers of 128 x 96
 
-template <class T, bool kBitNet>
+template <class T, bool kBitNet, bool kX16 = false>
 __global__ __launch_bounds__(T::NT_WS, 1) void lowbit_ws_kernel(const int8_t* __restrict__ act, int64_t ld_act, int M,
                                                                 const uint8_t* __restrict__ wq, int64_t ld_w, int N,
                                                                 int K, int32_t* __restrict__ out, int64_t ldo,
@@ -231,11 +242,21 @@ __global__ __launch_bounds__(T::NT_WS, 1) void lowbit_ws_kernel(const int8_t* __
   const int pw = T::wave() % T::NW;
   mp::DmaRowsOperand<T::BM, mp::DenseRows, T::NW> aop;
   aop.init(mp::DenseRows{act, ld_act, M}, m0, pw);
-  mp::LowBitRowsOperand<T::BN, kBitNet ? mp::LowBit::kInt2 : mp::LowBit::kSignedNibble, T::NW> bop;
+  constexpr mp::LowBit kFmt =
+      kBitNet ? mp::LowBit::kInt2 : (kX16 ? mp::LowBit::kSignedNibbleX16 : mp::LowBit::kSignedNibble);
+  mp::LowBitRowsOperand<T::BN, kFmt, T::NW> bop;
   bop.init(wq, ld_w, N, n0, pw);
   i32x16 acc[T::TI][T::TJ];
   if (!mp::mainloop_ws<T, mp::I8Math, 2, mp::DenseRows, decltype(bop), !kBitNet>(aop, bop, K / mp::ROWB, bufs, acc))
     return;
+  if constexpr (kX16) {
+#pragma unroll
+    for (int i = 0; i < T::TI; ++i)
+#pragma unroll
+      for (int j = 0; j < T::TJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] >>= 4;  // exact: every product is a multiple of 16
+  }
   if constexpr (kBitNet) {
     store_tile<T, Epi::kI32Bias>(acc, m0, n0, M, N, nullptr, nullptr, nullptr, out, ldo);
     return;
@@ -388,8 +409,12 @@ int launch_lowbit(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const uin
   const int mblocks = (int)((rows + T::BM - 1) / T::BM);
   const int64_t grid = (int64_t)mblocks * ((cols + T::BN - 1) / T::BN);
   INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
-  hipLaunchKernelGGL((lowbit_gemm_kernel<T, kBitNet>), dim3((unsigned)grid), dim3(T::NT), 0, (hipStream_t)stream, a,
-                     a_ld, (int)M, w, w_ld, (int)N, (int)K, out, out_ld, mblocks);
+  if (!kBitNet && K <= mp::kX16MaxK)
+    hipLaunchKernelGGL((lowbit_gemm_kernel<T, kBitNet, true>), dim3((unsigned)grid), dim3(T::NT), 0,
+                       (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, out, out_ld, mblocks);
+  else
+    hipLaunchKernelGGL((lowbit_gemm_kernel<T, kBitNet>), dim3((unsigned)grid), dim3(T::NT), 0, (hipStream_t)stream,
+                       a, a_ld, (int)M, w, w_ld, (int)N, (int)K, out, out_ld, mblocks);
   return intent::launch_status(name);
 }
 
@@ -421,8 +446,12 @@ int lowbit_entry(const int8_t* a, int64_t M, int64_t K, int64_t a_ld, const uint
     const int mblocks = (int)((M + TWs::BM - 1) / TWs::BM);
     const int64_t grid = (int64_t)mblocks * ((N + TWs::BN - 1) / TWs::BN);
     INTENT_REQUIRE(grid < (1ll << 31), INTENT_ERR_UNSUPPORTED, "%s: grid too large", name);
-    hipLaunchKernelGGL((lowbit_ws_kernel<TWs, kBitNet>), dim3((unsigned)grid), dim3(TWs::NT_WS), 0,
-                       (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, out, out_ld, mblocks);
+    if (!kBitNet && K <= mp::kX16MaxK)
+      hipLaunchKernelGGL((lowbit_ws_kernel<TWs, kBitNet, true>), dim3((unsigned)grid), dim3(TWs::NT_WS), 0,
+                         (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, out, out_ld, mblocks);
+    else
+      hipLaunchKernelGGL((lowbit_ws_kernel<TWs, kBitNet>), dim3((unsigned)grid), dim3(TWs::NT_WS), 0,
+                         (hipStream_t)stream, a, a_ld, (int)M, w, w_ld, (int)N, (int)K, out, out_ld, mblocks);
     return intent::launch_status(name);
   }
   return launch_lowbit<T128, kBitNet>(a, M, K, a_ld, w, N, w_ld, out, out_ld, stream, name);

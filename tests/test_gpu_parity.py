@@ -736,6 +736,25 @@ def test_w4a8_full_size_exact(gpu):
     assert torch.equal(got.to(torch.float64), ref)
 
 
+@pytest.mark.parametrize("M,N", [(64, 96), (4096, 4096)])
+@pytest.mark.parametrize("K", [130944, 131072])
+def test_w4a8_int32_extremes(gpu, M, N, K):
+    # Up to K = 130944 the kernels stage the nibbles as 16 * value and shift the
+    # accumulators right by 4; at the extreme operands (-128 x -8 every k) the
+    # scaled sum 16 * 1024 * K is then just below 2^31. K = 131072 takes the
+    # sign-extending decode. Small and large M, N cover both kernels.
+    a = torch.full((M, K), -128, dtype=torch.int8, device="cuda")
+    a[1::2] = 127
+    p = torch.full((N, K // 2), 0x88, dtype=torch.uint8, device="cuda")  # -8, -8
+    p[1::3] = 0x77  # 7, 7
+    got = art(intent.w4a8_packed_matmul).run(a, p)  # [N, M]
+    wv = torch.full((N,), -8, dtype=torch.int64, device="cuda")
+    wv[1::3] = 7
+    av = torch.full((M,), -128, dtype=torch.int64, device="cuda")
+    av[1::2] = 127
+    assert torch.equal(got.to(torch.int64), wv[:, None] * av[None, :] * K)
+
+
 # ---- MX block-scaled FP8 ------------------------------------------------------------
 
 def _mx_case(seed, M, K, N):
