@@ -765,7 +765,7 @@ INTENT_DEVICE void compute_stage_pairs(const char* buf, const uint32_t (&aaddr)[
         acc[i][j] = Math::mfma2(bf[s][0][j], bf[s][1][j], af[s][0][i], af[s][1][i], acc[i][j]);
   __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
   constexpr int PAIRS = NR < NM ? NR : NM;
-  static_for<0, PAIRS>([&](auto X) {
+  static_for_mp<0, PAIRS>([&](auto X) {
     constexpr int x = decltype(X)::value;
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, (x + 1) * NR / PAIRS - x * NR / PAIRS, 0);
