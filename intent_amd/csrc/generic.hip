@@ -14,6 +14,7 @@
 #include "common.h"
 #include "internal.h"
 
+#include <atomic>
 #include <type_traits>
 
 namespace {
@@ -120,6 +121,19 @@ int w8a16_generic_launch(const void* x, int64_t M, int64_t K, int64_t x_ld, cons
   hipLaunchKernelGGL(w8a16_generic_kernel, grid_for(M, N), dim3(kThreads), 0, (hipStream_t)stream, (const f16*)x,
                      x_ld, w, w_ld, (const f16*)scales, (int)K, (int)N, (f16*)y, y_ld);
   return launch_status("w8a16_generic_kernel");
+}
+
+int cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> known[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int n = known[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 0) n = 0;
+    known[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
 }
 
 int fill_launch(void* out, int64_t rows, int64_t cols, int64_t ld, int elem_bytes, uint32_t bits, void* stream) {

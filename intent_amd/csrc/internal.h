@@ -35,6 +35,10 @@ int launch_status_fmt(const char* fmt, ...) __attribute__((format(printf, 1, 2))
 // contraction over an empty K, which is its epilogue applied to zero.
 int fill_launch(void* out, int64_t rows, int64_t cols, int64_t ld, int elem_bytes, uint32_t bits, void* stream);
 
+// Compute units of the current device (queried once per device; 0 if the
+// query fails, which callers treat as "no round-fitting").
+int cu_count();
+
 }  // namespace intent
 
 #define INTENT_REQUIRE(cond, code, ...)            \

@@ -619,17 +619,12 @@ INTENT_DEVICE void store_rows_lds(char* smem, int m0, int n0, int M, int N, char
 }
 }  // namespace mxdma
 
-__global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
-                                                                const uint8_t* __restrict__ sa, int64_t ld_sa,
-                                                                const uint8_t* __restrict__ b, int64_t ldb, int N,
-                                                                const uint8_t* __restrict__ sb, int64_t ld_sb, int K,
-                                                                float* __restrict__ out, int64_t ldo, int mblocks) {
-  using T = mxdma::Tile;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * mxdma::kStage];
-  int tmb, tnb;
-  grid_tile(mblocks, 4, tmb, tnb);
-  const int m0 = tmb * T::BM;
-  const int n0 = tnb * T::BN;
+// One output tile of the MX product on dma_mainloop (four waves).
+template <class T>
+INTENT_DEVICE void mx_dma_tile(char* smem, const uint8_t* __restrict__ a, int64_t lda, int M,
+                               const uint8_t* __restrict__ sa, int64_t ld_sa, const uint8_t* __restrict__ b,
+                               int64_t ldb, int N, const uint8_t* __restrict__ sb, int64_t ld_sb, int K,
+                               float* __restrict__ out, int64_t ldo, int m0, int n0) {
   mxdma::Rows<T::BM, T::NW, true> aop;
   mxdma::Rows<T::BN, T::NW, true> bop;
   aop.init(a, lda, M, sa, ld_sa, m0, T::wave());
@@ -642,6 +637,31 @@ __global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* _
     return mxdma::Piece<4>{{(uint32_t)acc[i][j][4 * g], (uint32_t)acc[i][j][4 * g + 1], (uint32_t)acc[i][j][4 * g + 2],
                             (uint32_t)acc[i][j][4 * g + 3]}};
   });
+}
+
+// Workgroups 0 .. nbig-1 take the 256 x 256 tiles of columns [0, n_split)
+// (XCD-grouped order); the rest, dispatched last, take 256 x 128 tiles of
+// columns [n_split, N). The launch picks n_split so that the half-size tiles
+// fill what would otherwise be a partial last round of 256 x 256 tiles.
+using TMxHalf = mp::Tile<256, 128, 2, 2>;
+__global__ __launch_bounds__(256, 1) void mxfp8_gemm_dma_kernel(const uint8_t* __restrict__ a, int64_t lda, int M,
+                                                                const uint8_t* __restrict__ sa, int64_t ld_sa,
+                                                                const uint8_t* __restrict__ b, int64_t ldb, int N,
+                                                                const uint8_t* __restrict__ sb, int64_t ld_sb, int K,
+                                                                float* __restrict__ out, int64_t ldo, int mblocks,
+                                                                int nbig, int n_split) {
+  using T = mxdma::Tile;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * mxdma::kStage];
+  const int bid = blockIdx.x;
+  if (bid < nbig) {
+    int tmb, tnb;
+    grouped_tile(xcd_swizzle(bid, nbig), mblocks, nbig / mblocks, 4, tmb, tnb);
+    mx_dma_tile<T>(smem, a, lda, M, sa, ld_sa, b, ldb, N, sb, ld_sb, K, out, ldo, tmb * T::BM, tnb * T::BN);
+  } else {
+    const int t = bid - nbig;
+    mx_dma_tile<TMxHalf>(smem, a, lda, M, sa, ld_sa, b, ldb, N, sb, ld_sb, K, out, ldo, (t % mblocks) * TMxHalf::BM,
+                         n_split + (t / mblocks) * TMxHalf::BN);
+  }
 }
 
 // Per-tensor scaled FP8 GEMM with an f16 result (block_scaled.py:42-63 and,
@@ -1187,9 +1207,21 @@ extern "C" int intent_mxfp8_gemm(const uint8_t* a, int64_t M, int64_t K, int64_t
   const int64_t big = ((M + 255) / 256) * ((N + 255) / 256);
   if (big >= 256) {
     const int mblocks = (int)((M + 255) / 256);
+    const int nblocks = (int)((N + 255) / 256);
     INTENT_REQUIRE(big < (1ll << 31), INTENT_ERR_UNSUPPORTED, "mxfp8_gemm: grid too large");
-    hipLaunchKernelGGL(mxfp8_gemm_dma_kernel, dim3((unsigned)big), dim3(256), 0, (hipStream_t)stream, a, a_ld, (int)M,
-                       a_scales, a_scales_ld, b, b_ld, (int)N, b_scales, b_scales_ld, (int)K, out, out_ld, mblocks);
+    // One workgroup per CU: a last round of at most half the CUs is covered by
+    // half-width tiles instead (whole trailing column blocks of 256).
+    int split_cols = 0;
+    const int cus = intent::cu_count();
+    const int64_t tail = cus > 0 ? big % cus : 0;
+    if (tail > 0 && 2 * tail <= cus && tail % mblocks == 0 && tail / mblocks < nblocks)
+      split_cols = (int)(tail / mblocks);
+    const int nbig = mblocks * (nblocks - split_cols);
+    const int n_split = (nblocks - split_cols) * 256;
+    const int64_t nsmall = split_cols ? (int64_t)mblocks * ((N - n_split + TMxHalf::BN - 1) / TMxHalf::BN) : 0;
+    hipLaunchKernelGGL(mxfp8_gemm_dma_kernel, dim3((unsigned)(nbig + nsmall)), dim3(256), 0, (hipStream_t)stream, a,
+                       a_ld, (int)M, a_scales, a_scales_ld, b, b_ld, (int)N, b_scales, b_scales_ld, (int)K, out, out_ld,
+                       mblocks, nbig, n_split);
     return intent::launch_status("mxfp8_gemm");
   }
   return launch_mx<TMx128>(a, M, K, a_ld, a_scales, a_scales_ld, b, N, b_ld, b_scales, b_scales_ld, out, out_ld,

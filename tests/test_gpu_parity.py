@@ -770,7 +770,8 @@ def _mx_case(seed, M, K, N):
 
 @pytest.mark.parametrize("M,K,N,layout", [(64, 128, 64, "view"), (130, 256, 70, "view"), (512, 768, 512, "view"),
                                           (33, 384, 100, "contiguous"),
-                                          # 256 x 256 DMA-fed tiles: ragged edges, odd / even / single stage counts
+                                          # 256 x 256 DMA-fed tiles: ragged edges, odd / even / single stage counts;
+                                          # 272 tiles on 256 CUs: the last 16 as 32 half-width tiles
                                           (4000, 384, 4200, "view"), (4096, 256, 4096, "contiguous"),
                                           (4096, 128, 4352, "view")])
 def test_block_scaled_matmul(gpu, threads, M, K, N, layout):
