@@ -441,6 +441,7 @@ struct W4Operand {
   static constexpr int P = 32 / PIECE;                                                     // pieces per row per stage
   static constexpr int NS = ROWS * P / NT;                                                 // loads per thread per stage
   static_assert(NS * NT == ROWS * P, "W4 staging must divide evenly");
+  static_assert(P <= 8 && ROWS % (2 * (8 / P)) == 0 && NT % 16 == 0, "8-lane write blocks pair up over whole rows");
   static constexpr int NVM = 3 * NS;            // vector memory instructions per stage (at most)
   static constexpr int NVM_W = NS;              // ... of a windowed stage without group parameters
   static constexpr int NDS = NS * (PIECE / 4);  // LDS writes per stage
@@ -473,8 +474,15 @@ struct W4Operand {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int c = (int)(threadIdx.x % NT) + i * NT;
-      lrow[i] = c / P;
-      part[i] = c % P;
+      // The 16-byte LDS writes of 8 lanes (128 bytes) go out together; with
+      // c / P as the row, those 8 lanes would hold 8 / P consecutive rows, and
+      // rows 2m and 2m + 1 share swz, so their chunks would land on the same
+      // banks. Lanes are instead grouped so that an 8-lane block holds rows
+      // r0, r0 + 2, .. (distinct swz): block b takes rows (b & 1) +
+      // 2 * (8 / P) * (b >> 1) + 2k, k = 0 .. 8 / P - 1.
+      const int b = c >> 3, t = c & 7;
+      lrow[i] = (b & 1) + 2 * (8 / P) * (b >> 1) + 2 * (t / P);
+      part[i] = t % P;
       const int64_t w = wrow(lrow[i]);
       // gs == 32: a stage spans two groups; piece p starts at k = p * PIECE * 2.
       const int extra = !kWin && gsize == 32 ? (part[i] * PIECE * 2) / 32 : 0;
