@@ -47,6 +47,20 @@ INTENT_DEVICE int block_inclusive_scan(int v, int* wsum) {
   return v + (wave > 0 ? wsum[wave - 1] : 0);
 }
 
+// End of the member range: m1 = clampi(route_offsets[g + 1], m1, R) over the
+// groups g in order from m1 = m0 (as find_tile clamps it) equals
+// min(max(m0, max_g route_offsets[g + 1]), R): one block-wide max instead of
+// E dependent loads. Every thread of the workgroup calls it.
+INTENT_DEVICE int member_end(const int32_t* __restrict__ route_offsets, int E, int m0, int R, int* slot) {
+  if (threadIdx.x == 0) *slot = m0;
+  __syncthreads();
+  int mx = m0;
+  for (int g = threadIdx.x; g < E; g += blockDim.x) mx = max(mx, route_offsets[g + 1]);
+  atomicMax(slot, mx);
+  __syncthreads();
+  return min(*slot, R);
+}
+
 template <bool kLds>
 __global__ __launch_bounds__(kListThreads) void token_member_list_kernel(
     const int32_t* __restrict__ route_offsets, int E, const int32_t* __restrict__ members,
@@ -56,9 +70,9 @@ __global__ __launch_bounds__(kListThreads) void token_member_list_kernel(
   __shared__ int32_t wsum[kListThreads / 64];
   int32_t* cnt = kLds ? lds_cnt : count;
   const int tid = threadIdx.x;
+  __shared__ int m1_slot;
   const int m0 = clampi(route_offsets[0], 0, R);
-  int m1 = m0;  // end of the last non-empty group, as find_tile clamps it
-  for (int g = 0; g < E; ++g) m1 = clampi(route_offsets[g + 1], m1, R);
+  const int m1 = member_end(route_offsets, E, m0, R, &m1_slot);
   auto token_of = [&](int i) { return clampi(route_token[clampi(members[i], 0, NR - 1)], 0, T - 1); };
   for (int t = tid; t < T; t += kListThreads) cnt[t] = 0;
   __syncthreads();
@@ -96,6 +110,87 @@ __global__ __launch_bounds__(kListThreads) void token_member_list_kernel(
       list[c + 1] = v;
     }
   }
+}
+
+// The same list with every array in LDS (T, R <= kListLdsAll): the token of
+// each member is gathered once, all loads of a thread issued together (the
+// global-memory kernel above pays two dependent load latencies per member in
+// each of its passes, and its sort reads the list back from global memory);
+// counts, scan, placement and the per-token sort then run on LDS, and start /
+// list are written out at the end. The list is the same as the kernel above
+// produces: per token, its members in ascending index order.
+constexpr int kListLdsAll = 8192;
+constexpr int kListPer = kListLdsAll / kListThreads;  // members per thread
+
+__global__ __launch_bounds__(kListThreads) void token_member_list_lds_kernel(
+    const int32_t* __restrict__ route_offsets, int E, const int32_t* __restrict__ members,
+    const int32_t* __restrict__ route_token, int T, int R, int NR, int32_t* __restrict__ start_out,
+    int32_t* __restrict__ list_out) {
+  extern __shared__ int32_t list_lds[];
+  int32_t* cnt = list_lds;                 // T: counts, then placement cursors
+  int32_t* start = cnt + T;                // T + 1
+  int32_t* tok = start + T + 1;            // kListLdsAll: token of member m0 + j
+  int32_t* list = tok + kListLdsAll;       // kListLdsAll
+  __shared__ int32_t wsum[kListThreads / 64];
+  const int tid = threadIdx.x;
+  __shared__ int m1_slot;
+  const int m0 = clampi(route_offsets[0], 0, R);
+  const int m1 = member_end(route_offsets, E, m0, R, &m1_slot);
+  const int n = m1 - m0;  // <= R <= kListLdsAll
+  int mem[kListPer];
+#pragma unroll
+  for (int j = 0; j < kListPer; ++j) {
+    const int i = tid + j * kListThreads;
+    mem[j] = i < n ? members[m0 + i] : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < kListPer; ++j)
+    if (tid + j * kListThreads < n) mem[j] = route_token[clampi(mem[j], 0, NR - 1)];
+  for (int t = tid; t < T; t += kListThreads) cnt[t] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kListPer; ++j) {
+    const int i = tid + j * kListThreads;
+    if (i < n) {
+      const int t = clampi(mem[j], 0, T - 1);
+      tok[i] = t;
+      atomicAdd(&cnt[t], 1);
+    }
+  }
+  __syncthreads();
+  const int per = (T + kListThreads - 1) / kListThreads;
+  const int t0 = tid * per;
+  int sum = 0;
+  for (int t = t0; t < t0 + per && t < T; ++t) sum += cnt[t];
+  const int incl = block_inclusive_scan(sum, wsum);
+  int run = incl - sum;
+  if (tid == kListThreads - 1) start[T] = incl;
+  for (int t = t0; t < t0 + per && t < T; ++t) {
+    start[t] = run;
+    run += cnt[t];
+    cnt[t] = 0;
+  }
+  __syncthreads();
+  for (int i = tid; i < n; i += kListThreads) {
+    const int t = tok[i];
+    list[start[t] + atomicAdd(&cnt[t], 1)] = m0 + i;
+  }
+  __syncthreads();
+  for (int t = tid; t < T; t += kListThreads) {
+    const int b = start[t], e = start[t + 1];
+    for (int a = b + 1; a < e; ++a) {  // insertion sort: ascending member index
+      const int v = list[a];
+      int c = a - 1;
+      while (c >= b && list[c] > v) {
+        list[c + 1] = list[c];
+        --c;
+      }
+      list[c + 1] = v;
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t <= T; t += kListThreads) start_out[t] = start[t];
+  for (int i = tid; i < n; i += kListThreads) list_out[i] = list[i];
 }
 
 // y[t, d] += contrib[i, d] for the members i of token t in ascending order
@@ -197,8 +292,21 @@ extern "C" int intent_moe_expert_ffn(const void* x, int64_t T, int64_t D, int64_
                                                          D, s);
   st = intent::launch_status("grouped_kn_kernel<moe w2 weighted>");
   if (st != INTENT_OK) return st;
-  hipLaunchKernelGGL(T <= kListLdsTokens ? token_member_list_kernel<true> : token_member_list_kernel<false>, dim3(1), dim3(kListThreads), 0, s, route_offsets, (int)E,
-                     member_routes, route_token, (int)T, (int)R, (int)NR, count, start, list);
+  if (T <= kListLdsAll && R <= kListLdsAll) {
+    const size_t lds = sizeof(int32_t) * (size_t)(2 * T + 1 + 2 * kListLdsAll);
+    if (lds > 65536) {
+      const hipError_t e = hipFuncSetAttribute((const void*)token_member_list_lds_kernel,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      INTENT_REQUIRE(e == hipSuccess, INTENT_ERR_LAUNCH, "token_member_list: %zu bytes of LDS refused (%s)", lds,
+                     hipGetErrorString(e));
+    }
+    hipLaunchKernelGGL(token_member_list_lds_kernel, dim3(1), dim3(kListThreads), lds, s, route_offsets, (int)E,
+                       member_routes, route_token, (int)T, (int)R, (int)NR, start, list);
+  } else {
+    hipLaunchKernelGGL(T <= kListLdsTokens ? token_member_list_kernel<true> : token_member_list_kernel<false>, dim3(1),
+                       dim3(kListThreads), 0, s, route_offsets, (int)E, member_routes, route_token, (int)T, (int)R,
+                       (int)NR, count, start, list);
+  }
   st = intent::launch_status("token_member_list");
   if (st != INTENT_OK) return st;
   const int64_t items = T * ((D + 3) / 4);

@@ -13,7 +13,7 @@ import torch
 
 import intent_amd as intent
 import oracle
-from intent_amd import inputs
+from intent_amd import _native, inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -1216,6 +1216,42 @@ def test_moe_expert_ffn(gpu, threads, T, D, E, k, F, kind):
     assert_close_rms(got - y0, ref - y0, what=f"moe_expert_ffn {T}x{D}x{F}")
     again = _ffn_run(d, y0)
     assert np.array_equal(got, again), "the combine must be deterministic"
+
+
+@pytest.mark.parametrize("T,k", [(300, 2), (4096, 2), (8192, 1), (9000, 1), (5000, 2)])
+def test_moe_expert_ffn_member_list(gpu, T, k):
+    # The combine's per-token member list, read back from the workspace: for each token its
+    # members (positions in member_routes) in ascending order. T, R <= 8192 build it in LDS,
+    # larger ones in global memory (9000 x 1 and 5000 x 2 routes).
+    D, F, E = 64, 64, 4
+    d = inputs.moe_routes(T, k, E, "random", T)
+    R, NR = len(d["member_routes"]), len(d["route_token"])
+    dv = {key: torch.from_numpy(np.ascontiguousarray(v)).cuda() for key, v in d.items()}
+    x = torch.zeros(T, D, dtype=torch.float16, device="cuda")
+    w1 = torch.zeros(E, D, F, dtype=torch.float16, device="cuda")
+    w2 = torch.zeros(E, F, D, dtype=torch.float16, device="cuda")
+    y = torch.zeros(T, D, device="cuda")
+    lib = _native.library()
+    nbytes = int(lib.intent_moe_expert_ffn_workspace_size(T, R, D, F))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    _native.call("intent_moe_expert_ffn", x.data_ptr(), T, D, D, dv["route_offsets"].data_ptr(), E,
+                 dv["member_routes"].data_ptr(), R, dv["route_token"].data_ptr(), dv["route_weights"].data_ptr(), NR,
+                 w1.data_ptr(), w2.data_ptr(), F, y.data_ptr(), D, ws.data_ptr(), nbytes,
+                 torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    r256 = lambda v: (v + 255) // 256 * 256
+    o_start = r256(r256(r256(R * F * 2) + R * D * 4) + T * 4)
+    o_list = r256(o_start + (T + 1) * 4)
+    w = ws.cpu().numpy()
+    start = w[o_start:o_start + (T + 1) * 4].view(np.int32)
+    lst = w[o_list:o_list + R * 4].view(np.int32)
+    offs = d["route_offsets"]
+    tok = d["route_token"][d["member_routes"]]
+    members = np.arange(offs[0], offs[-1])
+    order = members[np.argsort(tok[members], kind="stable")]
+    counts = np.bincount(tok[members], minlength=T)
+    assert np.array_equal(start, np.r_[0, np.cumsum(counts)])
+    assert np.array_equal(lst[:len(order)], order)
 
 
 @pytest.mark.parametrize("T", [512, 4096])
