@@ -86,13 +86,6 @@ __global__ __launch_bounds__(256) void q8k_quantize_kernel(const float* __restri
 // v_dot4_i32_i8 (nibbles are non-negative, so signed bytes are exact); S and T
 // are summed over the record's four lanes (integer, exact); lane 4b computes
 // v_b and the wave adds v_b one record at a time into the row total.
-__device__ __forceinline__ int q4k_field(const u32x4 hdr, int r, int i) {
-  // Bytes 4..15 of the record are hdr dwords 1..3; byte k is (hdr[k/4] >> 8(k%4)).
-  auto byte = [&](int k) { return (int)((hdr[k >> 2] >> (8 * (k & 3))) & 255u); };
-  if (i < 4) return byte(4 + 4 * r + i) & 63;
-  const int t = i - 4;
-  return ((byte(12 + t) >> (4 * r)) & 15) | ((byte(4 + 4 * r + t) >> 6) << 4);
-}
 
 // v_b of the record pair a lane's quad works on (the same value in the four
 // lanes): hdr = bytes 0..15 of the Q4_K record, q0/q1 = packed group u
@@ -107,12 +100,30 @@ INTENT_DEVICE float record_value(const u32x4 hdr, const u32x4 q0, const u32x4 q1
     dlo = __builtin_amdgcn_sdot4((int)(qw[i] & 0x0F0F0F0Fu), (int)xqv[i], dlo, false);
     dhi = __builtin_amdgcn_sdot4((int)((qw[i] >> 4) & 0x0F0F0F0Fu), (int)xqv[8 + i], dhi, false);
   }
-  int S = q4k_field(hdr, 0, 2 * u) * dlo + q4k_field(hdr, 0, 2 * u + 1) * dhi;
-  int T = q4k_field(hdr, 1, 2 * u) * bsum_lo + q4k_field(hdr, 1, 2 * u + 1) * bsum_hi;
-  S += __shfl_xor(S, 1);
-  S += __shfl_xor(S, 2);
-  T += __shfl_xor(T, 1);
-  T += __shfl_xor(T, 2);
+  // The 6-bit scale sc[i] and min m[i] of sub-blocks i = 2u and 2u + 1
+  // (doc/dsl/quantized-operations.en.md:21-36), without branching on u: with
+  // t = i % 4, A = header byte 4 + t, B = byte 8 + t, C = byte 12 + t;
+  // i < 4: sc = A & 63, m = B & 63; i >= 4: sc = (C & 15) | (A >> 6) << 4,
+  // m = (C >> 4) | (B >> 6) << 4.
+  const bool high = u >= 2;
+  int sc[2], mn[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t sh = 8u * (uint32_t)((2 * u + h) & 3);
+    const uint32_t A = __builtin_amdgcn_ubfe(hdr[1], sh, 8);
+    const uint32_t B = __builtin_amdgcn_ubfe(hdr[2], sh, 8);
+    const uint32_t C = __builtin_amdgcn_ubfe(hdr[3], sh, 8);
+    sc[h] = (int)(high ? ((C & 15u) | ((A >> 6) << 4)) : (A & 63u));
+    mn[h] = (int)(high ? ((C >> 4) | ((B >> 6) << 4)) : (B & 63u));
+  }
+  // |products| < 2^22: 24-bit multiplies are exact
+  int S = __mul24(sc[0], dlo) + __mul24(sc[1], dhi);
+  int T = __mul24(mn[0], bsum_lo) + __mul24(mn[1], bsum_hi);
+  // sums over the quad (integer, so the order does not matter): quad_perm [1,0,3,2], [2,3,0,1]
+  S += __builtin_amdgcn_mov_dpp(S, 0xB1, 0xF, 0xF, false);
+  T += __builtin_amdgcn_mov_dpp(T, 0xB1, 0xF, 0xF, false);
+  S += __builtin_amdgcn_mov_dpp(S, 0x4E, 0xF, 0xF, false);
+  T += __builtin_amdgcn_mov_dpp(T, 0x4E, 0xF, 0xF, false);
   const float d = (float)bit_cast<f16>((uint16_t)(hdr[0] & 0xFFFFu));
   const float dmin = (float)bit_cast<f16>((uint16_t)(hdr[0] >> 16));
   const float p = __fmul_rn(d, (float)S);
