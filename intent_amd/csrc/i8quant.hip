@@ -75,7 +75,10 @@ __global__ __launch_bounds__(256) void i8_per_token_kernel(const uint16_t* __res
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       const int c = lane + 256 * i;
-      keep[i] = c < nchunks ? load16(xr + (int64_t)c * 8) : u32x4{0u, 0u, 0u, 0u};
+      // read once: non-temporal (19.7 -> 17.2 us at 4096 x 8192; the same hint on the
+      // int8 stores measured slower)
+      keep[i] = c < nchunks ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xr + (int64_t)c * 8))
+                            : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < R; ++i) amax = fmaxf(amax, chunk_absmax(keep[i], kBf16));

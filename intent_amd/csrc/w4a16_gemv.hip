@@ -120,6 +120,13 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_kernel(
 }
 
 
+// Cache policy of the packed-weight loads of the decode kernels: every weight
+// byte is read once per launch, so the loads are non-temporal (the NT bit of
+// the buffer instruction's cache-policy operand). Measured on the same box:
+// M = 1 3.30 -> 3.22 us, M = 16 6.99 -> 6.63 us. (Q4_K records, whose header
+// line is read by four lanes, measured 3% slower with it.)
+constexpr int kWeightPolicy = 2;
+
 // ---- 4 <= M <= 16: MFMA GEMV with every load issued up front ------------------
 // Same split and MFMA operand roles as w4a16_gemv_kernel: 16 weight rows per
 // workgroup, KW waves taking 128-wide K steps in turn, lane (r, quad) holding
@@ -229,13 +236,13 @@ __global__ __launch_bounds__(64 * KW) void w4a16_gemv_front_kernel(
     for (int h = 0; h < 2; ++h) {
       const int row = 8 * h + (lane >> 3);
       const int rr = n0 + row < N ? row : N - 1 - n0;
-      wl[h] = __builtin_amdgcn_raw_buffer_load_b128(wrs, rr * ldw + ls * 64 + (lane & 3) * 16, 0, 0);
+      wl[h] = __builtin_amdgcn_raw_buffer_load_b128(wrs, rr * ldw + ls * 64 + (lane & 3) * 16, 0, kWeightPolicy);
     }
   } else {
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
       const int s = min(step_of(wave, i), nsteps - 1);
-      wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo, s * 64, 0);
+      wv[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvo, s * 64, kWeightPolicy);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -571,7 +578,7 @@ __global__ __launch_bounds__(64 * WPB) void w4a16_gemv_dot_shared_kernel(
     const auto wr = make_rsrc(wq + (int64_t)n * ldw);
 #pragma unroll
     for (int i = 0; i < CH; ++i)
-      wv[r][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, cc[i] * 16, 0, 0);
+      wv[r][i] = __builtin_amdgcn_raw_buffer_load_b128(wr, cc[i] * 16, 0, kWeightPolicy);
   }
   __builtin_amdgcn_sched_barrier(0);
 
