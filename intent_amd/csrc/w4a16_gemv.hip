@@ -832,7 +832,7 @@ __global__ __launch_bounds__(64 * KW) void w8a16_gemv_kernel(const f16* __restri
   const int nsteps = K >> 6;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int s = wave; s < nsteps; s += KW) {
-    const u32x4 wv = load16(wrow + (int64_t)s * 64);
+    const u32x4 wv = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + (int64_t)s * 64));  // read once
     const u32x4 x0 = load16(xrow + (int64_t)s * 64);
     const u32x4 x1 = load16(xrow + (int64_t)s * 64 + 8);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(bit_cast<f16x8>(x0), int8x8_to_f16(wv[0], wv[1]), acc, 0, 0, 0);
