@@ -474,8 +474,8 @@ def decode_probe() -> None:
 
 def read_probe(steps: int) -> None:
     """Plain HBM read of the decode's bytes, without and with one small store per wave (a
-    GEMV writes its outputs, and a kernel's end waits for its stores), against the decode
-    GEMV, all rotated over the same copy count."""
+    GEMV writes its outputs, and a kernel's end waits for its stores), with plain and with
+    non-temporal loads, against the decode GEMV, all rotated over the same copy count."""
     import ctypes
 
     import torch
@@ -490,7 +490,7 @@ def read_probe(steps: int) -> None:
     sink = torch.zeros(words, dtype=torch.int32, device="cuda")
     lib = _native.library()
     results = {}
-    for store in (0, 1):
+    for store in (0, 1, 2, 3):  # bit 0: one store per wave; bit 1: non-temporal loads
         for unroll in (1, 2, 4, 8, 16):
             def make(buf, u=unroll, st_=store):
                 def go():
@@ -501,7 +501,7 @@ def read_probe(steps: int) -> None:
                         raise RuntimeError(_native.last_error())
                 return go
             ms = graph_time([make(b) for b in bufs], steps, 10)
-            name = f"hbm_read_probe_kernel<{unroll}, {'true' if store else 'false'}>"
+            name = f"hbm_read_probe_kernel<{unroll}, {store}>"
             results[name] = ms
             log(f"[probe] read unroll={unroll} store={store}: {ms * 1e3:.3f} us, "
                 f"{nbytes / (ms * 1e-3) / 1e9:.1f} GB/s")

@@ -22,7 +22,8 @@ extern "C" {
  * coincidence. store = 1: every wave also writes 8 bytes of its result to
  * sink[2w], sink[2w + 1] (w: the wave's index in the grid), as a GEMV writes
  * its outputs; sink_words must be at least 8 * ceil(bytes / (4096 * unroll)) (four waves per
- * workgroup).
+ * workgroup). store + 2 (2 or 3): the same with non-temporal loads (the cache policy of the
+ * decode kernels' weight loads).
  */
 int intent_hbm_read_probe(const void* buf, int64_t bytes, int unroll, int store, uint32_t* sink, int64_t sink_words,
                           void* stream);

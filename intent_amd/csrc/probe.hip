@@ -12,15 +12,16 @@
 
 namespace {
 
-template <int U, bool kStore>
+template <int U, int kMode>  // kMode bit 0: one store per wave; bit 1: non-temporal loads
 __global__ __launch_bounds__(256) void hbm_read_probe_kernel(const u32x4* __restrict__ src, int64_t n16,
                                                              uint32_t* __restrict__ sink) {
+  constexpr bool kStore = (kMode & 1) != 0, kNT = (kMode & 2) != 0;
   const int64_t base = (int64_t)blockIdx.x * 256 * U + threadIdx.x;
   u32x4 v[U];
 #pragma unroll
   for (int i = 0; i < U; ++i) {
     const int64_t idx = base + (int64_t)i * 256;
-    v[i] = idx < n16 ? src[idx] : u32x4{0u, 0u, 0u, 0u};
+    v[i] = idx < n16 ? (kNT ? __builtin_nontemporal_load(src + idx) : src[idx]) : u32x4{0u, 0u, 0u, 0u};
   }
   uint32_t s = 0;
 #pragma unroll
@@ -39,13 +40,16 @@ __global__ __launch_bounds__(256) void hbm_read_probe_kernel(const u32x4* __rest
 }
 
 template <int U>
-void launch_probe(const void* buf, int64_t n16, bool store, uint32_t* sink, hipStream_t st) {
+void launch_probe(const void* buf, int64_t n16, int mode, uint32_t* sink, hipStream_t st) {
   const int64_t per = 256 * U;
   const unsigned blocks = (unsigned)((n16 + per - 1) / per);
-  if (store)
-    hipLaunchKernelGGL((hbm_read_probe_kernel<U, true>), dim3(blocks), dim3(256), 0, st, (const u32x4*)buf, n16, sink);
-  else
-    hipLaunchKernelGGL((hbm_read_probe_kernel<U, false>), dim3(blocks), dim3(256), 0, st, (const u32x4*)buf, n16, sink);
+  const u32x4* src = (const u32x4*)buf;
+  switch (mode) {
+    case 0: hipLaunchKernelGGL((hbm_read_probe_kernel<U, 0>), dim3(blocks), dim3(256), 0, st, src, n16, sink); break;
+    case 1: hipLaunchKernelGGL((hbm_read_probe_kernel<U, 1>), dim3(blocks), dim3(256), 0, st, src, n16, sink); break;
+    case 2: hipLaunchKernelGGL((hbm_read_probe_kernel<U, 2>), dim3(blocks), dim3(256), 0, st, src, n16, sink); break;
+    default: hipLaunchKernelGGL((hbm_read_probe_kernel<U, 3>), dim3(blocks), dim3(256), 0, st, src, n16, sink); break;
+  }
 }
 
 // MFMA issue-rate probe: every wave runs `iters` rounds of four independent
@@ -107,9 +111,9 @@ extern "C" int intent_hbm_read_probe(const void* buf, int64_t bytes, int unroll,
                  "buffer must be 16-byte aligned, sink 4-byte aligned");
   INTENT_REQUIRE(unroll == 1 || unroll == 2 || unroll == 4 || unroll == 8 || unroll == 16, INTENT_ERR_UNSUPPORTED,
                  "unroll must be 1, 2, 4, 8 or 16, got %d", unroll);
-  INTENT_REQUIRE(store == 0 || store == 1, INTENT_ERR_INVALID_ARGUMENT, "store must be 0 or 1, got %d", store);
+  INTENT_REQUIRE(store >= 0 && store <= 3, INTENT_ERR_INVALID_ARGUMENT, "store must be 0..3, got %d", store);
   const int64_t waves = 4 * ((bytes + 4096LL * unroll - 1) / (4096LL * unroll));
-  const int64_t need = store ? 2 * waves : 256;
+  const int64_t need = (store & 1) ? 2 * waves : 256;
   INTENT_REQUIRE(sink_words >= need, INTENT_ERR_INVALID_ARGUMENT, "sink needs %lld words, got %lld", (long long)need,
                  (long long)sink_words);
   const int64_t n16 = bytes / 16;
@@ -121,5 +125,5 @@ extern "C" int intent_hbm_read_probe(const void* buf, int64_t bytes, int unroll,
     case 8: launch_probe<8>(buf, n16, store, sink, st); break;
     default: launch_probe<16>(buf, n16, store, sink, st); break;
   }
-  return intent::launch_status_fmt("hbm_read_probe_kernel<%d, %s>", unroll, store ? "true" : "false");
+  return intent::launch_status_fmt("hbm_read_probe_kernel<%d, %d>", unroll, store);
 }

@@ -131,7 +131,7 @@ def test_probe_checks():
     rp = "intent_hbm_read_probe"
     assert status(rp, P(FAKE), 4095, 1, 0, P(FAKE), 256, None) == e.INTENT_ERR_INVALID_ARGUMENT  # bytes % 16
     assert status(rp, P(FAKE), 4096, 3, 0, P(FAKE), 256, None) == e.INTENT_ERR_UNSUPPORTED  # unroll
-    assert status(rp, P(FAKE), 4096, 1, 2, P(FAKE), 256, None) == e.INTENT_ERR_INVALID_ARGUMENT  # store flag
+    assert status(rp, P(FAKE), 4096, 1, 4, P(FAKE), 256, None) == e.INTENT_ERR_INVALID_ARGUMENT  # store mode 0..3
     assert status(rp, P(FAKE), 4096, 1, 0, P(FAKE), 255, None) == e.INTENT_ERR_INVALID_ARGUMENT  # sink < 256
     # store mode: one workgroup of four waves per 4096 bytes at unroll 1, two words per wave
     assert status(rp, P(FAKE), 65536, 1, 1, P(FAKE), 127, None) == e.INTENT_ERR_INVALID_ARGUMENT
